@@ -1,0 +1,310 @@
+#!/usr/bin/env python
+"""Headline benchmark: packed decode attention on one MI355X (BASELINE config 2 by default).
+
+    python bench.py [--steps K] [--warmup W] [--config 2|3|4|5] [--cpu-baseline on|off]
+
+A step is one decode-attention call (rotate q, split-K page scan, merge + output
+rotation) over the whole batch, one new query token per sequence, with the
+packed pages already resident in HBM. Several identical copies of the page pool
+are rotated between steps so the 256 MB Infinity Cache cannot serve repeats.
+Prints ONE JSON line on stdout; details go to stderr.
+
+``value`` is decode tokens/s = B / step time (whole job, one GPU).
+``roofline.achieved`` is the algorithmic KV bytes of one step
+(sum_b L_b * Hkv * ((NB_K + 2) + (NB_V + 2)), the reference's traffic model,
+bench_packed_attention.py:91-98) divided by the mean duration of the page-scan
+kernel, timed with HIP events recorded on its stream around every launch.
+``cpu_baseline`` times the CPU restatement of the reference's CPU decode path
+(``tiled_compressed_attention``) on a bounded sample of page-table columns of
+the same workload and scales it to the full step.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode-attn tokens/s + HBM GB/s (% peak), 4-bit packed KV, 32k ctx, 1 GPU"
+HBM_PEAK_GBPS = 8000.0
+
+# BASELINE.json configs 2-5 (config 1 is the CPU plumbing/parity case).
+CONFIGS = {
+    2: dict(B=16, Hq=32, Hkv=8, D=128, L=32768, S=16, bwk=4, bwv=4, seed=1, table="contiguous",
+            data="outliers"),
+    3: dict(B=16, Hq=32, Hkv=8, D=128, L=32768, S=16, bwk=6, bwv=6, seed=2, table="contiguous",
+            data="outliers"),
+    4: dict(B=64, Hq=32, Hkv=8, D=128, L=None, S=16, bwk=4, bwv=4, seed=3, table="shuffled",
+            data="normal"),
+    5: dict(B=4, Hq=64, Hkv=8, D=128, L=131072, S=16, bwk=4, bwv=6, seed=4, table="contiguous",
+            data="lognormal_heads"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_workload(cfg: int, dev, copies: int):
+    """Pool pages for config ``cfg`` filled by the product append kernel, plus the query.
+
+    Seeded CPU generator: sequence lengths, page order, outlier channels, per-head
+    scales and q. K/V values are drawn on the device from a generator seeded with
+    the same seed (a billion CPU normals would take ~50 s) and cast to bf16.
+    """
+    import torch
+    from winnow_amd import packed_attention as pa
+    from winnow_amd import packed_backend as pb
+    from winnow_amd.packing import packed_bytes
+    from winnow_amd.quantizer import get_quantizer
+
+    c = CONFIGS[cfg]
+    B, Hq, Hkv, D, S = c["B"], c["Hq"], c["Hkv"], c["D"], c["S"]
+    g = torch.Generator().manual_seed(c["seed"])
+    gd = torch.Generator(device=dev).manual_seed(c["seed"])
+    if c["L"] is None:
+        lens = torch.randint(512, 65537, (B,), generator=g).tolist()
+    else:
+        lens = [c["L"]] * B
+    need = [(L + S - 1) // S for L in lens]
+    P = sum(need)
+    order = torch.randperm(P, generator=g) if c["table"] == "shuffled" else torch.arange(P)
+    table = torch.full((B, max(need)), -1, dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        table[b, :need[b]] = order[off:off + need[b]].to(torch.int32)
+        off += need[b]
+    # 1% of channels x10: max(1, round(0.01 * D)) = 1 channel per (kv head) for K and for V
+    n_out = max(1, round(0.01 * D))
+    k_ch = [torch.randperm(D, generator=g)[:n_out] for _ in range(Hkv)]
+    v_ch = [torch.randperm(D, generator=g)[:n_out] for _ in range(Hkv)]
+    head_std = torch.exp(torch.randn(B, Hkv, 2, generator=g) * 0.5)       # LogNormal(0, 0.5)
+    q = (torch.randn(B, Hq, 1, D, generator=g)).to(dev, torch.bfloat16)
+
+    kq = get_quantizer(c["bwk"], D, dev, 42)
+    vq = get_quantizer(c["bwv"], D, dev, 42)
+    nbk, nbv = packed_bytes(D, c["bwk"]), packed_bytes(D, c["bwv"])
+    kp = torch.zeros(P, Hkv, S, nbk, dtype=torch.uint8, device=dev)
+    vp = torch.zeros(P, Hkv, S, nbv, dtype=torch.uint8, device=dev)
+    kn = torch.zeros(P, Hkv, S, dtype=torch.float16, device=dev)
+    vn = torch.zeros(P, Hkv, S, dtype=torch.float16, device=dev)
+    dtable = table.to(dev)
+    sample = None
+    for b in range(B):
+        L = lens[b]
+        k = torch.randn(1, Hkv, L, D, generator=gd, device=dev)
+        v = torch.randn(1, Hkv, L, D, generator=gd, device=dev)
+        if c["data"] == "outliers":
+            for h in range(Hkv):
+                k[:, h, :, k_ch[h].to(dev)] *= 10
+                v[:, h, :, v_ch[h].to(dev)] *= 10
+        elif c["data"] == "lognormal_heads":
+            k *= head_std[b, :, 0].to(dev)[None, :, None, None]
+            v *= head_std[b, :, 1].to(dev)[None, :, None, None]
+        k, v = k.bfloat16(), v.bfloat16()
+        if b == 0:
+            sample = (k[:, :, :256].cpu(), v[:, :, :256].cpu())
+        pb.append_kv(k, v, kq, vq, kp, vp, kn, vn, dtable[b:b + 1],
+                     torch.zeros(1, dtype=torch.int32, device=dev))
+        del k, v
+    seq = torch.tensor(lens, dtype=torch.int32)
+    kvs = []
+    for i in range(copies):
+        t = (kp, kn, vp, vn) if i == 0 else tuple(x.clone() for x in (kp, kn, vp, vn))
+        kvs.append(pa.PackedKV(t[0], t[1], t[2], t[3], dtable, seq.to(dev), pa.Quantizer.from_tq(kq),
+                               pa.Quantizer.from_tq(vq), D, seq_lens_host=seq, page_table_host=table))
+    torch.cuda.synchronize()
+    return c, lens, q, kvs, (kq, vq), sample
+
+
+def kv_bytes(lens, Hkv, nbk, nbv):
+    return sum(lens) * Hkv * ((nbk + 2) + (nbv + 2))
+
+
+def parity(c, lens, q, kv, quants, sample):
+    """Same-run checks: two sequences' attention vs the CPU oracle on the same pages, and
+    the first 256 tokens of sequence 0 re-quantized by the oracle vs the pool bytes."""
+    import torch
+    sys.path.insert(0, str(ROOT / "tests"))
+    from adjudicate import adjudicate_codes
+    from cases import to_host
+    from oracle import attention as oa
+    from oracle import packing as opk
+    from oracle.quantizer import get_quantizer as oq
+    from winnow_amd import packed_attention as pa
+
+    D, S = c["D"], c["S"]
+    scale = oa.default_scale(D)
+    seqs = [0, len(lens) - 1]
+    got = pa.packed_decode_attention(q, kv, scale, out_dtype=torch.float32).cpu()[seqs]
+    sub = to_host(kv, seqs)
+    ref = oa.tiled_compressed_attention(q.float().cpu()[seqs], sub, scale)
+    err = (got - ref).abs().max().item()
+    ok = bool(torch.allclose(got, ref, atol=2e-3, rtol=1e-3))
+    f64 = oa.reconstruct_attention_f64(q.float().cpu()[seqs], sub, scale)
+    rel = ((got.double() - f64).norm() / f64.norm()).item()
+    flips = 0
+    for side, (src, quant, pages) in enumerate(((sample[0], oq(c["bwk"], D, 42), kv.k_pages),
+                                                (sample[1], oq(c["bwv"], D, 42), kv.v_pages))):
+        codes, _ = quant.quantize(src)                                   # (1, Hkv, 256, D)
+        ids = kv.page_table_host[0, :256 // S].long()
+        stored = pages[ids.to(pages.device)].cpu()                       # (16, Hkv, S, NB)
+        stored = torch.from_numpy(opk.unpack(stored.numpy(), quant.bit_width, D))
+        stored = stored.permute(1, 0, 2, 3).reshape(1, stored.shape[1], 256, D)
+        flips += adjudicate_codes(src, stored, codes, quant)
+    return {"attn_max_abs_err": err, "attn_within_2e-3_1e-3": ok, "rel_l2_vs_f64": rel,
+            "codes_checked": 2 * 256 * c["Hkv"] * D, "adjudicated_code_flips": flips}
+
+
+def cpu_baseline(c, lens, q, kv, budget_s: float):
+    """Oracle tiled CPU decode over a sample of page-table columns, scaled to the full step."""
+    import torch
+    from oracle import attention as oa
+
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    D, S, B = c["D"], c["S"], len(lens)
+    width = kv.page_table_host.shape[1]
+
+    def sample_kv(cols):
+        ids = kv.page_table_host[:, :cols].reshape(-1).long()
+        ids = ids.clamp(min=0)
+        dev_ids = ids.to(kv.k_pages.device)
+        table = torch.arange(B * cols, dtype=torch.int32).reshape(B, cols)
+        s_lens = torch.tensor([min(L, cols * S) for L in lens], dtype=torch.int32)
+        return oa.OracleKV(kv.k_pages[dev_ids].cpu(), kv.k_norms[dev_ids].cpu(), kv.v_pages[dev_ids].cpu(),
+                           kv.v_norms[dev_ids].cpu(), table, s_lens,
+                           oa.OracleQuant(kv.k_quant.Pi.cpu(), kv.k_quant.centroids.cpu(), kv.k_quant.bit_width),
+                           oa.OracleQuant(kv.v_quant.Pi.cpu(), kv.v_quant.centroids.cpu(), kv.v_quant.bit_width),
+                           D)
+
+    qc = q.float().cpu()
+    scale = oa.default_scale(D)
+    probe = sample_kv(4)
+    t0 = time.perf_counter()
+    oa.tiled_compressed_attention(qc, probe, scale)
+    per_col = (time.perf_counter() - t0) / 4
+    cols = int(max(8, min(width, budget_s / max(per_col, 1e-6))))
+    skv = sample_kv(cols)
+    t0 = time.perf_counter()
+    oa.tiled_compressed_attention(qc, skv, scale)
+    dt = time.perf_counter() - t0
+    t_step = dt / cols * width
+    return {"value": B / t_step, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"tiled_compressed_attention (torch CPU fp32) over {cols} of {width} page-table "
+                      f"columns of the same batch ({dt:.1f} s), scaled x{width / cols:.1f} to the full step",
+            "ms_per_step": t_step * 1e3}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--copies", type=int, default=2)
+    ap.add_argument("--splits", type=int, default=None)
+    ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
+    ap.add_argument("--parity", choices=["on", "off"], default="on")
+    args = ap.parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); the "
+              f"decode path has no collective, see DESIGN.md for how it would shard", file=sys.stderr)
+        return 2
+
+    import torch
+    from winnow_amd import packed_attention as pa
+    from winnow_amd.packing import packed_bytes
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    c, lens, q, kvs, quants, sample = build_workload(args.config, dev, args.copies)
+    log(f"workload config {args.config} built in {time.time() - t0:.1f} s: B={len(lens)} sum(L)={sum(lens)}")
+    D, Hkv, Hq = c["D"], c["Hkv"], c["Hq"]
+    nbk, nbv = packed_bytes(D, c["bwk"]), packed_bytes(D, c["bwv"])
+    bytes_step = kv_bytes(lens, Hkv, nbk, nbv)
+    scale = 1.0 / math.sqrt(D)
+    B = len(lens)
+    max_pages = kvs[0].page_table.shape[1]
+    pps, ns = pa.decode_plan(B, Hkv, max_pages, args.splits)
+    ws = torch.empty(pa.workspace_bytes(B, Hq, Hkv, D, ns), dtype=torch.uint8, device=dev)
+    for kv in kvs:
+        pa.check_kernel_contract(q, kv)          # full validation once, outside the timed region
+
+    def step(i, evs=None):
+        return pa.packed_decode_attention(q, kvs[i % len(kvs)], scale, num_splits=args.splits,
+                                          workspace=ws, check_ranges=False, timing_events=evs)
+
+    for i in range(args.warmup):
+        step(i)
+    ev_pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for _ in range(args.steps)]
+    for e0, e1 in ev_pairs:                       # materialise the underlying hipEvents
+        e0.record()
+        e1.record()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(args.steps):
+        e0, e1 = ev_pairs[i]
+        step(i, (ctypes.c_void_p(e0.cuda_event), ctypes.c_void_p(e1.cuda_event)))
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    kern = [e0.elapsed_time(e1) for e0, e1 in ev_pairs]
+    kern_ms = statistics.fmean(kern)
+    log(f"step {ms * 1e3:.1f} us; page-scan kernel mean {kern_ms * 1e3:.1f} us "
+        f"(median {statistics.median(kern) * 1e3:.1f}); plan {ns} splits x {pps} pages")
+    achieved = bytes_step / (kern_ms * 1e-3) / 1e9
+
+    par = parity(c, lens, q, kvs[0], quants, sample) if args.parity == "on" else None
+    if par:
+        log(f"parity: {par}")
+    cpu = cpu_baseline(c, lens, q, kvs[0], args.cpu_budget) if args.cpu_baseline == "on" else None
+    if cpu:
+        log(f"cpu baseline: {cpu}")
+
+    result = {
+        "metric": METRIC,
+        "value": B / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: bf16 K/V ~N(0,1) (config-specific outliers/scales), seeded; packed by the "
+                "product append kernel; q ~N(0,1) bf16",
+        "config": {"workload": f"BASELINE config {args.config}", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+                   "head_dim": D, "seq_len": c["L"] or "U[512,65536]", "sum_seq_len": sum(lens),
+                   "page_size": c["S"], "bits_k": c["bwk"], "bits_v": c["bwv"], "table": c["table"],
+                   "splits": ns, "pages_per_split": pps, "pool_copies": len(kvs)},
+        "step_GBps": bytes_step / (ms * 1e-3) / 1e9,
+        "kv_tokens_per_s": sum(lens) / (ms * 1e-3),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "decode_split_kernel", "kernel_us": kern_ms * 1e3,
+                     "algorithmic_bytes": bytes_step},
+        "cpu_baseline": cpu,
+        "parity": par,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,142 @@
+/*
+ * winnow_hip.h -- C ABI of the MI355X (gfx950) TurboQuant packed decode path.
+ *
+ * Every entry point is extern "C", takes plain device pointers, element or
+ * byte strides and sizes, returns 0 on success or a negative WN_E* code, and
+ * never aborts; wn_last_error() then holds a thread-local message. Nothing
+ * here allocates device memory: outputs and scratch are caller-owned (query
+ * the scratch size with wn_decode_workspace_bytes). Work is enqueued on the
+ * hipStream_t passed as `stream` (NULL = the default stream), in order, with
+ * no host synchronisation.
+ *
+ * Layouts (the reference's, byte for byte):
+ *   pages  (P, Hkv, S, NB) uint8, NB = D*bw/8, codes LSB-first along D
+ *   norms  (P, Hkv, S)     fp16 (passed as uint16 bits)
+ *   page_table (B, max_pages) int32, -1 past a sequence's last page
+ *   seq_lens   (B,) int32
+ * The (S, NB) rows of one (page, head) are contiguous; page and head strides
+ * are free, so one layer of a (layers, P, Hkv, S, NB) pool is passed as is.
+ *
+ * Reference interfaces replaced (paths relative to lgoyal6/winnow):
+ *   wn_decode_attention      turboquant_kv/packed_attention_triton.py:180-187
+ *                            (packed_decode_attention; kernels :51-159,
+ *                            host launch :204-262)
+ *   wn_append_kv             turboquant_kv/packed_backend.py:155-161
+ *                            (PagedPackedCache.update: quantize, pack, scatter)
+ *   wn_quantize              turboquant_kv/cache.py:108-115 (TurboQuantMSE.quantize)
+ *   wn_pack / wn_unpack      turboquant_kv/packing.py:37-89
+ *   wn_dequantize            turboquant_kv/cache.py:117-131
+ *                            (TurboQuantMSE.dequantize_into)
+ */
+#ifndef WINNOW_HIP_H
+#define WINNOW_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WN_ABI_VERSION 1
+
+/* element types of floating-point tensors crossing the ABI */
+enum { WN_F32 = 0, WN_F16 = 1, WN_BF16 = 2 };
+
+/* status codes */
+enum {
+  WN_OK = 0,
+  WN_E_INVALID = -1,     /* argument outside the supported contract        */
+  WN_E_UNSUPPORTED = -2, /* shape/width combination not compiled           */
+  WN_E_WORKSPACE = -3,   /* workspace missing or too small                 */
+  WN_E_LAUNCH = -4       /* the HIP runtime reported an error              */
+};
+
+/* ABI version of the loaded library (WN_ABI_VERSION). */
+int wn_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* wn_last_error(void);
+
+/* Split-K plan for a decode step: pages per split and number of splits.
+ * requested_splits > 0 asks for exactly that many splits over max_pages (the
+ * reference's num_splits, packed_attention_triton.py:211-216); 0 lets the
+ * library size splits to fill the GPU. */
+int wn_decode_plan(int B, int Hkv, int max_pages, int requested_splits,
+                   int* pages_per_split, int* num_splits);
+
+/* Bytes of scratch wn_decode_attention needs for this shape and split count:
+ * the rotated query plus compact per-split (acc, m, l) partials of the real
+ * query heads (B*Hq*num_splits rows). */
+int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int num_splits);
+
+/* Decode attention over paged packed K/V, one query token per sequence.
+ *   q      (B, Hq, D) with element strides q_stride_b, q_stride_h (last dim
+ *          contiguous), element type q_dtype
+ *   out    (B, Hq, D) contiguous, element type out_dtype
+ *   out = softmax(scale * q k_hat^T) v_hat computed in the quantizer bases:
+ *   q_rot = scale * q Pi_K^T; per key s = n_K (q_rot . c_K); online softmax
+ *   over pages; a = sum p n_V c_V; out = (a / l) Pi_V. Rows with no key are 0.
+ *   pages_per_split / num_splits come from wn_decode_plan.
+ *   ev_begin / ev_end (hipEvent_t or NULL) are recorded on `stream` around
+ *   the split-K page-scan kernel only, for in-situ timing of that kernel. */
+int wn_decode_attention(
+    const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+    const float* pi_k, const float* pi_v,
+    const float* codebook_k, const float* codebook_v,
+    const uint8_t* k_pages, int64_t k_stride_p, int64_t k_stride_h,
+    const uint8_t* v_pages, int64_t v_stride_p, int64_t v_stride_h,
+    const uint16_t* k_norms, int64_t kn_stride_p, int64_t kn_stride_h,
+    const uint16_t* v_norms, int64_t vn_stride_p, int64_t vn_stride_h,
+    const int32_t* page_table, int64_t table_stride_b,
+    const int32_t* seq_lens,
+    void* out, int out_dtype,
+    void* workspace, int64_t workspace_bytes,
+    int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
+    float scale, int pages_per_split, int num_splits,
+    void* stream, void* ev_begin, void* ev_end);
+
+/* Quantize, bit-pack and scatter n new tokens per sequence into pool pages,
+ * K and V in one launch (v may be NULL to append K only).
+ *   k, v       (B, Hkv, n, D) with element strides (s_b, s_h, s_n), last dim
+ *              contiguous, element type x_dtype
+ *   token i of sequence b lands at pos = start_pos[b] + i:
+ *              page page_table[b, pos / S], slot pos % S
+ *   per vector: n = max(||x||, 1e-10); y = (x / n) Pi^T; code = #{boundary < y};
+ *   the packed row goes to pages, fp16(n) to norms. max_pages is the width of
+ *   page_table; vectors whose position falls outside it, or whose page id is
+ *   outside [0, num_pages), are not written. */
+int wn_append_kv(
+    const void* k, int64_t ks_b, int64_t ks_h, int64_t ks_n,
+    const void* v, int64_t vs_b, int64_t vs_h, int64_t vs_n, int x_dtype,
+    const float* pi_k, const float* boundaries_k, int bw_k,
+    const float* pi_v, const float* boundaries_v, int bw_v,
+    const int32_t* page_table, int64_t table_stride_b,
+    const int32_t* start_pos,
+    uint8_t* k_pages, int64_t k_stride_p, int64_t k_stride_h,
+    uint8_t* v_pages, int64_t v_stride_p, int64_t v_stride_h,
+    uint16_t* k_norms, int64_t kn_stride_p, int64_t kn_stride_h,
+    uint16_t* v_norms, int64_t vn_stride_p, int64_t vn_stride_h,
+    int B, int Hkv, int n, int D, int S, int num_pages, int max_pages, void* stream);
+
+/* TurboQuantMSE.quantize on `rows` contiguous-D vectors at x + r*row_stride
+ * (elements): codes (rows, D) uint8 and fp32 norms (rows,). */
+int wn_quantize(const void* x, int x_dtype, int64_t rows, int64_t row_stride,
+                const float* pi, const float* boundaries, int bw, int D,
+                uint8_t* codes, float* norms, void* stream);
+
+/* Bit packing of contiguous (rows, D) uint8 codes <-> (rows, D*bw/8) bytes. */
+int wn_pack(const uint8_t* codes, int64_t rows, int D, int bw, uint8_t* packed, void* stream);
+int wn_unpack(const uint8_t* packed, int64_t rows, int D, int bw, uint8_t* codes, void* stream);
+
+/* TurboQuantMSE.dequantize_into: out = (centroids[codes] Pi) * norm for
+ * (rows, D) uint8 codes and fp16 norms; out (rows, D) contiguous of out_dtype. */
+int wn_dequantize(const uint8_t* codes, const uint16_t* norms, int64_t rows,
+                  const float* pi, const float* centroids, int bw, int D,
+                  void* out, int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WINNOW_HIP_H */

@@ -1,0 +1,83 @@
+"""The C-ABI library loads on the host and exports exactly what include/winnow_hip.h declares.
+
+No compute call is made here (there is no GPU in the CPU suite); only host-side
+entry points that touch no device (version, error string, split planning,
+workspace sizing, argument validation) are exercised.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "winnow_hip.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wn_[a-z_0-9]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from winnow_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} is not built: run `python -m winnow_amd.build`")
+    return _lib.lib()
+
+
+def test_header_declares_the_expected_entry_points():
+    names = declared_symbols()
+    for must in ("wn_abi_version", "wn_last_error", "wn_decode_plan", "wn_decode_workspace_bytes",
+                 "wn_decode_attention", "wn_append_kv", "wn_quantize", "wn_pack", "wn_unpack",
+                 "wn_dequantize"):
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    from winnow_amd import _lib
+    for name in declared_symbols():
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_abi_version_and_error_string(lib):
+    assert lib.wn_abi_version() == 1
+    assert isinstance(lib.wn_last_error(), bytes)
+
+
+def test_plan_reference_semantics(lib):
+    from winnow_amd.packed_attention import decode_plan
+    # explicit splits: clamp to [1, max_pages], cdiv(max_pages, splits) pages each
+    assert decode_plan(2, 4, 10, 3) == (4, 3)
+    assert decode_plan(2, 4, 10, 50) == (1, 10)
+    assert decode_plan(2, 4, 0, 1) == (1, 1)
+    # automatic: every plan covers the table
+    for B, Hkv, mp in ((16, 8, 2048), (4, 8, 8192), (64, 8, 4096), (1, 8, 64), (1, 1, 1)):
+        pps, ns = decode_plan(B, Hkv, mp)
+        assert pps * ns >= mp and pps >= 1 and ns >= 1
+        assert (ns - 1) * pps < max(mp, 1)
+
+
+def test_workspace_bytes(lib):
+    from winnow_amd.packed_attention import workspace_bytes
+    w1 = workspace_bytes(16, 32, 8, 128, 32)
+    w2 = workspace_bytes(16, 32, 8, 128, 64)
+    assert w2 > w1 > 16 * 32 * 32 * 128 * 4
+    assert lib.wn_decode_workspace_bytes(16, 30, 8, 128, 4) == -1     # Hq % Hkv
+
+
+def test_argument_errors_are_reported_not_fatal(lib):
+    from winnow_amd import _lib
+    with pytest.raises(_lib.WinnowHipError, match="bit width"):
+        _lib.call("wn_pack", None, 1, 128, 7, None, None)
+    assert b"bit width" in lib.wn_last_error()
+    with pytest.raises(_lib.WinnowHipError, match="head_dim"):
+        _lib.call("wn_quantize", None, 0, 1, 128, None, None, 4, 96, None, None, None)
+    # empty work is a successful no-op and clears the error
+    _lib.call("wn_pack", None, 0, 128, 4, None, None)
+    assert lib.wn_last_error() == b""

@@ -1,0 +1,178 @@
+"""GPU parity: the HIP packed decode attention vs the CPU oracle on identical inputs.
+
+Mirrors ``test_packed_attention_triton.py``: the frozen ``CASES`` matrix with
+its seeds (:51-68) at one, three and automatic splits; the bf16 output dtype
+(:86-92); a strided pool-layer view with a storage offset (:95-105); rejection
+before launch (:108-114); and extra memory that does not grow with history
+(:176-198). The bar is the north star's: fp32 output within 2e-3 max-abs and
+1e-3 relative of the oracle's fp32 tiled path (``tiled_compressed_attention``,
+packed_attention.py:260-311); rows of empty sequences are exactly zero.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from cases import CASE_SEEDS, CASES, build, to_device, to_host
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+RTOL = 1e-3
+DEV = "cuda"
+
+
+def _pa():
+    from winnow_amd import packed_attention as pa
+    return pa
+
+
+def _check(got, ref, lens=None):
+    got = got.float().cpu()
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs().max().item()
+    assert torch.allclose(got, ref, atol=ATOL, rtol=RTOL), f"max abs err {err:.3e}"
+    if lens is not None:
+        for b, L in enumerate(lens):
+            if L == 0:
+                assert (got[b] == 0).all()
+    return err
+
+
+@pytest.mark.parametrize("splits", [None, 1, 3])
+@pytest.mark.parametrize("name,B,Hq,Hkv,D,lens,S,bw,qs", CASES, ids=[c[0] for c in CASES])
+def test_kernel_matches_oracle(name, B, Hq, Hkv, D, lens, S, bw, qs, splits):
+    print(f"case {name} splits={splits}", flush=True)
+    q, kv = build(CASE_SEEDS[name], B, Hq, Hkv, D, lens, S, bw, qs)
+    scale = oa.default_scale(D)
+    ref = oa.tiled_compressed_attention(q, kv, scale)
+    got = _pa().packed_decode_attention(q.to(DEV), to_device(kv, DEV), scale, num_splits=splits,
+                                        out_dtype=torch.float32)
+    _check(got, ref, lens)
+
+
+@pytest.mark.parametrize("bwk,bwv,Hq,Hkv", [(6, 6, 32, 8), (4, 6, 64, 8), (2, 2, 16, 4), (5, 5, 8, 4),
+                                             (6, 4, 32, 8), (4, 8, 32, 8), (4, 4, 32, 2), (4, 4, 32, 16)])
+def test_widths_and_groups(bwk, bwv, Hq, Hkv):
+    """Every compiled width pair and GQA group size (n_rep 1..16), ragged lengths, S=16."""
+    print(f"widths {bwk}/{bwv} Hq={Hq} Hkv={Hkv}", flush=True)
+    lens = (0, 1, 15, 16, 17, 333, 1024)
+    q, kv = build(300 + bwk * 10 + bwv, len(lens), Hq, Hkv, 128, lens, 16, bwk, bw_v=bwv)
+    scale = oa.default_scale(128)
+    ref = oa.tiled_compressed_attention(q, kv, scale)
+    for splits in (None, 2):
+        got = _pa().packed_decode_attention(q.to(DEV), to_device(kv, DEV), scale, num_splits=splits,
+                                            out_dtype=torch.float32)
+        _check(got, ref, lens)
+
+
+def test_config1_plumbing():
+    """B1, 8/8 heads, D128, L1024, fp32 ~N(0,1) seed 0, 4-bit, S16."""
+    g = torch.Generator().manual_seed(0)
+    k = torch.randn(1, 8, 1024, 128, generator=g)
+    v = torch.randn(1, 8, 1024, 128, generator=g)
+    q = torch.randn(1, 8, 1, 128, generator=g)
+    from oracle.quantizer import get_quantizer
+    kq = vq = get_quantizer(4, 128, 42)
+    kv = oa.pages_from_dense(k, v, [1024], kq, vq, 16, generator=g)
+    scale = oa.default_scale(128)
+    ref = oa.tiled_compressed_attention(q, kv, scale)
+    got = _pa().packed_decode_attention(q.to(DEV), to_device(kv, DEV), scale, out_dtype=torch.float32)
+    _check(got, ref)
+    f64 = oa.reconstruct_attention_f64(q, kv, scale)
+    rel = ((got.double().cpu() - f64).norm() / f64.norm()).item()
+    print(f"config1 rel-L2 vs float64: {rel:.3e}")
+    assert rel < 1e-5
+
+
+def test_bf16_query_output_dtype():
+    q, kv = build(3, 2, 28, 4, 128, (60, 9), 16, 8)
+    scale = oa.default_scale(128)
+    got = _pa().packed_decode_attention(q.to(DEV, torch.bfloat16), to_device(kv, DEV), scale)
+    assert got.dtype == torch.bfloat16
+    ref = oa.tiled_compressed_attention(q.bfloat16().float(), kv, scale)
+    assert (got.float().cpu() - ref).abs().max() < 2e-2
+
+
+def test_fp16_query():
+    q, kv = build(31, 2, 32, 8, 128, (200, 90), 16, 4)
+    scale = oa.default_scale(128)
+    got = _pa().packed_decode_attention(q.to(DEV, torch.float16), to_device(kv, DEV), scale,
+                                        out_dtype=torch.float32)
+    ref = oa.tiled_compressed_attention(q.half().float(), kv, scale)
+    _check(got, ref)
+
+
+def test_strided_pool_layer_view():
+    """Pages handed over as one layer of a (layers, P, ...) pool tensor."""
+    q, kv = build(4, 2, 8, 2, 64, (45, 20), 16, 8)
+    dkv = to_device(kv, DEV)
+
+    def stack(t):
+        return torch.stack([torch.zeros_like(t), t, torch.zeros_like(t)])[1]
+
+    pa = _pa()
+    kv2 = pa.PackedKV(stack(dkv.k_pages), stack(dkv.k_norms), stack(dkv.v_pages), stack(dkv.v_norms),
+                      dkv.page_table, dkv.seq_lens, dkv.k_quant, dkv.v_quant, dkv.head_dim)
+    assert kv2.k_pages.storage_offset() > 0
+    scale = oa.default_scale(64)
+    got = pa.packed_decode_attention(q.to(DEV), kv2, scale, out_dtype=torch.float32)
+    _check(got, oa.tiled_compressed_attention(q, kv, scale))
+
+
+def test_rejects_before_launch():
+    pa = _pa()
+    q, kv = build(5, 2, 8, 2, 64, (20, 3), 16, 8)
+    with pytest.raises(pa.UnsupportedLayout):
+        pa.packed_decode_attention(q.repeat(1, 1, 2, 1).to(DEV), to_device(kv, DEV), 1.0)   # Q=2
+    q2, kv2 = build(6, 2, 8, 2, 64, (20, 3), 8, 8)                                          # S=8
+    with pytest.raises(pa.UnsupportedLayout):
+        pa.packed_decode_attention(q2.to(DEV), to_device(kv2, DEV), 1.0)
+    with pytest.raises(pa.UnsupportedLayout):
+        pa.packed_decode_attention(q.to(DEV), to_device(kv, DEV), 1.0, pages_per_iter=3)
+    bad = to_device(kv, DEV)
+    bad.page_table_host = bad.page_table_host.clone()
+    bad.page_table_host[0, 0] = bad.k_pages.shape[0]
+    with pytest.raises(pa.UnsupportedLayout):
+        pa.packed_decode_attention(q.to(DEV), bad, 1.0)
+    with pytest.raises(pa.UnsupportedLayout):
+        pa.packed_decode_attention(q.cpu(), kv, 1.0)                                       # host tensors
+
+
+def test_extra_memory_does_not_grow_with_history():
+    """Temporary allocation is set by batch, heads and splits, not sequence length."""
+    pa = _pa()
+    B, Hq, Hkv, D = 8, 28, 4, 128
+    extras = {}
+    for L in (1024, 16384):
+        q, kv = build(9, B, Hq, Hkv, D, (L,) * B, 32, 8)
+        kvd, qd = to_device(kv, DEV), q.to(DEV, torch.bfloat16)
+        pa.packed_decode_attention(qd, kvd, 0.1, num_splits=4)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        pa.packed_decode_attention(qd, kvd, 0.1, num_splits=4)
+        torch.cuda.synchronize()
+        extras[L] = torch.cuda.max_memory_allocated() - base
+    history_16k = B * Hkv * 16384 * D * 2
+    assert extras[16384] <= 1.05 * extras[1024], extras
+    assert extras[16384] < history_16k / 50, (extras, history_16k)
+
+
+def test_split_invariance_and_sampled_oracle_long():
+    """Long context through many splits: every split plan agrees, and two sequences
+    checked against the oracle on the same pages."""
+    pa = _pa()
+    lens = (8192, 5000, 1, 7777)
+    q, kv = build(77, 4, 32, 8, 128, lens, 16, 4)
+    dkv = to_device(kv, DEV)
+    qd = q.to(DEV)
+    scale = oa.default_scale(128)
+    outs = [pa.packed_decode_attention(qd, dkv, scale, num_splits=s, out_dtype=torch.float32).cpu()
+            for s in (None, 1, 7, 512)]
+    for o in outs[1:]:
+        assert (o - outs[0]).abs().max() < 1e-5
+    sub = to_host(dkv, [0, 3])
+    ref = oa.tiled_compressed_attention(q[[0, 3]], sub, scale)
+    _check(outs[0][[0, 3]], ref)

@@ -1,0 +1,505 @@
+// Decode attention over paged packed K/V for gfx950 (CDNA4, wave64).
+//
+// Three launches per step, all on the caller's stream:
+//   1. rotate_q_kernel     q_rot = scale * q Pi_K^T, padded to NREP rows per kv head
+//   2. decode_split_kernel one work-group per (split, kv head, sequence) scans its
+//                          page range once for all NREP query heads of the group:
+//                          score phase (lane = token), online softmax, value
+//                          phase (16 lanes per token row), then a cross-wave
+//                          max-stable merge into one compact (acc, m, l) partial
+//   3. merge_kernel        max-stable merge of the split partials, 1/l, a Pi_V,
+//                          cast to the output type
+// Algebra follows turboquant_kv/packed_attention.py:260-334 (the schedule the
+// reference kernel packed_attention_triton.py:51-159 implements).
+#include "wn_common.h"
+
+namespace wn {
+namespace {
+
+constexpr int kBlock = 256;  // 4 waves
+
+struct DecodeArgs {
+  const float* q_rot;  // (B, Hkv, NREP, D) fp32
+  const uint8_t* k_pages;
+  const uint8_t* v_pages;
+  const uint16_t* k_norms;
+  const uint16_t* v_norms;
+  const float* cb_k;
+  const float* cb_v;
+  const int32_t* table;
+  const int32_t* seq_lens;
+  float* part_acc;  // (B*Hkv*num_splits*n_rep, D)
+  float* part_ml;   // (B*Hkv*num_splits*n_rep, 2)
+  int64_t ksp, ksh, vsp, vsh;  // page strides, bytes
+  int64_t knp, knh, vnp, vnh;  // norm strides, elements
+  int64_t tsb;                 // page-table row stride, elements
+  int Hkv, n_rep, log2S, pages_per_split, num_splits;
+};
+
+// The bytes holding codes [8*g, 8*g+8) of a row: exactly BW bytes at byte
+// offset g*BW, loaded with the widest accesses their alignment allows.
+template <int BW>
+__device__ __forceinline__ void load_group(const uint8_t* p, uint32_t (&v)[2]) {
+  if constexpr (BW == 8) {
+    uint2 x = *reinterpret_cast<const uint2*>(p);
+    v[0] = x.x;
+    v[1] = x.y;
+  } else if constexpr (BW == 4) {
+    v[0] = *reinterpret_cast<const uint32_t*>(p);
+    v[1] = 0;
+  } else if constexpr (BW == 2) {
+    v[0] = *reinterpret_cast<const uint16_t*>(p);
+    v[1] = 0;
+  } else if constexpr (BW == 6) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+    v[0] = uint32_t(h[0]) | (uint32_t(h[1]) << 16);
+    v[1] = h[2];
+  } else if constexpr (BW == 3) {
+    v[0] = uint32_t(p[0]) | (uint32_t(p[1]) << 8) | (uint32_t(p[2]) << 16);
+    v[1] = 0;
+  } else {  // 5
+    v[0] = uint32_t(p[0]) | (uint32_t(p[1]) << 8) | (uint32_t(p[2]) << 16) | (uint32_t(p[3]) << 24);
+    v[1] = p[4];
+  }
+}
+
+// A whole packed row (NB bytes, NB a multiple of 8) into registers.
+template <int NB>
+__device__ __forceinline__ void load_row(const uint8_t* p, uint32_t (&w)[NB / 4]) {
+  if constexpr (NB % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < NB / 16; ++i) {
+      uint4 x = reinterpret_cast<const uint4*>(p)[i];
+      w[4 * i] = x.x;
+      w[4 * i + 1] = x.y;
+      w[4 * i + 2] = x.z;
+      w[4 * i + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NB / 8; ++i) {
+      uint2 x = reinterpret_cast<const uint2*>(p)[i];
+      w[2 * i] = x.x;
+      w[2 * i + 1] = x.y;
+    }
+  }
+}
+
+struct RotArgs {
+  const void* q;
+  int64_t qsb, qsh;  // element strides of q (B, Hq, D)
+  const float* pi_k;
+  float* q_rot;
+  float scale;
+  int Hkv, n_rep, q_dtype;
+};
+
+// q_rot[b, kvh, h, :] = scale * q[b, kvh*n_rep + h, :] Pi_K^T (zero rows for h >= n_rep).
+template <int D, int NREP>
+__global__ __launch_bounds__(D) void rotate_q_kernel(RotArgs a) {
+  __shared__ float qs[NREP][D];
+  const int kvh = blockIdx.x, b = blockIdx.y, j = threadIdx.x;
+#pragma unroll
+  for (int h = 0; h < NREP; ++h)
+    qs[h][j] = h < a.n_rep ? load_elem(a.q, b * a.qsb + int64_t(kvh * a.n_rep + h) * a.qsh + j, a.q_dtype) : 0.f;
+  __syncthreads();
+  float acc[NREP];
+#pragma unroll
+  for (int h = 0; h < NREP; ++h) acc[h] = 0.f;
+  const float4* row = reinterpret_cast<const float4*>(a.pi_k + int64_t(j) * D);
+#pragma unroll 4
+  for (int d4 = 0; d4 < D / 4; ++d4) {
+    const float4 p = row[d4];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+      acc[h] = fmaf(qs[h][4 * d4 + 0], p.x, acc[h]);
+      acc[h] = fmaf(qs[h][4 * d4 + 1], p.y, acc[h]);
+      acc[h] = fmaf(qs[h][4 * d4 + 2], p.z, acc[h]);
+      acc[h] = fmaf(qs[h][4 * d4 + 3], p.w, acc[h]);
+    }
+  }
+  float* out = a.q_rot + (int64_t(b) * a.Hkv + kvh) * NREP * D;
+#pragma unroll
+  for (int h = 0; h < NREP; ++h) out[h * D + j] = acc[h] * a.scale;
+}
+
+template <int D, int BWK, int BWV, int NREP>
+__global__ __launch_bounds__(kBlock) void decode_split_kernel(DecodeArgs a) {
+  constexpr int NBK = D * BWK / 8;
+  constexpr int NBV = D * BWV / 8;
+  constexpr int G = D / 8;     // lanes per token row in the value phase (8 dims each)
+  constexpr int TPS = 64 / G;  // token rows per value step
+  constexpr int LK = 1 << BWK, LV = 1 << BWV;
+
+  __shared__ float cbk[LK];
+  __shared__ float cbv[LV];
+  __shared__ float pw[4][64][NREP];  // p * n_V per token of the wave's chunk
+  __shared__ int pidl[4][64];        // page id per token of the chunk
+  __shared__ float red_m[4][NREP], red_l[4][NREP];
+  __shared__ float red_acc[4][NREP][D];
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int S = 1 << a.log2S;
+  const int L = a.seq_lens[b];
+  const int n_pages = (L + S - 1) >> a.log2S;
+  const int page_lo = split * a.pages_per_split;
+  if (page_lo >= n_pages) return;  // block-uniform: this split is past the sequence
+  const int page_hi = min(page_lo + a.pages_per_split, n_pages);
+  const int t_lo = page_lo << a.log2S;
+  const int t_hi = min(page_hi << a.log2S, L);
+
+  for (int i = tid; i < LK; i += kBlock) cbk[i] = a.cb_k[i];
+  for (int i = tid; i < LV; i += kBlock) cbv[i] = a.cb_v[i];
+  __syncthreads();
+
+  const float* __restrict__ qp = a.q_rot + (int64_t(b) * a.Hkv + kvh) * NREP * D;
+  const int32_t* __restrict__ trow = a.table + b * a.tsb;
+  const uint8_t* kbase = a.k_pages + kvh * a.ksh;
+  const uint8_t* vbase = a.v_pages + kvh * a.vsh;
+  const uint16_t* knb = a.k_norms + kvh * a.knh;
+  const uint16_t* vnb = a.v_norms + kvh * a.vnh;
+
+  float m[NREP], l[NREP], acc[NREP][8];
+#pragma unroll
+  for (int h = 0; h < NREP; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
+  }
+  const int tsub = lane / G, dg = lane % G;
+
+  for (int c0 = t_lo + w * 64; c0 < t_hi; c0 += 4 * 64) {
+    // ---- score phase: lane = token
+    const int t = c0 + lane;
+    const bool valid = t < t_hi;
+    int pid = 0;
+    float nv = 0.f;
+    float s[NREP];
+    if (valid) {
+      pid = trow[t >> a.log2S];
+      const int slot = t & (S - 1);
+      uint32_t kw[NBK / 4];
+      load_row<NBK>(kbase + pid * a.ksp + slot * NBK, kw);
+      const float nk = f16_to_f32(knb[pid * a.knp + slot]);
+      nv = f16_to_f32(vnb[pid * a.vnp + slot]);
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) s[h] = 0.f;
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const float c = cbk[code_at<BWK>(kw, d)];
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) s[h] = fmaf(qp[h * D + d], c, s[h]);
+      }
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) s[h] *= nk;
+    } else {
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) s[h] = -INFINITY;
+    }
+
+    wave_lds_sync();  // the previous chunk's value phase has read pw / pidl
+    float alpha[NREP];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+      const float mn = fmaxf(m[h], wave_max(s[h]));  // finite: lane 0 of a chunk is valid
+      alpha[h] = expf(m[h] - mn);                     // 0 on the first chunk (m = -inf)
+      const float p = valid ? expf(s[h] - mn) : 0.f;
+      l[h] = l[h] * alpha[h] + wave_sum(p);
+      m[h] = mn;
+      pw[w][lane][h] = p * nv;
+    }
+    pidl[w][lane] = pid;
+    wave_lds_sync();
+
+    // ---- value phase: G lanes per token row, 8 dims per lane
+#pragma unroll
+    for (int h = 0; h < NREP; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[h][i] *= alpha[h];
+#pragma unroll 2
+    for (int j = 0; j < 64 / TPS; ++j) {
+      const int tl = j * TPS + tsub;
+      const int tt = c0 + tl;
+      if (tt < t_hi) {
+        const int pv = pidl[w][tl];
+        uint32_t vb[2];
+        load_group<BWV>(vbase + pv * a.vsp + (tt & (S - 1)) * NBV + dg * BWV, vb);
+        float wv[NREP];
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) wv[h] = pw[w][tl][h];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float c = cbv[code_at<BWV>(vb, i)];
+#pragma unroll
+          for (int h = 0; h < NREP; ++h) acc[h][i] = fmaf(wv[h], c, acc[h][i]);
+        }
+      }
+    }
+  }
+
+  // Token subgroups of a wave share m: plain sums.
+#pragma unroll
+  for (int o = G; o < 64; o <<= 1)
+#pragma unroll
+    for (int h = 0; h < NREP; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[h][i] += __shfl_xor(acc[h][i], o, 64);
+  if (lane < G) {
+#pragma unroll
+    for (int h = 0; h < NREP; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) red_acc[w][h][dg * 8 + i] = acc[h][i];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+      red_m[w][h] = m[h];
+      red_l[w][h] = l[h];
+    }
+  }
+  __syncthreads();
+
+  // Max-stable merge of the four waves; a wave that saw no chunk has m = -inf.
+  const int64_t row0 = ((int64_t(b) * a.Hkv + kvh) * a.num_splits + split) * a.n_rep;
+  for (int e = tid; e < a.n_rep * D; e += kBlock) {
+    const int h = e / D, d = e % D;
+    float M = red_m[0][h];
+#pragma unroll
+    for (int ww = 1; ww < 4; ++ww) M = fmaxf(M, red_m[ww][h]);
+    float af = 0.f, lf = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float mw = red_m[ww][h];
+      if (mw != -INFINITY) {
+        const float sc = expf(mw - M);
+        af = fmaf(sc, red_acc[ww][h][d], af);
+        lf = fmaf(sc, red_l[ww][h], lf);
+      }
+    }
+    a.part_acc[(row0 + h) * D + d] = af;
+    if (d == 0) {
+      a.part_ml[2 * (row0 + h)] = M;
+      a.part_ml[2 * (row0 + h) + 1] = lf;
+    }
+  }
+}
+
+struct MergeArgs {
+  const float* part_acc;
+  const float* part_ml;
+  const float* pi_v;
+  const int32_t* seq_lens;
+  void* out;
+  int out_dtype, Hq, Hkv, n_rep, log2S, pages_per_split, num_splits;
+};
+
+// out[b, kvh*n_rep + h, :] = (sum_s w_s acc_s / sum_s w_s l_s) Pi_V, w_s = exp(m_s - max m),
+// zero when no key was seen (packed_attention_triton.py:137-159 plus :261).
+template <int D>
+__global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
+  __shared__ float av[16][D];
+  const int kvh = blockIdx.x, b = blockIdx.y, j = threadIdx.x;
+  const int S = 1 << a.log2S;
+  const int L = a.seq_lens[b];
+  const int n_pages = (L + S - 1) >> a.log2S;
+  const int nsb = (n_pages + a.pages_per_split - 1) / a.pages_per_split;
+  for (int h = 0; h < a.n_rep; ++h) {
+    const int64_t base = (int64_t(b) * a.Hkv + kvh) * a.num_splits * a.n_rep + h;
+    float M = -INFINITY;
+    for (int s = 0; s < nsb; ++s) M = fmaxf(M, a.part_ml[2 * (base + int64_t(s) * a.n_rep)]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < nsb; ++s) {
+      const int64_t r = base + int64_t(s) * a.n_rep;
+      const float mm = a.part_ml[2 * r];
+      if (mm == -INFINITY) continue;
+      const float wgt = expf(mm - M);
+      den = fmaf(wgt, a.part_ml[2 * r + 1], den);
+      num = fmaf(wgt, a.part_acc[r * D + j], num);
+    }
+    av[h][j] = den > 0.f ? num / fmaxf(den, 1e-30f) : 0.f;
+  }
+  __syncthreads();
+  for (int h = 0; h < a.n_rep; ++h) {
+    float o = 0.f;
+#pragma unroll 8
+    for (int d = 0; d < D; ++d) o = fmaf(av[h][d], a.pi_v[d * D + j], o);
+    store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + j, a.out_dtype, o);
+  }
+}
+
+using SplitFn = void (*)(DecodeArgs);
+using RotFn = void (*)(RotArgs);
+
+template <int D, int BWK, int BWV>
+SplitFn pick_nrep(int nrep) {
+  switch (nrep) {
+    case 1: return decode_split_kernel<D, BWK, BWV, 1>;
+    case 2: return decode_split_kernel<D, BWK, BWV, 2>;
+    case 4: return decode_split_kernel<D, BWK, BWV, 4>;
+    case 8: return decode_split_kernel<D, BWK, BWV, 8>;
+    case 16: return decode_split_kernel<D, BWK, BWV, 16>;
+  }
+  return nullptr;
+}
+
+template <int D>
+SplitFn pick_split(int bwk, int bwv, int nrep) {
+  if (bwk == bwv) {
+    switch (bwk) {
+      case 2: return pick_nrep<D, 2, 2>(nrep);
+      case 3: return pick_nrep<D, 3, 3>(nrep);
+      case 4: return pick_nrep<D, 4, 4>(nrep);
+      case 5: return pick_nrep<D, 5, 5>(nrep);
+      case 6: return pick_nrep<D, 6, 6>(nrep);
+      case 8: return pick_nrep<D, 8, 8>(nrep);
+    }
+    return nullptr;
+  }
+  if constexpr (D == 128) {
+    if (bwk == 4 && bwv == 6) return pick_nrep<D, 4, 6>(nrep);
+    if (bwk == 6 && bwv == 4) return pick_nrep<D, 6, 4>(nrep);
+    if (bwk == 4 && bwv == 8) return pick_nrep<D, 4, 8>(nrep);
+  }
+  return nullptr;
+}
+
+template <int D>
+RotFn pick_rot(int nrep) {
+  switch (nrep) {
+    case 1: return rotate_q_kernel<D, 1>;
+    case 2: return rotate_q_kernel<D, 2>;
+    case 4: return rotate_q_kernel<D, 4>;
+    case 8: return rotate_q_kernel<D, 8>;
+    case 16: return rotate_q_kernel<D, 16>;
+  }
+  return nullptr;
+}
+
+int pad_nrep(int n_rep) {
+  int p = 1;
+  while (p < n_rep) p <<= 1;
+  return p;
+}
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+struct WsLayout {
+  int64_t qrot, acc, ml, total;
+};
+
+WsLayout ws_layout(int B, int Hq, int Hkv, int D, int num_splits) {
+  WsLayout l;
+  const int nrp = pad_nrep(Hq / Hkv);
+  l.qrot = 0;
+  l.acc = align256(int64_t(B) * Hkv * nrp * D * 4);
+  l.ml = l.acc + align256(int64_t(B) * Hq * num_splits * D * 4);
+  l.total = l.ml + align256(int64_t(B) * Hq * num_splits * 2 * 4);
+  return l;
+}
+
+}  // namespace
+}  // namespace wn
+
+extern "C" int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int num_splits) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || D <= 0 || num_splits <= 0) return -1;
+  return wn::ws_layout(B, Hq, Hkv, D, num_splits).total;
+}
+
+extern "C" int wn_decode_attention(
+    const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+    const float* pi_k, const float* pi_v, const float* codebook_k, const float* codebook_v,
+    const uint8_t* k_pages, int64_t k_stride_p, int64_t k_stride_h,
+    const uint8_t* v_pages, int64_t v_stride_p, int64_t v_stride_h,
+    const uint16_t* k_norms, int64_t kn_stride_p, int64_t kn_stride_h,
+    const uint16_t* v_norms, int64_t vn_stride_p, int64_t vn_stride_h,
+    const int32_t* page_table, int64_t table_stride_b, const int32_t* seq_lens,
+    void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
+    int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
+    float scale, int pages_per_split, int num_splits,
+    void* stream, void* ev_begin, void* ev_end) {
+  using namespace wn;
+  clear_error();
+  WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, WN_E_INVALID,
+             "decode: need B>=0, Hq%%Hkv==0 (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
+  const int n_rep = Hq / Hkv;
+  WN_REQUIRE(n_rep <= 16, WN_E_UNSUPPORTED, "decode: n_rep=%d > 16 not compiled", n_rep);
+  WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "decode: head_dim %d not compiled (64, 128)", D);
+  WN_REQUIRE(valid_bw(bw_k) && valid_bw(bw_v), WN_E_INVALID, "decode: bit widths %d/%d", bw_k, bw_v);
+  WN_REQUIRE(is_pow2(S), WN_E_INVALID, "decode: page size %d is not a power of two", S);
+  WN_REQUIRE(q_dtype >= WN_F32 && q_dtype <= WN_BF16 && out_dtype >= WN_F32 && out_dtype <= WN_BF16,
+             WN_E_INVALID, "decode: dtype codes %d/%d", q_dtype, out_dtype);
+  WN_REQUIRE(pages_per_split > 0 && num_splits > 0 &&
+                 int64_t(pages_per_split) * num_splits >= int64_t(max_pages),
+             WN_E_INVALID, "decode: plan %d x %d does not cover %d pages", num_splits, pages_per_split,
+             max_pages);
+  if (B == 0) return WN_OK;
+  WN_REQUIRE(q && pi_k && pi_v && codebook_k && codebook_v && k_pages && v_pages && k_norms &&
+                 v_norms && page_table && seq_lens && out,
+             WN_E_INVALID, "decode: null operand");
+  const int nbk = D * bw_k / 8, nbv = D * bw_v / 8;
+  const int row_align = (nbk % 16 == 0) ? 16 : 8;
+  WN_REQUIRE(aligned(k_pages, row_align) && k_stride_p % row_align == 0 && k_stride_h % row_align == 0,
+             WN_E_INVALID, "decode: K pages need %d-byte aligned base and strides", row_align);
+  WN_REQUIRE(aligned(v_pages, 8) && v_stride_p % 8 == 0 && v_stride_h % 8 == 0, WN_E_INVALID,
+             "decode: V pages need 8-byte aligned base and strides");
+  WN_REQUIRE(k_stride_h >= int64_t(S) * nbk && v_stride_h >= int64_t(S) * nbv, WN_E_INVALID,
+             "decode: head stride smaller than one (S, NB) page block");
+  WN_REQUIRE(aligned(pi_k, 16) && aligned(pi_v, 4), WN_E_INVALID, "decode: rotation alignment");
+
+  const int nrp = pad_nrep(n_rep);
+  SplitFn split = D == 128 ? pick_split<128>(bw_k, bw_v, nrp) : pick_split<64>(bw_k, bw_v, nrp);
+  RotFn rot = D == 128 ? pick_rot<128>(nrp) : pick_rot<64>(nrp);
+  WN_REQUIRE(split && rot, WN_E_UNSUPPORTED, "decode: (D=%d, bw_k=%d, bw_v=%d) not compiled", D, bw_k,
+             bw_v);
+
+  const WsLayout lay = ws_layout(B, Hq, Hkv, D, num_splits);
+  WN_REQUIRE(workspace && workspace_bytes >= lay.total && aligned(workspace, 256), WN_E_WORKSPACE,
+             "decode: workspace needs %lld bytes, 256-aligned (got %lld)", (long long)lay.total,
+             (long long)workspace_bytes);
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  RotArgs ra{q, q_stride_b, q_stride_h, pi_k, reinterpret_cast<float*>(ws + lay.qrot), scale, Hkv, n_rep,
+             q_dtype};
+  hipLaunchKernelGGL(rot, dim3(Hkv, B), dim3(D), 0, st, ra);
+
+  DecodeArgs da;
+  da.q_rot = ra.q_rot;
+  da.k_pages = k_pages;
+  da.v_pages = v_pages;
+  da.k_norms = k_norms;
+  da.v_norms = v_norms;
+  da.cb_k = codebook_k;
+  da.cb_v = codebook_v;
+  da.table = page_table;
+  da.seq_lens = seq_lens;
+  da.part_acc = reinterpret_cast<float*>(ws + lay.acc);
+  da.part_ml = reinterpret_cast<float*>(ws + lay.ml);
+  da.ksp = k_stride_p;
+  da.ksh = k_stride_h;
+  da.vsp = v_stride_p;
+  da.vsh = v_stride_h;
+  da.knp = kn_stride_p;
+  da.knh = kn_stride_h;
+  da.vnp = vn_stride_p;
+  da.vnh = vn_stride_h;
+  da.tsb = table_stride_b;
+  da.Hkv = Hkv;
+  da.n_rep = n_rep;
+  da.log2S = ilog2(S);
+  da.pages_per_split = pages_per_split;
+  da.num_splits = num_splits;
+  if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
+  hipLaunchKernelGGL(split, dim3(num_splits, Hkv, B), dim3(kBlock), 0, st, da);
+  if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
+
+  MergeArgs ma{da.part_acc, da.part_ml, pi_v, seq_lens, out, out_dtype, Hq, Hkv, n_rep, da.log2S,
+               pages_per_split, num_splits};
+  if (D == 128)
+    hipLaunchKernelGGL(merge_kernel<128>, dim3(Hkv, B), dim3(128), 0, st, ma);
+  else
+    hipLaunchKernelGGL(merge_kernel<64>, dim3(Hkv, B), dim3(64), 0, st, ma);
+  return check_launch("wn_decode_attention");
+}

@@ -1,0 +1,96 @@
+// Shared device helpers and host error plumbing for the gfx950 TurboQuant path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/winnow_hip.h"
+
+namespace wn {
+
+// ---------------------------------------------------------------- host errors
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define WN_REQUIRE(cond, code, ...)         \
+  do {                                      \
+    if (!(cond)) {                          \
+      ::wn::set_error(__VA_ARGS__);         \
+      return (code);                        \
+    }                                       \
+  } while (0)
+
+int check_launch(const char* what);
+
+inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+inline int ilog2(int64_t x) {
+  int r = 0;
+  while ((int64_t(1) << r) < x) ++r;
+  return r;
+}
+inline bool valid_bw(int bw) { return bw == 2 || bw == 3 || bw == 4 || bw == 5 || bw == 6 || bw == 8; }
+inline bool aligned(const void* p, int a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// ------------------------------------------------------------- device helpers
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, uint32_t(b) << 16);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return float(__builtin_bit_cast(_Float16, h));
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {  // round to nearest even
+  return __builtin_bit_cast(uint16_t, _Float16(f));
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {  // round to nearest even, NaN kept quiet
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
+  if (dtype == WN_F32) return static_cast<const float*>(p)[i];
+  if (dtype == WN_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+__device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float v) {
+  if (dtype == WN_F32) static_cast<float*>(p)[i] = v;
+  else if (dtype == WN_BF16) static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+  else static_cast<uint16_t*>(p)[i] = f32_to_f16(v);
+}
+
+// Code `d` of a row held as little-endian 32-bit words, LSB-first, BW bits per
+// code; codes may straddle a word. With `d` known at compile time this folds
+// to one bit-field extract (or an align + mask on a straddle).
+template <int BW, int NW>
+__device__ __forceinline__ uint32_t code_at(const uint32_t (&w)[NW], int d) {
+  const int bit = d * BW;
+  const int wi = bit >> 5, sh = bit & 31;
+  uint32_t v = w[wi] >> sh;
+  if (sh + BW > 32) v |= w[wi + 1] << (32 - sh);
+  return v & ((1u << BW) - 1u);
+}
+
+// Wave-wide (64 lanes) reductions.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Orders this wave's LDS writes before its later LDS reads (no block barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace wn

@@ -1,0 +1,282 @@
+"""Decode attention over paged packed KV, computed in the compressed domain on MI355X.
+
+Drop-in for the operator API of ``turboquant_kv/packed_attention.py`` (the
+``UnsupportedLayout`` error, the ``Quantizer`` / ``PackedKV`` / ``DenseKV``
+handles, ``check_contract``, ``kv_head_for``, ``default_scale``) and of
+``turboquant_kv/packed_attention_triton.py`` (``packed_decode_attention``,
+``check_kernel_contract``). The algebra is the reference's
+(packed_attention.py:1-21):
+
+    q . k_hat_j = n_K,j (q Pi_K^T) . c_K,j          sum_j p_j v_hat_j = (sum_j p_j n_V,j c_V,j) Pi_V
+
+so the query is rotated once, every key is read as packed codes plus one fp16
+norm, and the softmax-weighted value sum is accumulated in the value
+quantizer's basis and rotated back once per output row. The work runs in the
+``wn_decode_attention`` HIP entry point (rotate-q, split-K page scan, merge +
+output rotation); nothing here computes attention on the host.
+
+Page layout (packed_attention.py:23-28):
+
+    k_pages, v_pages   (P, Hkv, S, NB) uint8   NB = D*bw/8, LSB-first codes
+    k_norms, v_norms   (P, Hkv, S)     fp16
+    page_table         (B, max_pages)  int32   -1 past the last page
+    seq_lens           (B,)            int32
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from winnow_amd import _lib
+from winnow_amd.packing import packed_bytes
+
+SUPPORTED_HEAD_DIMS = (64, 128)
+MAX_N_REP = 16
+
+
+class UnsupportedLayout(ValueError):
+    """Raised before any launch when inputs violate the operator contract
+    (packed_attention.py:55-56)."""
+
+
+@dataclass(frozen=True)
+class Quantizer:
+    """The pieces of a ``TurboQuantMSE`` the attention operator reads (packed_attention.py:59-69)."""
+
+    Pi: torch.Tensor          # (D, D) fp32, orthogonal
+    centroids: torch.Tensor   # (2**bw,) fp32
+    bit_width: int
+
+    @classmethod
+    def from_tq(cls, tq) -> "Quantizer":
+        return cls(tq.Pi, tq.centroids, tq.bit_width)
+
+
+@dataclass
+class PackedKV:
+    """Paged packed K/V plus the per-sequence view of it (packed_attention.py:72-92).
+
+    ``seq_lens_host`` / ``page_table_host`` are optional CPU mirrors of the two
+    metadata tensors. When present, ``check_contract`` validates against them and
+    the decode call never synchronises with the device.
+    """
+
+    k_pages: torch.Tensor
+    k_norms: torch.Tensor
+    v_pages: torch.Tensor
+    v_norms: torch.Tensor
+    page_table: torch.Tensor
+    seq_lens: torch.Tensor
+    k_quant: Quantizer
+    v_quant: Quantizer
+    head_dim: int
+    seq_lens_host: torch.Tensor | None = None
+    page_table_host: torch.Tensor | None = None
+
+    @property
+    def page_size(self) -> int:
+        return self.k_pages.shape[2]
+
+    @property
+    def num_kv_heads(self) -> int:
+        return self.k_pages.shape[1]
+
+
+@dataclass
+class DenseKV:
+    """Unquantized paged K/V: pages (P, Hkv, S, D) in the model dtype (packed_attention.py:95-111)."""
+
+    k_pages: torch.Tensor
+    v_pages: torch.Tensor
+    page_table: torch.Tensor
+    seq_lens: torch.Tensor
+    head_dim: int
+
+    @property
+    def page_size(self) -> int:
+        return self.k_pages.shape[2]
+
+    @property
+    def num_kv_heads(self) -> int:
+        return self.k_pages.shape[1]
+
+
+def kv_head_for(q_head: torch.Tensor, n_rep: int) -> torch.Tensor:
+    """Query head -> kv head under grouped-query attention (``repeat_kv`` order)."""
+    return q_head // n_rep
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)
+
+
+def check_contract(q: torch.Tensor, kv: PackedKV, *, check_ranges: bool = True) -> None:
+    """Reject anything the operator does not support, with the reason (packed_attention.py:114-163).
+
+    q is (B, Hq, Q, D). The sequence-length and page-id range checks read the
+    host mirrors when the handle carries them; otherwise they copy the two small
+    metadata tensors to the host, as the reference does. ``check_ranges=False``
+    skips only those two checks, for callers that own the metadata.
+    """
+    if q.dim() != 4:
+        raise UnsupportedLayout(f"q must be (B, Hq, Q, D), got {tuple(q.shape)}")
+    B, Hq, _, D = q.shape
+    if D != kv.head_dim:
+        raise UnsupportedLayout(f"q head_dim {D} != cache head_dim {kv.head_dim}")
+    for name, quant in (("k", kv.k_quant), ("v", kv.v_quant)):
+        if quant.Pi.shape != (D, D) or quant.Pi.dtype != torch.float32:
+            raise UnsupportedLayout(f"{name} rotation must be fp32 ({D}, {D})")
+        if quant.centroids.dtype != torch.float32 or quant.centroids.numel() != 2 ** quant.bit_width:
+            raise UnsupportedLayout(f"{name} codebook must be fp32 with 2**bw entries")
+    try:
+        nb_k = packed_bytes(D, kv.k_quant.bit_width)
+        nb_v = packed_bytes(D, kv.v_quant.bit_width)
+    except ValueError as e:
+        raise UnsupportedLayout(str(e)) from e
+    P, Hkv, S = kv.k_pages.shape[:3]
+    if kv.k_pages.dtype != torch.uint8 or kv.v_pages.dtype != torch.uint8:
+        raise UnsupportedLayout("packed pages must be uint8")
+    if kv.k_pages.shape != (P, Hkv, S, nb_k) or kv.v_pages.shape[:3] != (P, Hkv, S) \
+            or kv.v_pages.shape[3] != nb_v:
+        raise UnsupportedLayout(
+            f"page shapes {tuple(kv.k_pages.shape)}/{tuple(kv.v_pages.shape)} do not "
+            f"match (P, Hkv, S, NB) with NB={nb_k}/{nb_v}")
+    if kv.k_norms.shape != (P, Hkv, S) or kv.v_norms.shape != (P, Hkv, S):
+        raise UnsupportedLayout("norms must be (P, Hkv, S)")
+    if kv.k_norms.dtype != torch.float16 or kv.v_norms.dtype != torch.float16:
+        raise UnsupportedLayout("norms must be fp16")
+    if Hq % Hkv:
+        raise UnsupportedLayout(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
+    if kv.page_table.dim() != 2 or kv.page_table.shape[0] != B:
+        raise UnsupportedLayout("page_table must be (B, max_pages)")
+    if kv.seq_lens.shape != (B,):
+        raise UnsupportedLayout("seq_lens must be (B,)")
+    if kv.page_table.dtype != torch.int32 or kv.seq_lens.dtype != torch.int32:
+        raise UnsupportedLayout("page_table and seq_lens must be int32")
+    devices = {t.device for t in (q, kv.k_pages, kv.v_pages, kv.k_norms, kv.v_norms,
+                                  kv.page_table, kv.seq_lens, kv.k_quant.Pi, kv.v_quant.Pi,
+                                  kv.k_quant.centroids, kv.v_quant.centroids)}
+    if len(devices) != 1:
+        raise UnsupportedLayout(f"all operands must share a device, got {devices}")
+    if not check_ranges:
+        return
+    lens = kv.seq_lens_host if kv.seq_lens_host is not None else kv.seq_lens
+    table = kv.page_table_host if kv.page_table_host is not None else kv.page_table
+    lens = lens.to("cpu", torch.int64)
+    if (lens < 0).any() or (lens > kv.page_table.shape[1] * S).any():
+        raise UnsupportedLayout("seq_lens out of range for the page table")
+    used = (lens + S - 1) // S
+    table = table.to("cpu", torch.int64)
+    width = torch.arange(table.shape[1])[None, :]
+    live = width < used[:, None]
+    bad = live & ((table < 0) | (table >= P))
+    if bad.any():
+        b = int(bad.any(1).nonzero()[0])
+        raise UnsupportedLayout(f"sequence {b} references a page outside [0, {P})")
+
+
+def _pow2(x: int) -> bool:
+    return x >= 16 and (x & (x - 1)) == 0
+
+
+def check_kernel_contract(q: torch.Tensor, kv: PackedKV, *, check_ranges: bool = True) -> None:
+    """check_contract plus what the HIP kernel needs (packed_attention_triton.py:166-177)."""
+    check_contract(q, kv, check_ranges=check_ranges)
+    if q.shape[2] != 1:
+        raise UnsupportedLayout("the HIP kernel serves decode (one query token) only")
+    if not _lib.is_hip(q):
+        raise UnsupportedLayout("the HIP kernel needs tensors on a HIP device")
+    if not _pow2(kv.page_size) or not _pow2(kv.head_dim):
+        raise UnsupportedLayout("page_size and head_dim must be powers of two >= 16")
+    if kv.head_dim not in SUPPORTED_HEAD_DIMS:
+        raise UnsupportedLayout(f"head_dim {kv.head_dim} is not compiled {SUPPORTED_HEAD_DIMS}")
+    if q.shape[1] // kv.num_kv_heads > MAX_N_REP:
+        raise UnsupportedLayout(f"more than {MAX_N_REP} query heads per kv head")
+    if q.dtype not in _lib.DTYPE_CODE or q.stride(-1) != 1:
+        raise UnsupportedLayout("q must be fp32/fp16/bf16 with a contiguous head_dim")
+    for pages in (kv.k_pages, kv.v_pages):
+        if pages.stride(-1) != 1 or pages.stride(-2) != pages.shape[-1]:
+            raise UnsupportedLayout("pages need contiguous (S, NB) rows")
+        align = 16 if pages.shape[-1] % 16 == 0 else 8
+        if pages.data_ptr() % align or pages.stride(0) % align or pages.stride(1) % align:
+            raise UnsupportedLayout(f"page base and strides must be {align}-byte aligned")
+    for norms in (kv.k_norms, kv.v_norms):
+        if norms.stride(-1) != 1:
+            raise UnsupportedLayout("norms need a contiguous slot axis")
+    for quant in (kv.k_quant, kv.v_quant):
+        if not quant.Pi.is_contiguous() or not quant.centroids.is_contiguous():
+            raise UnsupportedLayout("rotations and codebooks must be contiguous")
+    if kv.page_table.stride(-1) != 1 or not kv.seq_lens.is_contiguous():
+        raise UnsupportedLayout("page_table rows and seq_lens must be contiguous")
+
+
+def decode_plan(batch: int, num_kv_heads: int, max_pages: int, num_splits: int | None = None):
+    """(pages_per_split, num_splits) the HIP decode uses for this shape (wn_decode_plan)."""
+    pps, ns = ctypes.c_int(0), ctypes.c_int(0)
+    _lib.call("wn_decode_plan", batch, num_kv_heads, max_pages, int(num_splits or 0),
+              ctypes.byref(pps), ctypes.byref(ns))
+    return pps.value, ns.value
+
+
+def workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, num_splits: int) -> int:
+    return int(_lib.lib().wn_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, num_splits))
+
+
+def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
+                            num_splits: int | None = None, allow_tf32: bool = False,
+                            num_warps: int = 4, num_stages: int = 2, pages_per_iter: int = 1,
+                            out_dtype: torch.dtype | None = None,
+                            workspace: torch.Tensor | None = None,
+                            check_ranges: bool = True,
+                            timing_events=None) -> torch.Tensor:
+    """q (B, Hq, 1, D) -> (B, Hq, 1, D) in q.dtype (packed_attention_triton.py:180-187).
+
+    ``num_splits=None`` lets the library split every sequence's pages to fill
+    the GPU; an integer asks for exactly that many splits over the page-table
+    width, as the reference does. ``allow_tf32``, ``num_warps``, ``num_stages``
+    are Triton schedule knobs, accepted for call compatibility and ignored;
+    ``pages_per_iter`` must still be a power of two. ``out_dtype=torch.float32``
+    returns the fp32 result before the cast (for parity checks). ``workspace``
+    is an optional caller-owned uint8 buffer of at least ``workspace_bytes``.
+    ``timing_events`` is an optional pair of raw ``hipEvent_t`` handles recorded
+    around the page-scan kernel.
+    """
+    del allow_tf32, num_warps, num_stages
+    if pages_per_iter < 1 or pages_per_iter & (pages_per_iter - 1):
+        raise UnsupportedLayout("pages_per_iter must be a power of two >= 1")
+    check_kernel_contract(q, kv, check_ranges=check_ranges)
+    B, Hq, _, D = q.shape
+    Hkv = kv.num_kv_heads
+    max_pages = kv.page_table.shape[1]
+    pps, ns = decode_plan(B, Hkv, max_pages, num_splits)
+    out_dtype = out_dtype or q.dtype
+    if out_dtype not in _lib.DTYPE_CODE:
+        raise UnsupportedLayout(f"output dtype {out_dtype} is not supported")
+    out = torch.empty(B, Hq, 1, D, dtype=out_dtype, device=q.device)
+    need = workspace_bytes(B, Hq, Hkv, D, ns)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    elif workspace.numel() * workspace.element_size() < need or workspace.device != q.device:
+        raise UnsupportedLayout(f"workspace needs {need} bytes on {q.device}")
+    ev0, ev1 = timing_events or (None, None)
+    qv = q[:, :, 0]
+    with torch.cuda.device(q.device):
+        _lib.call(
+            "wn_decode_attention",
+            _lib.ptr(qv), _lib.DTYPE_CODE[q.dtype], qv.stride(0), qv.stride(1),
+            _lib.ptr(kv.k_quant.Pi), _lib.ptr(kv.v_quant.Pi),
+            _lib.ptr(kv.k_quant.centroids), _lib.ptr(kv.v_quant.centroids),
+            _lib.ptr(kv.k_pages), kv.k_pages.stride(0), kv.k_pages.stride(1),
+            _lib.ptr(kv.v_pages), kv.v_pages.stride(0), kv.v_pages.stride(1),
+            _lib.ptr(kv.k_norms), kv.k_norms.stride(0), kv.k_norms.stride(1),
+            _lib.ptr(kv.v_norms), kv.v_norms.stride(0), kv.v_norms.stride(1),
+            _lib.ptr(kv.page_table), kv.page_table.stride(0), _lib.ptr(kv.seq_lens),
+            _lib.ptr(out), _lib.DTYPE_CODE[out_dtype],
+            _lib.ptr(workspace), workspace.numel() * workspace.element_size(),
+            B, Hq, Hkv, D, kv.page_size, kv.k_quant.bit_width, kv.v_quant.bit_width, max_pages,
+            float(scale), pps, ns,
+            _lib.stream_of(q.device), ev0, ev1)
+    return out
