@@ -137,7 +137,7 @@ def test_rejects_before_launch():
     with pytest.raises(pa.UnsupportedLayout):
         pa.packed_decode_attention(q.to(DEV), bad, 1.0)
     with pytest.raises(pa.UnsupportedLayout):
-        pa.packed_decode_attention(q.cpu(), kv, 1.0)                                       # host tensors
+        pa.packed_decode_attention(q.cpu(), to_device(kv, "cpu"), 1.0)                     # host tensors
 
 
 def test_extra_memory_does_not_grow_with_history():
