@@ -11,30 +11,12 @@
 //                          cast to the output type
 // Algebra follows turboquant_kv/packed_attention.py:260-334 (the schedule the
 // reference kernel packed_attention_triton.py:51-159 implements).
-#include "wn_common.h"
+#include "wn_decode.h"
 
 namespace wn {
 namespace {
 
 constexpr int kBlock = 256;  // 4 waves
-
-struct DecodeArgs {
-  const float* q_rot;  // (B, Hkv, NREP, D) fp32
-  const uint8_t* k_pages;
-  const uint8_t* v_pages;
-  const uint16_t* k_norms;
-  const uint16_t* v_norms;
-  const float* cb_k;
-  const float* cb_v;
-  const int32_t* table;
-  const int32_t* seq_lens;
-  float* part_acc;  // (B*Hkv*num_splits*n_rep, D)
-  float* part_ml;   // (B*Hkv*num_splits*n_rep, 2)
-  int64_t ksp, ksh, vsp, vsh;  // page strides, bytes
-  int64_t knp, knh, vnp, vnh;  // norm strides, elements
-  int64_t tsb;                 // page-table row stride, elements
-  int Hkv, n_rep, log2S, pages_per_split, num_splits;
-};
 
 // The bytes holding codes [8*g, 8*g+8) of a row: exactly BW bytes at byte
 // offset g*BW, loaded with the widest accesses their alignment allows.
@@ -92,35 +74,52 @@ struct RotArgs {
   float* q_rot;
   float scale;
   int Hkv, n_rep, q_dtype;
+  // set when the page scan merges its own splits: this kernel clears the
+  // arrival counters and writes the zero rows of empty sequences
+  int* counters;
+  const int32_t* seq_lens;
+  void* out;
+  int out_dtype, Hq;
 };
 
 // q_rot[b, kvh, h, :] = scale * q[b, kvh*n_rep + h, :] Pi_K^T (zero rows for h >= n_rep).
+// Pi_K is staged in LDS with a padded row stride (thread j reads row j: banks j + d).
 template <int D, int NREP>
-__global__ __launch_bounds__(D) void rotate_q_kernel(RotArgs a) {
+__global__ __launch_bounds__(256) void rotate_q_kernel(RotArgs a) {
+  constexpr int LDP = D + 1;
+  __shared__ float pis[D * LDP];
   __shared__ float qs[NREP][D];
-  const int kvh = blockIdx.x, b = blockIdx.y, j = threadIdx.x;
-#pragma unroll
-  for (int h = 0; h < NREP; ++h)
-    qs[h][j] = h < a.n_rep ? load_elem(a.q, b * a.qsb + int64_t(kvh * a.n_rep + h) * a.qsh + j, a.q_dtype) : 0.f;
-  __syncthreads();
-  float acc[NREP];
-#pragma unroll
-  for (int h = 0; h < NREP; ++h) acc[h] = 0.f;
-  const float4* row = reinterpret_cast<const float4*>(a.pi_k + int64_t(j) * D);
-#pragma unroll 4
-  for (int d4 = 0; d4 < D / 4; ++d4) {
-    const float4 p = row[d4];
-#pragma unroll
-    for (int h = 0; h < NREP; ++h) {
-      acc[h] = fmaf(qs[h][4 * d4 + 0], p.x, acc[h]);
-      acc[h] = fmaf(qs[h][4 * d4 + 1], p.y, acc[h]);
-      acc[h] = fmaf(qs[h][4 * d4 + 2], p.z, acc[h]);
-      acc[h] = fmaf(qs[h][4 * d4 + 3], p.w, acc[h]);
-    }
+  const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  if (a.counters) {
+    if (tid == 0) a.counters[b * a.Hkv + kvh] = 0;
+    if (a.seq_lens[b] == 0)
+      for (int i = tid; i < a.n_rep * D; i += 256)
+        store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep) * D + i, a.out_dtype, 0.f);
   }
+  const float4* src = reinterpret_cast<const float4*>(a.pi_k);
+  for (int i = tid; i < D * D / 4; i += 256) {
+    const float4 v = src[i];
+    const int r = (4 * i) / D, c = (4 * i) % D;
+    float* dst = pis + r * LDP + c;
+    dst[0] = v.x;
+    dst[1] = v.y;
+    dst[2] = v.z;
+    dst[3] = v.w;
+  }
+  for (int i = tid; i < NREP * D; i += 256) {
+    const int h = i / D, d = i % D;
+    qs[h][d] = h < a.n_rep ? load_elem(a.q, b * a.qsb + int64_t(kvh * a.n_rep + h) * a.qsh + d, a.q_dtype) : 0.f;
+  }
+  __syncthreads();
   float* out = a.q_rot + (int64_t(b) * a.Hkv + kvh) * NREP * D;
-#pragma unroll
-  for (int h = 0; h < NREP; ++h) out[h * D + j] = acc[h] * a.scale;
+  for (int i = tid; i < NREP * D; i += 256) {
+    const int h = i / D, j = i % D;
+    const float* prow = pis + j * LDP;
+    float acc = 0.f;
+#pragma unroll 8
+    for (int d = 0; d < D; ++d) acc = fmaf(qs[h][d], prow[d], acc);
+    out[h * D + j] = acc * a.scale;
+  }
 }
 
 template <int D, int BWK, int BWV, int NREP>
@@ -297,39 +296,53 @@ struct MergeArgs {
 
 // out[b, kvh*n_rep + h, :] = (sum_s w_s acc_s / sum_s w_s l_s) Pi_V, w_s = exp(m_s - max m),
 // zero when no key was seen (packed_attention_triton.py:137-159 plus :261).
+// One work-group per (kv head, sequence): wave w merges heads w, w+4, ... (lanes
+// over splits for the max and the denominator, over dims for the numerator),
+// then all threads rotate the merged rows by Pi_V staged in LDS.
 template <int D>
-__global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+  __shared__ float piv[D * D];
   __shared__ float av[16][D];
-  const int kvh = blockIdx.x, b = blockIdx.y, j = threadIdx.x;
+  const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const float4* src = reinterpret_cast<const float4*>(a.pi_v);
+  for (int i = tid; i < D * D / 4; i += 256) reinterpret_cast<float4*>(piv)[i] = src[i];
   const int S = 1 << a.log2S;
   const int L = a.seq_lens[b];
   const int n_pages = (L + S - 1) >> a.log2S;
   const int nsb = (n_pages + a.pages_per_split - 1) / a.pages_per_split;
-  for (int h = 0; h < a.n_rep; ++h) {
+  for (int h = w; h < a.n_rep; h += 4) {
     const int64_t base = (int64_t(b) * a.Hkv + kvh) * a.num_splits * a.n_rep + h;
     float M = -INFINITY;
-    for (int s = 0; s < nsb; ++s) M = fmaxf(M, a.part_ml[2 * (base + int64_t(s) * a.n_rep)]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < nsb; ++s) {
+    for (int s = lane; s < nsb; s += 64) M = fmaxf(M, a.part_ml[2 * (base + int64_t(s) * a.n_rep)]);
+    M = wave_max(M);
+    float den = 0.f;
+    for (int s = lane; s < nsb; s += 64) {
       const int64_t r = base + int64_t(s) * a.n_rep;
       const float mm = a.part_ml[2 * r];
-      if (mm == -INFINITY) continue;
-      const float wgt = expf(mm - M);
-      den = fmaf(wgt, a.part_ml[2 * r + 1], den);
-      num = fmaf(wgt, a.part_acc[r * D + j], num);
+      if (mm != -INFINITY) den = fmaf(expf(mm - M), a.part_ml[2 * r + 1], den);
     }
-    av[h][j] = den > 0.f ? num / fmaxf(den, 1e-30f) : 0.f;
+    den = wave_sum(den);
+    for (int d = lane; d < D; d += 64) {
+      float num = 0.f;
+#pragma unroll 4
+      for (int s = 0; s < nsb; ++s) {
+        const int64_t r = base + int64_t(s) * a.n_rep;
+        const float mm = a.part_ml[2 * r];
+        if (mm != -INFINITY) num = fmaf(expf(mm - M), a.part_acc[r * D + d], num);
+      }
+      av[h][d] = den > 0.f ? num / fmaxf(den, 1e-30f) : 0.f;
+    }
   }
   __syncthreads();
-  for (int h = 0; h < a.n_rep; ++h) {
+  for (int i = tid; i < a.n_rep * D; i += 256) {
+    const int h = i / D, j = i % D;
     float o = 0.f;
 #pragma unroll 8
-    for (int d = 0; d < D; ++d) o = fmaf(av[h][d], a.pi_v[d * D + j], o);
+    for (int d = 0; d < D; ++d) o = fmaf(av[h][d], piv[d * D + j], o);
     store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + j, a.out_dtype, o);
   }
 }
 
-using SplitFn = void (*)(DecodeArgs);
 using RotFn = void (*)(RotArgs);
 
 template <int D, int BWK, int BWV>
@@ -386,16 +399,17 @@ int pad_nrep(int n_rep) {
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 struct WsLayout {
-  int64_t qrot, acc, ml, total;
+  int64_t qrot, acc, ml, cnt, total;
 };
 
 WsLayout ws_layout(int B, int Hq, int Hkv, int D, int num_splits) {
   WsLayout l;
-  const int nrp = pad_nrep(Hq / Hkv);
+  const int nrp = max(pad_nrep(Hq / Hkv), 4);  // the matrix-core scan reads 4 rows per kv head
   l.qrot = 0;
   l.acc = align256(int64_t(B) * Hkv * nrp * D * 4);
   l.ml = l.acc + align256(int64_t(B) * Hq * num_splits * D * 4);
-  l.total = l.ml + align256(int64_t(B) * Hq * num_splits * 2 * 4);
+  l.cnt = l.ml + align256(int64_t(B) * Hq * num_splits * 2 * 4);
+  l.total = l.cnt + align256(int64_t(B) * Hkv * 4);
   return l;
 }
 
@@ -448,10 +462,20 @@ extern "C" int wn_decode_attention(
              "decode: head stride smaller than one (S, NB) page block");
   WN_REQUIRE(aligned(pi_k, 16) && aligned(pi_v, 4), WN_E_INVALID, "decode: rotation alignment");
 
-  const int nrp = pad_nrep(n_rep);
-  SplitFn split = D == 128 ? pick_split<128>(bw_k, bw_v, nrp) : pick_split<64>(bw_k, bw_v, nrp);
-  RotFn rot = D == 128 ? pick_rot<128>(nrp) : pick_rot<64>(nrp);
-  WN_REQUIRE(split && rot, WN_E_UNSUPPORTED, "decode: (D=%d, bw_k=%d, bw_v=%d) not compiled", D, bw_k,
+  // Matrix-core scan when it applies (D=128, <= 4 query heads per kv head, fp16 norm
+  // groups of 4 slots 8-byte aligned), else the vector-ALU scan.
+  SplitKernel sk;
+  const bool norms8 = aligned(k_norms, 8) && aligned(v_norms, 8) && kn_stride_p % 4 == 0 &&
+                      kn_stride_h % 4 == 0 && vn_stride_p % 4 == 0 && vn_stride_h % 4 == 0;
+  if (D == 128 && n_rep <= 4 && S >= 16 && norms8) sk = pick_split_mfma(bw_k, bw_v);
+  if (!sk.fn) {
+    const int nrp = pad_nrep(n_rep);
+    sk.fn = D == 128 ? pick_split<128>(bw_k, bw_v, nrp) : pick_split<64>(bw_k, bw_v, nrp);
+    sk.block = kBlock;
+    sk.nrep = nrp;
+  }
+  RotFn rot = D == 128 ? pick_rot<128>(sk.nrep) : pick_rot<64>(sk.nrep);
+  WN_REQUIRE(sk.fn && rot, WN_E_UNSUPPORTED, "decode: (D=%d, bw_k=%d, bw_v=%d) not compiled", D, bw_k,
              bw_v);
 
   const WsLayout lay = ws_layout(B, Hq, Hkv, D, num_splits);
@@ -461,9 +485,13 @@ extern "C" int wn_decode_attention(
   char* ws = static_cast<char*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  RotArgs ra{q, q_stride_b, q_stride_h, pi_k, reinterpret_cast<float*>(ws + lay.qrot), scale, Hkv, n_rep,
-             q_dtype};
-  hipLaunchKernelGGL(rot, dim3(Hkv, B), dim3(D), 0, st, ra);
+  int* counters = sk.fused_merge ? reinterpret_cast<int*>(ws + lay.cnt) : nullptr;
+  // the matrix-core scan keeps scores in log2 units: fold log2(e) into q_rot
+  const float q_scale = sk.fused_merge ? float(double(scale) * 1.4426950408889634) : scale;
+  RotArgs ra{q,       q_stride_b, q_stride_h, pi_k,      reinterpret_cast<float*>(ws + lay.qrot),
+             q_scale, Hkv,        n_rep,      q_dtype,   counters,
+             seq_lens, out,       out_dtype,  Hq};
+  hipLaunchKernelGGL(rot, dim3(Hkv, B), dim3(256), 0, st, ra);
 
   DecodeArgs da;
   da.q_rot = ra.q_rot;
@@ -491,15 +519,21 @@ extern "C" int wn_decode_attention(
   da.log2S = ilog2(S);
   da.pages_per_split = pages_per_split;
   da.num_splits = num_splits;
+  da.counters = counters;
+  da.pi_v = pi_v;
+  da.out = out;
+  da.out_dtype = out_dtype;
+  da.Hq = Hq;
   if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
-  hipLaunchKernelGGL(split, dim3(num_splits, Hkv, B), dim3(kBlock), 0, st, da);
+  hipLaunchKernelGGL(sk.fn, dim3(num_splits, Hkv, B), dim3(sk.block), 0, st, da);
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
+  if (sk.fused_merge) return check_launch("wn_decode_attention");
   MergeArgs ma{da.part_acc, da.part_ml, pi_v, seq_lens, out, out_dtype, Hq, Hkv, n_rep, da.log2S,
                pages_per_split, num_splits};
   if (D == 128)
-    hipLaunchKernelGGL(merge_kernel<128>, dim3(Hkv, B), dim3(128), 0, st, ma);
+    hipLaunchKernelGGL(merge_kernel<128>, dim3(Hkv, B), dim3(256), 0, st, ma);
   else
-    hipLaunchKernelGGL(merge_kernel<64>, dim3(Hkv, B), dim3(64), 0, st, ma);
+    hipLaunchKernelGGL(merge_kernel<64>, dim3(Hkv, B), dim3(256), 0, st, ma);
   return check_launch("wn_decode_attention");
 }

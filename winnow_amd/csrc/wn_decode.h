@@ -1,0 +1,45 @@
+// Internal interface shared by the decode translation units.
+#pragma once
+
+#include "wn_common.h"
+
+namespace wn {
+
+struct DecodeArgs {
+  const float* q_rot;  // (B, Hkv, NREP, D) fp32, rows >= n_rep are zero
+  const uint8_t* k_pages;
+  const uint8_t* v_pages;
+  const uint16_t* k_norms;
+  const uint16_t* v_norms;
+  const float* cb_k;
+  const float* cb_v;
+  const int32_t* table;
+  const int32_t* seq_lens;
+  float* part_acc;  // (B*Hkv*num_splits*n_rep, D)
+  float* part_ml;   // (B*Hkv*num_splits*n_rep, 2)
+  int64_t ksp, ksh, vsp, vsh;  // page strides, bytes
+  int64_t knp, knh, vnp, vnh;  // norm strides, elements
+  int64_t tsb;                 // page-table row stride, elements
+  int Hkv, n_rep, log2S, pages_per_split, num_splits;
+  // fused merge (matrix-core scan): the last split of each (sequence, kv head)
+  // to finish merges all splits, rotates by Pi_V and writes the output rows.
+  int* counters;       // (B*Hkv) arrival counters, zero at launch
+  const float* pi_v;   // (D, D) fp32
+  void* out;           // (B, Hq, D) contiguous
+  int out_dtype, Hq;
+};
+
+using SplitFn = void (*)(DecodeArgs);
+
+struct SplitKernel {
+  SplitFn fn = nullptr;
+  int block = 0;  // threads per work-group
+  int nrep = 0;   // query-head rows per kv head the kernel reads from q_rot
+  bool fused_merge = false;  // writes the output itself (no merge kernel)
+};
+
+// Matrix-core page scan for head_dim 128 and up to four query heads per kv
+// head, or an empty SplitKernel when (bw_k, bw_v) is not compiled.
+SplitKernel pick_split_mfma(int bw_k, int bw_v);
+
+}  // namespace wn
