@@ -74,12 +74,6 @@ struct RotArgs {
   float* q_rot;
   float scale;
   int Hkv, n_rep, q_dtype;
-  // set when the page scan merges its own splits: this kernel clears the
-  // arrival counters and writes the zero rows of empty sequences
-  int* counters;
-  const int32_t* seq_lens;
-  void* out;
-  int out_dtype, Hq;
 };
 
 // q_rot[b, kvh, h, :] = scale * q[b, kvh*n_rep + h, :] Pi_K^T (zero rows for h >= n_rep).
@@ -90,12 +84,6 @@ __global__ __launch_bounds__(256) void rotate_q_kernel(RotArgs a) {
   __shared__ float pis[D * LDP];
   __shared__ float qs[NREP][D];
   const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  if (a.counters) {
-    if (tid == 0) a.counters[b * a.Hkv + kvh] = 0;
-    if (a.seq_lens[b] == 0)
-      for (int i = tid; i < a.n_rep * D; i += 256)
-        store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep) * D + i, a.out_dtype, 0.f);
-  }
   const float4* src = reinterpret_cast<const float4*>(a.pi_k);
   for (int i = tid; i < D * D / 4; i += 256) {
     const float4 v = src[i];
@@ -292,17 +280,24 @@ struct MergeArgs {
   const int32_t* seq_lens;
   void* out;
   int out_dtype, Hq, Hkv, n_rep, log2S, pages_per_split, num_splits;
+  int log2_units;  // partial maxima are in log2 units (weights 2^(m - M))
 };
 
-// out[b, kvh*n_rep + h, :] = (sum_s w_s acc_s / sum_s w_s l_s) Pi_V, w_s = exp(m_s - max m),
-// zero when no key was seen (packed_attention_triton.py:137-159 plus :261).
-// One work-group per (kv head, sequence): wave w merges heads w, w+4, ... (lanes
-// over splits for the max and the denominator, over dims for the numerator),
-// then all threads rotate the merged rows by Pi_V staged in LDS.
+// out[b, kvh*n_rep + h, :] = (sum_s w_s acc_s / sum_s w_s l_s) Pi_V, w_s = exp(m_s - max m)
+// (2^(m_s - max m) for log2-unit partials), zero when no key was seen
+// (packed_attention_triton.py:137-159 plus :261). One work-group per (kv head,
+// sequence). Wave w handles heads w, w+4, ...: its lanes load the split maxima in
+// parallel, reduce the max, and leave each split's weight in LDS together with
+// the denominator; then every thread accumulates (head, dim) numerators from
+// independent loads, and finally rotates the rows by Pi_V staged in LDS.
+constexpr int kMergeTile = 256;  // splits per weight tile
+
 template <int D>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   __shared__ float piv[D * D];
   __shared__ float av[16][D];
+  __shared__ float wts[16][kMergeTile];
+  __shared__ float hmax[16], hden[16];
   const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const float4* src = reinterpret_cast<const float4*>(a.pi_v);
   for (int i = tid; i < D * D / 4; i += 256) reinterpret_cast<float4*>(piv)[i] = src[i];
@@ -310,35 +305,52 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int L = a.seq_lens[b];
   const int n_pages = (L + S - 1) >> a.log2S;
   const int nsb = (n_pages + a.pages_per_split - 1) / a.pages_per_split;
+  const int64_t base = (int64_t(b) * a.Hkv + kvh) * a.num_splits * a.n_rep;
+  auto wexp = [&](float x) { return a.log2_units ? __builtin_amdgcn_exp2f(x) : expf(x); };
   for (int h = w; h < a.n_rep; h += 4) {
-    const int64_t base = (int64_t(b) * a.Hkv + kvh) * a.num_splits * a.n_rep + h;
     float M = -INFINITY;
-    for (int s = lane; s < nsb; s += 64) M = fmaxf(M, a.part_ml[2 * (base + int64_t(s) * a.n_rep)]);
+    for (int s = lane; s < nsb; s += 64) M = fmaxf(M, a.part_ml[2 * (base + int64_t(s) * a.n_rep + h)]);
     M = wave_max(M);
     float den = 0.f;
     for (int s = lane; s < nsb; s += 64) {
-      const int64_t r = base + int64_t(s) * a.n_rep;
+      const int64_t r = base + int64_t(s) * a.n_rep + h;
       const float mm = a.part_ml[2 * r];
-      if (mm != -INFINITY) den = fmaf(expf(mm - M), a.part_ml[2 * r + 1], den);
+      den += mm == -INFINITY ? 0.f : wexp(mm - M) * a.part_ml[2 * r + 1];
     }
     den = wave_sum(den);
-    for (int d = lane; d < D; d += 64) {
+    if (lane == 0) {
+      hmax[h] = M;
+      hden[h] = den;
+    }
+  }
+  for (int i = tid; i < a.n_rep * D; i += 256) av[i / D][i % D] = 0.f;
+  for (int t0 = 0; t0 < nsb; t0 += kMergeTile) {
+    const int tn = min(kMergeTile, nsb - t0);
+    __syncthreads();
+    for (int i = tid; i < a.n_rep * tn; i += 256) {
+      const int h = i / tn, s = t0 + i % tn;
+      const float mm = a.part_ml[2 * (base + int64_t(s) * a.n_rep + h)];
+      wts[h][s - t0] = mm == -INFINITY ? 0.f : wexp(mm - hmax[h]);
+    }
+    __syncthreads();
+    for (int i = tid; i < a.n_rep * D; i += 256) {
+      const int h = i / D, d = i % D;
+      const float* col = a.part_acc + (base + int64_t(t0) * a.n_rep + h) * D + d;
       float num = 0.f;
-#pragma unroll 4
-      for (int s = 0; s < nsb; ++s) {
-        const int64_t r = base + int64_t(s) * a.n_rep;
-        const float mm = a.part_ml[2 * r];
-        if (mm != -INFINITY) num = fmaf(expf(mm - M), a.part_acc[r * D + d], num);
-      }
-      av[h][d] = den > 0.f ? num / fmaxf(den, 1e-30f) : 0.f;
+#pragma unroll 8
+      for (int s = 0; s < tn; ++s) num = fmaf(wts[h][s], col[int64_t(s) * a.n_rep * D], num);
+      av[h][d] += num;
     }
   }
   __syncthreads();
   for (int i = tid; i < a.n_rep * D; i += 256) {
     const int h = i / D, j = i % D;
+    const float den = hden[h];
     float o = 0.f;
 #pragma unroll 8
     for (int d = 0; d < D; ++d) o = fmaf(av[h][d], piv[d * D + j], o);
+    // (a / l) Pi_V == (a Pi_V) / l up to rounding; l > 0 whenever a key was seen
+    o = den > 0.f ? o / fmaxf(den, 1e-30f) : 0.f;
     store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + j, a.out_dtype, o);
   }
 }
@@ -399,7 +411,7 @@ int pad_nrep(int n_rep) {
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 struct WsLayout {
-  int64_t qrot, acc, ml, cnt, total;
+  int64_t qrot, acc, ml, total;
 };
 
 WsLayout ws_layout(int B, int Hq, int Hkv, int D, int num_splits) {
@@ -408,8 +420,7 @@ WsLayout ws_layout(int B, int Hq, int Hkv, int D, int num_splits) {
   l.qrot = 0;
   l.acc = align256(int64_t(B) * Hkv * nrp * D * 4);
   l.ml = l.acc + align256(int64_t(B) * Hq * num_splits * D * 4);
-  l.cnt = l.ml + align256(int64_t(B) * Hq * num_splits * 2 * 4);
-  l.total = l.cnt + align256(int64_t(B) * Hkv * 4);
+  l.total = l.ml + align256(int64_t(B) * Hq * num_splits * 2 * 4);
   return l;
 }
 
@@ -485,12 +496,10 @@ extern "C" int wn_decode_attention(
   char* ws = static_cast<char*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  int* counters = sk.fused_merge ? reinterpret_cast<int*>(ws + lay.cnt) : nullptr;
   // the matrix-core scan keeps scores in log2 units: fold log2(e) into q_rot
-  const float q_scale = sk.fused_merge ? float(double(scale) * 1.4426950408889634) : scale;
-  RotArgs ra{q,       q_stride_b, q_stride_h, pi_k,      reinterpret_cast<float*>(ws + lay.qrot),
-             q_scale, Hkv,        n_rep,      q_dtype,   counters,
-             seq_lens, out,       out_dtype,  Hq};
+  const float q_scale = sk.log2_units ? float(double(scale) * 1.4426950408889634) : scale;
+  RotArgs ra{q, q_stride_b, q_stride_h, pi_k, reinterpret_cast<float*>(ws + lay.qrot), q_scale, Hkv, n_rep,
+             q_dtype};
   hipLaunchKernelGGL(rot, dim3(Hkv, B), dim3(256), 0, st, ra);
 
   DecodeArgs da;
@@ -519,18 +528,12 @@ extern "C" int wn_decode_attention(
   da.log2S = ilog2(S);
   da.pages_per_split = pages_per_split;
   da.num_splits = num_splits;
-  da.counters = counters;
-  da.pi_v = pi_v;
-  da.out = out;
-  da.out_dtype = out_dtype;
-  da.Hq = Hq;
   if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
   hipLaunchKernelGGL(sk.fn, dim3(num_splits, Hkv, B), dim3(sk.block), 0, st, da);
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
-  if (sk.fused_merge) return check_launch("wn_decode_attention");
   MergeArgs ma{da.part_acc, da.part_ml, pi_v, seq_lens, out, out_dtype, Hq, Hkv, n_rep, da.log2S,
-               pages_per_split, num_splits};
+               pages_per_split, num_splits, sk.log2_units ? 1 : 0};
   if (D == 128)
     hipLaunchKernelGGL(merge_kernel<128>, dim3(Hkv, B), dim3(256), 0, st, ma);
   else

@@ -21,11 +21,12 @@
 //          -> acc[g] lane l, reg r : head r, dim 64h+16(l%4)+g, summed over the
 //          tokens of block l/4; blocks are folded once at the end.
 //
-// Online softmax with a lazy reference maximum: a head's reference max moves
-// (rescaling its accumulators) only when a score exceeds it by more than
-// kRescale nats, so exp(s - m) <= e^kRescale and nothing overflows; the merge
-// downstream is exact for any reference max. The wave-wide max reduction runs
-// only on the first chunk and when that happens.
+// Online softmax in log2 units (q_rot carries log2 e) with a lazy reference
+// maximum: a head's reference max moves (rescaling its accumulators) only when
+// a score exceeds it by more than kRescale, so 2^(s - m) <= 2^kRescale and
+// nothing overflows; the split merge is exact for any reference max. The
+// wave-wide max reduction runs only on the first chunk and when that happens.
+// Partials (m in log2 units, l, acc) go to the workspace for merge_kernel.
 //
 // Codebooks live in LDS (2^bw fp32 entries: the 64 lanes of a lookup read at
 // most 2^bw distinct words). Page ids are fetched one chunk ahead and the packed
@@ -288,39 +289,6 @@ __device__ __forceinline__ void process_chunk(const ChunkRegs<BWK, BWV>& cur, in
   value_pipelined<BWV>(cur.v, cbv, p, st.acc);
 }
 
-// Merge of the split partials of one (sequence, kv head) and the output rotation,
-// run by the 128 threads of the last work-group to finish (thread = dim):
-//   out[h] = (sum_s w_s acc_s / sum_s w_s l_s) Pi_V,  w_s = 2^(m_s - max m)
-// (packed_attention_triton.py:137-159 then :261; m in log2 units here).
-__device__ __forceinline__ void merge_rotate_tail(const DecodeArgs& a, int b, int kvh, int nsb, int tid,
-                                                  float* av) {
-  constexpr int D = 128;
-  for (int hh = 0; hh < a.n_rep; ++hh) {
-    const int64_t base = (int64_t(b) * a.Hkv + kvh) * a.num_splits * a.n_rep + hh;
-    float M = -INFINITY;
-    for (int s = 0; s < nsb; ++s) M = fmaxf(M, a.part_ml[2 * (base + int64_t(s) * a.n_rep)]);
-    float num = 0.f, den = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < nsb; ++s) {
-      const int64_t r = base + int64_t(s) * a.n_rep;
-      const float wgt = __builtin_amdgcn_exp2f(a.part_ml[2 * r] - M);
-      den = fmaf(wgt, a.part_ml[2 * r + 1], den);
-      num = fmaf(wgt, a.part_acc[r * D + tid], num);
-    }
-    av[hh * D + tid] = den > 0.f ? num / fmaxf(den, 1e-30f) : 0.f;
-  }
-  __syncthreads();
-  float o[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 16
-  for (int d = 0; d < D; ++d) {
-    const float pv = a.pi_v[d * D + tid];
-#pragma unroll
-    for (int hh = 0; hh < 4; ++hh) o[hh] = fmaf(av[hh * D + d], pv, o[hh]);
-  }
-  for (int hh = 0; hh < a.n_rep; ++hh)
-    store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + hh) * D + tid, a.out_dtype, o[hh]);
-}
-
 template <int BWK, int BWV>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) void decode_mfma4_kernel(
     DecodeArgs a) {
@@ -329,7 +297,6 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
   __shared__ float cbk[LK];
   __shared__ float cbv[LV];
   __shared__ float xs[2][2][4][64];  // [chunk parity][half][head][token] partial scores
-  __shared__ int s_last;
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, h = tid >> 6, lane = tid & 63;
@@ -405,16 +372,6 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     }
   }
 
-  // ---- the last split of this (sequence, kv head) to arrive merges all of them
-  const int nsb = (n_pages + a.pages_per_split - 1) / a.pages_per_split;
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(a.counters + b * a.Hkv + kvh, 1) == nsb - 1;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  merge_rotate_tail(a, b, kvh, nsb, tid, &xs[0][0][0][0]);
-  if (tid == 0) a.counters[b * a.Hkv + kvh] = 0;
 }
 
 }  // namespace
@@ -442,7 +399,7 @@ SplitKernel pick_split_mfma(int bw_k, int bw_v) {
     k.fn = f;
     k.block = 128;
     k.nrep = 4;
-    k.fused_merge = true;
+    k.log2_units = true;
   }
   return k;
 }

@@ -21,12 +21,6 @@ struct DecodeArgs {
   int64_t knp, knh, vnp, vnh;  // norm strides, elements
   int64_t tsb;                 // page-table row stride, elements
   int Hkv, n_rep, log2S, pages_per_split, num_splits;
-  // fused merge (matrix-core scan): the last split of each (sequence, kv head)
-  // to finish merges all splits, rotates by Pi_V and writes the output rows.
-  int* counters;       // (B*Hkv) arrival counters, zero at launch
-  const float* pi_v;   // (D, D) fp32
-  void* out;           // (B, Hq, D) contiguous
-  int out_dtype, Hq;
 };
 
 using SplitFn = void (*)(DecodeArgs);
@@ -35,7 +29,7 @@ struct SplitKernel {
   SplitFn fn = nullptr;
   int block = 0;  // threads per work-group
   int nrep = 0;   // query-head rows per kv head the kernel reads from q_rot
-  bool fused_merge = false;  // writes the output itself (no merge kernel)
+  bool log2_units = false;  // scores/maxima in log2 units (q_rot scaled by log2 e)
 };
 
 // Matrix-core page scan for head_dim 128 and up to four query heads per kv
