@@ -129,6 +129,30 @@ def kv_bytes(lens, Hkv, nbk, nbv):
     return sum(lens) * Hkv * ((nbk + 2) + (nbv + 2))
 
 
+def copy_peak(dev, nbytes: int = 1 << 30, reps: int = 10):
+    """Device-to-device copy of ``nbytes`` (torch's copy kernel): GB/s of read + write bytes.
+
+    Gives the measured bandwidth ceiling on this box beside the 8 TB/s data-sheet
+    peak, and a plain copy kernel of known size for scaling the FETCH_SIZE /
+    WRITE_SIZE counters of a profiling run.
+    """
+    import torch
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / reps * 1e-3
+    del src, dst
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": t * 1e6, "GBps": 2 * nbytes / t / 1e9}
+
+
 def parity(c, lens, q, kv, quants, sample):
     """Same-run checks: two sequences' attention vs the CPU oracle on the same pages, and
     the first 256 tokens of sequence 0 re-quantized by the oracle vs the pool bytes."""
@@ -215,6 +239,7 @@ def main(argv=None):
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--parity", choices=["on", "off"], default="on")
+    ap.add_argument("--copy-peak", choices=["on", "off"], default="on")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -267,6 +292,9 @@ def main(argv=None):
     log(f"step {ms * 1e3:.1f} us; page-scan kernel mean {kern_ms * 1e3:.1f} us "
         f"(median {statistics.median(kern) * 1e3:.1f}); plan {ns} splits x {pps} pages")
     achieved = bytes_step / (kern_ms * 1e-3) / 1e9
+    cp = copy_peak(dev) if args.copy_peak == "on" else None
+    if cp:
+        log(f"copy peak: {cp}")
 
     par = parity(c, lens, q, kvs[0], quants, sample) if args.parity == "on" else None
     if par:
@@ -298,7 +326,9 @@ def main(argv=None):
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
                      "kernel": "decode_split_kernel", "kernel_us": kern_ms * 1e3,
-                     "algorithmic_bytes": bytes_step},
+                     "algorithmic_bytes": bytes_step,
+                     "copy_peak_GBps": cp["GBps"] if cp else None,
+                     "frac_of_copy_peak": achieved / cp["GBps"] if cp else None},
         "cpu_baseline": cpu,
         "parity": par,
     }
