@@ -125,6 +125,15 @@ def build_workload(cfg: int, dev, copies: int):
     return c, lens, q, kvs, (kq, vq), sample
 
 
+def scan_kernel_name(c) -> str:
+    """Symbol of the page-scan kernel wn_decode_attention launches for this shape."""
+    scan = os.environ.get("WN_DECODE_SCAN", "rows") or "rows"
+    n_rep = c["Hq"] // c["Hkv"]
+    if c["D"] == 128 and n_rep <= 4 and c["S"] >= 16 and scan != "valu":
+        return "decode_rows_kernel"
+    return "decode_split_kernel"
+
+
 def kv_bytes(lens, Hkv, nbk, nbv):
     return sum(lens) * Hkv * ((nbk + 2) + (nbv + 2))
 
@@ -262,8 +271,8 @@ def main(argv=None):
     scale = 1.0 / math.sqrt(D)
     B = len(lens)
     max_pages = kvs[0].page_table.shape[1]
-    pps, ns = pa.decode_plan(B, Hkv, max_pages, args.splits)
-    ws = torch.empty(pa.workspace_bytes(B, Hq, Hkv, D, ns), dtype=torch.uint8, device=dev)
+    pps, ns = pa.plan_for(q, kvs[0], args.splits)
+    ws = torch.empty(pa.workspace_bytes(B, Hq, Hkv, D, pps, ns), dtype=torch.uint8, device=dev)
     for kv in kvs:
         pa.check_kernel_contract(q, kv)          # full validation once, outside the timed region
 
@@ -325,7 +334,7 @@ def main(argv=None):
         "kv_tokens_per_s": sum(lens) / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "decode_split_kernel", "kernel_us": kern_ms * 1e3,
+                     "kernel": scan_kernel_name(c), "kernel_us": kern_ms * 1e3,
                      "algorithmic_bytes": bytes_step,
                      "copy_peak_GBps": cp["GBps"] if cp else None,
                      "frac_of_copy_peak": achieved / cp["GBps"] if cp else None},

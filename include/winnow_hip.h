@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define WN_ABI_VERSION 1
+#define WN_ABI_VERSION 2
 
 /* element types of floating-point tensors crossing the ABI */
 enum { WN_F32 = 0, WN_F16 = 1, WN_BF16 = 2 };
@@ -58,17 +58,24 @@ int wn_abi_version(void);
 /* Message for the last failing call on this thread ("" if none). */
 const char* wn_last_error(void);
 
-/* Split-K plan for a decode step: pages per split and number of splits.
+/* Split-K plan for a decode step of this shape.
  * requested_splits > 0 asks for exactly that many splits over max_pages (the
- * reference's num_splits, packed_attention_triton.py:211-216); 0 lets the
- * library size splits to fill the GPU. */
-int wn_decode_plan(int B, int Hkv, int max_pages, int requested_splits,
-                   int* pages_per_split, int* num_splits);
+ * reference's num_splits, packed_attention_triton.py:211-216): *pages_per_split
+ * = cdiv(max_pages, splits), one partial per (sequence, kv head, split).
+ * requested_splits == 0 lets the library choose. Where the row-per-lane
+ * matrix-core scan applies (head_dim 128, <= 4 query heads per kv head, page
+ * size >= 16) the plan is balanced: *pages_per_split = 0 and *num_splits = the
+ * number of resident waves on the current device, which then share the
+ * flattened (sequence, kv head, 64-token chunk) space equally, ragged batches
+ * included. Otherwise fixed splits sized to fill the GPU. */
+int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
+                   int requested_splits, int* pages_per_split, int* num_splits);
 
-/* Bytes of scratch wn_decode_attention needs for this shape and split count:
- * the rotated query plus compact per-split (acc, m, l) partials of the real
- * query heads (B*Hq*num_splits rows). */
-int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int num_splits);
+/* Bytes of scratch wn_decode_attention needs for this shape and plan: the
+ * rotated query, a per-sequence chunk prefix, and the (acc, m, l) partials of
+ * the real query heads (B*Hkv*num_splits rows for fixed splits, num_splits +
+ * B*Hkv rows for a balanced plan). -1 for invalid sizes. */
+int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int pages_per_split, int num_splits);
 
 /* Decode attention over paged packed K/V, one query token per sequence.
  *   q      (B, Hq, D) with element strides q_stride_b, q_stride_h (last dim
@@ -77,7 +84,8 @@ int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int num_splits)
  *   out = softmax(scale * q k_hat^T) v_hat computed in the quantizer bases:
  *   q_rot = scale * q Pi_K^T; per key s = n_K (q_rot . c_K); online softmax
  *   over pages; a = sum p n_V c_V; out = (a / l) Pi_V. Rows with no key are 0.
- *   pages_per_split / num_splits come from wn_decode_plan.
+ *   pages_per_split / num_splits come from wn_decode_plan (pages_per_split 0
+ *   = balanced plan).
  *   ev_begin / ev_end (hipEvent_t or NULL) are recorded on `stream` around
  *   the split-K page-scan kernel only, for in-situ timing of that kernel. */
 int wn_decode_attention(

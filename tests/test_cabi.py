@@ -46,29 +46,34 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.wn_abi_version() == 1
+    assert lib.wn_abi_version() == 2
     assert isinstance(lib.wn_last_error(), bytes)
 
 
 def test_plan_reference_semantics(lib):
     from winnow_amd.packed_attention import decode_plan
     # explicit splits: clamp to [1, max_pages], cdiv(max_pages, splits) pages each
-    assert decode_plan(2, 4, 10, 3) == (4, 3)
-    assert decode_plan(2, 4, 10, 50) == (1, 10)
-    assert decode_plan(2, 4, 0, 1) == (1, 1)
-    # automatic: every plan covers the table
-    for B, Hkv, mp in ((16, 8, 2048), (4, 8, 8192), (64, 8, 4096), (1, 8, 64), (1, 1, 1)):
-        pps, ns = decode_plan(B, Hkv, mp)
+    assert decode_plan(2, 8, 4, 128, 16, 4, 4, 10, 3) == (4, 3)
+    assert decode_plan(2, 8, 4, 128, 16, 4, 4, 10, 50) == (1, 10)
+    assert decode_plan(2, 8, 4, 128, 16, 4, 4, 0, 1) == (1, 1)
+    # automatic plans for shapes the vector-ALU scan serves (no device query): fixed
+    # splits covering the table
+    for B, Hq, Hkv, D, mp in ((16, 64, 8, 128, 2048), (4, 64, 8, 128, 8192), (64, 8, 8, 64, 4096),
+                              (1, 16, 1, 64, 64), (1, 1, 1, 64, 1)):
+        pps, ns = decode_plan(B, Hq, Hkv, D, 16, 4, 4, mp)
         assert pps * ns >= mp and pps >= 1 and ns >= 1
         assert (ns - 1) * pps < max(mp, 1)
 
 
 def test_workspace_bytes(lib):
     from winnow_amd.packed_attention import workspace_bytes
-    w1 = workspace_bytes(16, 32, 8, 128, 32)
-    w2 = workspace_bytes(16, 32, 8, 128, 64)
+    w1 = workspace_bytes(16, 32, 8, 128, 64, 32)
+    w2 = workspace_bytes(16, 32, 8, 128, 32, 64)
     assert w2 > w1 > 16 * 32 * 32 * 128 * 4
-    assert lib.wn_decode_workspace_bytes(16, 30, 8, 128, 4) == -1     # Hq % Hkv
+    # balanced plan: num_splits + B*Hkv partial rows of every real query head
+    wb = workspace_bytes(16, 32, 8, 128, 0, 3072)
+    assert wb >= (3072 + 128) * 4 * 130 * 4
+    assert lib.wn_decode_workspace_bytes(16, 30, 8, 128, 4, 4) == -1     # Hq % Hkv
 
 
 def test_argument_errors_are_reported_not_fatal(lib):

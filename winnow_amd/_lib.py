@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libwinnow_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 WN_F32, WN_F16, WN_BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: WN_F32, torch.float16: WN_F16, torch.bfloat16: WN_BF16}
@@ -27,8 +27,9 @@ _c_p = ctypes.c_void_p
 SIGNATURES = {
     "wn_abi_version": (_c_i, []),
     "wn_last_error": (ctypes.c_char_p, []),
-    "wn_decode_plan": (_c_i, [_c_i, _c_i, _c_i, _c_i, ctypes.POINTER(_c_i), ctypes.POINTER(_c_i)]),
-    "wn_decode_workspace_bytes": (_c_i64, [_c_i, _c_i, _c_i, _c_i, _c_i]),
+    "wn_decode_plan": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,
+                              ctypes.POINTER(_c_i), ctypes.POINTER(_c_i)]),
+    "wn_decode_workspace_bytes": (_c_i64, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i]),
     "wn_decode_attention": (_c_i, [
         _c_p, _c_i, _c_i64, _c_i64,                 # q, dtype, strides
         _c_p, _c_p, _c_p, _c_p,                     # pi_k, pi_v, codebooks

@@ -1,16 +1,25 @@
 // Decode attention over paged packed K/V for gfx950 (CDNA4, wave64).
 //
 // Three launches per step, all on the caller's stream:
-//   1. rotate_q_kernel     q_rot = scale * q Pi_K^T, padded to NREP rows per kv head
-//   2. decode_split_kernel one work-group per (split, kv head, sequence) scans its
-//                          page range once for all NREP query heads of the group:
-//                          score phase (lane = token), online softmax, value
-//                          phase (16 lanes per token row), then a cross-wave
-//                          max-stable merge into one compact (acc, m, l) partial
-//   3. merge_kernel        max-stable merge of the split partials, 1/l, a Pi_V,
-//                          cast to the output type
+//   1. rotate_q_kernel   q_rot = scale * q Pi_K^T, padded to NREP rows per kv head;
+//                        one block also writes the per-sequence chunk prefix the
+//                        balanced scan partitions by
+//   2. page scan         the row-per-lane matrix-core scan (decode_rows.hip) where
+//                        it applies (head_dim 128, <= 4 query heads per kv head),
+//                        else decode_split_kernel below: one work-group per
+//                        (split, kv head, sequence), score phase (lane = token),
+//                        online softmax, value phase (16 lanes per token row),
+//                        cross-wave max-stable merge into one (acc, m, l) partial
+//   3. merge_kernel      per (sequence, query head): max-stable merge of its
+//                        partials, 1/l, a Pi_V, cast to the output type
 // Algebra follows turboquant_kv/packed_attention.py:260-334 (the schedule the
 // reference kernel packed_attention_triton.py:51-159 implements).
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "wn_decode.h"
 
 namespace wn {
@@ -72,20 +81,50 @@ struct RotArgs {
   int64_t qsb, qsh;  // element strides of q (B, Hq, D)
   const float* pi_k;
   float* q_rot;
+  const int32_t* seq_lens;
+  int32_t* chunk_prefix;  // written by block (0, 0, 0) when not null
   float scale;
-  int Hkv, n_rep, q_dtype;
+  int B, Hkv, n_rep, q_dtype;
 };
 
-// q_rot[b, kvh, h, :] = scale * q[b, kvh*n_rep + h, :] Pi_K^T (zero rows for h >= n_rep).
-// Pi_K is staged in LDS with a padded row stride (thread j reads row j: banks j + d).
+// chunk_prefix[b] = sum over b' < b of ceil(L_b' / 64), b = 0..B (one 256-thread block).
+__device__ void chunk_prefix_block(const int32_t* seq_lens, int B, int32_t* prefix) {
+  __shared__ int part[4];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  int carry = 0;
+  for (int b0 = 0; b0 < B; b0 += 256) {
+    const int b = b0 + tid;
+    const int n = b < B ? (seq_lens[b] + 63) >> 6 : 0;
+    int x = n;  // inclusive wave scan
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) part[w] = x;
+    __syncthreads();
+    int off = carry;
+    for (int i = 0; i < w; ++i) off += part[i];
+    if (b < B) prefix[b] = off + x - n;  // exclusive
+    const int tile = part[0] + part[1] + part[2] + part[3];
+    __syncthreads();
+    carry += tile;
+  }
+  if (tid == 0) prefix[B] = carry;
+}
+
+// q_rot[b, kvh, h, j] = scale * sum_d q[b, kvh*n_rep + h, d] Pi_K[j, d] for output dims
+// j in quarter blockIdx.z of [0, D) (zero rows for h >= n_rep). The quarter's 32 rows
+// of Pi_K are staged in LDS with a padded stride (thread j reads row j: banks j + d).
 template <int D, int NREP>
 __global__ __launch_bounds__(256) void rotate_q_kernel(RotArgs a) {
-  constexpr int LDP = D + 1;
-  __shared__ float pis[D * LDP];
+  constexpr int LDP = D + 1, JQ = D / 4;
+  __shared__ float pis[JQ * LDP];
   __shared__ float qs[NREP][D];
-  const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const float4* src = reinterpret_cast<const float4*>(a.pi_k);
-  for (int i = tid; i < D * D / 4; i += 256) {
+  const int kvh = blockIdx.x, b = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
+  if (a.chunk_prefix && kvh == 0 && b == 0 && z == 0) chunk_prefix_block(a.seq_lens, a.B, a.chunk_prefix);
+  const float4* src = reinterpret_cast<const float4*>(a.pi_k + z * JQ * D);
+  for (int i = tid; i < JQ * D / 4; i += 256) {
     const float4 v = src[i];
     const int r = (4 * i) / D, c = (4 * i) % D;
     float* dst = pis + r * LDP + c;
@@ -99,9 +138,9 @@ __global__ __launch_bounds__(256) void rotate_q_kernel(RotArgs a) {
     qs[h][d] = h < a.n_rep ? load_elem(a.q, b * a.qsb + int64_t(kvh * a.n_rep + h) * a.qsh + d, a.q_dtype) : 0.f;
   }
   __syncthreads();
-  float* out = a.q_rot + (int64_t(b) * a.Hkv + kvh) * NREP * D;
-  for (int i = tid; i < NREP * D; i += 256) {
-    const int h = i / D, j = i % D;
+  float* out = a.q_rot + (int64_t(b) * a.Hkv + kvh) * NREP * D + z * JQ;
+  for (int i = tid; i < NREP * JQ; i += 256) {
+    const int h = i / JQ, j = i % JQ;
     const float* prow = pis + j * LDP;
     float acc = 0.f;
 #pragma unroll 8
@@ -278,81 +317,99 @@ struct MergeArgs {
   const float* part_ml;
   const float* pi_v;
   const int32_t* seq_lens;
+  const int32_t* chunk_prefix;
   void* out;
-  int out_dtype, Hq, Hkv, n_rep, log2S, pages_per_split, num_splits;
+  int out_dtype, Hq, Hkv, n_rep, log2S, pages_per_split, num_splits, balanced;
   int log2_units;  // partial maxima are in log2 units (weights 2^(m - M))
 };
 
-// out[b, kvh*n_rep + h, :] = (sum_s w_s acc_s / sum_s w_s l_s) Pi_V, w_s = exp(m_s - max m)
-// (2^(m_s - max m) for log2-unit partials), zero when no key was seen
-// (packed_attention_triton.py:137-159 plus :261). One work-group per (kv head,
-// sequence). Wave w handles heads w, w+4, ...: its lanes load the split maxima in
-// parallel, reduce the max, and leave each split's weight in LDS together with
-// the denominator; then every thread accumulates (head, dim) numerators from
-// independent loads, and finally rotates the rows by Pi_V staged in LDS.
-constexpr int kMergeTile = 256;  // splits per weight tile
+constexpr int kMergeTile = 256;  // partials per weight tile
 
+// out[b, kvh*n_rep + h, :] = (sum_s w_s acc_s / sum_s w_s l_s) Pi_V with
+// w_s = exp(m_s - max m) (2^(m_s - max m) for log2-unit partials), zero when no
+// key was seen (packed_attention_triton.py:137-159 plus :261). One work-group of D
+// threads per (query head h, kv head, sequence): thread d accumulates dim d over
+// the partials, then thread j forms output dim j from Pi_V rows read coalesced.
+// The partials of the group are rows r0 + s*stride, s < n: fixed splits give
+// r0 = (b*Hkv + kvh)*num_splits, stride 1, n = splits holding tokens; the
+// balanced scan gives rows w + b*Hkv + kvh for the waves w that touched it.
 template <int D>
-__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
-  __shared__ float piv[D * D];
-  __shared__ float av[16][D];
-  __shared__ float wts[16][kMergeTile];
-  __shared__ float hmax[16], hden[16];
-  const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const float4* src = reinterpret_cast<const float4*>(a.pi_v);
-  for (int i = tid; i < D * D / 4; i += 256) reinterpret_cast<float4*>(piv)[i] = src[i];
-  const int S = 1 << a.log2S;
+__global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
+  __shared__ float wts[kMergeTile];
+  __shared__ float red[D / 64];
+  __shared__ float av[D];
+  const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int wv = tid >> 6, lane = tid & 63;
+  int64_t r0 = 0;
+  int n = 0;
   const int L = a.seq_lens[b];
-  const int n_pages = (L + S - 1) >> a.log2S;
-  const int nsb = (n_pages + a.pages_per_split - 1) / a.pages_per_split;
-  const int64_t base = (int64_t(b) * a.Hkv + kvh) * a.num_splits * a.n_rep;
+  if (!a.balanced) {
+    const int S = 1 << a.log2S;
+    const int n_pages = (L + S - 1) >> a.log2S;
+    n = (n_pages + a.pages_per_split - 1) / a.pages_per_split;
+    r0 = (int64_t(b) * a.Hkv + kvh) * a.num_splits;
+  } else {
+    const int32_t* pre = a.chunk_prefix;
+    const int nb = pre[b + 1] - pre[b];
+    if (nb > 0) {
+      const int64_t C = int64_t(a.Hkv) * pre[gridDim.z];
+      const int64_t Wp = min(int64_t(a.num_splits), C);
+      const int64_t U0 = int64_t(a.Hkv) * pre[b] + int64_t(kvh) * nb, U1 = U0 + nb;
+      const int64_t wf = ((U0 + 1) * Wp + C - 1) / C - 1;  // last wave starting at or before U0
+      const int64_t wl = (U1 * Wp + C - 1) / C - 1;        // last wave starting before U1
+      r0 = wf + int64_t(b) * a.Hkv + kvh;
+      n = int(wl - wf + 1);
+    }
+  }
   auto wexp = [&](float x) { return a.log2_units ? __builtin_amdgcn_exp2f(x) : expf(x); };
-  for (int h = w; h < a.n_rep; h += 4) {
-    float M = -INFINITY;
-    for (int s = lane; s < nsb; s += 64) M = fmaxf(M, a.part_ml[2 * (base + int64_t(s) * a.n_rep + h)]);
-    M = wave_max(M);
-    float den = 0.f;
-    for (int s = lane; s < nsb; s += 64) {
-      const int64_t r = base + int64_t(s) * a.n_rep + h;
-      const float mm = a.part_ml[2 * r];
-      den += mm == -INFINITY ? 0.f : wexp(mm - M) * a.part_ml[2 * r + 1];
-    }
-    den = wave_sum(den);
-    if (lane == 0) {
-      hmax[h] = M;
-      hden[h] = den;
-    }
-  }
-  for (int i = tid; i < a.n_rep * D; i += 256) av[i / D][i % D] = 0.f;
-  for (int t0 = 0; t0 < nsb; t0 += kMergeTile) {
-    const int tn = min(kMergeTile, nsb - t0);
-    __syncthreads();
-    for (int i = tid; i < a.n_rep * tn; i += 256) {
-      const int h = i / tn, s = t0 + i % tn;
-      const float mm = a.part_ml[2 * (base + int64_t(s) * a.n_rep + h)];
-      wts[h][s - t0] = mm == -INFINITY ? 0.f : wexp(mm - hmax[h]);
-    }
-    __syncthreads();
-    for (int i = tid; i < a.n_rep * D; i += 256) {
-      const int h = i / D, d = i % D;
-      const float* col = a.part_acc + (base + int64_t(t0) * a.n_rep + h) * D + d;
-      float num = 0.f;
-#pragma unroll 8
-      for (int s = 0; s < tn; ++s) num = fmaf(wts[h][s], col[int64_t(s) * a.n_rep * D], num);
-      av[h][d] += num;
-    }
-  }
+  const float* ml = a.part_ml + 2 * (r0 * a.n_rep + h);
+  const int64_t mstride = 2 * int64_t(a.n_rep);  // floats between consecutive partials of (h)
+  // maximum and denominator over the partials
+  float M = -INFINITY;
+  for (int s = tid; s < n; s += D) M = fmaxf(M, ml[s * mstride]);
+  M = wave_max(M);
+  if (lane == 0) red[wv] = M;
   __syncthreads();
-  for (int i = tid; i < a.n_rep * D; i += 256) {
-    const int h = i / D, j = i % D;
-    const float den = hden[h];
-    float o = 0.f;
-#pragma unroll 8
-    for (int d = 0; d < D; ++d) o = fmaf(av[h][d], piv[d * D + j], o);
-    // (a / l) Pi_V == (a Pi_V) / l up to rounding; l > 0 whenever a key was seen
-    o = den > 0.f ? o / fmaxf(den, 1e-30f) : 0.f;
-    store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + j, a.out_dtype, o);
+  M = red[0];
+  for (int i = 1; i < D / 64; ++i) M = fmaxf(M, red[i]);
+  __syncthreads();
+  float num = 0.f, den = 0.f;
+  const float* acc = a.part_acc + (r0 * a.n_rep + h) * D + tid;
+  const int64_t astride = int64_t(a.n_rep) * D;
+  for (int t0 = 0; t0 < n; t0 += kMergeTile) {
+    const int tn = min(kMergeTile, n - t0);
+    for (int s = tid; s < tn; s += D) {
+      const float mm = ml[(t0 + s) * mstride];
+      const float wgt = mm == -INFINITY ? 0.f : wexp(mm - M);
+      wts[s] = wgt;
+      den = fmaf(wgt, ml[(t0 + s) * mstride + 1], den);
+    }
+    __syncthreads();
+    int s = 0;
+    for (; s + 4 <= tn; s += 4) {
+      const float x0 = acc[(t0 + s) * astride], x1 = acc[(t0 + s + 1) * astride];
+      const float x2 = acc[(t0 + s + 2) * astride], x3 = acc[(t0 + s + 3) * astride];
+      num = fmaf(wts[s], x0, num);
+      num = fmaf(wts[s + 1], x1, num);
+      num = fmaf(wts[s + 2], x2, num);
+      num = fmaf(wts[s + 3], x3, num);
+    }
+    for (; s < tn; ++s) num = fmaf(wts[s], acc[(t0 + s) * astride], num);
+    __syncthreads();
   }
+  den = wave_sum(den);
+  if (lane == 0) red[wv] = den;
+  av[tid] = num;
+  __syncthreads();
+  den = 0.f;
+  for (int i = 0; i < D / 64; ++i) den += red[i];
+  // out_j = sum_d a_d Pi_V[d, j]; (a / l) Pi_V == (a Pi_V) / l up to rounding
+  float o = 0.f;
+  const float* pv = a.pi_v + tid;
+#pragma unroll 16
+  for (int d = 0; d < D; ++d) o = fmaf(av[d], pv[d * D], o);
+  o = (L > 0 && den > 0.f) ? o / fmaxf(den, 1e-30f) : 0.f;
+  store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + tid, a.out_dtype, o);
 }
 
 using RotFn = void (*)(RotArgs);
@@ -402,34 +459,127 @@ RotFn pick_rot(int nrep) {
   return nullptr;
 }
 
+// Page-scan kernel preference, read once from WN_DECODE_SCAN: "rows" (default)
+// uses the pipelined row-per-lane matrix-core scan where it applies, "rows1" its
+// one-phase-at-a-time form, "valu" always the vector-ALU scan. Every choice
+// computes the same result; the knob exists to compare them on one machine.
+int scan_choice() {
+  static const int choice = [] {
+    const char* e = getenv("WN_DECODE_SCAN");
+    if (e && !strcmp(e, "valu")) return 2;
+    if (e && !strcmp(e, "rows1")) return 1;
+    return 0;
+  }();
+  return choice;
+}
+
 int pad_nrep(int n_rep) {
   int p = 1;
   while (p < n_rep) p <<= 1;
   return p;
 }
 
+// The scan wn_decode_attention runs for this shape.
+SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v) {
+  SplitKernel sk;
+  const int n_rep = Hq / Hkv;
+  if (D == 128 && n_rep <= 4 && S >= 16 && scan_choice() < 2) sk = pick_split_rows(bw_k, bw_v, scan_choice() == 0);
+  if (!sk.fn) {
+    const int nrp = pad_nrep(n_rep);
+    sk.fn = D == 128 ? pick_split<128>(bw_k, bw_v, nrp) : pick_split<64>(bw_k, bw_v, nrp);
+    sk.block = kBlock;
+    sk.nrep = nrp;
+  }
+  return sk;
+}
+
+// Resident one-wave groups of `fn` on the current device (blocks per CU x CUs).
+int resident_waves(SplitFn fn) {
+  static std::mutex mu;
+  static std::map<std::pair<int, SplitFn>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find({dev, fn});
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), 64, 0) !=
+          hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  const int w = per_cu * cus;
+  cache[{dev, fn}] = w;
+  return w;
+}
+
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 struct WsLayout {
-  int64_t qrot, acc, ml, total;
+  int64_t qrot, prefix, acc, ml, total;
 };
 
-WsLayout ws_layout(int B, int Hq, int Hkv, int D, int num_splits) {
+// Scratch: q_rot (B, Hkv, max(NREP, 4), D) fp32, chunk prefix (B+1) int32, and
+// the partials, (rows * n_rep) x D for acc and x 2 for (m, l).
+WsLayout ws_layout(int B, int Hq, int Hkv, int D, int pages_per_split, int num_splits) {
   WsLayout l;
-  const int nrp = max(pad_nrep(Hq / Hkv), 4);  // the matrix-core scan reads 4 rows per kv head
+  const int n_rep = Hq / Hkv;
+  const int nrp = max(pad_nrep(n_rep), 4);  // the matrix-core scan reads 4 rows per kv head
+  const int64_t rows = pages_per_split > 0 ? int64_t(B) * Hkv * num_splits : int64_t(num_splits) + int64_t(B) * Hkv;
   l.qrot = 0;
-  l.acc = align256(int64_t(B) * Hkv * nrp * D * 4);
-  l.ml = l.acc + align256(int64_t(B) * Hq * num_splits * D * 4);
-  l.total = l.ml + align256(int64_t(B) * Hq * num_splits * 2 * 4);
+  l.prefix = align256(int64_t(B) * Hkv * nrp * D * 4);
+  l.acc = l.prefix + align256(int64_t(B + 1) * 4);
+  l.ml = l.acc + align256(rows * n_rep * D * 4);
+  l.total = l.ml + align256(rows * n_rep * 2 * 4);
   return l;
 }
 
 }  // namespace
 }  // namespace wn
 
-extern "C" int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int num_splits) {
-  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || D <= 0 || num_splits <= 0) return -1;
-  return wn::ws_layout(B, Hq, Hkv, D, num_splits).total;
+// Work-groups the fixed-split plan aims for: 256 CUs x ~16 resident waves / 4
+// waves per group, so every CU keeps several groups in flight while the
+// per-split partials stay a few percent of the page bytes.
+static constexpr int64_t kTargetGroups = 4096;
+
+extern "C" int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
+                              int requested_splits, int* pages_per_split, int* num_splits) {
+  using namespace wn;
+  clear_error();
+  WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && max_pages >= 0, WN_E_INVALID,
+             "wn_decode_plan: bad sizes B=%d Hq=%d Hkv=%d max_pages=%d", B, Hq, Hkv, max_pages);
+  WN_REQUIRE(pages_per_split && num_splits, WN_E_INVALID, "wn_decode_plan: null output");
+  const int mp = max_pages > 0 ? max_pages : 1;
+  if (requested_splits > 0) {
+    // packed_attention_triton.py:211-216: splits clamp to [1, max_pages],
+    // each covering cdiv(max_pages, splits) page slots.
+    const int ns = requested_splits < mp ? requested_splits : mp;
+    *num_splits = ns;
+    *pages_per_split = (mp + ns - 1) / ns;
+    return WN_OK;
+  }
+  const SplitKernel sk = choose_scan(Hq, Hkv, D, S, bw_k, bw_v);
+  if (sk.fn && sk.block == 64) {  // row scan: balanced persistent waves
+    const int w = resident_waves(sk.fn);
+    WN_REQUIRE(w > 0, WN_E_LAUNCH, "wn_decode_plan: cannot query the device occupancy");
+    *pages_per_split = 0;
+    *num_splits = w;
+    return WN_OK;
+  }
+  const int64_t units = int64_t(B > 0 ? B : 1) * Hkv;
+  int64_t want = (kTargetGroups + units - 1) / units;
+  if (want < 1) want = 1;
+  if (want > mp) want = mp;
+  int64_t pps = (mp + want - 1) / want;
+  if (pps < 16) pps = 16;  // >= 256 tokens at S=16: all four waves of a group busy
+  if (pps > mp) pps = mp;
+  *pages_per_split = int(pps);
+  *num_splits = int((mp + pps - 1) / pps);
+  return WN_OK;
+}
+
+extern "C" int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int pages_per_split, int num_splits) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || D <= 0 || num_splits <= 0 || pages_per_split < 0) return -1;
+  return wn::ws_layout(B, Hq, Hkv, D, pages_per_split, num_splits).total;
 }
 
 extern "C" int wn_decode_attention(
@@ -455,8 +605,9 @@ extern "C" int wn_decode_attention(
   WN_REQUIRE(is_pow2(S), WN_E_INVALID, "decode: page size %d is not a power of two", S);
   WN_REQUIRE(q_dtype >= WN_F32 && q_dtype <= WN_BF16 && out_dtype >= WN_F32 && out_dtype <= WN_BF16,
              WN_E_INVALID, "decode: dtype codes %d/%d", q_dtype, out_dtype);
-  WN_REQUIRE(pages_per_split > 0 && num_splits > 0 &&
-                 int64_t(pages_per_split) * num_splits >= int64_t(max_pages),
+  const bool balanced = pages_per_split == 0;
+  WN_REQUIRE(num_splits > 0 && pages_per_split >= 0 &&
+                 (balanced || int64_t(pages_per_split) * num_splits >= int64_t(max_pages)),
              WN_E_INVALID, "decode: plan %d x %d does not cover %d pages", num_splits, pages_per_split,
              max_pages);
   if (B == 0) return WN_OK;
@@ -473,34 +624,26 @@ extern "C" int wn_decode_attention(
              "decode: head stride smaller than one (S, NB) page block");
   WN_REQUIRE(aligned(pi_k, 16) && aligned(pi_v, 4), WN_E_INVALID, "decode: rotation alignment");
 
-  // Matrix-core scan when it applies (D=128, <= 4 query heads per kv head, fp16 norm
-  // groups of 4 slots 8-byte aligned), else the vector-ALU scan.
-  SplitKernel sk;
-  const bool norms8 = aligned(k_norms, 8) && aligned(v_norms, 8) && kn_stride_p % 4 == 0 &&
-                      kn_stride_h % 4 == 0 && vn_stride_p % 4 == 0 && vn_stride_h % 4 == 0;
-  if (D == 128 && n_rep <= 4 && S >= 16 && norms8) sk = pick_split_mfma(bw_k, bw_v);
-  if (!sk.fn) {
-    const int nrp = pad_nrep(n_rep);
-    sk.fn = D == 128 ? pick_split<128>(bw_k, bw_v, nrp) : pick_split<64>(bw_k, bw_v, nrp);
-    sk.block = kBlock;
-    sk.nrep = nrp;
-  }
-  RotFn rot = D == 128 ? pick_rot<128>(sk.nrep) : pick_rot<64>(sk.nrep);
+  const SplitKernel sk = choose_scan(Hq, Hkv, D, S, bw_k, bw_v);
+  RotFn rot = D == 128 ? pick_rot<128>(max(sk.nrep, 1)) : pick_rot<64>(max(sk.nrep, 1));
   WN_REQUIRE(sk.fn && rot, WN_E_UNSUPPORTED, "decode: (D=%d, bw_k=%d, bw_v=%d) not compiled", D, bw_k,
              bw_v);
+  WN_REQUIRE(!balanced || sk.block == 64, WN_E_INVALID,
+             "decode: a balanced plan (pages_per_split 0) needs the row scan; ask wn_decode_plan");
 
-  const WsLayout lay = ws_layout(B, Hq, Hkv, D, num_splits);
+  const WsLayout lay = ws_layout(B, Hq, Hkv, D, pages_per_split, num_splits);
   WN_REQUIRE(workspace && workspace_bytes >= lay.total && aligned(workspace, 256), WN_E_WORKSPACE,
              "decode: workspace needs %lld bytes, 256-aligned (got %lld)", (long long)lay.total,
              (long long)workspace_bytes);
   char* ws = static_cast<char*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  int32_t* prefix = balanced ? reinterpret_cast<int32_t*>(ws + lay.prefix) : nullptr;
 
   // the matrix-core scan keeps scores in log2 units: fold log2(e) into q_rot
   const float q_scale = sk.log2_units ? float(double(scale) * 1.4426950408889634) : scale;
-  RotArgs ra{q, q_stride_b, q_stride_h, pi_k, reinterpret_cast<float*>(ws + lay.qrot), q_scale, Hkv, n_rep,
-             q_dtype};
-  hipLaunchKernelGGL(rot, dim3(Hkv, B), dim3(256), 0, st, ra);
+  RotArgs ra{q, q_stride_b, q_stride_h, pi_k, reinterpret_cast<float*>(ws + lay.qrot), seq_lens, prefix,
+             q_scale, B, Hkv, n_rep, q_dtype};
+  hipLaunchKernelGGL(rot, dim3(Hkv, B, 4), dim3(256), 0, st, ra);
 
   DecodeArgs da;
   da.q_rot = ra.q_rot;
@@ -523,20 +666,24 @@ extern "C" int wn_decode_attention(
   da.vnp = vn_stride_p;
   da.vnh = vn_stride_h;
   da.tsb = table_stride_b;
+  da.chunk_prefix = prefix;
+  da.B = B;
   da.Hkv = Hkv;
   da.n_rep = n_rep;
   da.log2S = ilog2(S);
   da.pages_per_split = pages_per_split;
   da.num_splits = num_splits;
+  da.balanced = balanced ? 1 : 0;
+  const dim3 grid = balanced ? dim3(num_splits) : dim3(num_splits, Hkv, B);
   if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
-  hipLaunchKernelGGL(sk.fn, dim3(num_splits, Hkv, B), dim3(sk.block), 0, st, da);
+  hipLaunchKernelGGL(sk.fn, grid, dim3(sk.block), 0, st, da);
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
-  MergeArgs ma{da.part_acc, da.part_ml, pi_v, seq_lens, out, out_dtype, Hq, Hkv, n_rep, da.log2S,
-               pages_per_split, num_splits, sk.log2_units ? 1 : 0};
+  MergeArgs ma{da.part_acc, da.part_ml, pi_v, seq_lens, prefix, out, out_dtype, Hq, Hkv, n_rep, da.log2S,
+               pages_per_split, num_splits, da.balanced, sk.log2_units ? 1 : 0};
   if (D == 128)
-    hipLaunchKernelGGL(merge_kernel<128>, dim3(Hkv, B), dim3(256), 0, st, ma);
+    hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep, Hkv, B), dim3(128), 0, st, ma);
   else
-    hipLaunchKernelGGL(merge_kernel<64>, dim3(Hkv, B), dim3(256), 0, st, ma);
+    hipLaunchKernelGGL(merge_kernel<64>, dim3(n_rep, Hkv, B), dim3(64), 0, st, ma);
   return check_launch("wn_decode_attention");
 }

@@ -1,0 +1,584 @@
+// Row-per-lane matrix-core page scan of the packed decode attention (head_dim 128,
+// power-of-two page size >= 16, up to four query heads per kv head), gfx950.
+//
+// One wave per work-group, independent of every other wave. With fixed splits a
+// wave owns a range of pages of one (sequence, kv head); with a balanced plan
+// the resident waves split the flattened (sequence, kv head, chunk) space into
+// equal shares. Either way a wave walks its tokens in 64-token chunks.
+//
+//   scores  lane l holds the packed K row of token c0+l. For each dim k one
+//           v_mfma_f32_4x4x1_16b_f32 with A = q_rot[head i][k] broadcast to all
+//           16 blocks (CBSZ=4, ABID=k%16) and B = c_K[code(token, k)] gives
+//           D[block][i][j] = partial s(head i, token 4*block+j): lane l ends with
+//           the four heads' scores of its own token. 128 MFMAs per chunk.
+//   softmax per head in log2 units (q_rot carries log2 e), lane = token, with a
+//           lazy reference maximum: it moves (rescaling the accumulators) only
+//           when a score exceeds it by more than kRescale, so 2^(s - m) <= 2^kRescale.
+//   values  p * n_V goes through a 1.3 KB LDS tile so that lanes 16G+i hold
+//           p(head i, token c0+4q+G) for the 16 token quads q. Lanes 16G..16G+15
+//           hold the packed V codes of dims 8p..8p+7 (p = lane%16) of that token.
+//           A v_mfma_f32_4x4x1_16b_f32 with CBSZ=2 broadcasts A inside each group of
+//           four blocks, so block group G accumulates token c0+4q+G into
+//           acc[m] register i = (head i, dim 8p+m). 8 MFMAs per quad, 128 per chunk;
+//           the four groups are folded once per split.
+//
+// Codebooks (2^bw fp32) sit in LDS; every product is an exact fp32 multiply-add.
+// 4-bit codes become LDS byte offsets with one SDWA byte-select AND each. Page ids
+// run two chunks ahead and the packed rows of chunk c+1 load while chunk c computes.
+// Algebra: turboquant_kv/packed_attention.py:260-334 (the schedule of the
+// reference kernel packed_attention_triton.py:51-134).
+#include <utility>
+
+#include "wn_decode.h"
+
+namespace wn {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kRescale = 8.0f;
+constexpr int kPStride = 20;  // floats per (head, token group) row of the p tile (16 + pad, 16-B rows)
+
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// Byte K of x AND m, one VOP2 SDWA instruction.
+template <int K>
+__device__ __forceinline__ uint32_t byte_and(uint32_t x, uint32_t m) {
+  uint32_t r;
+  if constexpr (K == 0)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
+        : "=v"(r) : "v"(x), "v"(m));
+  else if constexpr (K == 1)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:DWORD"
+        : "=v"(r) : "v"(x), "v"(m));
+  else if constexpr (K == 2)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:DWORD"
+        : "=v"(r) : "v"(x), "v"(m));
+  else
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:DWORD"
+        : "=v"(r) : "v"(x), "v"(m));
+  return r;
+}
+
+// LDS byte offsets (code * 4) of codes [8g, 8g+8) of a packed little-endian word
+// array, LSB-first, BW bits per code. For 4-bit codes word g holds exactly these
+// eight codes: even codes sit at bits 2..5 of the bytes of w<<2, odd codes at
+// bits 2..5 of the bytes of w>>2.
+template <int BW, int G, int NW>
+__device__ __forceinline__ void code_offsets8(const uint32_t (&w)[NW], uint32_t mask3c, uint32_t (&off)[8]) {
+  if constexpr (BW == 4) {
+    const uint32_t e = w[G] << 2, o = w[G] >> 2;
+    off[0] = byte_and<0>(e, mask3c);
+    off[1] = byte_and<0>(o, mask3c);
+    off[2] = byte_and<1>(e, mask3c);
+    off[3] = byte_and<1>(o, mask3c);
+    off[4] = byte_and<2>(e, mask3c);
+    off[5] = byte_and<2>(o, mask3c);
+    off[6] = byte_and<3>(e, mask3c);
+    off[7] = byte_and<3>(o, mask3c);
+  } else {
+    static_for<0, 8>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      constexpr int bit = (8 * G + j) * BW, wi = bit >> 5, sh = bit & 31;
+      uint32_t v = w[wi] >> sh;
+      if constexpr (sh + BW > 32) v |= w[wi + 1] << (32 - sh);
+      off[j] = (v & ((1u << BW) - 1u)) << 2;
+    });
+  }
+}
+
+__device__ __forceinline__ float lds_at(const float* tab, uint32_t byte_off) {
+  return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(tab) + byte_off);
+}
+
+__device__ __forceinline__ float half_lo(uint32_t h) { return f16_to_f32(uint16_t(h & 0xffffu)); }
+
+// Words of the V codes one lane reads per token: BWV bytes (8 codes).
+template <int BWV>
+struct VWords {
+  static constexpr int N = BWV <= 4 ? 1 : 2;
+};
+
+// Packed K row and norms of token c0 + lane.
+template <int BWK>
+struct KChunk {
+  uint32_t k[4 * BWK];  // 16*BWK bytes
+  uint32_t nk, nv;      // fp16 norms (low 16 bits)
+};
+
+// For quad q: codes 8p..8p+7 of token c0 + 4q + G (G = lane/16, p = lane%16).
+template <int BWV>
+struct VChunk {
+  uint32_t v[16][BWV <= 4 ? 1 : 2];
+};
+
+// BWV bytes at p (8 codes of one lane) into little-endian words. p is aligned to
+// gcd(BWV, 8)-ish: 4 and 8 are naturally aligned, 2 and 6 use 2-byte pieces.
+template <int BWV>
+__device__ __forceinline__ void load_vcodes(const uint8_t* p, bool odd_lane, uint32_t (&out)[VWords<BWV>::N]) {
+  if constexpr (BWV == 4) {
+    out[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else if constexpr (BWV == 8) {
+    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    out[0] = x.x;
+    out[1] = x.y;
+  } else if constexpr (BWV == 2) {
+    out[0] = *reinterpret_cast<const uint16_t*>(p);
+  } else if constexpr (BWV == 6) {
+    // bytes [6p, 6p+6): a 4-byte-aligned dword and a 2-byte piece, placed by lane parity
+    const uint32_t d = *reinterpret_cast<const uint32_t*>(p + (odd_lane ? 2 : 0));
+    const uint32_t h = *reinterpret_cast<const uint16_t*>(p + (odd_lane ? 0 : 4));
+    out[0] = odd_lane ? (h | (d << 16)) : d;
+    out[1] = odd_lane ? (d >> 16) : h;
+  } else {  // 3 or 5 bytes, byte-aligned
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int i = 0; i < BWV; ++i) {
+      const uint32_t bv = p[i];
+      if (i < 4) w0 |= bv << (8 * i);
+      else w1 |= bv << (8 * (i - 4));
+    }
+    out[0] = w0;
+    if constexpr (VWords<BWV>::N > 1) out[1] = w1;
+  }
+}
+
+struct RowState {
+  f32x4 acc[8];  // register i: head i, dim 8p+m (partial over this lane's token group)
+  float m[4];    // reference maxima (wave-uniform), log2 units
+  float l[4];    // sum of 2^(s - m) over this lane's tokens
+};
+
+// K side of chunk [c0, c0+64): the packed K row and both norms of token c0+lane,
+// whose page is pid_lane.
+template <int BWK>
+__device__ __forceinline__ void load_k(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane, KChunk<BWK>& r) {
+  constexpr int NBK = 16 * BWK;
+  const int slot = (c0 + lane) & ((1 << a.log2S) - 1);
+  const uint8_t* krow = a.k_pages + int64_t(pid_lane) * a.ksp + kvh * a.ksh + slot * NBK;
+#pragma unroll
+  for (int i = 0; i < NBK / 16; ++i) {
+    const uint4 x = reinterpret_cast<const uint4*>(krow)[i];
+    r.k[4 * i] = x.x;
+    r.k[4 * i + 1] = x.y;
+    r.k[4 * i + 2] = x.z;
+    r.k[4 * i + 3] = x.w;
+  }
+  r.nk = a.k_norms[int64_t(pid_lane) * a.knp + kvh * a.knh + slot];
+  r.nv = a.v_norms[int64_t(pid_lane) * a.vnp + kvh * a.vnh + slot];
+}
+
+// V side of chunk [c0, c0+64): for every token quad q the BWV bytes of codes
+// 8p..8p+7 of token c0+4q+G (G = lane/16, p = lane%16). c0 is a multiple of 16 and
+// pages hold >= 16 tokens, so the four quads of 16-token block j share the page of
+// lane 16j (pid_lane is the page of token c0+lane).
+template <int BWV>
+__device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane, VChunk<BWV>& r) {
+  constexpr int NBV = 16 * BWV;
+  const int smask = (1 << a.log2S) - 1;
+  const int p = lane & 15;
+  const int lane_off = (lane >> 4) * NBV + BWV * p;
+  static_for<0, 4>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    const int pid_j = __builtin_amdgcn_readlane(pid_lane, 16 * j);
+    const uint8_t* vj = a.v_pages + int64_t(pid_j) * a.vsp + kvh * a.vsh + ((c0 + 16 * j) & smask) * NBV + lane_off;
+    static_for<0, 4>([&](auto qc) {
+      constexpr int qq = decltype(qc)::value;
+      load_vcodes<BWV>(vj + 4 * qq * NBV, p & 1, r.v[4 * j + qq]);
+    });
+  });
+}
+
+// Score lookups of dims [8g, 8g+8) of this lane's K row.
+template <int BWK, int G>
+__device__ __forceinline__ void score_look(const uint32_t (&k)[4 * BWK], const float* cbk, float (&kv)[8]) {
+  uint32_t off[8];
+  code_offsets8<BWK, G>(k, 0x3c, off);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) kv[j] = lds_at(cbk, off[j]);
+}
+
+// The 8 score MFMAs of dims [8g, 8g+8): A = q_rot[head][k] broadcast from block k%16.
+template <int G>
+__device__ __forceinline__ void score_mfma(const float (&qb)[8], const float (&kv)[8], f32x4& s0, f32x4& s1) {
+  static_for<0, 8>([&](auto jc) {
+    constexpr int j = decltype(jc)::value, k = 8 * G + j;
+    if constexpr (j & 1)
+      s1 = __builtin_amdgcn_mfma_f32_4x4x1f32(qb[k >> 4], kv[j], s1, 4, k & 15, 0);
+    else
+      s0 = __builtin_amdgcn_mfma_f32_4x4x1f32(qb[k >> 4], kv[j], s0, 4, k & 15, 0);
+  });
+}
+
+// Value lookups of quad q (this lane's 8 dims of token c0+4q+G).
+template <int BWV, int Q>
+__device__ __forceinline__ void value_look(const VChunk<BWV>& v, const float* cbv, float (&vv)[8]) {
+  uint32_t off[8];
+  code_offsets8<BWV, 0>(v.v[Q], 0x3c, off);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) vv[j] = lds_at(cbv, off[j]);
+}
+
+// The 8 value MFMAs of quad q: A = p*n_V broadcast inside each group of four blocks.
+__device__ __forceinline__ void value_mfma(float a_q, const float (&vv)[8], f32x4 (&acc)[8]) {
+  static_for<0, 8>([&](auto mc) {
+    constexpr int mm = decltype(mc)::value;
+    acc[mm] = __builtin_amdgcn_mfma_f32_4x4x1f32(a_q, vv[mm], acc[mm], 2, 0, 0);
+  });
+}
+
+// Scores of the chunk's 64 tokens (lane = token, register i = head i); lookups of
+// group g+1 are issued before the MFMAs of group g.
+template <int BWK>
+__device__ __forceinline__ f32x4 score_phase(const KChunk<BWK>& kc, const float* cbk, const float (&qb)[8]) {
+  f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+  float kv[2][8];
+  score_look<BWK, 0>(kc.k, cbk, kv[0]);
+  static_for<0, 16>([&](auto gc) {
+    constexpr int g = decltype(gc)::value;
+    if constexpr (g + 1 < 16) score_look<BWK, g + 1>(kc.k, cbk, kv[(g + 1) & 1]);
+    score_mfma<g>(qb, kv[g & 1], s0, s1);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  return s0 + s1;
+}
+
+// Values of a chunk; lookups of quad q+1 are issued before the MFMAs of quad q.
+template <int BWV>
+__device__ __forceinline__ void value_phase(const VChunk<BWV>& vc, const float* cbv, const float (&A)[16],
+                                            f32x4 (&acc)[8]) {
+  float vv[2][8];
+  value_look<BWV, 0>(vc, cbv, vv[0]);
+  static_for<0, 16>([&](auto qc) {
+    constexpr int q = decltype(qc)::value;
+    if constexpr (q + 1 < 16) value_look<BWV, q + 1>(vc, cbv, vv[(q + 1) & 1]);
+    value_mfma(A[q], vv[q & 1], acc);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
+// Values of chunk c and scores of chunk c+1, interleaved group by group: two
+// independent MFMA chains, so one stream's lookups are in flight while the
+// other's MFMAs run.
+template <int BWK, int BWV>
+__device__ __forceinline__ f32x4 value_and_score(const VChunk<BWV>& vc, const float* cbv, const float (&A)[16],
+                                                 f32x4 (&acc)[8], const KChunk<BWK>& kc, const float* cbk,
+                                                 const float (&qb)[8]) {
+  f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+  float kv[2][8], vv[2][8];
+  score_look<BWK, 0>(kc.k, cbk, kv[0]);
+  value_look<BWV, 0>(vc, cbv, vv[0]);
+  static_for<0, 16>([&](auto gc) {
+    constexpr int g = decltype(gc)::value;
+    if constexpr (g + 1 < 16) {
+      score_look<BWK, g + 1>(kc.k, cbk, kv[(g + 1) & 1]);
+      value_look<BWV, g + 1>(vc, cbv, vv[(g + 1) & 1]);
+    }
+    value_mfma(A[g], vv[g & 1], acc);
+    score_mfma<g>(qb, kv[g & 1], s0, s1);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  return s0 + s1;
+}
+
+// Online softmax of one chunk (lane = token) and the p * n_V transposition: on
+// return lane 16G+i holds A[q] = p(head i, token c0+4q+G) * n_V for q = 0..15.
+__device__ __forceinline__ void softmax_phase(f32x4 s, uint32_t nk_h, uint32_t nv_h, bool valid, int lane,
+                                              float* pt, RowState& st, float (&A)[16]) {
+  const float nk = half_lo(nk_h);
+  const float nv = valid ? half_lo(nv_h) : 0.f;
+  float sv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sv[i] = valid ? s[i] * nk : -INFINITY;
+  bool move = st.m[0] == -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) move = move || __any(sv[i] > st.m[i] + kRescale);
+  if (move) {  // wave-uniform
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float m_new = fmaxf(st.m[i], wave_max(sv[i]));
+      const float alpha = __builtin_amdgcn_exp2f(st.m[i] - m_new);  // 0 on the first chunk
+      st.m[i] = m_new;
+      st.l[i] *= alpha;
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) st.acc[mm][i] *= alpha;
+    }
+  }
+  float pv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float p = __builtin_amdgcn_exp2f(sv[i] - st.m[i]);  // 0 for masked tokens
+    st.l[i] += p;
+    pv[i] = p * nv;
+  }
+  wave_lds_sync();  // the previous chunk's reads of the tile are done
+  {
+    const int G = lane & 3, q = lane >> 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pt[(i * 4 + G) * kPStride + q] = pv[i];
+  }
+  wave_lds_sync();
+  const float4* src = reinterpret_cast<const float4*>(pt + ((lane & 3) * 4 + (lane >> 4)) * kPStride);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 x = src[i];
+    A[4 * i] = x.x;
+    A[4 * i + 1] = x.y;
+    A[4 * i + 2] = x.z;
+    A[4 * i + 3] = x.w;
+  }
+}
+
+// Folds the four token groups and the per-lane sums and writes the (acc, m, l)
+// partial of each query head h < n_rep to row prow * n_rep + h.
+__device__ __forceinline__ void write_partial(const DecodeArgs& a, RowState& st, int64_t prow, int lane) {
+  constexpr int D = 128;
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = st.acc[mm][i];
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      st.acc[mm][i] = x;
+    }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) st.l[i] = wave_sum(st.l[i]);
+  const int64_t row0 = prow * a.n_rep;
+  if (lane < 16) {  // lane p: dims 8p..8p+7 of every head
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i < a.n_rep) {
+        float* dst = a.part_acc + (row0 + i) * D + 8 * lane;
+        *reinterpret_cast<float4*>(dst) = make_float4(st.acc[0][i], st.acc[1][i], st.acc[2][i], st.acc[3][i]);
+        *reinterpret_cast<float4*>(dst + 4) =
+            make_float4(st.acc[4][i], st.acc[5][i], st.acc[6][i], st.acc[7][i]);
+      }
+    }
+  }
+  // m and l are wave-uniform: lane 0 writes every head's (a lane-indexed pick would
+  // turn the register arrays into an indexed stack object)
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i < a.n_rep) {
+        a.part_ml[2 * (row0 + i)] = st.m[i];
+        a.part_ml[2 * (row0 + i) + 1] = st.l[i];
+      }
+    }
+  }
+}
+
+// Scans tokens [t_lo, t_hi) of (sequence b, kv head kvh) in 64-token chunks (t_lo a
+// multiple of 16) and writes one partial at row prow. PIPE overlaps the values of
+// chunk c with the scores of chunk c+1; otherwise each chunk runs score, softmax,
+// values in turn. Loads run one chunk ahead of use either way.
+template <int BWK, int BWV, bool PIPE>
+__device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, int t_lo, int t_hi, int64_t prow,
+                                           int lane, const float* cbk, const float* cbv, float* ptile) {
+  constexpr int D = 128;
+  const int page_hi = (t_hi + (1 << a.log2S) - 1) >> a.log2S;
+  const int n = (t_hi - t_lo + 63) >> 6;
+
+  // register m of lane 4j+i holds q_rot[head i][16m + j]
+  float qb[8];
+  {
+    const float* qp = a.q_rot + ((int64_t(b) * a.Hkv + kvh) * 4 + (lane & 3)) * D + (lane >> 2);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) qb[m] = qp[16 * m];
+  }
+  const int32_t* trow = a.table + b * a.tsb;
+  // page of this lane's token in chunk c (tokens past the range read its last page and are masked)
+  auto pid_of = [&](int c) {
+    const int col = min((t_lo + 64 * c + lane) >> a.log2S, page_hi - 1);
+    return trow[col];
+  };
+
+  RowState st;
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) st.acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    st.m[i] = -INFINITY;
+    st.l[i] = 0.f;
+  }
+  float A[16];
+  KChunk<BWK> kc, kn;
+  VChunk<BWV> vc, vn;
+
+  if constexpr (!PIPE) {
+    int pid = pid_of(0);
+    load_k(a, kvh, lane, t_lo, pid, kc);
+    load_v(a, kvh, lane, t_lo, pid, vc);
+    int pid_next = n > 1 ? pid_of(1) : 0;
+    for (int c = 0; c < n; ++c) {
+      const int c0 = t_lo + 64 * c;
+      if (c + 1 < n) {
+        load_k(a, kvh, lane, c0 + 64, pid_next, kn);
+        load_v(a, kvh, lane, c0 + 64, pid_next, vn);
+      }
+      if (c + 2 < n) pid_next = pid_of(c + 2);
+      const f32x4 s = score_phase(kc, cbk, qb);
+      softmax_phase(s, kc.nk, kc.nv, c0 + lane < t_hi, lane, ptile, st, A);
+      value_phase(vc, cbv, A, st.acc);
+      kc = kn;
+      vc = vn;
+    }
+  } else {
+    // prologue: chunk 0 through its softmax; K of chunk 1 in flight
+    const int pid0 = pid_of(0);
+    load_k(a, kvh, lane, t_lo, pid0, kc);
+    load_v(a, kvh, lane, t_lo, pid0, vc);
+    int pid_a = n > 1 ? pid_of(1) : 0;  // page of chunk c+1 at the top of iteration c
+    if (n > 1) load_k(a, kvh, lane, t_lo + 64, pid_a, kn);
+    int pid_b = n > 2 ? pid_of(2) : 0;  // page of chunk c+2
+    softmax_phase(score_phase(kc, cbk, qb), kc.nk, kc.nv, t_lo + lane < t_hi, lane, ptile, st, A);
+    kc = kn;
+    for (int c = 0; c < n; ++c) {
+      const int c1 = t_lo + 64 * (c + 1);
+      if (c + 2 < n) load_k(a, kvh, lane, c1 + 64, pid_b, kn);
+      if (c + 1 < n) load_v(a, kvh, lane, c1, pid_a, vn);
+      pid_a = pid_b;
+      if (c + 3 < n) pid_b = pid_of(c + 3);
+      if (c + 1 < n) {
+        const f32x4 s = value_and_score(vc, cbv, A, st.acc, kc, cbk, qb);
+        softmax_phase(s, kc.nk, kc.nv, c1 + lane < t_hi, lane, ptile, st, A);
+      } else {
+        value_phase(vc, cbv, A, st.acc);
+      }
+      kc = kn;
+      vc = vn;
+    }
+  }
+  write_partial(a, st, prow, lane);
+}
+
+// Fixed splits: work-group (split, kv head, sequence) scans pages
+// [split * pages_per_split, ...) of its sequence.
+// Balanced (a.balanced): the W = gridDim.x waves share the flattened space of
+// 64-token chunks ordered (sequence, kv head, chunk); wave w takes chunks
+// [C w / W', C (w+1) / W') with C the total and W' = min(W, C), and writes one
+// partial per (sequence, kv head) it touches, at row w + b*Hkv + kvh.
+template <int BWK, int BWV, bool PIPE>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void decode_rows_kernel(
+    DecodeArgs a) {
+  constexpr int LK = 1 << BWK, LV = 1 << BWV;
+  __shared__ float cbk[LK];
+  __shared__ float cbv[LV];
+  __shared__ __align__(16) float ptile[16 * kPStride];
+  const int lane = threadIdx.x;
+
+  // The work list: one (sequence, kv head, token range) for a fixed split, or the
+  // units overlapping this wave's share of the flattened chunk space. One call site
+  // for the scan keeps a single copy of its code.
+  int b, kvh, t_lo, t_hi;
+  int64_t prow;
+  int64_t s = 0, e = 0;  // balanced: flattened chunks [s, e) still to do
+  const int32_t* pre = a.chunk_prefix;
+  if (!a.balanced) {
+    const int split = blockIdx.x;
+    kvh = blockIdx.y;
+    b = blockIdx.z;
+    const int L = a.seq_lens[b];
+    const int S = 1 << a.log2S;
+    const int n_pages = (L + S - 1) >> a.log2S;
+    const int page_lo = split * a.pages_per_split;
+    if (page_lo >= n_pages) return;  // wave-uniform: this split is past the sequence
+    const int page_hi = min(page_lo + a.pages_per_split, n_pages);
+    t_lo = page_lo << a.log2S;
+    t_hi = min(page_hi << a.log2S, L);
+    prow = (int64_t(b) * a.Hkv + kvh) * a.num_splits + split;
+  } else {
+    const int64_t C = int64_t(a.Hkv) * pre[a.B];
+    const int64_t Wp = min(int64_t(gridDim.x), C);
+    const int w = blockIdx.x;
+    if (w >= Wp) return;
+    s = C * w / Wp;
+    e = C * (w + 1) / Wp;
+    // sequence holding flattened chunk s: the largest b with Hkv * pre[b] <= s
+    int lo = 0, hi = a.B;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (int64_t(a.Hkv) * pre[mid] <= s) lo = mid;
+      else hi = mid;
+    }
+    b = lo;
+    kvh = t_lo = t_hi = 0;
+    prow = 0;
+  }
+  for (int i = lane; i < LK; i += 64) cbk[i] = a.cb_k[i];
+  for (int i = lane; i < LV; i += 64) cbv[i] = a.cb_v[i];
+  wave_lds_sync();
+
+  while (true) {
+    int nb = 0, c_hi = 0;
+    if (a.balanced) {
+      nb = pre[b + 1] - pre[b];
+      while (nb == 0) {  // sequences without tokens own no chunks
+        ++b;
+        nb = pre[b + 1] - pre[b];
+      }
+      const int64_t base = int64_t(a.Hkv) * pre[b];
+      kvh = int((s - base) / nb);
+      const int c_lo = int((s - base) % nb);
+      c_hi = int(min(int64_t(nb), c_lo + (e - s)));
+      t_lo = 64 * c_lo;
+      t_hi = min(64 * c_hi, a.seq_lens[b]);
+      prow = int64_t(blockIdx.x) + int64_t(b) * a.Hkv + kvh;
+      s += c_hi - c_lo;
+    }
+    scan_range<BWK, BWV, PIPE>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+    if (!a.balanced || s >= e) break;
+    if (kvh + 1 == a.Hkv && c_hi == nb) ++b;
+  }
+}
+
+}  // namespace
+
+template <bool PIPE>
+SplitFn pick_rows(int bw_k, int bw_v) {
+  if constexpr (PIPE) {
+    if (bw_v == 4 && bw_k == 4) return decode_rows_kernel<4, 4, true>;
+    if (bw_v == 4 && bw_k == 6) return decode_rows_kernel<6, 4, true>;
+    return nullptr;
+  }
+  if (bw_k == bw_v) {
+    switch (bw_k) {
+      case 2: return decode_rows_kernel<2, 2, PIPE>;
+      case 3: return decode_rows_kernel<3, 3, PIPE>;
+      case 4: return decode_rows_kernel<4, 4, PIPE>;
+      case 5: return decode_rows_kernel<5, 5, PIPE>;
+      case 6: return decode_rows_kernel<6, 6, PIPE>;
+      case 8: return decode_rows_kernel<8, 8, PIPE>;
+    }
+  } else if (bw_k == 4 && bw_v == 6) {
+    return decode_rows_kernel<4, 6, PIPE>;
+  } else if (bw_k == 6 && bw_v == 4) {
+    return decode_rows_kernel<6, 4, PIPE>;
+  } else if (bw_k == 4 && bw_v == 8) {
+    return decode_rows_kernel<4, 8, PIPE>;
+  }
+  return nullptr;
+}
+
+SplitKernel pick_split_rows(int bw_k, int bw_v, bool pipelined) {
+  SplitKernel k;
+  // the pipelined form holds two chunks' codes and lookups; it fits the register
+  // file without spilling for 4-bit values with 4- or 6-bit keys only
+  const bool pipe_fits = bw_v == 4 && (bw_k == 4 || bw_k == 6);
+  k.fn = pipelined && pipe_fits ? pick_rows<true>(bw_k, bw_v) : pick_rows<false>(bw_k, bw_v);
+  if (k.fn) {
+    k.block = 64;
+    k.nrep = 4;
+    k.log2_units = true;
+  }
+  return k;
+}
+
+}  // namespace wn

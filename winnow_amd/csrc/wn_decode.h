@@ -15,12 +15,14 @@ struct DecodeArgs {
   const float* cb_v;
   const int32_t* table;
   const int32_t* seq_lens;
-  float* part_acc;  // (B*Hkv*num_splits*n_rep, D)
-  float* part_ml;   // (B*Hkv*num_splits*n_rep, 2)
+  float* part_acc;  // (rows * n_rep, D): rows = B*Hkv*num_splits, or num_splits + B*Hkv balanced
+  float* part_ml;   // (rows * n_rep, 2): running max (log2 units for the matrix-core scan), sum
   int64_t ksp, ksh, vsp, vsh;  // page strides, bytes
   int64_t knp, knh, vnp, vnh;  // norm strides, elements
   int64_t tsb;                 // page-table row stride, elements
-  int Hkv, n_rep, log2S, pages_per_split, num_splits;
+  const int32_t* chunk_prefix;  // (B+1) running count of 64-token chunks per sequence (balanced)
+  int B, Hkv, n_rep, log2S, pages_per_split, num_splits;
+  int balanced;  // 1: persistent waves share the flattened chunk space (pages_per_split unused)
 };
 
 using SplitFn = void (*)(DecodeArgs);
@@ -32,8 +34,10 @@ struct SplitKernel {
   bool log2_units = false;  // scores/maxima in log2 units (q_rot scaled by log2 e)
 };
 
-// Matrix-core page scan for head_dim 128 and up to four query heads per kv
-// head, or an empty SplitKernel when (bw_k, bw_v) is not compiled.
-SplitKernel pick_split_mfma(int bw_k, int bw_v);
+// Row-per-lane matrix-core page scan for head_dim 128, power-of-two page sizes
+// >= 16 and up to four query heads per kv head (one independent wave per
+// work-group, fixed splits or balanced persistent waves), or an empty
+// SplitKernel when (bw_k, bw_v) is not compiled.
+SplitKernel pick_split_rows(int bw_k, int bw_v, bool pipelined);
 
 }  // namespace wn

@@ -213,16 +213,31 @@ def check_kernel_contract(q: torch.Tensor, kv: PackedKV, *, check_ranges: bool =
         raise UnsupportedLayout("page_table rows and seq_lens must be contiguous")
 
 
-def decode_plan(batch: int, num_kv_heads: int, max_pages: int, num_splits: int | None = None):
-    """(pages_per_split, num_splits) the HIP decode uses for this shape (wn_decode_plan)."""
+def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+                bits_k: int, bits_v: int, max_pages: int, num_splits: int | None = None):
+    """(pages_per_split, num_splits) the HIP decode uses for this shape (wn_decode_plan).
+
+    pages_per_split == 0 is a balanced plan: num_splits persistent waves share
+    the batch's 64-token chunks equally.
+    """
     pps, ns = ctypes.c_int(0), ctypes.c_int(0)
-    _lib.call("wn_decode_plan", batch, num_kv_heads, max_pages, int(num_splits or 0),
-              ctypes.byref(pps), ctypes.byref(ns))
+    _lib.call("wn_decode_plan", batch, num_q_heads, num_kv_heads, head_dim, page_size, bits_k, bits_v,
+              max_pages, int(num_splits or 0), ctypes.byref(pps), ctypes.byref(ns))
     return pps.value, ns.value
 
 
-def workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, num_splits: int) -> int:
-    return int(_lib.lib().wn_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, num_splits))
+def workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                    pages_per_split: int, num_splits: int) -> int:
+    return int(_lib.lib().wn_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim,
+                                                    pages_per_split, num_splits))
+
+
+def plan_for(q: torch.Tensor, kv: PackedKV, num_splits: int | None = None):
+    """decode_plan for a query and a PackedKV handle, on the query's device."""
+    B, Hq, _, D = q.shape
+    with torch.cuda.device(q.device):
+        return decode_plan(B, Hq, kv.num_kv_heads, D, kv.page_size, kv.k_quant.bit_width,
+                           kv.v_quant.bit_width, kv.page_table.shape[1], num_splits)
 
 
 def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
@@ -234,8 +249,9 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
                             timing_events=None) -> torch.Tensor:
     """q (B, Hq, 1, D) -> (B, Hq, 1, D) in q.dtype (packed_attention_triton.py:180-187).
 
-    ``num_splits=None`` lets the library split every sequence's pages to fill
-    the GPU; an integer asks for exactly that many splits over the page-table
+    ``num_splits=None`` lets the library plan the split: persistent waves that
+    share the batch's chunks equally where the row scan applies, else splits
+    sized to fill the GPU; an integer asks for exactly that many splits over the page-table
     width, as the reference does. ``allow_tf32``, ``num_warps``, ``num_stages``
     are Triton schedule knobs, accepted for call compatibility and ignored;
     ``pages_per_iter`` must still be a power of two. ``out_dtype=torch.float32``
@@ -251,12 +267,12 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
     B, Hq, _, D = q.shape
     Hkv = kv.num_kv_heads
     max_pages = kv.page_table.shape[1]
-    pps, ns = decode_plan(B, Hkv, max_pages, num_splits)
+    pps, ns = plan_for(q, kv, num_splits)
     out_dtype = out_dtype or q.dtype
     if out_dtype not in _lib.DTYPE_CODE:
         raise UnsupportedLayout(f"output dtype {out_dtype} is not supported")
     out = torch.empty(B, Hq, 1, D, dtype=out_dtype, device=q.device)
-    need = workspace_bytes(B, Hq, Hkv, D, ns)
+    need = workspace_bytes(B, Hq, Hkv, D, pps, ns)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     elif workspace.numel() * workspace.element_size() < need or workspace.device != q.device:
