@@ -202,8 +202,10 @@ def cpu_baseline(c, lens, q, kv, budget_s: float):
     import torch
     from oracle import attention as oa
 
-    cores = os.cpu_count() or 1
+    # the host share this process may use (OMP_NUM_THREADS on the GPU box), not the whole machine
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
     torch.set_num_threads(cores)
+    cores = torch.get_num_threads()
     D, S, B = c["D"], c["S"], len(lens)
     width = kv.page_table_host.shape[1]
 
@@ -221,15 +223,16 @@ def cpu_baseline(c, lens, q, kv, budget_s: float):
 
     qc = q.float().cpu()
     scale = oa.default_scale(D)
-    probe = sample_kv(4)
-    t0 = time.perf_counter()
-    oa.tiled_compressed_attention(qc, probe, scale)
-    per_col = (time.perf_counter() - t0) / 4
-    cols = int(max(8, min(width, budget_s / max(per_col, 1e-6))))
-    skv = sample_kv(cols)
-    t0 = time.perf_counter()
-    oa.tiled_compressed_attention(qc, skv, scale)
-    dt = time.perf_counter() - t0
+    # grow the sample until it holds about budget_s of CPU work (or the whole table)
+    cols, dt = 4, 0.0
+    while True:
+        skv = sample_kv(cols)
+        t0 = time.perf_counter()
+        oa.tiled_compressed_attention(qc, skv, scale)
+        dt = time.perf_counter() - t0
+        if dt >= 0.5 * budget_s or cols >= width:
+            break
+        cols = int(min(width, max(2 * cols, cols * budget_s / max(dt, 1e-3))))
     t_step = dt / cols * width
     return {"value": B / t_step, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"tiled_compressed_attention (torch CPU fp32) over {cols} of {width} page-table "
@@ -249,6 +252,8 @@ def main(argv=None):
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--parity", choices=["on", "off"], default="on")
     ap.add_argument("--copy-peak", choices=["on", "off"], default="on")
+    ap.add_argument("--settle", type=float, default=0.5,
+                    help="seconds of untimed steps before the warm-up, to reach sustained clocks")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -280,6 +285,16 @@ def main(argv=None):
         return pa.packed_decode_attention(q, kvs[i % len(kvs)], scale, num_splits=args.splits,
                                           workspace=ws, check_ranges=False, timing_events=evs)
 
+    # Bring the GPU to its sustained clocks before the W warm-up steps: a few ms of
+    # work (30 steps) otherwise times a part-clocked GPU, which a decode server
+    # running continuously never sees.
+    t_settle = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t_settle < args.settle:
+        for _ in range(20):
+            step(i)
+            i += 1
+        torch.cuda.synchronize()
     for i in range(args.warmup):
         step(i)
     ev_pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))

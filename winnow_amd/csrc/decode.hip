@@ -10,8 +10,8 @@
 //                        (split, kv head, sequence), score phase (lane = token),
 //                        online softmax, value phase (16 lanes per token row),
 //                        cross-wave max-stable merge into one (acc, m, l) partial
-//   3. merge_kernel      per (sequence, query head): max-stable merge of its
-//                        partials, 1/l, a Pi_V, cast to the output type
+//   3. merge_kernel      per (query head, kv head, sequence): max-stable merge
+//                        of its partials, 1/l, a Pi_V, cast to the output type
 // Algebra follows turboquant_kv/packed_attention.py:260-334 (the schedule the
 // reference kernel packed_attention_triton.py:51-159 implements).
 #include <cstdlib>
@@ -323,23 +323,22 @@ struct MergeArgs {
   int log2_units;  // partial maxima are in log2 units (weights 2^(m - M))
 };
 
-constexpr int kMergeTile = 256;  // partials per weight tile
+constexpr int kMergeBatch = 32;  // partials whose loads are in flight together
 
 // out[b, kvh*n_rep + h, :] = (sum_s w_s acc_s / sum_s w_s l_s) Pi_V with
 // w_s = exp(m_s - max m) (2^(m_s - max m) for log2-unit partials), zero when no
 // key was seen (packed_attention_triton.py:137-159 plus :261). One work-group of D
-// threads per (query head h, kv head, sequence): thread d accumulates dim d over
-// the partials, then thread j forms output dim j from Pi_V rows read coalesced.
-// The partials of the group are rows r0 + s*stride, s < n: fixed splits give
-// r0 = (b*Hkv + kvh)*num_splits, stride 1, n = splits holding tokens; the
-// balanced scan gives rows w + b*Hkv + kvh for the waves w that touched it.
+// threads per (query head h, kv head, sequence): thread d merges dim d over the
+// partials in a single max-stable pass with the loads of 32 partials issued
+// together (a balanced plan has about num_splits / (B*Hkv) partials per group, so
+// one round trip), then thread j forms output dim j from Pi_V rows read coalesced.
+// The partials of the group are rows r0 + s, s < n: fixed splits give
+// r0 = (b*Hkv + kvh)*num_splits and n = splits holding tokens; the balanced scan
+// gives rows w + b*Hkv + kvh for the waves w that touched the group.
 template <int D>
 __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
-  __shared__ float wts[kMergeTile];
-  __shared__ float red[D / 64];
   __shared__ float av[D];
-  const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
-  const int wv = tid >> 6, lane = tid & 63;
+  const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
   int64_t r0 = 0;
   int n = 0;
   const int L = a.seq_lens[b];
@@ -363,53 +362,38 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
   }
   auto wexp = [&](float x) { return a.log2_units ? __builtin_amdgcn_exp2f(x) : expf(x); };
   const float* ml = a.part_ml + 2 * (r0 * a.n_rep + h);
-  const int64_t mstride = 2 * int64_t(a.n_rep);  // floats between consecutive partials of (h)
-  // maximum and denominator over the partials
-  float M = -INFINITY;
-  for (int s = tid; s < n; s += D) M = fmaxf(M, ml[s * mstride]);
-  M = wave_max(M);
-  if (lane == 0) red[wv] = M;
-  __syncthreads();
-  M = red[0];
-  for (int i = 1; i < D / 64; ++i) M = fmaxf(M, red[i]);
-  __syncthreads();
-  float num = 0.f, den = 0.f;
-  const float* acc = a.part_acc + (r0 * a.n_rep + h) * D + tid;
-  const int64_t astride = int64_t(a.n_rep) * D;
-  for (int t0 = 0; t0 < n; t0 += kMergeTile) {
-    const int tn = min(kMergeTile, n - t0);
-    for (int s = tid; s < tn; s += D) {
-      const float mm = ml[(t0 + s) * mstride];
-      const float wgt = mm == -INFINITY ? 0.f : wexp(mm - M);
-      wts[s] = wgt;
-      den = fmaf(wgt, ml[(t0 + s) * mstride + 1], den);
+  const float* acc = a.part_acc + (r0 * a.n_rep + h) * D + d;
+  const int64_t pstride = a.n_rep;  // partial rows between consecutive partials of a head
+  float M = -INFINITY, num = 0.f, den = 0.f;
+  for (int s0 = 0; s0 < n; s0 += kMergeBatch) {
+    float mv[kMergeBatch], lv[kMergeBatch], xv[kMergeBatch];
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const bool ok = s0 + k < n;
+      const int64_t r = int64_t(s0 + k) * pstride;
+      mv[k] = ok ? ml[2 * r] : -INFINITY;
+      lv[k] = ok ? ml[2 * r + 1] : 0.f;
+      xv[k] = ok ? acc[r * D] : 0.f;
     }
-    __syncthreads();
-    int s = 0;
-    for (; s + 4 <= tn; s += 4) {
-      const float x0 = acc[(t0 + s) * astride], x1 = acc[(t0 + s + 1) * astride];
-      const float x2 = acc[(t0 + s + 2) * astride], x3 = acc[(t0 + s + 3) * astride];
-      num = fmaf(wts[s], x0, num);
-      num = fmaf(wts[s + 1], x1, num);
-      num = fmaf(wts[s + 2], x2, num);
-      num = fmaf(wts[s + 3], x3, num);
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      if (mv[k] == -INFINITY) continue;  // a partial that saw no key (block-uniform)
+      const float Mn = fmaxf(M, mv[k]);
+      const float r_old = M == -INFINITY ? 0.f : wexp(M - Mn);
+      const float w = wexp(mv[k] - Mn);
+      num = fmaf(num, r_old, w * xv[k]);
+      den = fmaf(den, r_old, w * lv[k]);
+      M = Mn;
     }
-    for (; s < tn; ++s) num = fmaf(wts[s], acc[(t0 + s) * astride], num);
-    __syncthreads();
   }
-  den = wave_sum(den);
-  if (lane == 0) red[wv] = den;
-  av[tid] = num;
+  av[d] = (L > 0 && den > 0.f) ? num / fmaxf(den, 1e-30f) : 0.f;
   __syncthreads();
-  den = 0.f;
-  for (int i = 0; i < D / 64; ++i) den += red[i];
   // out_j = sum_d a_d Pi_V[d, j]; (a / l) Pi_V == (a Pi_V) / l up to rounding
   float o = 0.f;
-  const float* pv = a.pi_v + tid;
+  const float* pv = a.pi_v + d;
 #pragma unroll 16
-  for (int d = 0; d < D; ++d) o = fmaf(av[d], pv[d * D], o);
-  o = (L > 0 && den > 0.f) ? o / fmaxf(den, 1e-30f) : 0.f;
-  store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + tid, a.out_dtype, o);
+  for (int k = 0; k < D; ++k) o = fmaf(av[k], pv[k * D], o);
+  store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + d, a.out_dtype, o);
 }
 
 using RotFn = void (*)(RotArgs);
@@ -460,17 +444,15 @@ RotFn pick_rot(int nrep) {
 }
 
 // Page-scan kernel preference, read once from WN_DECODE_SCAN: "rows" (default)
-// uses the pipelined row-per-lane matrix-core scan where it applies, "rows1" its
-// one-phase-at-a-time form, "valu" always the vector-ALU scan. Every choice
-// computes the same result; the knob exists to compare them on one machine.
-int scan_choice() {
-  static const int choice = [] {
+// uses the row-per-lane matrix-core scan where it applies, "valu" always the
+// vector-ALU scan. Both compute the same result; the knob exists to compare
+// them on one machine.
+bool rows_allowed() {
+  static const bool allowed = [] {
     const char* e = getenv("WN_DECODE_SCAN");
-    if (e && !strcmp(e, "valu")) return 2;
-    if (e && !strcmp(e, "rows1")) return 1;
-    return 0;
+    return !(e && !strcmp(e, "valu"));
   }();
-  return choice;
+  return allowed;
 }
 
 int pad_nrep(int n_rep) {
@@ -483,7 +465,7 @@ int pad_nrep(int n_rep) {
 SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v) {
   SplitKernel sk;
   const int n_rep = Hq / Hkv;
-  if (D == 128 && n_rep <= 4 && S >= 16 && scan_choice() < 2) sk = pick_split_rows(bw_k, bw_v, scan_choice() == 0);
+  if (D == 128 && n_rep <= 4 && S >= 16 && rows_allowed()) sk = pick_split_rows(bw_k, bw_v);
   if (!sk.fn) {
     const int nrp = pad_nrep(n_rep);
     sk.fn = D == 128 ? pick_split<128>(bw_k, bw_v, nrp) : pick_split<64>(bw_k, bw_v, nrp);

@@ -22,8 +22,9 @@
 //           acc[m] register i = (head i, dim 8p+m). 8 MFMAs per quad, 128 per chunk;
 //           the four groups are folded once per split.
 //
-// Codebooks (2^bw fp32) sit in LDS; every product is an exact fp32 multiply-add.
-// 4-bit codes become LDS byte offsets with one SDWA byte-select AND each. Page ids
+// Codebooks sit in LDS; every product is an exact fp32 multiply-add. 4-bit codes
+// are looked up two at a time: a byte of packed codes, shifted by 3 with one SDWA
+// instruction, addresses a 256-entry float2 table of (c[lo nibble], c[hi nibble]). Page ids
 // run two chunks ahead and the packed rows of chunk c+1 load while chunk c computes.
 // Algebra: turboquant_kv/packed_attention.py:260-334 (the schedule of the
 // reference kernel packed_attention_triton.py:51-134).
@@ -47,54 +48,72 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Byte K of x AND m, one VOP2 SDWA instruction.
+// (byte K of x) * 8, one VOP2 SDWA instruction: the LDS byte offset of entry
+// `byte` of a float2 table.
 template <int K>
-__device__ __forceinline__ uint32_t byte_and(uint32_t x, uint32_t m) {
+__device__ __forceinline__ uint32_t byte_x8(uint32_t x) {
   uint32_t r;
   if constexpr (K == 0)
-    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
-        : "=v"(r) : "v"(x), "v"(m));
+    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+        : "=v"(r) : "v"(x));
   else if constexpr (K == 1)
-    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:DWORD"
-        : "=v"(r) : "v"(x), "v"(m));
+    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+        : "=v"(r) : "v"(x));
   else if constexpr (K == 2)
-    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:DWORD"
-        : "=v"(r) : "v"(x), "v"(m));
+    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+        : "=v"(r) : "v"(x));
   else
-    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:DWORD"
-        : "=v"(r) : "v"(x), "v"(m));
+    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=v"(r) : "v"(x));
   return r;
 }
 
-// LDS byte offsets (code * 4) of codes [8g, 8g+8) of a packed little-endian word
-// array, LSB-first, BW bits per code. For 4-bit codes word g holds exactly these
-// eight codes: even codes sit at bits 2..5 of the bytes of w<<2, odd codes at
-// bits 2..5 of the bytes of w>>2.
+// Codebook values of the 8 codes of a word (LSB-first, BW bits each), code 8G+j of
+// the word array into v[j]. 4-bit codes go through the byte-indexed pair table
+// (entry b = (c[b & 15], c[b >> 4]), 256 float2): one SDWA shift and one 8-byte
+// LDS read per two codes. Other widths read the 2^BW-entry table per code.
 template <int BW, int G, int NW>
-__device__ __forceinline__ void code_offsets8(const uint32_t (&w)[NW], uint32_t mask3c, uint32_t (&off)[8]) {
+__device__ __forceinline__ void lookup8(const uint32_t (&w)[NW], const float* tab, float (&v)[8]) {
   if constexpr (BW == 4) {
-    const uint32_t e = w[G] << 2, o = w[G] >> 2;
-    off[0] = byte_and<0>(e, mask3c);
-    off[1] = byte_and<0>(o, mask3c);
-    off[2] = byte_and<1>(e, mask3c);
-    off[3] = byte_and<1>(o, mask3c);
-    off[4] = byte_and<2>(e, mask3c);
-    off[5] = byte_and<2>(o, mask3c);
-    off[6] = byte_and<3>(e, mask3c);
-    off[7] = byte_and<3>(o, mask3c);
+    const char* t = reinterpret_cast<const char*>(tab);
+    const float2 a = *reinterpret_cast<const float2*>(t + byte_x8<0>(w[G]));
+    const float2 b = *reinterpret_cast<const float2*>(t + byte_x8<1>(w[G]));
+    const float2 c = *reinterpret_cast<const float2*>(t + byte_x8<2>(w[G]));
+    const float2 d = *reinterpret_cast<const float2*>(t + byte_x8<3>(w[G]));
+    v[0] = a.x;
+    v[1] = a.y;
+    v[2] = b.x;
+    v[3] = b.y;
+    v[4] = c.x;
+    v[5] = c.y;
+    v[6] = d.x;
+    v[7] = d.y;
   } else {
     static_for<0, 8>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
       constexpr int bit = (8 * G + j) * BW, wi = bit >> 5, sh = bit & 31;
-      uint32_t v = w[wi] >> sh;
-      if constexpr (sh + BW > 32) v |= w[wi + 1] << (32 - sh);
-      off[j] = (v & ((1u << BW) - 1u)) << 2;
+      uint32_t x = w[wi] >> sh;
+      if constexpr (sh + BW > 32) x |= w[wi + 1] << (32 - sh);
+      v[j] = tab[x & ((1u << BW) - 1u)];
     });
   }
 }
 
-__device__ __forceinline__ float lds_at(const float* tab, uint32_t byte_off) {
-  return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(tab) + byte_off);
+// LDS floats a codebook of BW-bit codes occupies (the 4-bit pair table: 512).
+template <int BW>
+constexpr int table_floats() { return BW == 4 ? 512 : (1 << BW); }
+
+// Stages the codebook in LDS: the pair table for 4-bit codes, else the plain table.
+template <int BW>
+__device__ __forceinline__ void stage_table(const float* cb, float* tab, int lane) {
+  if constexpr (BW == 4) {
+    for (int i = lane; i < 256; i += 64) {
+      tab[2 * i] = cb[i & 15];
+      tab[2 * i + 1] = cb[i >> 4];
+    }
+  } else {
+    for (int i = lane; i < (1 << BW); i += 64) tab[i] = cb[i];
+  }
 }
 
 __device__ __forceinline__ float half_lo(uint32_t h) { return f16_to_f32(uint16_t(h & 0xffffu)); }
@@ -198,10 +217,7 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, i
 // Score lookups of dims [8g, 8g+8) of this lane's K row.
 template <int BWK, int G>
 __device__ __forceinline__ void score_look(const uint32_t (&k)[4 * BWK], const float* cbk, float (&kv)[8]) {
-  uint32_t off[8];
-  code_offsets8<BWK, G>(k, 0x3c, off);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) kv[j] = lds_at(cbk, off[j]);
+  lookup8<BWK, G>(k, cbk, kv);
 }
 
 // The 8 score MFMAs of dims [8g, 8g+8): A = q_rot[head][k] broadcast from block k%16.
@@ -219,10 +235,7 @@ __device__ __forceinline__ void score_mfma(const float (&qb)[8], const float (&k
 // Value lookups of quad q (this lane's 8 dims of token c0+4q+G).
 template <int BWV, int Q>
 __device__ __forceinline__ void value_look(const VChunk<BWV>& v, const float* cbv, float (&vv)[8]) {
-  uint32_t off[8];
-  code_offsets8<BWV, 0>(v.v[Q], 0x3c, off);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) vv[j] = lds_at(cbv, off[j]);
+  lookup8<BWV, 0>(v.v[Q], cbv, vv);
 }
 
 // The 8 value MFMAs of quad q: A = p*n_V broadcast inside each group of four blocks.
@@ -261,30 +274,6 @@ __device__ __forceinline__ void value_phase(const VChunk<BWV>& vc, const float* 
     value_mfma(A[q], vv[q & 1], acc);
     __builtin_amdgcn_sched_barrier(0);
   });
-}
-
-// Values of chunk c and scores of chunk c+1, interleaved group by group: two
-// independent MFMA chains, so one stream's lookups are in flight while the
-// other's MFMAs run.
-template <int BWK, int BWV>
-__device__ __forceinline__ f32x4 value_and_score(const VChunk<BWV>& vc, const float* cbv, const float (&A)[16],
-                                                 f32x4 (&acc)[8], const KChunk<BWK>& kc, const float* cbk,
-                                                 const float (&qb)[8]) {
-  f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
-  float kv[2][8], vv[2][8];
-  score_look<BWK, 0>(kc.k, cbk, kv[0]);
-  value_look<BWV, 0>(vc, cbv, vv[0]);
-  static_for<0, 16>([&](auto gc) {
-    constexpr int g = decltype(gc)::value;
-    if constexpr (g + 1 < 16) {
-      score_look<BWK, g + 1>(kc.k, cbk, kv[(g + 1) & 1]);
-      value_look<BWV, g + 1>(vc, cbv, vv[(g + 1) & 1]);
-    }
-    value_mfma(A[g], vv[g & 1], acc);
-    score_mfma<g>(qb, kv[g & 1], s0, s1);
-    __builtin_amdgcn_sched_barrier(0);
-  });
-  return s0 + s1;
 }
 
 // Online softmax of one chunk (lane = token) and the p * n_V transposition: on
@@ -376,10 +365,10 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, RowState& st,
 }
 
 // Scans tokens [t_lo, t_hi) of (sequence b, kv head kvh) in 64-token chunks (t_lo a
-// multiple of 16) and writes one partial at row prow. PIPE overlaps the values of
-// chunk c with the scores of chunk c+1; otherwise each chunk runs score, softmax,
-// values in turn. Loads run one chunk ahead of use either way.
-template <int BWK, int BWV, bool PIPE>
+// multiple of 16) and writes one partial at row prow. Each chunk runs score,
+// softmax and values in turn; the packed codes of chunk c+1 load while chunk c
+// computes and page ids run two chunks ahead.
+template <int BWK, int BWV>
 __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, int t_lo, int t_hi, int64_t prow,
                                            int lane, const float* cbk, const float* cbv, float* ptile) {
   constexpr int D = 128;
@@ -411,50 +400,22 @@ __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, 
   float A[16];
   KChunk<BWK> kc, kn;
   VChunk<BWV> vc, vn;
-
-  if constexpr (!PIPE) {
-    int pid = pid_of(0);
-    load_k(a, kvh, lane, t_lo, pid, kc);
-    load_v(a, kvh, lane, t_lo, pid, vc);
-    int pid_next = n > 1 ? pid_of(1) : 0;
-    for (int c = 0; c < n; ++c) {
-      const int c0 = t_lo + 64 * c;
-      if (c + 1 < n) {
-        load_k(a, kvh, lane, c0 + 64, pid_next, kn);
-        load_v(a, kvh, lane, c0 + 64, pid_next, vn);
-      }
-      if (c + 2 < n) pid_next = pid_of(c + 2);
-      const f32x4 s = score_phase(kc, cbk, qb);
-      softmax_phase(s, kc.nk, kc.nv, c0 + lane < t_hi, lane, ptile, st, A);
-      value_phase(vc, cbv, A, st.acc);
-      kc = kn;
-      vc = vn;
+  int pid = pid_of(0);
+  load_k(a, kvh, lane, t_lo, pid, kc);
+  load_v(a, kvh, lane, t_lo, pid, vc);
+  int pid_next = n > 1 ? pid_of(1) : 0;
+  for (int c = 0; c < n; ++c) {
+    const int c0 = t_lo + 64 * c;
+    if (c + 1 < n) {
+      load_k(a, kvh, lane, c0 + 64, pid_next, kn);
+      load_v(a, kvh, lane, c0 + 64, pid_next, vn);
     }
-  } else {
-    // prologue: chunk 0 through its softmax; K of chunk 1 in flight
-    const int pid0 = pid_of(0);
-    load_k(a, kvh, lane, t_lo, pid0, kc);
-    load_v(a, kvh, lane, t_lo, pid0, vc);
-    int pid_a = n > 1 ? pid_of(1) : 0;  // page of chunk c+1 at the top of iteration c
-    if (n > 1) load_k(a, kvh, lane, t_lo + 64, pid_a, kn);
-    int pid_b = n > 2 ? pid_of(2) : 0;  // page of chunk c+2
-    softmax_phase(score_phase(kc, cbk, qb), kc.nk, kc.nv, t_lo + lane < t_hi, lane, ptile, st, A);
+    if (c + 2 < n) pid_next = pid_of(c + 2);
+    const f32x4 s = score_phase(kc, cbk, qb);
+    softmax_phase(s, kc.nk, kc.nv, c0 + lane < t_hi, lane, ptile, st, A);
+    value_phase(vc, cbv, A, st.acc);
     kc = kn;
-    for (int c = 0; c < n; ++c) {
-      const int c1 = t_lo + 64 * (c + 1);
-      if (c + 2 < n) load_k(a, kvh, lane, c1 + 64, pid_b, kn);
-      if (c + 1 < n) load_v(a, kvh, lane, c1, pid_a, vn);
-      pid_a = pid_b;
-      if (c + 3 < n) pid_b = pid_of(c + 3);
-      if (c + 1 < n) {
-        const f32x4 s = value_and_score(vc, cbv, A, st.acc, kc, cbk, qb);
-        softmax_phase(s, kc.nk, kc.nv, c1 + lane < t_hi, lane, ptile, st, A);
-      } else {
-        value_phase(vc, cbv, A, st.acc);
-      }
-      kc = kn;
-      vc = vn;
-    }
+    vc = vn;
   }
   write_partial(a, st, prow, lane);
 }
@@ -465,12 +426,11 @@ __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, 
 // 64-token chunks ordered (sequence, kv head, chunk); wave w takes chunks
 // [C w / W', C (w+1) / W') with C the total and W' = min(W, C), and writes one
 // partial per (sequence, kv head) it touches, at row w + b*Hkv + kvh.
-template <int BWK, int BWV, bool PIPE>
+template <int BWK, int BWV>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void decode_rows_kernel(
     DecodeArgs a) {
-  constexpr int LK = 1 << BWK, LV = 1 << BWV;
-  __shared__ float cbk[LK];
-  __shared__ float cbv[LV];
+  __shared__ __align__(16) float cbk[table_floats<BWK>()];
+  __shared__ __align__(16) float cbv[table_floats<BWV>()];
   __shared__ __align__(16) float ptile[16 * kPStride];
   const int lane = threadIdx.x;
 
@@ -512,8 +472,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void
     kvh = t_lo = t_hi = 0;
     prow = 0;
   }
-  for (int i = lane; i < LK; i += 64) cbk[i] = a.cb_k[i];
-  for (int i = lane; i < LV; i += 64) cbv[i] = a.cb_v[i];
+  stage_table<BWK>(a.cb_k, cbk, lane);
+  stage_table<BWV>(a.cb_v, cbv, lane);
   wave_lds_sync();
 
   while (true) {
@@ -533,7 +493,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void
       prow = int64_t(blockIdx.x) + int64_t(b) * a.Hkv + kvh;
       s += c_hi - c_lo;
     }
-    scan_range<BWK, BWV, PIPE>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+    scan_range<BWK, BWV>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
     if (!a.balanced || s >= e) break;
     if (kvh + 1 == a.Hkv && c_hi == nb) ++b;
   }
@@ -541,39 +501,27 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void
 
 }  // namespace
 
-template <bool PIPE>
-SplitFn pick_rows(int bw_k, int bw_v) {
-  if constexpr (PIPE) {
-    if (bw_v == 4 && bw_k == 4) return decode_rows_kernel<4, 4, true>;
-    if (bw_v == 4 && bw_k == 6) return decode_rows_kernel<6, 4, true>;
-    return nullptr;
-  }
+SplitKernel pick_split_rows(int bw_k, int bw_v) {
+  SplitFn f = nullptr;
   if (bw_k == bw_v) {
     switch (bw_k) {
-      case 2: return decode_rows_kernel<2, 2, PIPE>;
-      case 3: return decode_rows_kernel<3, 3, PIPE>;
-      case 4: return decode_rows_kernel<4, 4, PIPE>;
-      case 5: return decode_rows_kernel<5, 5, PIPE>;
-      case 6: return decode_rows_kernel<6, 6, PIPE>;
-      case 8: return decode_rows_kernel<8, 8, PIPE>;
+      case 2: f = decode_rows_kernel<2, 2>; break;
+      case 3: f = decode_rows_kernel<3, 3>; break;
+      case 4: f = decode_rows_kernel<4, 4>; break;
+      case 5: f = decode_rows_kernel<5, 5>; break;
+      case 6: f = decode_rows_kernel<6, 6>; break;
+      case 8: f = decode_rows_kernel<8, 8>; break;
     }
   } else if (bw_k == 4 && bw_v == 6) {
-    return decode_rows_kernel<4, 6, PIPE>;
+    f = decode_rows_kernel<4, 6>;
   } else if (bw_k == 6 && bw_v == 4) {
-    return decode_rows_kernel<6, 4, PIPE>;
+    f = decode_rows_kernel<6, 4>;
   } else if (bw_k == 4 && bw_v == 8) {
-    return decode_rows_kernel<4, 8, PIPE>;
+    f = decode_rows_kernel<4, 8>;
   }
-  return nullptr;
-}
-
-SplitKernel pick_split_rows(int bw_k, int bw_v, bool pipelined) {
   SplitKernel k;
-  // the pipelined form holds two chunks' codes and lookups; it fits the register
-  // file without spilling for 4-bit values with 4- or 6-bit keys only
-  const bool pipe_fits = bw_v == 4 && (bw_k == 4 || bw_k == 6);
-  k.fn = pipelined && pipe_fits ? pick_rows<true>(bw_k, bw_v) : pick_rows<false>(bw_k, bw_v);
-  if (k.fn) {
+  if (f) {
+    k.fn = f;
     k.block = 64;
     k.nrep = 4;
     k.log2_units = true;

@@ -38,6 +38,6 @@ struct SplitKernel {
 // >= 16 and up to four query heads per kv head (one independent wave per
 // work-group, fixed splits or balanced persistent waves), or an empty
 // SplitKernel when (bw_k, bw_v) is not compiled.
-SplitKernel pick_split_rows(int bw_k, int bw_v, bool pipelined);
+SplitKernel pick_split_rows(int bw_k, int bw_v);
 
 }  // namespace wn
