@@ -475,22 +475,23 @@ SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v) {
   return sk;
 }
 
-// Resident one-wave groups of `fn` on the current device (blocks per CU x CUs).
-int resident_waves(SplitFn fn) {
+// Resident waves of the row scan `sk` on the current device: work-groups per CU
+// x CUs x waves per work-group.
+int resident_waves(const SplitKernel& sk) {
   static std::mutex mu;
   static std::map<std::pair<int, SplitFn>, int> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   std::lock_guard<std::mutex> lock(mu);
-  auto it = cache.find({dev, fn});
+  auto it = cache.find({dev, sk.fn});
   if (it != cache.end()) return it->second;
   int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), 64, 0) !=
-          hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(sk.fn), sk.block,
+                                                   0) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return 0;
-  const int w = per_cu * cus;
-  cache[{dev, fn}] = w;
+  const int w = per_cu * cus * sk.wpb;
+  cache[{dev, sk.fn}] = w;
   return w;
 }
 
@@ -540,8 +541,8 @@ extern "C" int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, in
     return WN_OK;
   }
   const SplitKernel sk = choose_scan(Hq, Hkv, D, S, bw_k, bw_v);
-  if (sk.fn && sk.block == 64) {  // row scan: balanced persistent waves
-    const int w = resident_waves(sk.fn);
+  if (sk.fn && sk.rows) {  // row scan: balanced persistent waves
+    const int w = resident_waves(sk);
     WN_REQUIRE(w > 0, WN_E_LAUNCH, "wn_decode_plan: cannot query the device occupancy");
     *pages_per_split = 0;
     *num_splits = w;
@@ -610,7 +611,7 @@ extern "C" int wn_decode_attention(
   RotFn rot = D == 128 ? pick_rot<128>(max(sk.nrep, 1)) : pick_rot<64>(max(sk.nrep, 1));
   WN_REQUIRE(sk.fn && rot, WN_E_UNSUPPORTED, "decode: (D=%d, bw_k=%d, bw_v=%d) not compiled", D, bw_k,
              bw_v);
-  WN_REQUIRE(!balanced || sk.block == 64, WN_E_INVALID,
+  WN_REQUIRE(!balanced || sk.rows, WN_E_INVALID,
              "decode: a balanced plan (pages_per_split 0) needs the row scan; ask wn_decode_plan");
 
   const WsLayout lay = ws_layout(B, Hq, Hkv, D, pages_per_split, num_splits);
@@ -656,7 +657,9 @@ extern "C" int wn_decode_attention(
   da.pages_per_split = pages_per_split;
   da.num_splits = num_splits;
   da.balanced = balanced ? 1 : 0;
-  const dim3 grid = balanced ? dim3(num_splits) : dim3(num_splits, Hkv, B);
+  // the row scan numbers its waves across work-groups of sk.wpb waves
+  const int64_t waves = balanced ? int64_t(num_splits) : int64_t(num_splits) * Hkv * B;
+  const dim3 grid = sk.rows ? dim3(unsigned((waves + sk.wpb - 1) / sk.wpb)) : dim3(num_splits, Hkv, B);
   if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
   hipLaunchKernelGGL(sk.fn, grid, dim3(sk.block), 0, st, da);
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);

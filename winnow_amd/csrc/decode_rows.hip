@@ -23,9 +23,12 @@
 //           the four groups are folded once per split.
 //
 // Codebooks sit in LDS; every product is an exact fp32 multiply-add. 4-bit codes
-// are looked up two at a time: a byte of packed codes, shifted by 3 with one SDWA
-// instruction, addresses a 256-entry float2 table of (c[lo nibble], c[hi nibble]). Page ids
-// run two chunks ahead and the packed rows of chunk c+1 load while chunk c computes.
+// are looked up two at a time in a byte-indexed table of (c[lo nibble], c[hi nibble])
+// pairs that is replicated once per lane of a half-wave, so that the 32 lanes LDS
+// serves together always read 32 distinct bank pairs: a lookup never waits on a
+// bank conflict, whatever the codes. Twelve waves per work-group share the tables.
+// Page ids run two chunks ahead and the packed rows of chunk c+1 load while chunk c
+// computes.
 // Algebra: turboquant_kv/packed_attention.py:260-334 (the schedule of the
 // reference kernel packed_attention_triton.py:51-134).
 #include <utility>
@@ -36,6 +39,7 @@ namespace wn {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 
 constexpr float kRescale = 8.0f;
 constexpr int kPStride = 20;  // floats per (head, token group) row of the p tile (16 + pad, 16-B rows)
@@ -48,73 +52,89 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// (byte K of x) * 8, one VOP2 SDWA instruction: the LDS byte offset of entry
-// `byte` of a float2 table.
+// Byte K of x written into byte 1 of r, the other bytes of r kept: one VOP2 SDWA
+// move. With r = 8*(lane % 32) | slot << 16 this is the LDS byte address of entry
+// (byte K of x, lane % 32) of the replicated pair table in 64 KB slot `slot`.
 template <int K>
-__device__ __forceinline__ uint32_t byte_x8(uint32_t x) {
-  uint32_t r;
+__device__ __forceinline__ uint32_t put_byte1(uint32_t r, uint32_t x) {
   if constexpr (K == 0)
-    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
-        : "=v"(r) : "v"(x));
+    asm("v_mov_b32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0" : "+v"(r) : "v"(x));
   else if constexpr (K == 1)
-    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
-        : "=v"(r) : "v"(x));
+    asm("v_mov_b32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1" : "+v"(r) : "v"(x));
   else if constexpr (K == 2)
-    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
-        : "=v"(r) : "v"(x));
+    asm("v_mov_b32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_2" : "+v"(r) : "v"(x));
   else
-    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
-        : "=v"(r) : "v"(x));
+    asm("v_mov_b32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3" : "+v"(r) : "v"(x));
   return r;
 }
 
-// Codebook values of the 8 codes of a word (LSB-first, BW bits each), code 8G+j of
-// the word array into v[j]. 4-bit codes go through the byte-indexed pair table
-// (entry b = (c[b & 15], c[b >> 4]), 256 float2): one SDWA shift and one 8-byte
-// LDS read per two codes. Other widths read the 2^BW-entry table per code.
-template <int BW, int G, int NW>
-__device__ __forceinline__ void lookup8(const uint32_t (&w)[NW], const float* tab, float (&v)[8]) {
+constexpr int kPairTableBytes = 256 * 32 * 8;  // 256 byte values x 32 lanes x float2
+
+// LDS bytes the codebook of BW-bit codes occupies: the replicated pair table for
+// 4-bit codes, else the plain 2^BW-entry table (padded to 16 bytes).
+template <int BW>
+constexpr int table_bytes() { return BW == 4 ? kPairTableBytes : (4 << BW) < 16 ? 16 : (4 << BW); }
+
+// A codebook in LDS as one lane reads it.
+template <int BW>
+struct Tab {
+  const float* t;  // plain table: lanes sharing a code share an address (LDS broadcasts)
+};
+template <>
+struct Tab<4> {
+  const char* lds;  // LDS block base; the table sits at 64 KB slot `slot` of it
+  uint32_t r[4];    // address registers, one per byte position of a code word
+  __device__ void init(const char* base, int slot, int lane) {
+    lds = base;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r[k] = uint32_t(8 * (lane & 31)) | (uint32_t(slot) << 16);
+  }
+};
+
+// Stages a codebook into LDS at `dst` with all `nthr` threads of the work-group:
+// the replicated pair table for 4-bit codes (entry (b, r) at byte 256*b + 8*r holds
+// (c[b & 15], c[b >> 4])), else the plain table.
+template <int BW>
+__device__ __forceinline__ void stage_table(const float* cb, char* dst, int tid, int nthr) {
   if constexpr (BW == 4) {
-    const char* t = reinterpret_cast<const char*>(tab);
-    const float2 a = *reinterpret_cast<const float2*>(t + byte_x8<0>(w[G]));
-    const float2 b = *reinterpret_cast<const float2*>(t + byte_x8<1>(w[G]));
-    const float2 c = *reinterpret_cast<const float2*>(t + byte_x8<2>(w[G]));
-    const float2 d = *reinterpret_cast<const float2*>(t + byte_x8<3>(w[G]));
-    v[0] = a.x;
-    v[1] = a.y;
-    v[2] = b.x;
-    v[3] = b.y;
-    v[4] = c.x;
-    v[5] = c.y;
-    v[6] = d.x;
-    v[7] = d.y;
+    float2* t = reinterpret_cast<float2*>(dst);
+    for (int i = tid; i < 256 * 32; i += nthr) {
+      const int b = i >> 5;
+      t[i] = make_float2(cb[b & 15], cb[b >> 4]);
+    }
+  } else {
+    float* t = reinterpret_cast<float*>(dst);
+    for (int i = tid; i < (1 << BW); i += nthr) t[i] = cb[i];
+  }
+}
+
+// Codebook values of the 8 codes of a word (LSB-first, BW bits each), code 8G+j of
+// the word array into v[j]: one SDWA move and one 8-byte LDS read per two 4-bit
+// codes; other widths extract each code and read the plain table.
+template <int BW, int G, int NW>
+__device__ __forceinline__ void lookup8(const uint32_t (&w)[NW], Tab<BW>& tab, float (&v)[8]) {
+  if constexpr (BW == 4) {
+    static_for<0, 4>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      tab.r[k] = put_byte1<k>(tab.r[k], w[G]);
+      const float2 e = *reinterpret_cast<const float2*>(tab.lds + tab.r[k]);
+      v[2 * k] = e.x;
+      v[2 * k + 1] = e.y;
+    });
   } else {
     static_for<0, 8>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
       constexpr int bit = (8 * G + j) * BW, wi = bit >> 5, sh = bit & 31;
       uint32_t x = w[wi] >> sh;
       if constexpr (sh + BW > 32) x |= w[wi + 1] << (32 - sh);
-      v[j] = tab[x & ((1u << BW) - 1u)];
+      v[j] = tab.t[x & ((1u << BW) - 1u)];
     });
   }
 }
 
-// LDS floats a codebook of BW-bit codes occupies (the 4-bit pair table: 512).
-template <int BW>
-constexpr int table_floats() { return BW == 4 ? 512 : (1 << BW); }
-
-// Stages the codebook in LDS: the pair table for 4-bit codes, else the plain table.
-template <int BW>
-__device__ __forceinline__ void stage_table(const float* cb, float* tab, int lane) {
-  if constexpr (BW == 4) {
-    for (int i = lane; i < 256; i += 64) {
-      tab[2 * i] = cb[i & 15];
-      tab[2 * i + 1] = cb[i >> 4];
-    }
-  } else {
-    for (int i = lane; i < (1 << BW); i += 64) tab[i] = cb[i];
-  }
-}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): every vector
+// memory load this wave issued has returned.
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 __device__ __forceinline__ float half_lo(uint32_t h) { return f16_to_f32(uint16_t(h & 0xffffu)); }
 
@@ -216,7 +236,7 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, i
 
 // Score lookups of dims [8g, 8g+8) of this lane's K row.
 template <int BWK, int G>
-__device__ __forceinline__ void score_look(const uint32_t (&k)[4 * BWK], const float* cbk, float (&kv)[8]) {
+__device__ __forceinline__ void score_look(const uint32_t (&k)[4 * BWK], Tab<BWK>& cbk, float (&kv)[8]) {
   lookup8<BWK, G>(k, cbk, kv);
 }
 
@@ -234,7 +254,7 @@ __device__ __forceinline__ void score_mfma(const float (&qb)[8], const float (&k
 
 // Value lookups of quad q (this lane's 8 dims of token c0+4q+G).
 template <int BWV, int Q>
-__device__ __forceinline__ void value_look(const VChunk<BWV>& v, const float* cbv, float (&vv)[8]) {
+__device__ __forceinline__ void value_look(const VChunk<BWV>& v, Tab<BWV>& cbv, float (&vv)[8]) {
   lookup8<BWV, 0>(v.v[Q], cbv, vv);
 }
 
@@ -249,7 +269,7 @@ __device__ __forceinline__ void value_mfma(float a_q, const float (&vv)[8], f32x
 // Scores of the chunk's 64 tokens (lane = token, register i = head i); lookups of
 // group g+1 are issued before the MFMAs of group g.
 template <int BWK>
-__device__ __forceinline__ f32x4 score_phase(const KChunk<BWK>& kc, const float* cbk, const float (&qb)[8]) {
+__device__ __forceinline__ f32x4 score_phase(const KChunk<BWK>& kc, Tab<BWK>& cbk, const float (&qb)[8]) {
   f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
   float kv[2][8];
   score_look<BWK, 0>(kc.k, cbk, kv[0]);
@@ -264,7 +284,7 @@ __device__ __forceinline__ f32x4 score_phase(const KChunk<BWK>& kc, const float*
 
 // Values of a chunk; lookups of quad q+1 are issued before the MFMAs of quad q.
 template <int BWV>
-__device__ __forceinline__ void value_phase(const VChunk<BWV>& vc, const float* cbv, const float (&A)[16],
+__device__ __forceinline__ void value_phase(const VChunk<BWV>& vc, Tab<BWV>& cbv, const float (&A)[16],
                                             f32x4 (&acc)[8]) {
   float vv[2][8];
   value_look<BWV, 0>(vc, cbv, vv[0]);
@@ -370,7 +390,7 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, RowState& st,
 // computes and page ids run two chunks ahead.
 template <int BWK, int BWV>
 __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, int t_lo, int t_hi, int64_t prow,
-                                           int lane, const float* cbk, const float* cbv, float* ptile) {
+                                           int lane, Tab<BWK>& cbk, Tab<BWV>& cbv, float* ptile) {
   constexpr int D = 128;
   const int page_hi = (t_hi + (1 << a.log2S) - 1) >> a.log2S;
   const int n = (t_hi - t_lo + 63) >> 6;
@@ -403,36 +423,75 @@ __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, 
   int pid = pid_of(0);
   load_k(a, kvh, lane, t_lo, pid, kc);
   load_v(a, kvh, lane, t_lo, pid, vc);
-  int pid_next = n > 1 ? pid_of(1) : 0;
+  int pid_next = pid_of(1);
+  // The prologue's loads land before the loop: the compiler's wait analysis then
+  // sees nothing outstanding at the loop head, so no wait inside the body covers
+  // the next chunk's loads, and they overlap the whole of this chunk's compute.
+  wait_vmem_all();
   for (int c = 0; c < n; ++c) {
     const int c0 = t_lo + 64 * c;
+    // page ids two chunks ahead, issued before the next chunk's rows so that the
+    // wait for them never waits for those rows; clamped, so always a valid read
+    const int pid_after = pid_of(c + 2);
     if (c + 1 < n) {
       load_k(a, kvh, lane, c0 + 64, pid_next, kn);
       load_v(a, kvh, lane, c0 + 64, pid_next, vn);
     }
-    if (c + 2 < n) pid_next = pid_of(c + 2);
     const f32x4 s = score_phase(kc, cbk, qb);
     softmax_phase(s, kc.nk, kc.nv, c0 + lane < t_hi, lane, ptile, st, A);
     value_phase(vc, cbv, A, st.acc);
     kc = kn;
     vc = vn;
+    pid_next = pid_after;
   }
   write_partial(a, st, prow, lane);
 }
 
-// Fixed splits: work-group (split, kv head, sequence) scans pages
-// [split * pages_per_split, ...) of its sequence.
-// Balanced (a.balanced): the W = gridDim.x waves share the flattened space of
+// LDS of a work-group of WPB waves: the codebook tables (a replicated pair table
+// first, at a 64 KB slot, so that its address registers need no base add), then
+// one p tile per wave.
+template <int BWK, int BWV, int WPB>
+struct RowsLds {
+  static constexpr int k_off = (BWK == 4 || BWV != 4) ? 0 : kPairTableBytes;
+  static constexpr int v_off = BWV == 4 ? (BWK == 4 ? kPairTableBytes : 0) : (BWK == 4 ? kPairTableBytes
+                                                                                      : table_bytes<BWK>());
+  static constexpr int k_slot = k_off >> 16, v_slot = v_off >> 16;
+  static constexpr int tiles = (BWK == 4 && BWV != 4) ? v_off + table_bytes<BWV>()
+                               : (BWV == 4 && BWK != 4) ? k_off + table_bytes<BWK>()
+                                                        : v_off + table_bytes<BWV>();
+  static constexpr int tile_bytes = 16 * kPStride * 4;
+  static constexpr int total = tiles + WPB * tile_bytes;
+  static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
+};
+
+template <int BW>
+__device__ __forceinline__ Tab<BW> make_tab(const char* lds, int off, int lane) {
+  Tab<BW> t;
+  if constexpr (BW == 4) t.init(lds, off >> 16, lane);
+  else t.t = reinterpret_cast<const float*>(lds + off);
+  return t;
+}
+
+// Work-group of WPB independent waves sharing the codebook tables; wave w =
+// blockIdx.x * WPB + wave-in-group.
+// Fixed splits: wave w is unit (split, kv head, sequence) of the flattened
+// num_splits x Hkv x B space and scans pages [split * pages_per_split, ...) of its
+// sequence.
+// Balanced (a.balanced): the W = num_splits waves share the flattened space of
 // 64-token chunks ordered (sequence, kv head, chunk); wave w takes chunks
 // [C w / W', C (w+1) / W') with C the total and W' = min(W, C), and writes one
 // partial per (sequence, kv head) it touches, at row w + b*Hkv + kvh.
-template <int BWK, int BWV>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void decode_rows_kernel(
-    DecodeArgs a) {
-  __shared__ __align__(16) float cbk[table_floats<BWK>()];
-  __shared__ __align__(16) float cbv[table_floats<BWV>()];
-  __shared__ __align__(16) float ptile[16 * kPStride];
-  const int lane = threadIdx.x;
+template <int BWK, int BWV, int WPB>
+__global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
+  using Lay = RowsLds<BWK, BWV, WPB>;
+  __shared__ __align__(16) char lds[Lay::total];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
+  stage_table<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
+  stage_table<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
+  __syncthreads();  // the only block-wide barrier: waves run independently from here
+  const int64_t w = int64_t(blockIdx.x) * WPB + wig;
+  float* ptile = reinterpret_cast<float*>(lds + Lay::tiles + wig * Lay::tile_bytes);
 
   // The work list: one (sequence, kv head, token range) for a fixed split, or the
   // units overlapping this wave's share of the flattened chunk space. One call site
@@ -442,9 +501,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void
   int64_t s = 0, e = 0;  // balanced: flattened chunks [s, e) still to do
   const int32_t* pre = a.chunk_prefix;
   if (!a.balanced) {
-    const int split = blockIdx.x;
-    kvh = blockIdx.y;
-    b = blockIdx.z;
+    if (w >= int64_t(a.num_splits) * a.Hkv * a.B) return;
+    const int split = int(w % a.num_splits);
+    kvh = int((w / a.num_splits) % a.Hkv);
+    b = int(w / (int64_t(a.num_splits) * a.Hkv));
     const int L = a.seq_lens[b];
     const int S = 1 << a.log2S;
     const int n_pages = (L + S - 1) >> a.log2S;
@@ -456,8 +516,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void
     prow = (int64_t(b) * a.Hkv + kvh) * a.num_splits + split;
   } else {
     const int64_t C = int64_t(a.Hkv) * pre[a.B];
-    const int64_t Wp = min(int64_t(gridDim.x), C);
-    const int w = blockIdx.x;
+    const int64_t Wp = min(int64_t(a.num_splits), C);
     if (w >= Wp) return;
     s = C * w / Wp;
     e = C * (w + 1) / Wp;
@@ -472,9 +531,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void
     kvh = t_lo = t_hi = 0;
     prow = 0;
   }
-  stage_table<BWK>(a.cb_k, cbk, lane);
-  stage_table<BWV>(a.cb_v, cbv, lane);
-  wave_lds_sync();
+  Tab<BWK> cbk = make_tab<BWK>(lds, Lay::k_off, lane);
+  Tab<BWV> cbv = make_tab<BWV>(lds, Lay::v_off, lane);
 
   while (true) {
     int nb = 0, c_hi = 0;
@@ -490,7 +548,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void
       c_hi = int(min(int64_t(nb), c_lo + (e - s)));
       t_lo = 64 * c_lo;
       t_hi = min(64 * c_hi, a.seq_lens[b]);
-      prow = int64_t(blockIdx.x) + int64_t(b) * a.Hkv + kvh;
+      prow = w + int64_t(b) * a.Hkv + kvh;
       s += c_hi - c_lo;
     }
     scan_range<BWK, BWV>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
@@ -499,34 +557,43 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 8))) void
   }
 }
 
+// Waves per work-group: three per SIMD where the scan fits in 168 VGPRs, else two.
+template <int BWK, int BWV>
+constexpr int rows_wpb() { return BWK <= 4 && BWV <= 4 ? 12 : 8; }
+
+template <int BWK, int BWV>
+SplitKernel rows_kernel() {
+  constexpr int wpb = rows_wpb<BWK, BWV>();
+  SplitKernel k;
+  k.fn = decode_rows_kernel<BWK, BWV, wpb>;
+  k.block = 64 * wpb;
+  k.wpb = wpb;
+  k.nrep = 4;
+  k.log2_units = true;
+  k.rows = true;
+  return k;
+}
+
 }  // namespace
 
 SplitKernel pick_split_rows(int bw_k, int bw_v) {
-  SplitFn f = nullptr;
   if (bw_k == bw_v) {
     switch (bw_k) {
-      case 2: f = decode_rows_kernel<2, 2>; break;
-      case 3: f = decode_rows_kernel<3, 3>; break;
-      case 4: f = decode_rows_kernel<4, 4>; break;
-      case 5: f = decode_rows_kernel<5, 5>; break;
-      case 6: f = decode_rows_kernel<6, 6>; break;
-      case 8: f = decode_rows_kernel<8, 8>; break;
+      case 2: return rows_kernel<2, 2>();
+      case 3: return rows_kernel<3, 3>();
+      case 4: return rows_kernel<4, 4>();
+      case 5: return rows_kernel<5, 5>();
+      case 6: return rows_kernel<6, 6>();
+      case 8: return rows_kernel<8, 8>();
     }
   } else if (bw_k == 4 && bw_v == 6) {
-    f = decode_rows_kernel<4, 6>;
+    return rows_kernel<4, 6>();
   } else if (bw_k == 6 && bw_v == 4) {
-    f = decode_rows_kernel<6, 4>;
+    return rows_kernel<6, 4>();
   } else if (bw_k == 4 && bw_v == 8) {
-    f = decode_rows_kernel<4, 8>;
+    return rows_kernel<4, 8>();
   }
-  SplitKernel k;
-  if (f) {
-    k.fn = f;
-    k.block = 64;
-    k.nrep = 4;
-    k.log2_units = true;
-  }
-  return k;
+  return SplitKernel{};
 }
 
 }  // namespace wn

@@ -30,14 +30,16 @@ using SplitFn = void (*)(DecodeArgs);
 struct SplitKernel {
   SplitFn fn = nullptr;
   int block = 0;  // threads per work-group
+  int wpb = 1;    // independent waves per work-group (row scan); grid counts waves / wpb
   int nrep = 0;   // query-head rows per kv head the kernel reads from q_rot
   bool log2_units = false;  // scores/maxima in log2 units (q_rot scaled by log2 e)
+  bool rows = false;        // the row-per-lane matrix-core scan (balanced plans allowed)
 };
 
 // Row-per-lane matrix-core page scan for head_dim 128, power-of-two page sizes
-// >= 16 and up to four query heads per kv head (one independent wave per
-// work-group, fixed splits or balanced persistent waves), or an empty
-// SplitKernel when (bw_k, bw_v) is not compiled.
+// >= 16 and up to four query heads per kv head (wpb independent waves per
+// work-group sharing the codebook tables, fixed splits or balanced persistent
+// waves), or an empty SplitKernel when (bw_k, bw_v) is not compiled.
 SplitKernel pick_split_rows(int bw_k, int bw_v);
 
 }  // namespace wn
