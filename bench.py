@@ -14,6 +14,9 @@ Prints ONE JSON line on stdout; details go to stderr.
 (sum_b L_b * Hkv * ((NB_K + 2) + (NB_V + 2)), the reference's traffic model,
 bench_packed_attention.py:91-98) divided by the mean duration of the page-scan
 kernel, timed with HIP events recorded on its stream around every launch.
+``roofline.traffic`` is the HBM bytes one scan launch moves, read from the
+FETCH_SIZE and WRITE_SIZE counters of two ``rocprofv3 --pmc`` child runs and
+scaled by what the same counters read for a 1 GiB device copy.
 ``cpu_baseline`` times the CPU restatement of the reference's CPU decode path
 (``tiled_compressed_attention``) on a bounded sample of page-table columns of
 the same workload and scales it to the full step.
@@ -162,6 +165,61 @@ def copy_peak(dev, nbytes: int = 1 << 30, reps: int = 10):
     return {"bytes_read": nbytes, "bytes_written": nbytes, "us": t * 1e6, "GBps": 2 * nbytes / t / 1e9}
 
 
+def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
+    """HBM bytes one launch of ``kernel`` moves, from two ``rocprofv3 --pmc`` child runs.
+
+    Each pass profiles a short run of this script (3 steps plus the 1 GiB device
+    copy of ``copy_peak``) with one counter, FETCH_SIZE then WRITE_SIZE (KiB per
+    dispatch). Each counter is scaled by what it reads for that copy of known size
+    (bytes / counter), so the figure is in real bytes whatever fraction of the
+    memory channels the counter samples. Returns None when the profiler is absent
+    or a pass fails; the bench line then carries ``traffic: null``.
+    """
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return None
+    out = {}
+    with tempfile.TemporaryDirectory(prefix="wn_pmc_", dir="/tmp") as tmp:
+        env = dict(os.environ, TMPDIR="/tmp")
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            d = Path(tmp) / counter
+            cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "run", "--",
+                   sys.executable, str(ROOT / "bench.py"), "--config", str(cfg), "--steps", "3", "--warmup", "1",
+                   "--settle", "0", "--parity", "off", "--cpu-baseline", "off", "--traffic", "off",
+                   "--copy-peak", "on"]
+            try:
+                subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                               timeout=timeout_s, check=True)
+            except (subprocess.SubprocessError, OSError) as e:
+                log(f"traffic pass {counter} failed: {e}")
+                return None
+            files = list(d.rglob("*counter_collection.csv"))
+            if not files:
+                return None
+            scan, copy = [], []
+            for r in csv.DictReader(open(files[0])):
+                v = float(r["Counter_Value"])
+                if kernel in r["Kernel_Name"]:
+                    scan.append(v)
+                elif "copyBuffer" in r["Kernel_Name"]:
+                    copy.append(v)
+            # the 13 copies of copy_peak move 1 GiB each, more than any other copy of the run
+            copy = sorted(copy)[-10:]
+            if not scan or len(copy) < 10:
+                return None
+            copy_kib = statistics.median(copy)
+            factor = (1 << 30) / (copy_kib * 1024)
+            out[counter] = {"kib_per_launch": statistics.fmean(scan), "copy_kib": copy_kib, "factor": factor,
+                            "bytes_per_launch": statistics.fmean(scan) * 1024 * factor}
+    out["bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
+    return out
+
+
 def parity(c, lens, q, kv, quants, sample):
     """Same-run checks: two sequences' attention vs the CPU oracle on the same pages, and
     the first 256 tokens of sequence 0 re-quantized by the oracle vs the pool bytes."""
@@ -252,6 +310,8 @@ def main(argv=None):
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--parity", choices=["on", "off"], default="on")
     ap.add_argument("--copy-peak", choices=["on", "off"], default="on")
+    ap.add_argument("--traffic", choices=["on", "off"], default="on",
+                    help="measure HBM bytes per scan launch with two rocprofv3 --pmc child runs")
     ap.add_argument("--settle", type=float, default=0.5,
                     help="seconds of untimed steps before the warm-up, to reach sustained clocks")
     args = ap.parse_args(argv)
@@ -320,6 +380,9 @@ def main(argv=None):
     if cp:
         log(f"copy peak: {cp}")
 
+    traffic = hbm_traffic(args.config, scan_kernel_name(c)) if args.traffic == "on" else None
+    if traffic:
+        log(f"traffic: {traffic}")
     par = parity(c, lens, q, kvs[0], quants, sample) if args.parity == "on" else None
     if par:
         log(f"parity: {par}")
@@ -348,7 +411,12 @@ def main(argv=None):
         "step_GBps": bytes_step / (ms * 1e-3) / 1e9,
         "kv_tokens_per_s": sum(lens) / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBPS,
+                     "traffic": traffic["bytes_per_launch"] if traffic else None,
+                     "traffic_read_bytes": traffic["FETCH_SIZE"]["bytes_per_launch"] if traffic else None,
+                     "traffic_write_bytes": traffic["WRITE_SIZE"]["bytes_per_launch"] if traffic else None,
+                     "counter_scale": {k: traffic[k]["factor"] for k in ("FETCH_SIZE", "WRITE_SIZE")}
+                     if traffic else None,
                      "kernel": scan_kernel_name(c), "kernel_us": kern_ms * 1e3,
                      "algorithmic_bytes": bytes_step,
                      "copy_peak_GBps": cp["GBps"] if cp else None,
