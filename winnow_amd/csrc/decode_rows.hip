@@ -52,6 +52,14 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+template <int K>
+__device__ __forceinline__ float comp(const float4& x) {
+  if constexpr (K == 0) return x.x;
+  else if constexpr (K == 1) return x.y;
+  else if constexpr (K == 2) return x.z;
+  else return x.w;
+}
+
 // Byte K of x written into byte 1 of r, the other bytes of r kept: one VOP2 SDWA
 // move. With r = 8*(lane % 32) | slot << 16 this is the LDS byte address of entry
 // (byte K of x, lane % 32) of the replicated pair table in 64 KB slot `slot`.
@@ -108,15 +116,16 @@ __device__ __forceinline__ void stage_table(const float* cb, char* dst, int tid,
   }
 }
 
-// Codebook values of the 8 codes of a word (LSB-first, BW bits each), code 8G+j of
-// the word array into v[j]: one SDWA move and one 8-byte LDS read per two 4-bit
+// Codebook values of the 8 codes starting at bit BIT0 of the word array (LSB-first,
+// BW bits each) into v[0..7]: one SDWA move and one 8-byte LDS read per two 4-bit
 // codes; other widths extract each code and read the plain table.
-template <int BW, int G, int NW>
+template <int BW, int BIT0, int NW>
 __device__ __forceinline__ void lookup8(const uint32_t (&w)[NW], Tab<BW>& tab, float (&v)[8]) {
   if constexpr (BW == 4) {
+    static_assert(BIT0 % 32 == 0, "4-bit groups are word aligned");
     static_for<0, 4>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
-      tab.r[k] = put_byte1<k>(tab.r[k], w[G]);
+      tab.r[k] = put_byte1<k>(tab.r[k], w[BIT0 / 32]);
       const float2 e = *reinterpret_cast<const float2*>(tab.lds + tab.r[k]);
       v[2 * k] = e.x;
       v[2 * k + 1] = e.y;
@@ -124,7 +133,7 @@ __device__ __forceinline__ void lookup8(const uint32_t (&w)[NW], Tab<BW>& tab, f
   } else {
     static_for<0, 8>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
-      constexpr int bit = (8 * G + j) * BW, wi = bit >> 5, sh = bit & 31;
+      constexpr int bit = BIT0 + j * BW, wi = bit >> 5, sh = bit & 31;
       uint32_t x = w[wi] >> sh;
       if constexpr (sh + BW > 32) x |= w[wi + 1] << (32 - sh);
       v[j] = tab.t[x & ((1u << BW) - 1u)];
@@ -136,6 +145,11 @@ __device__ __forceinline__ void lookup8(const uint32_t (&w)[NW], Tab<BW>& tab, f
 // memory load this wave issued has returned.
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// A value every lane holds alike, moved to a scalar register.
+__device__ __forceinline__ float uniform(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
+
 __device__ __forceinline__ float half_lo(uint32_t h) { return f16_to_f32(uint16_t(h & 0xffffu)); }
 
 // Words of the V codes one lane reads per token: BWV bytes (8 codes).
@@ -144,17 +158,17 @@ struct VWords {
   static constexpr int N = BWV <= 4 ? 1 : 2;
 };
 
-// Packed K row and norms of token c0 + lane.
-template <int BWK>
-struct KChunk {
-  uint32_t k[4 * BWK];  // 16*BWK bytes
-  uint32_t nk, nv;      // fp16 norms (low 16 bits)
-};
-
-// For quad q: codes 8p..8p+7 of token c0 + 4q + G (G = lane/16, p = lane%16).
-template <int BWV>
-struct VChunk {
-  uint32_t v[16][BWV <= 4 ? 1 : 2];
+// One buffer of packed rows. As a K buffer it holds the packed K row of token
+// c0 + lane (words [0, KW)) and that token's fp16 K and V norms (words KW, KW+1);
+// as a V buffer, for each token quad q, the codes 8p..8p+7 of token c0 + 4q + G
+// (G = lane/16, p = lane%16) at words [q*VW, q*VW + VW). A chunk's K buffer is
+// refilled with the next chunk's V codes once the softmax has used the norms.
+template <int BWK, int BWV>
+struct RowBuf {
+  static constexpr int KW = 4 * BWK;
+  static constexpr int VW = VWords<BWV>::N;
+  static constexpr int W = KW + 2 > 16 * VW ? KW + 2 : 16 * VW;
+  uint32_t w[W];
 };
 
 // BWV bytes at p (8 codes of one lane) into little-endian words. p is aligned to
@@ -196,30 +210,32 @@ struct RowState {
 
 // K side of chunk [c0, c0+64): the packed K row and both norms of token c0+lane,
 // whose page is pid_lane.
-template <int BWK>
-__device__ __forceinline__ void load_k(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane, KChunk<BWK>& r) {
-  constexpr int NBK = 16 * BWK;
+template <int BWK, int BWV>
+__device__ __forceinline__ void load_k(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane,
+                                       RowBuf<BWK, BWV>& r) {
+  constexpr int NBK = 16 * BWK, KW = RowBuf<BWK, BWV>::KW;
   const int slot = (c0 + lane) & ((1 << a.log2S) - 1);
   const uint8_t* krow = a.k_pages + int64_t(pid_lane) * a.ksp + kvh * a.ksh + slot * NBK;
 #pragma unroll
   for (int i = 0; i < NBK / 16; ++i) {
     const uint4 x = reinterpret_cast<const uint4*>(krow)[i];
-    r.k[4 * i] = x.x;
-    r.k[4 * i + 1] = x.y;
-    r.k[4 * i + 2] = x.z;
-    r.k[4 * i + 3] = x.w;
+    r.w[4 * i] = x.x;
+    r.w[4 * i + 1] = x.y;
+    r.w[4 * i + 2] = x.z;
+    r.w[4 * i + 3] = x.w;
   }
-  r.nk = a.k_norms[int64_t(pid_lane) * a.knp + kvh * a.knh + slot];
-  r.nv = a.v_norms[int64_t(pid_lane) * a.vnp + kvh * a.vnh + slot];
+  r.w[KW] = a.k_norms[int64_t(pid_lane) * a.knp + kvh * a.knh + slot];
+  r.w[KW + 1] = a.v_norms[int64_t(pid_lane) * a.vnp + kvh * a.vnh + slot];
 }
 
 // V side of chunk [c0, c0+64): for every token quad q the BWV bytes of codes
 // 8p..8p+7 of token c0+4q+G (G = lane/16, p = lane%16). c0 is a multiple of 16 and
 // pages hold >= 16 tokens, so the four quads of 16-token block j share the page of
 // lane 16j (pid_lane is the page of token c0+lane).
-template <int BWV>
-__device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane, VChunk<BWV>& r) {
-  constexpr int NBV = 16 * BWV;
+template <int BWK, int BWV>
+__device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane,
+                                       RowBuf<BWK, BWV>& r) {
+  constexpr int NBV = 16 * BWV, VW = RowBuf<BWK, BWV>::VW;
   const int smask = (1 << a.log2S) - 1;
   const int p = lane & 15;
   const int lane_off = (lane >> 4) * NBV + BWV * p;
@@ -229,15 +245,18 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, i
     const uint8_t* vj = a.v_pages + int64_t(pid_j) * a.vsp + kvh * a.vsh + ((c0 + 16 * j) & smask) * NBV + lane_off;
     static_for<0, 4>([&](auto qc) {
       constexpr int qq = decltype(qc)::value;
-      load_vcodes<BWV>(vj + 4 * qq * NBV, p & 1, r.v[4 * j + qq]);
+      uint32_t t[VW];
+      load_vcodes<BWV>(vj + 4 * qq * NBV, p & 1, t);
+#pragma unroll
+      for (int x = 0; x < VW; ++x) r.w[(4 * j + qq) * VW + x] = t[x];
     });
   });
 }
 
 // Score lookups of dims [8g, 8g+8) of this lane's K row.
-template <int BWK, int G>
-__device__ __forceinline__ void score_look(const uint32_t (&k)[4 * BWK], Tab<BWK>& cbk, float (&kv)[8]) {
-  lookup8<BWK, G>(k, cbk, kv);
+template <int BWK, int G, int NW>
+__device__ __forceinline__ void score_look(const uint32_t (&k)[NW], Tab<BWK>& cbk, float (&kv)[8]) {
+  lookup8<BWK, 8 * G * BWK>(k, cbk, kv);
 }
 
 // The 8 score MFMAs of dims [8g, 8g+8): A = q_rot[head][k] broadcast from block k%16.
@@ -253,9 +272,9 @@ __device__ __forceinline__ void score_mfma(const float (&qb)[8], const float (&k
 }
 
 // Value lookups of quad q (this lane's 8 dims of token c0+4q+G).
-template <int BWV, int Q>
-__device__ __forceinline__ void value_look(const VChunk<BWV>& v, Tab<BWV>& cbv, float (&vv)[8]) {
-  lookup8<BWV, 0>(v.v[Q], cbv, vv);
+template <int BWV, int Q, int NW>
+__device__ __forceinline__ void value_look(const uint32_t (&v)[NW], Tab<BWV>& cbv, float (&vv)[8]) {
+  lookup8<BWV, 32 * VWords<BWV>::N * Q>(v, cbv, vv);
 }
 
 // The 8 value MFMAs of quad q: A = p*n_V broadcast inside each group of four blocks.
@@ -266,40 +285,62 @@ __device__ __forceinline__ void value_mfma(float a_q, const float (&vv)[8], f32x
   });
 }
 
-// Scores of the chunk's 64 tokens (lane = token, register i = head i); lookups of
-// group g+1 are issued before the MFMAs of group g.
-template <int BWK>
-__device__ __forceinline__ f32x4 score_phase(const KChunk<BWK>& kc, Tab<BWK>& cbk, const float (&qb)[8]) {
+// Scores of the chunk's 64 tokens (lane = token, register i = head i). The
+// lookups of group g+2 are issued before the MFMAs of group g, so every LDS read
+// has sixteen of this wave's MFMAs to land before its value is needed; the sched
+// barriers keep the compiler from sinking the reads next to their consumers.
+template <int BWK, int NW>
+__device__ __forceinline__ f32x4 score_phase(const uint32_t (&kc)[NW], Tab<BWK>& cbk, const float (&qb)[8]) {
   f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
-  float kv[2][8];
-  score_look<BWK, 0>(kc.k, cbk, kv[0]);
+  float kv[3][8];
+  score_look<BWK, 0>(kc, cbk, kv[0]);
+  score_look<BWK, 1>(kc, cbk, kv[1]);
+  __builtin_amdgcn_sched_barrier(0);
   static_for<0, 16>([&](auto gc) {
     constexpr int g = decltype(gc)::value;
-    if constexpr (g + 1 < 16) score_look<BWK, g + 1>(kc.k, cbk, kv[(g + 1) & 1]);
-    score_mfma<g>(qb, kv[g & 1], s0, s1);
+    if constexpr (g + 2 < 16) {
+      score_look<BWK, g + 2>(kc, cbk, kv[(g + 2) % 3]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    score_mfma<g>(qb, kv[g % 3], s0, s1);
     __builtin_amdgcn_sched_barrier(0);
   });
   return s0 + s1;
 }
 
-// Values of a chunk; lookups of quad q+1 are issued before the MFMAs of quad q.
-template <int BWV>
-__device__ __forceinline__ void value_phase(const VChunk<BWV>& vc, Tab<BWV>& cbv, const float (&A)[16],
-                                            f32x4 (&acc)[8]) {
-  float vv[2][8];
+// Lookups of the first two value quads, issued before the softmax so that they
+// land while it runs.
+template <int BWV, int NW>
+__device__ __forceinline__ void value_prime(const uint32_t (&vc)[NW], Tab<BWV>& cbv, float (&vv)[3][8]) {
   value_look<BWV, 0>(vc, cbv, vv[0]);
+  value_look<BWV, 1>(vc, cbv, vv[1]);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Values of a chunk; lookups of quad q+2 are issued before the MFMAs of quad q,
+// and the p * n_V operands of four quads are read from the tile two quads before
+// the first of them.
+template <int BWV, int NW>
+__device__ __forceinline__ void value_phase(const uint32_t (&vc)[NW], Tab<BWV>& cbv, const float4* arow,
+                                            f32x4 (&acc)[8], float (&vv)[3][8]) {
+  float4 ab[2];
+  ab[0] = arow[0];
   static_for<0, 16>([&](auto qc) {
     constexpr int q = decltype(qc)::value;
-    if constexpr (q + 1 < 16) value_look<BWV, q + 1>(vc, cbv, vv[(q + 1) & 1]);
-    value_mfma(A[q], vv[q & 1], acc);
+    if constexpr ((q & 3) == 2 && q + 2 < 16) ab[((q >> 2) + 1) & 1] = arow[(q >> 2) + 1];
+    if constexpr (q + 2 < 16) value_look<BWV, q + 2>(vc, cbv, vv[(q + 2) % 3]);
+    __builtin_amdgcn_sched_barrier(0);
+    value_mfma(comp<q & 3>(ab[(q >> 2) & 1]), vv[q % 3], acc);
     __builtin_amdgcn_sched_barrier(0);
   });
 }
 
 // Online softmax of one chunk (lane = token) and the p * n_V transposition: on
-// return lane 16G+i holds A[q] = p(head i, token c0+4q+G) * n_V for q = 0..15.
+// return the tile holds p(head i, token c0+4q+G) * n_V at row 4i+G, column q, and
+// lane 16G+i finds its value-MFMA operands for quads 4j..4j+3 at float4 j of row
+// 4(lane%4) + lane/16 (tile_row).
 __device__ __forceinline__ void softmax_phase(f32x4 s, uint32_t nk_h, uint32_t nv_h, bool valid, int lane,
-                                              float* pt, RowState& st, float (&A)[16]) {
+                                              float* pt, RowState& st) {
   const float nk = half_lo(nk_h);
   const float nv = valid ? half_lo(nv_h) : 0.f;
   float sv[4];
@@ -311,7 +352,8 @@ __device__ __forceinline__ void softmax_phase(f32x4 s, uint32_t nk_h, uint32_t n
   if (move) {  // wave-uniform
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float m_new = fmaxf(st.m[i], wave_max(sv[i]));
+      // wave-uniform: kept in a scalar register, which frees a VGPR per head
+      const float m_new = uniform(fmaxf(st.m[i], wave_max(sv[i])));
       const float alpha = __builtin_amdgcn_exp2f(st.m[i] - m_new);  // 0 on the first chunk
       st.m[i] = m_new;
       st.l[i] *= alpha;
@@ -333,16 +375,12 @@ __device__ __forceinline__ void softmax_phase(f32x4 s, uint32_t nk_h, uint32_t n
     for (int i = 0; i < 4; ++i) pt[(i * 4 + G) * kPStride + q] = pv[i];
   }
   wave_lds_sync();
-  const float4* src = reinterpret_cast<const float4*>(pt + ((lane & 3) * 4 + (lane >> 4)) * kPStride);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float4 x = src[i];
-    A[4 * i] = x.x;
-    A[4 * i + 1] = x.y;
-    A[4 * i + 2] = x.z;
-    A[4 * i + 3] = x.w;
-  }
 }
+
+__device__ __forceinline__ const float4* tile_row(const float* pt, int lane) {
+  return reinterpret_cast<const float4*>(pt + ((lane & 3) * 4 + (lane >> 4)) * kPStride);
+}
+
 
 // Folds the four token groups and the per-lane sums and writes the (acc, m, l)
 // partial of each query head h < n_rep to row prow * n_rep + h.
@@ -417,32 +455,42 @@ __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, 
     st.m[i] = -INFINITY;
     st.l[i] = 0.f;
   }
-  float A[16];
-  KChunk<BWK> kc, kn;
-  VChunk<BWV> vc, vn;
-  int pid = pid_of(0);
-  load_k(a, kvh, lane, t_lo, pid, kc);
-  load_v(a, kvh, lane, t_lo, pid, vc);
-  int pid_next = pid_of(1);
+  using Buf = RowBuf<BWK, BWV>;
+  // Chunk c with its K rows in X and its V codes in Y; Z is free. The K rows of
+  // chunk c+1 load into Z at the start, its V codes into X once the softmax has
+  // read the norms, so each load has about one chunk of compute to land, and
+  // three buffers rotate through the roles: (X, Y, Z) -> (Z, X, Y).
+  int pid_next;
+  auto step = [&](int c, Buf& X, Buf& Y, Buf& Z) {
+    const int c0 = t_lo + 64 * c;
+    // page ids two chunks ahead, issued before the next chunk's rows, so the wait
+    // for them never waits for those rows; clamped, so always a valid read
+    const int pid_after = pid_of(c + 2);
+    const bool more = c + 1 < n;
+    if (more) load_k(a, kvh, lane, c0 + 64, pid_next, Z);
+    float vv[3][8];
+    const f32x4 s = score_phase<BWK>(X.w, cbk, qb);
+    value_prime<BWV>(Y.w, cbv, vv);
+    softmax_phase(s, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
+    if (more) load_v(a, kvh, lane, c0 + 64, pid_next, X);
+    value_phase<BWV>(Y.w, cbv, tile_row(ptile, lane), st.acc, vv);
+    pid_next = pid_after;
+  };
+
+  Buf b0, b1, b2;
+  load_k(a, kvh, lane, t_lo, pid_of(0), b0);
+  load_v(a, kvh, lane, t_lo, pid_of(0), b1);
+  pid_next = pid_of(1);
   // The prologue's loads land before the loop: the compiler's wait analysis then
   // sees nothing outstanding at the loop head, so no wait inside the body covers
-  // the next chunk's loads, and they overlap the whole of this chunk's compute.
+  // a load issued for a later chunk.
   wait_vmem_all();
-  for (int c = 0; c < n; ++c) {
-    const int c0 = t_lo + 64 * c;
-    // page ids two chunks ahead, issued before the next chunk's rows so that the
-    // wait for them never waits for those rows; clamped, so always a valid read
-    const int pid_after = pid_of(c + 2);
-    if (c + 1 < n) {
-      load_k(a, kvh, lane, c0 + 64, pid_next, kn);
-      load_v(a, kvh, lane, c0 + 64, pid_next, vn);
-    }
-    const f32x4 s = score_phase(kc, cbk, qb);
-    softmax_phase(s, kc.nk, kc.nv, c0 + lane < t_hi, lane, ptile, st, A);
-    value_phase(vc, cbv, A, st.acc);
-    kc = kn;
-    vc = vn;
-    pid_next = pid_after;
+  for (int c = 0; c < n; c += 3) {
+    step(c, b0, b1, b2);
+    if (c + 1 >= n) break;
+    step(c + 1, b2, b0, b1);
+    if (c + 2 >= n) break;
+    step(c + 2, b1, b2, b0);
   }
   write_partial(a, st, prow, lane);
 }
