@@ -319,7 +319,7 @@ struct MergeArgs {
   const int32_t* seq_lens;
   const int32_t* chunk_prefix;
   void* out;
-  int out_dtype, Hq, Hkv, n_rep, log2S, pages_per_split, num_splits, balanced;
+  int out_dtype, B, Hq, Hkv, n_rep, log2S, pages_per_split, num_splits, balanced;
   int log2_units;  // partial maxima are in log2 units (weights 2^(m - M))
 };
 
@@ -327,11 +327,14 @@ constexpr int kMergeBatch = 32;  // partials whose loads are in flight together
 
 // out[b, kvh*n_rep + h, :] = (sum_s w_s acc_s / sum_s w_s l_s) Pi_V with
 // w_s = exp(m_s - max m) (2^(m_s - max m) for log2-unit partials), zero when no
-// key was seen (packed_attention_triton.py:137-159 plus :261). One work-group of D
-// threads per (query head h, kv head, sequence): thread d merges dim d over the
-// partials in a single max-stable pass with the loads of 32 partials issued
-// together (a balanced plan has about num_splits / (B*Hkv) partials per group, so
-// one round trip), then thread j forms output dim j from Pi_V rows read coalesced.
+// key was seen (packed_attention_triton.py:137-159 plus :261).
+//
+// One work-group of D threads per (query head h, kv head, sequence). Thread d
+// first issues the loads of column d of Pi_V, so that they travel together with
+// the partials' (one round trip for both), then merges dim d over the partials in
+// a single max-stable pass with the loads of 32 partials in flight together (a
+// balanced plan has about num_splits / (B*Hkv) partials per group), and finally
+// forms output dim d from its Pi_V column and the merged row in LDS.
 // The partials of the group are rows r0 + s, s < n: fixed splits give
 // r0 = (b*Hkv + kvh)*num_splits and n = splits holding tokens; the balanced scan
 // gives rows w + b*Hkv + kvh for the waves w that touched the group.
@@ -339,6 +342,10 @@ template <int D>
 __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
   __shared__ float av[D];
   const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
+  float pc[D];  // column d of Pi_V
+#pragma unroll
+  for (int k = 0; k < D; ++k) pc[k] = a.pi_v[k * D + d];
+
   int64_t r0 = 0;
   int n = 0;
   const int L = a.seq_lens[b];
@@ -351,7 +358,7 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
     const int32_t* pre = a.chunk_prefix;
     const int nb = pre[b + 1] - pre[b];
     if (nb > 0) {
-      const int64_t C = int64_t(a.Hkv) * pre[gridDim.z];
+      const int64_t C = int64_t(a.Hkv) * pre[a.B];
       const int64_t Wp = min(int64_t(a.num_splits), C);
       const int64_t U0 = int64_t(a.Hkv) * pre[b] + int64_t(kvh) * nb, U1 = U0 + nb;
       const int64_t wf = ((U0 + 1) * Wp + C - 1) / C - 1;  // last wave starting at or before U0
@@ -388,11 +395,10 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
   }
   av[d] = (L > 0 && den > 0.f) ? num / fmaxf(den, 1e-30f) : 0.f;
   __syncthreads();
-  // out_j = sum_d a_d Pi_V[d, j]; (a / l) Pi_V == (a Pi_V) / l up to rounding
+  // out_j = sum_k a_k Pi_V[k, j]; (a / l) Pi_V == (a Pi_V) / l up to rounding
   float o = 0.f;
-  const float* pv = a.pi_v + d;
-#pragma unroll 16
-  for (int k = 0; k < D; ++k) o = fmaf(av[k], pv[k * D], o);
+#pragma unroll
+  for (int k = 0; k < D; ++k) o = fmaf(av[k], pc[k], o);
   store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + d, a.out_dtype, o);
 }
 
@@ -664,7 +670,7 @@ extern "C" int wn_decode_attention(
   hipLaunchKernelGGL(sk.fn, grid, dim3(sk.block), 0, st, da);
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
-  MergeArgs ma{da.part_acc, da.part_ml, pi_v, seq_lens, prefix, out, out_dtype, Hq, Hkv, n_rep, da.log2S,
+  MergeArgs ma{da.part_acc, da.part_ml, pi_v, seq_lens, prefix, out, out_dtype, B, Hq, Hkv, n_rep, da.log2S,
                pages_per_split, num_splits, da.balanced, sk.log2_units ? 1 : 0};
   if (D == 128)
     hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep, Hkv, B), dim3(128), 0, st, ma);
