@@ -5,7 +5,7 @@
 //                        one block also writes the per-sequence chunk prefix the
 //                        balanced scan partitions by
 //   2. page scan         the row-per-lane matrix-core scan (decode_rows.hip) where
-//                        it applies (head_dim 128, <= 4 query heads per kv head),
+//                        it applies (head_dim 128, <= 8 query heads per kv head),
 //                        else decode_split_kernel below: one work-group per
 //                        (split, kv head, sequence), score phase (lane = token),
 //                        online softmax, value phase (16 lanes per token row),
@@ -471,7 +471,7 @@ int pad_nrep(int n_rep) {
 SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v) {
   SplitKernel sk;
   const int n_rep = Hq / Hkv;
-  if (D == 128 && n_rep <= 4 && S >= 16 && rows_allowed()) sk = pick_split_rows(bw_k, bw_v);
+  if (D == 128 && n_rep <= 8 && S >= 16 && rows_allowed()) sk = pick_split_rows(bw_k, bw_v, n_rep);
   if (!sk.fn) {
     const int nrp = pad_nrep(n_rep);
     sk.fn = D == 128 ? pick_split<128>(bw_k, bw_v, nrp) : pick_split<64>(bw_k, bw_v, nrp);

@@ -1,5 +1,6 @@
 // Row-per-lane matrix-core page scan of the packed decode attention (head_dim 128,
-// power-of-two page size >= 16, up to four query heads per kv head), gfx950.
+// power-of-two page size >= 16, up to eight query heads per kv head in one or two
+// groups of four), gfx950.
 //
 // One wave per work-group, independent of every other wave. With fixed splits a
 // wave owns a range of pages of one (sequence, kv head); with a balanced plan
@@ -7,10 +8,11 @@
 // equal shares. Either way a wave walks its tokens in 64-token chunks.
 //
 //   scores  lane l holds the packed K row of token c0+l. For each dim k one
-//           v_mfma_f32_4x4x1_16b_f32 with A = q_rot[head i][k] broadcast to all
-//           16 blocks (CBSZ=4, ABID=k%16) and B = c_K[code(token, k)] gives
-//           D[block][i][j] = partial s(head i, token 4*block+j): lane l ends with
-//           the four heads' scores of its own token. 128 MFMAs per chunk.
+//           v_mfma_f32_4x4x1_16b_f32 per group of four heads, with A = q_rot[head i][k]
+//           broadcast to all 16 blocks (CBSZ=4, ABID=k%16) and B = c_K[code(token, k)],
+//           gives D[block][i][j] = partial s(head i, token 4*block+j): lane l ends
+//           with its own token's scores. 128 MFMAs per chunk and head group; each
+//           codebook lookup feeds every group.
 //   softmax per head in log2 units (q_rot carries log2 e), lane = token, with a
 //           lazy reference maximum: it moves (rescaling the accumulators) only
 //           when a score exceeds it by more than kRescale, so 2^(s - m) <= 2^kRescale.
@@ -58,6 +60,12 @@ __device__ __forceinline__ float comp(const float4& x) {
   else if constexpr (K == 1) return x.y;
   else if constexpr (K == 2) return x.z;
   else return x.w;
+}
+
+// Row of the p tile lane 16G+i reads its value-MFMA operands of head group g from:
+// p(head 4g+i, token c0+4q+G) * n_V sits at row 16g + 4i + G, column q.
+__device__ __forceinline__ const float4* tile_row(const float* pt, int g, int lane) {
+  return reinterpret_cast<const float4*>(pt + (16 * g + (lane & 3) * 4 + (lane >> 4)) * kPStride);
 }
 
 // Byte K of x written into byte 1 of r, the other bytes of r kept: one VOP2 SDWA
@@ -202,10 +210,12 @@ __device__ __forceinline__ void load_vcodes(const uint8_t* p, bool odd_lane, uin
   }
 }
 
+// Running state of NG groups of four query heads (head 4g+i is register i of group g).
+template <int NG>
 struct RowState {
-  f32x4 acc[8];  // register i: head i, dim 8p+m (partial over this lane's token group)
-  float m[4];    // reference maxima (wave-uniform), log2 units
-  float l[4];    // sum of 2^(s - m) over this lane's tokens
+  f32x4 acc[NG][8];  // acc[g][m] register i: head 4g+i, dim 8p+m (partial over this lane's token group)
+  float m[4 * NG];   // reference maxima (wave-uniform), log2 units
+  float l[4 * NG];   // sum of 2^(s - m) over this lane's tokens
 };
 
 // K side of chunk [c0, c0+64): the packed K row and both norms of token c0+lane,
@@ -259,15 +269,20 @@ __device__ __forceinline__ void score_look(const uint32_t (&k)[NW], Tab<BWK>& cb
   lookup8<BWK, 8 * G * BWK>(k, cbk, kv);
 }
 
-// The 8 score MFMAs of dims [8g, 8g+8): A = q_rot[head][k] broadcast from block k%16.
-template <int G>
-__device__ __forceinline__ void score_mfma(const float (&qb)[8], const float (&kv)[8], f32x4& s0, f32x4& s1) {
+// The score MFMAs of dims [8g, 8g+8), eight per head group: A = q_rot[head][k]
+// broadcast from block k%16; every lookup feeds one MFMA per group.
+template <int G, int NG>
+__device__ __forceinline__ void score_mfma(const float (&qb)[NG][8], const float (&kv)[8], f32x4 (&s0)[NG],
+                                           f32x4 (&s1)[NG]) {
   static_for<0, 8>([&](auto jc) {
     constexpr int j = decltype(jc)::value, k = 8 * G + j;
-    if constexpr (j & 1)
-      s1 = __builtin_amdgcn_mfma_f32_4x4x1f32(qb[k >> 4], kv[j], s1, 4, k & 15, 0);
-    else
-      s0 = __builtin_amdgcn_mfma_f32_4x4x1f32(qb[k >> 4], kv[j], s0, 4, k & 15, 0);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if constexpr (j & 1)
+        s1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(qb[g][k >> 4], kv[j], s1[g], 4, k & 15, 0);
+      else
+        s0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(qb[g][k >> 4], kv[j], s0[g], 4, k & 15, 0);
+    }
   });
 }
 
@@ -277,11 +292,14 @@ __device__ __forceinline__ void value_look(const uint32_t (&v)[NW], Tab<BWV>& cb
   lookup8<BWV, 32 * VWords<BWV>::N * Q>(v, cbv, vv);
 }
 
-// The 8 value MFMAs of quad q: A = p*n_V broadcast inside each group of four blocks.
-__device__ __forceinline__ void value_mfma(float a_q, const float (&vv)[8], f32x4 (&acc)[8]) {
+// The value MFMAs of quad q, eight per head group: A = p*n_V broadcast inside each
+// group of four blocks.
+template <int NG>
+__device__ __forceinline__ void value_mfma(const float (&a_q)[NG], const float (&vv)[8], f32x4 (&acc)[NG][8]) {
   static_for<0, 8>([&](auto mc) {
     constexpr int mm = decltype(mc)::value;
-    acc[mm] = __builtin_amdgcn_mfma_f32_4x4x1f32(a_q, vv[mm], acc[mm], 2, 0, 0);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) acc[g][mm] = __builtin_amdgcn_mfma_f32_4x4x1f32(a_q[g], vv[mm], acc[g][mm], 2, 0, 0);
   });
 }
 
@@ -289,9 +307,12 @@ __device__ __forceinline__ void value_mfma(float a_q, const float (&vv)[8], f32x
 // lookups of group g+2 are issued before the MFMAs of group g, so every LDS read
 // has sixteen of this wave's MFMAs to land before its value is needed; the sched
 // barriers keep the compiler from sinking the reads next to their consumers.
-template <int BWK, int NW>
-__device__ __forceinline__ f32x4 score_phase(const uint32_t (&kc)[NW], Tab<BWK>& cbk, const float (&qb)[8]) {
-  f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+template <int BWK, int NG, int NW>
+__device__ __forceinline__ void score_phase(const uint32_t (&kc)[NW], Tab<BWK>& cbk, const float (&qb)[NG][8],
+                                            f32x4 (&out)[NG]) {
+  f32x4 s0[NG], s1[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) s0[g] = s1[g] = f32x4{0.f, 0.f, 0.f, 0.f};
   float kv[3][8];
   score_look<BWK, 0>(kc, cbk, kv[0]);
   score_look<BWK, 1>(kc, cbk, kv[1]);
@@ -302,10 +323,11 @@ __device__ __forceinline__ f32x4 score_phase(const uint32_t (&kc)[NW], Tab<BWK>&
       score_look<BWK, g + 2>(kc, cbk, kv[(g + 2) % 3]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    score_mfma<g>(qb, kv[g % 3], s0, s1);
+    score_mfma<g, NG>(qb, kv[g % 3], s0, s1);
     __builtin_amdgcn_sched_barrier(0);
   });
-  return s0 + s1;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) out[g] = s0[g] + s1[g];
 }
 
 // Lookups of the first two value quads, issued before the softmax so that they
@@ -320,50 +342,63 @@ __device__ __forceinline__ void value_prime(const uint32_t (&vc)[NW], Tab<BWV>& 
 // Values of a chunk; lookups of quad q+2 are issued before the MFMAs of quad q,
 // and the p * n_V operands of four quads are read from the tile two quads before
 // the first of them.
-template <int BWV, int NW>
-__device__ __forceinline__ void value_phase(const uint32_t (&vc)[NW], Tab<BWV>& cbv, const float4* arow,
-                                            f32x4 (&acc)[8], float (&vv)[3][8]) {
-  float4 ab[2];
-  ab[0] = arow[0];
+template <int BWV, int NG, int NW>
+__device__ __forceinline__ void value_phase(const uint32_t (&vc)[NW], Tab<BWV>& cbv, const float* pt, int lane,
+                                            f32x4 (&acc)[NG][8], float (&vv)[3][8]) {
+  const float4* arow[NG];
+  float4 ab[NG][2];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    arow[g] = tile_row(pt, g, lane);
+    ab[g][0] = arow[g][0];
+  }
   static_for<0, 16>([&](auto qc) {
     constexpr int q = decltype(qc)::value;
-    if constexpr ((q & 3) == 2 && q + 2 < 16) ab[((q >> 2) + 1) & 1] = arow[(q >> 2) + 1];
+    if constexpr ((q & 3) == 2 && q + 2 < 16) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) ab[g][((q >> 2) + 1) & 1] = arow[g][(q >> 2) + 1];
+    }
     if constexpr (q + 2 < 16) value_look<BWV, q + 2>(vc, cbv, vv[(q + 2) % 3]);
     __builtin_amdgcn_sched_barrier(0);
-    value_mfma(comp<q & 3>(ab[(q >> 2) & 1]), vv[q % 3], acc);
+    float aq[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) aq[g] = comp<q & 3>(ab[g][(q >> 2) & 1]);
+    value_mfma<NG>(aq, vv[q % 3], acc);
     __builtin_amdgcn_sched_barrier(0);
   });
 }
 
 // Online softmax of one chunk (lane = token) and the p * n_V transposition: on
-// return the tile holds p(head i, token c0+4q+G) * n_V at row 4i+G, column q, and
-// lane 16G+i finds its value-MFMA operands for quads 4j..4j+3 at float4 j of row
-// 4(lane%4) + lane/16 (tile_row).
-__device__ __forceinline__ void softmax_phase(f32x4 s, uint32_t nk_h, uint32_t nv_h, bool valid, int lane,
-                                              float* pt, RowState& st) {
+// return the tile holds p(head 4g+i, token c0+4q+G) * n_V at row 16g+4i+G, column q,
+// and lane 16G+i finds its value-MFMA operands of group g for quads 4j..4j+3 at
+// float4 j of row 16g + 4(lane%4) + lane/16 (tile_row).
+template <int NG>
+__device__ __forceinline__ void softmax_phase(const f32x4 (&s)[NG], uint32_t nk_h, uint32_t nv_h, bool valid,
+                                              int lane, float* pt, RowState<NG>& st) {
+  constexpr int H = 4 * NG;
   const float nk = half_lo(nk_h);
   const float nv = valid ? half_lo(nv_h) : 0.f;
-  float sv[4];
+  float sv[H];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sv[i] = valid ? s[i] * nk : -INFINITY;
+  for (int i = 0; i < H; ++i) sv[i] = valid ? s[i >> 2][i & 3] * nk : -INFINITY;
   bool move = st.m[0] == -INFINITY;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) move = move || __any(sv[i] > st.m[i] + kRescale);
+  for (int i = 0; i < H; ++i) move = move || __any(sv[i] > st.m[i] + kRescale);
   if (move) {  // wave-uniform
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < H; ++i) {
       // wave-uniform: kept in a scalar register, which frees a VGPR per head
       const float m_new = uniform(fmaxf(st.m[i], wave_max(sv[i])));
       const float alpha = __builtin_amdgcn_exp2f(st.m[i] - m_new);  // 0 on the first chunk
       st.m[i] = m_new;
       st.l[i] *= alpha;
 #pragma unroll
-      for (int mm = 0; mm < 8; ++mm) st.acc[mm][i] *= alpha;
+      for (int mm = 0; mm < 8; ++mm) st.acc[i >> 2][mm][i & 3] *= alpha;
     }
   }
-  float pv[4];
+  float pv[H];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < H; ++i) {
     const float p = __builtin_amdgcn_exp2f(sv[i] - st.m[i]);  // 0 for masked tokens
     st.l[i] += p;
     pv[i] = p * nv;
@@ -372,40 +407,40 @@ __device__ __forceinline__ void softmax_phase(f32x4 s, uint32_t nk_h, uint32_t n
   {
     const int G = lane & 3, q = lane >> 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pt[(i * 4 + G) * kPStride + q] = pv[i];
+    for (int i = 0; i < H; ++i) pt[(16 * (i >> 2) + (i & 3) * 4 + G) * kPStride + q] = pv[i];
   }
   wave_lds_sync();
 }
 
-__device__ __forceinline__ const float4* tile_row(const float* pt, int lane) {
-  return reinterpret_cast<const float4*>(pt + ((lane & 3) * 4 + (lane >> 4)) * kPStride);
-}
 
 
 // Folds the four token groups and the per-lane sums and writes the (acc, m, l)
 // partial of each query head h < n_rep to row prow * n_rep + h.
-__device__ __forceinline__ void write_partial(const DecodeArgs& a, RowState& st, int64_t prow, int lane) {
-  constexpr int D = 128;
+template <int NG>
+__device__ __forceinline__ void write_partial(const DecodeArgs& a, RowState<NG>& st, int64_t prow, int lane) {
+  constexpr int D = 128, H = 4 * NG;
 #pragma unroll
-  for (int mm = 0; mm < 8; ++mm)
+  for (int g = 0; g < NG; ++g)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float x = st.acc[mm][i];
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
-      st.acc[mm][i] = x;
-    }
+    for (int mm = 0; mm < 8; ++mm)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) st.l[i] = wave_sum(st.l[i]);
+      for (int i = 0; i < 4; ++i) {
+        float x = st.acc[g][mm][i];
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        st.acc[g][mm][i] = x;
+      }
+#pragma unroll
+  for (int i = 0; i < H; ++i) st.l[i] = wave_sum(st.l[i]);
   const int64_t row0 = prow * a.n_rep;
   if (lane < 16) {  // lane p: dims 8p..8p+7 of every head
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < H; ++i) {
       if (i < a.n_rep) {
+        const f32x4* ac = st.acc[i >> 2];
         float* dst = a.part_acc + (row0 + i) * D + 8 * lane;
-        *reinterpret_cast<float4*>(dst) = make_float4(st.acc[0][i], st.acc[1][i], st.acc[2][i], st.acc[3][i]);
-        *reinterpret_cast<float4*>(dst + 4) =
-            make_float4(st.acc[4][i], st.acc[5][i], st.acc[6][i], st.acc[7][i]);
+        *reinterpret_cast<float4*>(dst) = make_float4(ac[0][i & 3], ac[1][i & 3], ac[2][i & 3], ac[3][i & 3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(ac[4][i & 3], ac[5][i & 3], ac[6][i & 3], ac[7][i & 3]);
       }
     }
   }
@@ -413,7 +448,7 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, RowState& st,
   // turn the register arrays into an indexed stack object)
   if (lane == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < H; ++i) {
       if (i < a.n_rep) {
         a.part_ml[2 * (row0 + i)] = st.m[i];
         a.part_ml[2 * (row0 + i) + 1] = st.l[i];
@@ -426,19 +461,20 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, RowState& st,
 // multiple of 16) and writes one partial at row prow. Each chunk runs score,
 // softmax and values in turn; the packed codes of chunk c+1 load while chunk c
 // computes and page ids run two chunks ahead.
-template <int BWK, int BWV>
+template <int BWK, int BWV, int NG>
 __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, int t_lo, int t_hi, int64_t prow,
                                            int lane, Tab<BWK>& cbk, Tab<BWV>& cbv, float* ptile) {
   constexpr int D = 128;
   const int page_hi = (t_hi + (1 << a.log2S) - 1) >> a.log2S;
   const int n = (t_hi - t_lo + 63) >> 6;
 
-  // register m of lane 4j+i holds q_rot[head i][16m + j]
-  float qb[8];
-  {
-    const float* qp = a.q_rot + ((int64_t(b) * a.Hkv + kvh) * 4 + (lane & 3)) * D + (lane >> 2);
+  // register m of group g of lane 4j+i holds q_rot[head 4g+i][16m + j]
+  float qb[NG][8];
 #pragma unroll
-    for (int m = 0; m < 8; ++m) qb[m] = qp[16 * m];
+  for (int g = 0; g < NG; ++g) {
+    const float* qp = a.q_rot + ((int64_t(b) * a.Hkv + kvh) * (4 * NG) + 4 * g + (lane & 3)) * D + (lane >> 2);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) qb[g][m] = qp[16 * m];
   }
   const int32_t* trow = a.table + b * a.tsb;
   // page of this lane's token in chunk c (tokens past the range read its last page and are masked)
@@ -447,11 +483,13 @@ __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, 
     return trow[col];
   };
 
-  RowState st;
+  RowState<NG> st;
 #pragma unroll
-  for (int mm = 0; mm < 8; ++mm) st.acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < NG; ++g)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+    for (int mm = 0; mm < 8; ++mm) st.acc[g][mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4 * NG; ++i) {
     st.m[i] = -INFINITY;
     st.l[i] = 0.f;
   }
@@ -469,11 +507,12 @@ __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, 
     const bool more = c + 1 < n;
     if (more) load_k(a, kvh, lane, c0 + 64, pid_next, Z);
     float vv[3][8];
-    const f32x4 s = score_phase<BWK>(X.w, cbk, qb);
+    f32x4 s[NG];
+    score_phase<BWK, NG>(X.w, cbk, qb, s);
     value_prime<BWV>(Y.w, cbv, vv);
-    softmax_phase(s, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
+    softmax_phase<NG>(s, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
     if (more) load_v(a, kvh, lane, c0 + 64, pid_next, X);
-    value_phase<BWV>(Y.w, cbv, tile_row(ptile, lane), st.acc, vv);
+    value_phase<BWV, NG>(Y.w, cbv, ptile, lane, st.acc, vv);
     pid_next = pid_after;
   };
 
@@ -498,7 +537,7 @@ __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, 
 // LDS of a work-group of WPB waves: the codebook tables (a replicated pair table
 // first, at a 64 KB slot, so that its address registers need no base add), then
 // one p tile per wave.
-template <int BWK, int BWV, int WPB>
+template <int BWK, int BWV, int NG, int WPB>
 struct RowsLds {
   static constexpr int k_off = (BWK == 4 || BWV != 4) ? 0 : kPairTableBytes;
   static constexpr int v_off = BWV == 4 ? (BWK == 4 ? kPairTableBytes : 0) : (BWK == 4 ? kPairTableBytes
@@ -507,7 +546,7 @@ struct RowsLds {
   static constexpr int tiles = (BWK == 4 && BWV != 4) ? v_off + table_bytes<BWV>()
                                : (BWV == 4 && BWK != 4) ? k_off + table_bytes<BWK>()
                                                         : v_off + table_bytes<BWV>();
-  static constexpr int tile_bytes = 16 * kPStride * 4;
+  static constexpr int tile_bytes = NG * 16 * kPStride * 4;
   static constexpr int total = tiles + WPB * tile_bytes;
   static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
 };
@@ -529,9 +568,9 @@ __device__ __forceinline__ Tab<BW> make_tab(const char* lds, int off, int lane) 
 // 64-token chunks ordered (sequence, kv head, chunk); wave w takes chunks
 // [C w / W', C (w+1) / W') with C the total and W' = min(W, C), and writes one
 // partial per (sequence, kv head) it touches, at row w + b*Hkv + kvh.
-template <int BWK, int BWV, int WPB>
+template <int BWK, int BWV, int NG, int WPB>
 __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
-  using Lay = RowsLds<BWK, BWV, WPB>;
+  using Lay = RowsLds<BWK, BWV, NG, WPB>;
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -599,48 +638,55 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
       prow = w + int64_t(b) * a.Hkv + kvh;
       s += c_hi - c_lo;
     }
-    scan_range<BWK, BWV>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+    scan_range<BWK, BWV, NG>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
     if (!a.balanced || s >= e) break;
     if (kvh + 1 == a.Hkv && c_hi == nb) ++b;
   }
 }
 
 // Waves per work-group: three per SIMD where the scan fits in 168 VGPRs, else two.
-template <int BWK, int BWV>
-constexpr int rows_wpb() { return BWK <= 4 && BWV <= 4 ? 12 : 8; }
+template <int BWK, int BWV, int NG>
+constexpr int rows_wpb() { return NG == 1 && BWK <= 4 && BWV <= 4 ? 12 : 8; }
 
-template <int BWK, int BWV>
+template <int BWK, int BWV, int NG>
 SplitKernel rows_kernel() {
-  constexpr int wpb = rows_wpb<BWK, BWV>();
+  constexpr int wpb = rows_wpb<BWK, BWV, NG>();
   SplitKernel k;
-  k.fn = decode_rows_kernel<BWK, BWV, wpb>;
+  k.fn = decode_rows_kernel<BWK, BWV, NG, wpb>;
   k.block = 64 * wpb;
   k.wpb = wpb;
-  k.nrep = 4;
+  k.nrep = 4 * NG;
   k.log2_units = true;
   k.rows = true;
   return k;
 }
 
-}  // namespace
-
-SplitKernel pick_split_rows(int bw_k, int bw_v) {
+template <int NG>
+SplitKernel rows_for(int bw_k, int bw_v) {
   if (bw_k == bw_v) {
     switch (bw_k) {
-      case 2: return rows_kernel<2, 2>();
-      case 3: return rows_kernel<3, 3>();
-      case 4: return rows_kernel<4, 4>();
-      case 5: return rows_kernel<5, 5>();
-      case 6: return rows_kernel<6, 6>();
-      case 8: return rows_kernel<8, 8>();
+      case 2: return rows_kernel<2, 2, NG>();
+      case 3: return rows_kernel<3, 3, NG>();
+      case 4: return rows_kernel<4, 4, NG>();
+      case 5: return rows_kernel<5, 5, NG>();
+      case 6: return rows_kernel<6, 6, NG>();
+      case 8: return rows_kernel<8, 8, NG>();
     }
   } else if (bw_k == 4 && bw_v == 6) {
-    return rows_kernel<4, 6>();
+    return rows_kernel<4, 6, NG>();
   } else if (bw_k == 6 && bw_v == 4) {
-    return rows_kernel<6, 4>();
+    return rows_kernel<6, 4, NG>();
   } else if (bw_k == 4 && bw_v == 8) {
-    return rows_kernel<4, 8>();
+    return rows_kernel<4, 8, NG>();
   }
+  return SplitKernel{};
+}
+
+}  // namespace
+
+SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep) {
+  if (n_rep <= 4) return rows_for<1>(bw_k, bw_v);
+  if (n_rep <= 8) return rows_for<2>(bw_k, bw_v);
   return SplitKernel{};
 }
 

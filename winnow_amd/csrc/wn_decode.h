@@ -37,9 +37,10 @@ struct SplitKernel {
 };
 
 // Row-per-lane matrix-core page scan for head_dim 128, power-of-two page sizes
-// >= 16 and up to four query heads per kv head (wpb independent waves per
-// work-group sharing the codebook tables, fixed splits or balanced persistent
-// waves), or an empty SplitKernel when (bw_k, bw_v) is not compiled.
-SplitKernel pick_split_rows(int bw_k, int bw_v);
+// >= 16 and up to eight query heads per kv head, in one or two groups of four
+// (wpb independent waves per work-group sharing the codebook tables, fixed
+// splits or balanced persistent waves), or an empty SplitKernel when
+// (bw_k, bw_v, n_rep) is not compiled.
+SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep);
 
 }  // namespace wn
