@@ -79,3 +79,32 @@ def to_host(kv, seqs=None):
     return oa.OracleKV(kv.k_pages[dev_ids].cpu(), kv.k_norms[dev_ids].cpu(), kv.v_pages[dev_ids].cpu(),
                        kv.v_norms[dev_ids].cpu(), new_table,
                        torch.tensor([int(lens[b]) for b in seqs], dtype=torch.int32), kq, vq, kv.head_dim)
+
+
+def config1_inputs():
+    """B1, 8 q = 8 kv heads, D128, 1024 tokens, fp32 K/V/q ~N(0,1) from seed 0
+    (drawn K, then V, then q), 4-bit, 16-token pages in table order 0..63, quantizer seed 42 for
+    K and V (the reference's default, packed_backend.py:298-303)."""
+    g = torch.Generator().manual_seed(0)
+    k = torch.randn(1, 8, 1024, 128, generator=g)
+    v = torch.randn(1, 8, 1024, 128, generator=g)
+    q = torch.randn(1, 8, 1, 128, generator=g)
+    return q, k, v
+
+
+def config1_kv():
+    """The oracle's packed pages of config 1: contiguous table, K and V through oracle.append."""
+    from oracle import append as oapp
+    q, k, v = config1_inputs()
+    tq = oracle_quantizer(4, 128, 42)
+    P, S = 64, 16
+    kp = torch.zeros(P, 8, S, 64, dtype=torch.uint8)
+    vp = torch.zeros(P, 8, S, 64, dtype=torch.uint8)
+    kn = torch.zeros(P, 8, S, dtype=torch.float16)
+    vn = torch.zeros(P, 8, S, dtype=torch.float16)
+    table = torch.arange(P, dtype=torch.int32)[None]
+    oapp.append(k, tq, kp, kn, table, [0])
+    oapp.append(v, tq, vp, vn, table, [0])
+    quant = oa.OracleQuant.from_tq(tq)
+    kv = oa.OracleKV(kp, kn, vp, vn, table, torch.tensor([1024], dtype=torch.int32), quant, quant, 128)
+    return q, k, v, kv

@@ -1,0 +1,133 @@
+"""Golden fixtures of ``tests/golden`` (written by ``tests/golden/make_golden.py``).
+
+CPU: the oracle and the product's host-side quantizer construction reproduce the
+committed quantizer constants bit for bit, and the oracle reproduces BASELINE
+config 1 (page bytes and norms by SHA-256, outputs to 1e-6).
+
+GPU: the HIP append of config 1's inputs gives the oracle's page bytes (under
+the adjudication protocol of ``adjudicate.py``), and the HIP decode over those
+pages gives the committed output within the north star's 2e-3 abs / 1e-3 rel,
+and within 1e-5 relative L2 of the float64 operator.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from cases import config1_inputs, config1_kv
+from oracle.quantizer import get_quantizer as oracle_quantizer
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _sha(t: torch.Tensor) -> str:
+    return hashlib.sha256(t.contiguous().numpy().tobytes()).hexdigest()
+
+
+def _hex(t: torch.Tensor) -> list[str]:
+    return [f"{int(x) & 0xffffffff:08x}" for x in t.float().view(torch.int32).tolist()]
+
+
+@pytest.fixture(scope="module")
+def constants():
+    return json.loads((GOLDEN / "quantizer_constants.json").read_text())
+
+
+@pytest.fixture(scope="module")
+def c1():
+    with np.load(GOLDEN / "config1.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope="module")
+def oracle_c1():
+    threads = torch.get_num_threads()
+    torch.set_num_threads(1)            # the summation order the fixture was written with
+    try:
+        return config1_kv()
+    finally:
+        torch.set_num_threads(threads)
+
+
+@pytest.mark.parametrize("seed", [42, 43])
+def test_oracle_rotation_matches_fixture(constants, seed):
+    assert _sha(oracle_quantizer(4, 128, seed).Pi) == constants["pi_sha256"][str(seed)]
+
+
+@pytest.mark.parametrize("bw", [2, 3, 4, 5, 6, 8])
+def test_oracle_codebooks_match_fixture(constants, bw):
+    tq = oracle_quantizer(bw, 128, 42)
+    assert _hex(tq.centroids) == constants["codebooks"][str(bw)]["centroids"]
+    assert _hex(tq.boundaries) == constants["codebooks"][str(bw)]["boundaries"]
+
+
+@pytest.mark.parametrize("bw", [2, 4, 6, 8])
+def test_product_builds_the_same_constants(constants, bw):
+    """The product computes its constants on the host the same way (no GPU needed)."""
+    import math
+
+    from winnow_amd.quantizer import lloyd_max_gaussian, seeded_rotation
+    for seed in (42, 43):
+        assert _sha(seeded_rotation(128, seed)) == constants["pi_sha256"][str(seed)]
+    c, b = lloyd_max_gaussian(2 ** bw, sigma=1.0 / math.sqrt(128))
+    assert _hex(torch.tensor(c, dtype=torch.float32)) == constants["codebooks"][str(bw)]["centroids"]
+    assert _hex(torch.tensor(b[1:-1], dtype=torch.float32)) == constants["codebooks"][str(bw)]["boundaries"]
+
+
+def test_oracle_reproduces_config1(c1, oracle_c1):
+    from oracle import attention as oa
+    q, _, _, kv = oracle_c1
+    assert _sha(kv.k_pages) == str(c1["sha_k_pages"]) and _sha(kv.v_pages) == str(c1["sha_v_pages"])
+    assert _sha(kv.k_norms.view(torch.int16)) == str(c1["sha_k_norms"])
+    assert _sha(kv.v_norms.view(torch.int16)) == str(c1["sha_v_norms"])
+    assert np.array_equal(kv.k_pages[:4].numpy(), c1["k_pages_0_4"])
+    out = oa.tiled_compressed_attention(q, kv, oa.default_scale(128))
+    assert np.abs(out.numpy() - c1["out_tiled_f32"]).max() < 1e-6
+    rel = np.linalg.norm(c1["out_tiled_f32"] - c1["out_f64"]) / np.linalg.norm(c1["out_f64"])
+    assert rel < 1e-5
+
+
+@pytest.mark.gpu
+def test_hip_append_of_config1_matches_oracle_pages(oracle_c1):
+    from adjudicate import adjudicate_codes, adjudicate_fp16_norms
+    from oracle import packing as opk
+    from winnow_amd import packed_backend as pb
+    from winnow_amd.quantizer import get_quantizer
+    _, k, v, kv = oracle_c1
+    dev = "cuda"
+    tq = get_quantizer(4, 128, dev, 42)
+    kp = torch.zeros(64, 8, 16, 64, dtype=torch.uint8, device=dev)
+    vp = torch.zeros_like(kp)
+    kn = torch.zeros(64, 8, 16, dtype=torch.float16, device=dev)
+    vn = torch.zeros_like(kn)
+    table = torch.arange(64, dtype=torch.int32, device=dev)[None]
+    pb.append_kv(k.to(dev), v.to(dev), tq, tq, kp, vp, kn, vn, table, torch.zeros(1, dtype=torch.int32, device=dev))
+    otq = oracle_quantizer(4, 128, 42)
+    flips = 0
+    for src, got, want, gotn, wantn in ((k, kp, kv.k_pages, kn, kv.k_norms), (v, vp, kv.v_pages, vn, kv.v_norms)):
+        gc = torch.from_numpy(opk.unpack(got.cpu().numpy(), 4, 128))          # (64, 8, 16, 128)
+        wc = torch.from_numpy(opk.unpack(want.numpy(), 4, 128))
+        as_seq = lambda c: c.permute(1, 0, 2, 3).reshape(1, 8, 1024, 128)    # noqa: E731
+        flips += adjudicate_codes(src, as_seq(gc), as_seq(wc), otq)
+        n32 = src.float().norm(dim=-1).clamp(min=1e-10)
+        adjudicate_fp16_norms(n32, n32, gotn.cpu().permute(1, 0, 2).reshape(1, 8, 1024),
+                              wantn.permute(1, 0, 2).reshape(1, 8, 1024))
+    print(f"config 1 append: {flips} adjudicated code flips in {2 * 8 * 1024 * 128} codes")
+
+
+@pytest.mark.gpu
+def test_hip_decode_of_config1_matches_fixture(c1, oracle_c1):
+    from cases import to_device
+    from winnow_amd import packed_attention as pa
+    q, _, _, kv = oracle_c1
+    got = pa.packed_decode_attention(q.to("cuda"), to_device(kv, "cuda"), 1.0 / 128 ** 0.5,
+                                     out_dtype=torch.float32).cpu().numpy()
+    want = c1["out_tiled_f32"]
+    assert np.allclose(got, want, atol=2e-3, rtol=1e-3), np.abs(got - want).max()
+    f64 = c1["out_f64"]
+    assert np.linalg.norm(got - f64) / np.linalg.norm(f64) < 1e-5
