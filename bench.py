@@ -190,7 +190,7 @@ def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
             d = Path(tmp) / counter
             cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "run", "--",
                    sys.executable, str(ROOT / "bench.py"), "--config", str(cfg), "--steps", "3", "--warmup", "1",
-                   "--settle", "0", "--parity", "off", "--cpu-baseline", "off", "--traffic", "off",
+                   "--settle", "0", "--parity", "off", "--cpu-baseline", "off", "--traffic", "off", "--append", "off",
                    "--copy-peak", "on"]
             try:
                 subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
@@ -218,6 +218,84 @@ def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
                             "bytes_per_launch": statistics.fmean(scan) * 1024 * factor}
     out["bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
     return out
+
+
+def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
+    """The append path of ``PagedPackedCache.update`` (packed_backend.py:136-170): quantize,
+    pack and scatter ``n_new`` new tokens per sequence, K and V, at positions
+    L_b .. L_b + n_new - 1, timed separately from attention.
+
+    The new tokens go to one fresh page per sequence, addressed through the
+    sequence's page-table column L_b / S as in the cache; they land in a small
+    separate pool so the decode pool is left as it is. Timed with hipEvents over
+    ``reps`` back-to-back calls; checked against the CPU restatement (codes under
+    the adjudication protocol) and timed beside it.
+    """
+    import torch
+    sys.path.insert(0, str(ROOT / "tests"))
+    from adjudicate import adjudicate_codes
+    from oracle import append as oapp
+    from oracle import packing as opk
+    from oracle.quantizer import get_quantizer as oq
+    from winnow_amd import packed_backend as pb
+    from winnow_amd.packing import packed_bytes
+
+    B, Hkv, D, S = len(lens), c["Hkv"], c["D"], c["S"]
+    kq, vq = quants
+    nbk, nbv = packed_bytes(D, c["bwk"]), packed_bytes(D, c["bwv"])
+    g = torch.Generator().manual_seed(c["seed"] + 100)
+    k = torch.randn(B, Hkv, n_new, D, generator=g).bfloat16()
+    v = torch.randn(B, Hkv, n_new, D, generator=g).bfloat16()
+    start = torch.tensor(lens, dtype=torch.int32)
+    width = max((L + n_new + S - 1) // S for L in lens)
+    tab = torch.full((B, width), -1, dtype=torch.int32)
+    P = 0
+    for b, L in enumerate(lens):                 # fresh pages for the new tokens' columns
+        for col in range(L // S, (L + n_new + S - 1) // S):
+            tab[b, col] = P
+            P += 1
+    kp = torch.zeros(P, Hkv, S, nbk, dtype=torch.uint8, device=dev)
+    vp = torch.zeros(P, Hkv, S, nbv, dtype=torch.uint8, device=dev)
+    kn = torch.zeros(P, Hkv, S, dtype=torch.float16, device=dev)
+    vn = torch.zeros(P, Hkv, S, dtype=torch.float16, device=dev)
+    kd, vd, td, sd = k.to(dev), v.to(dev), tab.to(dev), start.to(dev)
+
+    def call():
+        pb.append_kv(kd, vd, kq, vq, kp, vp, kn, vn, td, sd)
+
+    for _ in range(20):
+        call()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / reps * 1e3
+
+    # CPU restatement on the same inputs, timed, then the byte check
+    ref = [torch.zeros(P, Hkv, S, nb, dtype=torch.uint8) for nb in (nbk, nbv)]
+    refn = [torch.zeros(P, Hkv, S, dtype=torch.float16) for _ in range(2)]
+    okq, ovq = oq(c["bwk"], D, 42), oq(c["bwv"], D, 42)
+    t0 = time.perf_counter()
+    oapp.append(k, okq, ref[0], refn[0], tab, lens)
+    oapp.append(v, ovq, ref[1], refn[1], tab, lens)
+    cpu_us = (time.perf_counter() - t0) * 1e6
+    flips = 0
+    for src, got, want, bw, tq in ((k, kp, ref[0], c["bwk"], okq), (v, vp, ref[1], c["bwv"], ovq)):
+        gc = torch.from_numpy(opk.unpack(got.cpu().numpy(), bw, D))
+        wc = torch.from_numpy(opk.unpack(want.numpy(), bw, D))
+        pos = torch.tensor([[L + i for i in range(n_new)] for L in lens])
+        pids = torch.gather(tab.long(), 1, pos // S)
+        sel = lambda t: t[pids, :, pos % S].permute(0, 2, 1, 3)      # noqa: E731
+        flips += adjudicate_codes(src, sel(gc), sel(wc), tq)
+    vectors = 2 * B * Hkv * n_new
+    return {"us_per_call": us, "vectors_per_call": vectors, "vectors_per_s": vectors / (us * 1e-6),
+            "new_tokens_per_seq": n_new, "bytes_read": 2 * B * Hkv * n_new * D * 2,
+            "bytes_written": B * Hkv * n_new * (nbk + 2 + nbv + 2),
+            "cpu_us_per_call": cpu_us, "cpu_kind": "port", "adjudicated_code_flips": flips,
+            "codes_checked": vectors * D}
 
 
 def parity(c, lens, q, kv, quants, sample):
@@ -310,6 +388,8 @@ def main(argv=None):
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--parity", choices=["on", "off"], default="on")
     ap.add_argument("--copy-peak", choices=["on", "off"], default="on")
+    ap.add_argument("--append", choices=["on", "off"], default="on",
+                    help="time the quantize+pack append of 16 new tokens per sequence (BASELINE config 3)")
     ap.add_argument("--traffic", choices=["on", "off"], default="on",
                     help="measure HBM bytes per scan launch with two rocprofv3 --pmc child runs")
     ap.add_argument("--settle", type=float, default=0.5,
@@ -380,6 +460,9 @@ def main(argv=None):
     if cp:
         log(f"copy peak: {cp}")
 
+    app = append_bench(c, lens, kvs[0].page_table_host, quants, dev) if args.append == "on" else None
+    if app:
+        log(f"append: {app}")
     traffic = hbm_traffic(args.config, scan_kernel_name(c)) if args.traffic == "on" else None
     if traffic:
         log(f"traffic: {traffic}")
@@ -422,6 +505,7 @@ def main(argv=None):
                      "copy_peak_GBps": cp["GBps"] if cp else None,
                      "frac_of_copy_peak": achieved / cp["GBps"] if cp else None},
         "cpu_baseline": cpu,
+        "append": app,
         "parity": par,
     }
     print(json.dumps(result), flush=True)

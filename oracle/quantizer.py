@@ -56,10 +56,19 @@ def lloyd_max_gaussian(levels: int, sigma: float = 1.0, iters: int = 200, tol: f
 
 
 def rotation(head_dim: int, seed: int) -> torch.Tensor:
-    """Seeded random orthogonal matrix (cache.py:92-97): Q of QR(randn) times sign(diag R)."""
+    """Seeded random orthogonal matrix (cache.py:92-97): Q of QR(randn) times sign(diag R).
+
+    The QR runs on one thread: its fp32 rounding depends on the thread count, and
+    one thread gives the same bits on every host of this image.
+    """
     gen = torch.Generator(device="cpu").manual_seed(seed)
     G = torch.randn(head_dim, head_dim, generator=gen, dtype=torch.float32)
-    Q, R = torch.linalg.qr(G)
+    threads = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        Q, R = torch.linalg.qr(G)
+    finally:
+        torch.set_num_threads(threads)
     ds = torch.sign(torch.diag(R))
     ds[ds == 0] = 1.0
     return (Q * ds.unsqueeze(0)).contiguous()

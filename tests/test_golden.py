@@ -6,8 +6,10 @@ config 1 (page bytes and norms by SHA-256, outputs to 1e-6).
 
 GPU: the HIP append of config 1's inputs gives the oracle's page bytes (under
 the adjudication protocol of ``adjudicate.py``), and the HIP decode over those
-pages gives the committed output within the north star's 2e-3 abs / 1e-3 rel,
-and within 1e-5 relative L2 of the float64 operator.
+pages gives the committed output within the north star's 2e-3 abs / 1e-3 rel.
+The oracle's CPU GEMM may round a near-tie code differently on another host, so
+the pages the GPU test decodes can differ from the fixture's in a few codes: the
+float64 comparison on identical pages is ``test_gpu_decode.test_config1_plumbing``.
 """
 from __future__ import annotations
 
@@ -129,5 +131,3 @@ def test_hip_decode_of_config1_matches_fixture(c1, oracle_c1):
                                      out_dtype=torch.float32).cpu().numpy()
     want = c1["out_tiled_f32"]
     assert np.allclose(got, want, atol=2e-3, rtol=1e-3), np.abs(got - want).max()
-    f64 = c1["out_f64"]
-    assert np.linalg.norm(got - f64) / np.linalg.norm(f64) < 1e-5

@@ -3,19 +3,19 @@
 //
 // quantize (turboquant_kv/cache.py:108-115):
 //   n = max(||x||_2, 1e-10);  y = (x / n) Pi^T;  code = #{boundaries < y}
-// Each vector is handled by one wave. The squared norm and the rotation are
+// Each wave handles four vectors at once. The squared norm and the rotation are
 // accumulated in float64 from exact fp32 inputs and rounded once to fp32, and
 // x / n is the correctly rounded fp32 quotient, so every code is the bucket of
 // the correctly rounded fp32 y; an fp32 GEMM elsewhere can differ from it only
-// when its own rounding error crosses a boundary. Pi^T is staged in LDS with
-// a padded row stride so the 64 lanes of a wave read 64 distinct banks.
+// when its own rounding error crosses a boundary.
 #include "wn_common.h"
 
 namespace wn {
 namespace {
 
-constexpr int kQBlock = 256;  // 4 waves
-constexpr int kVecPerBlock = 64;
+constexpr int kQBlock = 256;                // 4 waves
+constexpr int kVW = 4;                      // vectors a wave quantizes together
+constexpr int kVecPerBlock = 4 * kVW;       // 16 per work-group
 
 struct QuantSide {
   const void* x;
@@ -60,55 +60,101 @@ __device__ __forceinline__ uint8_t packed_byte(const uint8_t* codes, int k, int 
   return uint8_t(v & 0xffu);
 }
 
+// Each wave quantizes kVW vectors together (lane j forms output dims j, j+64 of all
+// of them: 2*kVW independent float64 accumulation chains), so the 128-term dot
+// products overlap instead of running one after another; sixteen vectors per
+// work-group keep even a 4096-vector append spread over the whole GPU. Pi is
+// staged in LDS in 16-byte rows of stride D+4 floats: the 16 lanes a 16-byte LDS
+// read serves hit distinct banks.
 template <int D>
 __global__ __launch_bounds__(kQBlock) void quantize_kernel(QuantArgs a) {
-  constexpr int LD = D + 1;  // padded row stride of Pi in LDS
-  constexpr int KPL = D / 64;  // outputs per lane
-  __shared__ float pis[D * LD];
+  constexpr int LD = D + 4;
+  constexpr int KPL = D / 64;  // output dims per lane
+  __shared__ __align__(16) float pis[D * LD];
   __shared__ float bnd[255];
-  __shared__ float xs[4][D];
-  __shared__ uint8_t cs[4][D];
+  __shared__ __align__(16) double xs[4][kVW][D];
+  __shared__ uint8_t cs[4][kVW][D];
 
   const QuantSide& sd = a.side[blockIdx.y];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int nb = (1 << sd.bw) - 1;
   const int64_t v0 = int64_t(blockIdx.x) * kVecPerBlock;
   if (v0 >= a.total) return;
-  for (int i = tid; i < D * D; i += kQBlock) pis[(i / D) * LD + (i % D)] = sd.pi[i];
+  for (int i = tid; i < D * D / 4; i += kQBlock) {
+    const float4 pv = reinterpret_cast<const float4*>(sd.pi)[i];
+    *reinterpret_cast<float4*>(pis + (4 * i / D) * LD + (4 * i) % D) = pv;
+  }
   for (int i = tid; i < nb; i += kQBlock) bnd[i] = sd.bnd[i];
   __syncthreads();
 
-  const int64_t v1 = min(v0 + kVecPerBlock, a.total);
+  const int64_t vw = v0 + int64_t(w) * kVW;  // this wave's first vector
+  float nrm[kVW];
+#pragma unroll
+  for (int t = 0; t < kVW; ++t) {
+    const int64_t v = vw + t;
+    nrm[t] = 1e-10f;
+    if (v < a.total) {  // wave-uniform
+      const int i = int(v % a.n);
+      const int h = int((v / a.n) % a.H);
+      const int b = int(v / (int64_t(a.n) * a.H));
+      const int64_t xo = b * sd.sb + h * sd.sh + i * sd.sn;
+      float xv[KPL];
+      double ss = 0.0;
+#pragma unroll
+      for (int k = 0; k < KPL; ++k) {
+        xv[k] = load_elem(sd.x, xo + lane + 64 * k, a.x_dtype);
+        ss = fma(double(xv[k]), double(xv[k]), ss);
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      nrm[t] = fmaxf(float(sqrt(ss)), 1e-10f);
+#pragma unroll
+      for (int k = 0; k < KPL; ++k) xs[w][t][lane + 64 * k] = double(float(double(xv[k]) / double(nrm[t])));
+    } else {
+#pragma unroll
+      for (int k = 0; k < KPL; ++k) xs[w][t][lane + 64 * k] = 0.0;
+    }
+  }
+  wave_lds_sync();
+  // y[t][k] = sum_d (x_t / n_t)[d] * Pi[lane + 64k][d], exact products, float64 sums
+  double y[kVW][KPL];
+#pragma unroll
+  for (int t = 0; t < kVW; ++t)
+#pragma unroll
+    for (int k = 0; k < KPL; ++k) y[t][k] = 0.0;
+#pragma unroll 2
+  for (int d = 0; d < D; d += 4) {
+    float4 pr[KPL];
+#pragma unroll
+    for (int k = 0; k < KPL; ++k) pr[k] = *reinterpret_cast<const float4*>(pis + (lane + 64 * k) * LD + d);
+#pragma unroll
+    for (int t = 0; t < kVW; ++t) {
+      const double2 xa = *reinterpret_cast<const double2*>(&xs[w][t][d]);
+      const double2 xb = *reinterpret_cast<const double2*>(&xs[w][t][d + 2]);
+#pragma unroll
+      for (int k = 0; k < KPL; ++k) {
+        y[t][k] = fma(xa.x, double(pr[k].x), y[t][k]);
+        y[t][k] = fma(xa.y, double(pr[k].y), y[t][k]);
+        y[t][k] = fma(xb.x, double(pr[k].z), y[t][k]);
+        y[t][k] = fma(xb.y, double(pr[k].w), y[t][k]);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kVW; ++t)
+#pragma unroll
+    for (int k = 0; k < KPL; ++k) cs[w][t][lane + 64 * k] = uint8_t(bucketize(bnd, sd.bw, float(y[t][k])));
+  wave_lds_sync();
+
   const int S = 1 << a.log2S;
   const int NB = D * sd.bw / 8;
-  for (int64_t v = v0 + w; v < v1; v += 4) {
+#pragma unroll
+  for (int t = 0; t < kVW; ++t) {
+    const int64_t v = vw + t;
+    if (v >= a.total) break;  // wave-uniform
     const int i = int(v % a.n);
     const int h = int((v / a.n) % a.H);
     const int b = int(v / (int64_t(a.n) * a.H));
-    const int64_t xo = b * sd.sb + h * sd.sh + i * sd.sn;
-    float xv[KPL];
-    double ss = 0.0;
-#pragma unroll
-    for (int k = 0; k < KPL; ++k) {
-      xv[k] = load_elem(sd.x, xo + lane + 64 * k, a.x_dtype);
-      ss = fma(double(xv[k]), double(xv[k]), ss);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    const float nrm = fmaxf(float(sqrt(ss)), 1e-10f);
-#pragma unroll
-    for (int k = 0; k < KPL; ++k) xs[w][lane + 64 * k] = float(double(xv[k]) / double(nrm));
-    wave_lds_sync();
-#pragma unroll
-    for (int k = 0; k < KPL; ++k) {
-      const int j = lane + 64 * k;
-      const float* prow = pis + j * LD;
-      double y = 0.0;
-#pragma unroll 8
-      for (int d = 0; d < D; ++d) y = fma(double(xs[w][d]), double(prow[d]), y);
-      cs[w][j] = uint8_t(bucketize(bnd, sd.bw, float(y)));
-    }
-    wave_lds_sync();
     if (a.scatter) {
       const int pos = a.start_pos[b] + i;
       const int col = pos >> a.log2S;
@@ -116,15 +162,14 @@ __global__ __launch_bounds__(kQBlock) void quantize_kernel(QuantArgs a) {
       if (pid >= 0 && pid < a.num_pages) {
         const int slot = pos & (S - 1);
         uint8_t* row = sd.pages + pid * sd.psp + h * sd.psh + int64_t(slot) * NB;
-        for (int k = lane; k < NB; k += 64) row[k] = packed_byte(cs[w], k, sd.bw, D);
-        if (lane == 0) sd.norms[pid * sd.nsp + h * sd.nsh + slot] = f32_to_f16(nrm);
+        for (int k = lane; k < NB; k += 64) row[k] = packed_byte(cs[w][t], k, sd.bw, D);
+        if (lane == 0) sd.norms[pid * sd.nsp + h * sd.nsh + slot] = f32_to_f16(nrm[t]);
       }
     } else {
 #pragma unroll
-      for (int k = 0; k < KPL; ++k) sd.codes_out[v * D + lane + 64 * k] = cs[w][lane + 64 * k];
-      if (lane == 0) sd.norms_out[v] = nrm;
+      for (int k = 0; k < KPL; ++k) sd.codes_out[v * D + lane + 64 * k] = cs[w][t][lane + 64 * k];
+      if (lane == 0) sd.norms_out[v] = nrm[t];
     }
-    wave_lds_sync();  // xs / cs are rewritten by this wave's next vector
   }
 }
 

@@ -44,10 +44,20 @@ def lloyd_max_gaussian(levels: int, sigma: float = 1.0, iters: int = 200, tol: f
 
 def seeded_rotation(head_dim: int, seed: int) -> torch.Tensor:
     """Q of the QR factorisation of a seeded Gaussian matrix, columns signed so R has a
-    positive diagonal (cache.py:92-97). Built on the host, fp32."""
+    positive diagonal (cache.py:92-97). Built on the host, fp32.
+
+    The fp32 QR's rounding depends on how many threads LAPACK splits it over, so it
+    runs on one thread: the bits of Pi (and so every code) are then the same on
+    every host of this image, whatever its core count.
+    """
     gen = torch.Generator(device="cpu").manual_seed(seed)
     g = torch.randn(head_dim, head_dim, generator=gen, dtype=torch.float32)
-    q, r = torch.linalg.qr(g)
+    threads = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        q, r = torch.linalg.qr(g)
+    finally:
+        torch.set_num_threads(threads)
     signs = torch.sign(torch.diag(r))
     signs[signs == 0] = 1.0
     return (q * signs.unsqueeze(0)).contiguous()
