@@ -83,6 +83,7 @@ struct RotArgs {
   float* q_rot;
   const int32_t* seq_lens;
   int32_t* chunk_prefix;  // written by block (0, 0, 0) when not null
+  int2* unit_meta;        // (B*Hkv) cleared to (0, 0): the scan fills in the groups that have keys
   float scale;
   int B, Hkv, n_rep, q_dtype;
 };
@@ -123,6 +124,7 @@ __global__ __launch_bounds__(256) void rotate_q_kernel(RotArgs a) {
   __shared__ float qs[NREP][D];
   const int kvh = blockIdx.x, b = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
   if (a.chunk_prefix && kvh == 0 && b == 0 && z == 0) chunk_prefix_block(a.seq_lens, a.B, a.chunk_prefix);
+  if (z == 0 && tid == 0) a.unit_meta[b * a.Hkv + kvh] = make_int2(0, 0);
   const float4* src = reinterpret_cast<const float4*>(a.pi_k + z * JQ * D);
   for (int i = tid; i < JQ * D / 4; i += 256) {
     const float4 v = src[i];
@@ -175,6 +177,9 @@ __global__ __launch_bounds__(kBlock) void decode_split_kernel(DecodeArgs a) {
   const int t_lo = page_lo << a.log2S;
   const int t_hi = min(page_hi << a.log2S, L);
 
+  if (split == 0 && tid == 0)
+    a.unit_meta[b * a.Hkv + kvh] =
+        make_int2((b * a.Hkv + kvh) * a.num_splits, (n_pages + a.pages_per_split - 1) / a.pages_per_split);
   for (int i = tid; i < LK; i += kBlock) cbk[i] = a.cb_k[i];
   for (int i = tid; i < LV; i += kBlock) cbv[i] = a.cb_v[i];
   __syncthreads();
@@ -316,10 +321,9 @@ struct MergeArgs {
   const float* part_acc;
   const float* part_ml;
   const float* pi_v;
-  const int32_t* seq_lens;
-  const int32_t* chunk_prefix;
+  const int2* unit_meta;
   void* out;
-  int out_dtype, B, Hq, Hkv, n_rep, log2S, pages_per_split, num_splits, balanced;
+  int out_dtype, Hq, Hkv, n_rep;
   int log2_units;  // partial maxima are in log2 units (weights 2^(m - M))
 };
 
@@ -335,9 +339,10 @@ constexpr int kMergeBatch = 32;  // partials whose loads are in flight together
 // a single max-stable pass with the loads of 32 partials in flight together (a
 // balanced plan has about num_splits / (B*Hkv) partials per group), and finally
 // forms output dim d from its Pi_V column and the merged row in LDS.
-// The partials of the group are rows r0 + s, s < n: fixed splits give
-// r0 = (b*Hkv + kvh)*num_splits and n = splits holding tokens; the balanced scan
-// gives rows w + b*Hkv + kvh for the waves w that touched the group.
+// The partials of the group are rows r0 + s, s < n, with (r0, n) left by the scan
+// in unit_meta (fixed splits: r0 = (b*Hkv + kvh)*num_splits and n the splits
+// holding tokens; balanced: rows w + b*Hkv + kvh of the waves w that touched the
+// group); a group without keys has n = 0 and an output row of zeros.
 template <int D>
 __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
   __shared__ float av[D];
@@ -345,42 +350,28 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
   float pc[D];  // column d of Pi_V
 #pragma unroll
   for (int k = 0; k < D; ++k) pc[k] = a.pi_v[k * D + d];
-
-  int64_t r0 = 0;
-  int n = 0;
-  const int L = a.seq_lens[b];
-  if (!a.balanced) {
-    const int S = 1 << a.log2S;
-    const int n_pages = (L + S - 1) >> a.log2S;
-    n = (n_pages + a.pages_per_split - 1) / a.pages_per_split;
-    r0 = (int64_t(b) * a.Hkv + kvh) * a.num_splits;
-  } else {
-    const int32_t* pre = a.chunk_prefix;
-    const int nb = pre[b + 1] - pre[b];
-    if (nb > 0) {
-      const int64_t C = int64_t(a.Hkv) * pre[a.B];
-      const int64_t Wp = min(int64_t(a.num_splits), C);
-      const int64_t U0 = int64_t(a.Hkv) * pre[b] + int64_t(kvh) * nb, U1 = U0 + nb;
-      const int64_t wf = ((U0 + 1) * Wp + C - 1) / C - 1;  // last wave starting at or before U0
-      const int64_t wl = (U1 * Wp + C - 1) / C - 1;        // last wave starting before U1
-      r0 = wf + int64_t(b) * a.Hkv + kvh;
-      n = int(wl - wf + 1);
-    }
-  }
+  const int2 meta = a.unit_meta[b * a.Hkv + kvh];
+  const int64_t r0 = meta.x;
+  const int n = meta.y;
   auto wexp = [&](float x) { return a.log2_units ? __builtin_amdgcn_exp2f(x) : expf(x); };
   const float* ml = a.part_ml + 2 * (r0 * a.n_rep + h);
   const float* acc = a.part_acc + (r0 * a.n_rep + h) * D + d;
   const int64_t pstride = a.n_rep;  // partial rows between consecutive partials of a head
   float M = -INFINITY, num = 0.f, den = 0.f;
   for (int s0 = 0; s0 < n; s0 += kMergeBatch) {
+    // every load is issued, clamped to the last partial, and the extras masked after:
+    // guarded loads would become one branch and one round trip per partial
     float mv[kMergeBatch], lv[kMergeBatch], xv[kMergeBatch];
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k) {
-      const bool ok = s0 + k < n;
-      const int64_t r = int64_t(s0 + k) * pstride;
-      mv[k] = ok ? ml[2 * r] : -INFINITY;
-      lv[k] = ok ? ml[2 * r + 1] : 0.f;
-      xv[k] = ok ? acc[r * D] : 0.f;
+      const int64_t r = int64_t(min(s0 + k, n - 1)) * pstride;
+      mv[k] = ml[2 * r];
+      lv[k] = ml[2 * r + 1];
+      xv[k] = acc[r * D];
+    }
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      if (s0 + k >= n) mv[k] = -INFINITY;
     }
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k) {
@@ -393,7 +384,7 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
       M = Mn;
     }
   }
-  av[d] = (L > 0 && den > 0.f) ? num / fmaxf(den, 1e-30f) : 0.f;
+  av[d] = (n > 0 && den > 0.f) ? num / fmaxf(den, 1e-30f) : 0.f;
   __syncthreads();
   // out_j = sum_k a_k Pi_V[k, j]; (a / l) Pi_V == (a Pi_V) / l up to rounding
   float o = 0.f;
@@ -504,7 +495,7 @@ int resident_waves(const SplitKernel& sk) {
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 struct WsLayout {
-  int64_t qrot, prefix, acc, ml, total;
+  int64_t qrot, prefix, meta, acc, ml, total;
 };
 
 // Scratch: q_rot (B, Hkv, max(NREP, 4), D) fp32, chunk prefix (B+1) int32, and
@@ -516,7 +507,8 @@ WsLayout ws_layout(int B, int Hq, int Hkv, int D, int pages_per_split, int num_s
   const int64_t rows = pages_per_split > 0 ? int64_t(B) * Hkv * num_splits : int64_t(num_splits) + int64_t(B) * Hkv;
   l.qrot = 0;
   l.prefix = align256(int64_t(B) * Hkv * nrp * D * 4);
-  l.acc = l.prefix + align256(int64_t(B + 1) * 4);
+  l.meta = l.prefix + align256(int64_t(B + 1) * 4);
+  l.acc = l.meta + align256(int64_t(B) * Hkv * 8);
   l.ml = l.acc + align256(rows * n_rep * D * 4);
   l.total = l.ml + align256(rows * n_rep * 2 * 4);
   return l;
@@ -630,7 +622,8 @@ extern "C" int wn_decode_attention(
 
   // the matrix-core scan keeps scores in log2 units: fold log2(e) into q_rot
   const float q_scale = sk.log2_units ? float(double(scale) * 1.4426950408889634) : scale;
-  RotArgs ra{q, q_stride_b, q_stride_h, pi_k, reinterpret_cast<float*>(ws + lay.qrot), seq_lens, prefix,
+  int2* meta = reinterpret_cast<int2*>(ws + lay.meta);
+  RotArgs ra{q, q_stride_b, q_stride_h, pi_k, reinterpret_cast<float*>(ws + lay.qrot), seq_lens, prefix, meta,
              q_scale, B, Hkv, n_rep, q_dtype};
   hipLaunchKernelGGL(rot, dim3(Hkv, B, 4), dim3(256), 0, st, ra);
 
@@ -656,6 +649,7 @@ extern "C" int wn_decode_attention(
   da.vnh = vn_stride_h;
   da.tsb = table_stride_b;
   da.chunk_prefix = prefix;
+  da.unit_meta = meta;
   da.B = B;
   da.Hkv = Hkv;
   da.n_rep = n_rep;
@@ -670,8 +664,7 @@ extern "C" int wn_decode_attention(
   hipLaunchKernelGGL(sk.fn, grid, dim3(sk.block), 0, st, da);
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
-  MergeArgs ma{da.part_acc, da.part_ml, pi_v, seq_lens, prefix, out, out_dtype, B, Hq, Hkv, n_rep, da.log2S,
-               pages_per_split, num_splits, da.balanced, sk.log2_units ? 1 : 0};
+  MergeArgs ma{da.part_acc, da.part_ml, pi_v, meta, out, out_dtype, Hq, Hkv, n_rep, sk.log2_units ? 1 : 0};
   if (D == 128)
     hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep, Hkv, B), dim3(128), 0, st, ma);
   else

@@ -601,6 +601,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
     t_lo = page_lo << a.log2S;
     t_hi = min(page_hi << a.log2S, L);
     prow = (int64_t(b) * a.Hkv + kvh) * a.num_splits + split;
+    if (split == 0 && lane == 0)  // the merge reads the group's partial rows from here
+      a.unit_meta[b * a.Hkv + kvh] = make_int2(int(prow), (n_pages + a.pages_per_split - 1) / a.pages_per_split);
   } else {
     const int64_t C = int64_t(a.Hkv) * pre[a.B];
     const int64_t Wp = min(int64_t(a.num_splits), C);
@@ -636,6 +638,15 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
       t_lo = 64 * c_lo;
       t_hi = min(64 * c_hi, a.seq_lens[b]);
       prow = w + int64_t(b) * a.Hkv + kvh;
+      if (c_lo == 0 && lane == 0) {
+        // the group's first wave: its partials are rows prow .. prow + n - 1, one per
+        // wave up to the last wave starting before the group's end U1
+        const int64_t C = int64_t(a.Hkv) * pre[a.B];
+        const int64_t Wp = min(int64_t(a.num_splits), C);
+        const int64_t U1 = base + int64_t(kvh + 1) * nb;
+        const int64_t wl = (U1 * Wp + C - 1) / C - 1;
+        a.unit_meta[b * a.Hkv + kvh] = make_int2(int(prow), int(wl - w + 1));
+      }
       s += c_hi - c_lo;
     }
     scan_range<BWK, BWV, NG>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);

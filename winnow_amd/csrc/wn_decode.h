@@ -21,6 +21,7 @@ struct DecodeArgs {
   int64_t knp, knh, vnp, vnh;  // norm strides, elements
   int64_t tsb;                 // page-table row stride, elements
   const int32_t* chunk_prefix;  // (B+1) running count of 64-token chunks per sequence (balanced)
+  int2* unit_meta;              // (B*Hkv): first partial row and partial count of each (sequence, kv head)
   int B, Hkv, n_rep, log2S, pages_per_split, num_splits;
   int balanced;  // 1: persistent waves share the flattened chunk space (pages_per_split unused)
 };
