@@ -63,7 +63,7 @@ const char* wn_last_error(void);
  * reference's num_splits, packed_attention_triton.py:211-216): *pages_per_split
  * = cdiv(max_pages, splits), one partial per (sequence, kv head, split).
  * requested_splits == 0 lets the library choose. Where the row-per-lane
- * matrix-core scan applies (head_dim 128, <= 4 query heads per kv head, page
+ * matrix-core scan applies (head_dim 128, <= 8 query heads per kv head, page
  * size >= 16) the plan is balanced: *pages_per_split = 0 and *num_splits = the
  * number of resident waves on the current device, which then share the
  * flattened (sequence, kv head, 64-token chunk) space equally, ragged batches
@@ -72,7 +72,8 @@ int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int
                    int requested_splits, int* pages_per_split, int* num_splits);
 
 /* Bytes of scratch wn_decode_attention needs for this shape and plan: the
- * rotated query, a per-sequence chunk prefix, and the (acc, m, l) partials of
+ * rotated query, a per-sequence chunk prefix, each (sequence, kv head)'s
+ * partial range (two int32), and the (acc, m, l) partials of
  * the real query heads (B*Hkv*num_splits rows for fixed splits, num_splits +
  * B*Hkv rows for a balanced plan). -1 for invalid sizes. */
 int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int pages_per_split, int num_splits);

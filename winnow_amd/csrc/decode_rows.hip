@@ -2,8 +2,9 @@
 // power-of-two page size >= 16, up to eight query heads per kv head in one or two
 // groups of four), gfx950.
 //
-// One wave per work-group, independent of every other wave. With fixed splits a
-// wave owns a range of pages of one (sequence, kv head); with a balanced plan
+// Waves are independent of each other; the waves of a work-group only share the
+// codebook tables staged in LDS. With fixed splits a wave owns a range of pages of
+// one (sequence, kv head); with a balanced plan
 // the resident waves split the flattened (sequence, kv head, chunk) space into
 // equal shares. Either way a wave walks its tokens in 64-token chunks.
 //
@@ -28,7 +29,8 @@
 // are looked up two at a time in a byte-indexed table of (c[lo nibble], c[hi nibble])
 // pairs that is replicated once per lane of a half-wave, so that the 32 lanes LDS
 // serves together always read 32 distinct bank pairs: a lookup never waits on a
-// bank conflict, whatever the codes. Twelve waves per work-group share the tables.
+// bank conflict, whatever the codes. Twelve waves per work-group (eight with two
+// head groups or wider codes) share the tables.
 // Page ids run two chunks ahead and the packed rows of chunk c+1 load while chunk c
 // computes.
 // Algebra: turboquant_kv/packed_attention.py:260-334 (the schedule of the
