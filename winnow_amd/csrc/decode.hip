@@ -327,7 +327,7 @@ struct MergeArgs {
   int log2_units;  // partial maxima are in log2 units (weights 2^(m - M))
 };
 
-constexpr int kMergeBatch = 32;  // partials whose loads are in flight together
+constexpr int kMergeBatch = 32;  // partial rows whose loads are in flight together
 
 // out[b, kvh*n_rep + h, :] = (sum_s w_s acc_s / sum_s w_s l_s) Pi_V with
 // w_s = exp(m_s - max m) (2^(m_s - max m) for log2-unit partials), zero when no
@@ -335,10 +335,12 @@ constexpr int kMergeBatch = 32;  // partials whose loads are in flight together
 //
 // One work-group of D threads per (query head h, kv head, sequence). Thread d
 // first issues the loads of column d of Pi_V, so that they travel together with
-// the partials' (one round trip for both), then merges dim d over the partials in
-// a single max-stable pass with the loads of 32 partials in flight together (a
-// balanced plan has about num_splits / (B*Hkv) partials per group), and finally
-// forms output dim d from its Pi_V column and the merged row in LDS.
+// the partials' (one round trip for both). The partials are taken 64 at a time:
+// lane k of each wave loads (m, l) of partial k, the wave reduces the maximum,
+// and lane k forms the weight of partial k with one exponential; thread d then
+// sums its dim of the acc rows against those weights (read from the lanes that
+// hold them), 32 rows' loads in flight together. Output dim d is finally formed
+// from the Pi_V column and the merged row in LDS.
 // The partials of the group are rows r0 + s, s < n, with (r0, n) left by the scan
 // in unit_meta (fixed splits: r0 = (b*Hkv + kvh)*num_splits and n the splits
 // holding tokens; balanced: rows w + b*Hkv + kvh of the waves w that touched the
@@ -347,6 +349,7 @@ template <int D>
 __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
   __shared__ float av[D];
   const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
+  const int lane = d & 63;
   float pc[D];  // column d of Pi_V
 #pragma unroll
   for (int k = 0; k < D; ++k) pc[k] = a.pi_v[k * D + d];
@@ -354,34 +357,36 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
   const int64_t r0 = meta.x;
   const int n = meta.y;
   auto wexp = [&](float x) { return a.log2_units ? __builtin_amdgcn_exp2f(x) : expf(x); };
-  const float* ml = a.part_ml + 2 * (r0 * a.n_rep + h);
-  const float* acc = a.part_acc + (r0 * a.n_rep + h) * D + d;
   const int64_t pstride = a.n_rep;  // partial rows between consecutive partials of a head
+  const float* ml = a.part_ml + 2 * (r0 * pstride + h);
+  const float* acc = a.part_acc + (r0 * pstride + h) * D + d;
   float M = -INFINITY, num = 0.f, den = 0.f;
-  for (int s0 = 0; s0 < n; s0 += kMergeBatch) {
-    // every load is issued, clamped to the last partial, and the extras masked after:
-    // guarded loads would become one branch and one round trip per partial
-    float mv[kMergeBatch], lv[kMergeBatch], xv[kMergeBatch];
-#pragma unroll
-    for (int k = 0; k < kMergeBatch; ++k) {
-      const int64_t r = int64_t(min(s0 + k, n - 1)) * pstride;
-      mv[k] = ml[2 * r];
-      lv[k] = ml[2 * r + 1];
-      xv[k] = acc[r * D];
+  for (int s0 = 0; s0 < n; s0 += 64) {
+    const int cnt = min(64, n - s0);
+    float mk = -INFINITY, lk = 0.f;
+    if (lane < cnt) {
+      const float2 x = *reinterpret_cast<const float2*>(ml + 2 * (int64_t(s0 + lane) * pstride));
+      mk = x.x;
+      lk = x.y;
     }
+    const float Mn = fmaxf(M, wave_max(mk));
+    // a partial that saw no key (m = -inf) and the lanes past the batch weigh 0
+    const float wk = mk == -INFINITY ? 0.f : wexp(mk - Mn);
+    const float r_old = M == -INFINITY ? 0.f : wexp(M - Mn);
+    den = fmaf(den, r_old, wave_sum(wk * lk));
+    num *= r_old;
+    M = Mn;
+    for (int k0 = 0; k0 < cnt; k0 += kMergeBatch) {
+      // every load is issued, clamped to the last partial; the extras weigh 0
+      float xv[kMergeBatch];
 #pragma unroll
-    for (int k = 0; k < kMergeBatch; ++k) {
-      if (s0 + k >= n) mv[k] = -INFINITY;
-    }
+      for (int k = 0; k < kMergeBatch; ++k)
+        xv[k] = acc[int64_t(min(s0 + k0 + k, n - 1)) * pstride * D];
 #pragma unroll
-    for (int k = 0; k < kMergeBatch; ++k) {
-      if (mv[k] == -INFINITY) continue;  // a partial that saw no key (block-uniform)
-      const float Mn = fmaxf(M, mv[k]);
-      const float r_old = M == -INFINITY ? 0.f : wexp(M - Mn);
-      const float w = wexp(mv[k] - Mn);
-      num = fmaf(num, r_old, w * xv[k]);
-      den = fmaf(den, r_old, w * lv[k]);
-      M = Mn;
+      for (int k = 0; k < kMergeBatch; ++k) {
+        const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k0 + k));
+        num = fmaf(w, xv[k], num);
+      }
     }
   }
   av[d] = (n > 0 && den > 0.f) ? num / fmaxf(den, 1e-30f) : 0.f;
