@@ -561,6 +561,13 @@ __device__ __forceinline__ Tab<BW> make_tab(const char* lds, int off, int lane) 
   return t;
 }
 
+// Logical index of work-group p of n when groups go to the 8 XCDs round robin:
+// XCD x holds groups x, x+8, ...; they become a contiguous run of logical indices.
+__device__ __forceinline__ int xcd_major(int p, int n) {
+  const int q = n >> 3, r = n & 7, x = p & 7, s = p >> 3;
+  return x * q + min(x, r) + s;
+}
+
 // Work-group of WPB independent waves sharing the codebook tables; wave w =
 // blockIdx.x * WPB + wave-in-group.
 // Fixed splits: wave w is unit (split, kv head, sequence) of the flattened
@@ -579,7 +586,11 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
   stage_table<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
   stage_table<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
-  const int64_t w = int64_t(blockIdx.x) * WPB + wig;
+  // Work-groups are dealt to the eight XCDs round robin (group p on XCD p % 8); the
+  // logical group index gives each XCD a contiguous stretch of the flattened work,
+  // so the kv heads of a sequence run on one XCD and share the 128-byte lines that
+  // hold their norms in its L2.
+  const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   float* ptile = reinterpret_cast<float*>(lds + Lay::tiles + wig * Lay::tile_bytes);
 
   // The work list: one (sequence, kv head, token range) for a fixed split, or the
