@@ -191,6 +191,7 @@ def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
             cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "run", "--",
                    sys.executable, str(ROOT / "bench.py"), "--config", str(cfg), "--steps", "3", "--warmup", "1",
                    "--settle", "0", "--parity", "off", "--cpu-baseline", "off", "--traffic", "off", "--append", "off",
+                   "--dequant", "off",
                    "--copy-peak", "on"]
             try:
                 subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
@@ -298,6 +299,72 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
             "codes_checked": vectors * D}
 
 
+def dequant_bench(dev, bws=(4, 6), reps: int = 50, check_rows: int = 2048, cpu_rows: int = 32768):
+    """The fused history dequantization (``wn_tq_dequant``) at the shape the reference
+    publishes its dequant numbers for: N = 1,048,576 vectors (B16 x H4 x L16384), D 128,
+    bf16 out (``turboquant_kv/README.md:203-204``, ``results/phaseC_kernel_tf32.json``).
+
+    Random packed bytes are valid codes at every width. Bytes per vector: NB packed +
+    2 norm read, 2 D written. Timed with hipEvents over ``reps`` calls; the first
+    ``check_rows`` rows are checked against the float64 closed form, and the CPU
+    restatement (torch fp32 ``centroids[idx] @ Pi * n``) is timed on ``cpu_rows`` rows
+    and scaled to N.
+    """
+    import torch
+    from oracle import packing as opk
+    from winnow_amd.kernel import tq_dequant
+    from winnow_amd.packing import packed_bytes
+    from winnow_amd.quantizer import get_quantizer
+
+    B, H, L, D = 16, 4, 16384, 128
+    N = B * H * L
+    res = {}
+    for bw in bws:
+        nb = packed_bytes(D, bw)
+        tq = get_quantizer(bw, D, dev, 42)
+        g = torch.Generator(device=dev).manual_seed(bw)
+        packed = torch.randint(0, 256, (B, H, L, nb), dtype=torch.uint8, device=dev, generator=g)
+        norms = (torch.rand(B, H, L, device=dev, generator=g) * 20 + 1).half()
+        out = torch.empty(B, H, L, D, dtype=torch.bfloat16, device=dev)
+
+        def call():
+            tq_dequant(packed, norms, tq.centroids, tq.Pi, bw, D, out=out)
+
+        for _ in range(5):
+            call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        moved = N * (nb + 2 + 2 * D)
+        # float64 check of the first rows
+        pc = packed.view(N, nb)[:check_rows].cpu().numpy()
+        idx = torch.from_numpy(opk.unpack(pc, bw, D)).long()
+        c64, pi64 = tq.centroids.cpu().double(), tq.Pi.cpu().double()
+        ref = (c64[idx] @ pi64) * norms.view(N)[:check_rows].cpu().double()[:, None]
+        got = out.view(N, D)[:check_rows].cpu().double()
+        err = (got - ref).abs().max().item()
+        ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp(min=1e-30))) - 7)
+        ok = bool(((got - ref).abs() <= ulp + 2e-5 * ref.abs().max()).all())
+        # CPU restatement, bounded sample
+        c32, pi32 = tq.centroids.cpu(), tq.Pi.cpu()
+        pcs = torch.from_numpy(opk.unpack(packed.view(N, nb)[:cpu_rows].cpu().numpy(), bw, D)).long()
+        ns = norms.view(N)[:cpu_rows].cpu().float()
+        t0 = time.perf_counter()
+        _ = ((c32[pcs] @ pi32) * ns[:, None]).bfloat16()
+        cpu_us = (time.perf_counter() - t0) * 1e6 * N / cpu_rows
+        res[f"{bw}bit"] = {"us_per_call": us, "vectors": N, "GBps": moved / (us * 1e-6) / 1e9,
+                           "frac_of_8TBps": moved / (us * 1e-6) / 8e12, "bytes_per_call": moved,
+                           "max_abs_err_vs_f64": err, "within_bf16_step": ok,
+                           "cpu_us_per_call": cpu_us, "cpu_sample_rows": cpu_rows, "cpu_threads": torch.get_num_threads(),
+                           "reference_a6000_us": {4: 1298.8, 6: 1298.8}.get(bw)}
+    return res
+
+
 def parity(c, lens, q, kv, quants, sample):
     """Same-run checks: two sequences' attention vs the CPU oracle on the same pages, and
     the first 256 tokens of sequence 0 re-quantized by the oracle vs the pool bytes."""
@@ -388,6 +455,9 @@ def main(argv=None):
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--parity", choices=["on", "off"], default="on")
     ap.add_argument("--copy-peak", choices=["on", "off"], default="on")
+    ap.add_argument("--dequant", choices=["on", "off"], default="on",
+                    help="time the fused history dequantization at the reference's published shape "
+                         "(N = 1,048,576 vectors, 4- and 6-bit)")
     ap.add_argument("--append", choices=["on", "off"], default="on",
                     help="time the quantize+pack append of 16 new tokens per sequence (BASELINE config 3)")
     ap.add_argument("--traffic", choices=["on", "off"], default="on",
@@ -461,6 +531,7 @@ def main(argv=None):
         log(f"copy peak: {cp}")
 
     app = append_bench(c, lens, kvs[0].page_table_host, quants, dev) if args.append == "on" else None
+    deq = dequant_bench(dev) if args.dequant == "on" else None
     if app:
         log(f"append: {app}")
     traffic = hbm_traffic(args.config, scan_kernel_name(c)) if args.traffic == "on" else None
@@ -506,6 +577,7 @@ def main(argv=None):
                      "frac_of_copy_peak": achieved / cp["GBps"] if cp else None},
         "cpu_baseline": cpu,
         "append": app,
+        "dequant": deq,
         "parity": par,
     }
     print(json.dumps(result), flush=True)

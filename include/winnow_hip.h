@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define WN_ABI_VERSION 2
+#define WN_ABI_VERSION 3
 
 /* element types of floating-point tensors crossing the ABI */
 enum { WN_F32 = 0, WN_F16 = 1, WN_BF16 = 2 };
@@ -143,6 +143,31 @@ int wn_unpack(const uint8_t* packed, int64_t rows, int D, int bw, uint8_t* codes
 int wn_dequantize(const uint8_t* codes, const uint16_t* norms, int64_t rows,
                   const float* pi, const float* centroids, int bw, int D,
                   void* out, int out_dtype, void* stream);
+
+/* Fused dequantization of packed rows, unpack + codebook gather + inverse rotation
+ * + norm rescale in one pass (replaces tq_dequant, turboquant_kv/kernel.py:78-115,
+ * and tq_dequant_cuda, csrc/tq_dequant.cu:186-215). planes x L rows: row (p, t)
+ * reads its D*bw/8 packed bytes at packed + (p * plane_rows + t) * (D*bw/8) and its
+ * fp16 norm at norms + p * plane_rows + t, so a (..., MAXLEN, NB) cache buffer
+ * sliced to its first L positions needs no copy (plane_rows = MAXLEN).
+ * out (planes * L, D) contiguous of out_dtype (fp32, bf16 or fp16):
+ * out[r] = (centroids[codes(r)] Pi) * norm(r). head_dim 128. */
+int wn_tq_dequant(const uint8_t* packed, const uint16_t* norms, int64_t planes, int64_t L,
+                  int64_t plane_rows, const float* centroids, const float* pi, int bw, int D,
+                  void* out, int out_dtype, void* stream);
+
+/* The dequantized history of one sequence straight from pool pages (replaces the
+ * gather + unpack + dequantize of packed_backend.py:192-208 dequantize_history).
+ * Position t < L of kv head h reads page table_row[t / S], slot t % S, at
+ * pages + page * page_stride + h * head_stride + slot * (D*bw/8) (bytes) and its
+ * norm at norms + page * norm_page_stride + h * norm_head_stride + slot
+ * (elements). out (Hkv, L, D) contiguous of out_dtype. head_dim 128, S a power
+ * of two. */
+int wn_dequantize_history(const uint8_t* pages, int64_t page_stride, int64_t head_stride,
+                          const uint16_t* norms, int64_t norm_page_stride, int64_t norm_head_stride,
+                          const int32_t* table_row, int L, int Hkv, int S,
+                          const float* centroids, const float* pi, int bw, int D,
+                          void* out, int out_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libwinnow_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 WN_F32, WN_F16, WN_BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: WN_F32, torch.float16: WN_F16, torch.bfloat16: WN_BF16}
@@ -57,6 +57,13 @@ SIGNATURES = {
     "wn_pack": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_p, _c_p]),
     "wn_unpack": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_p, _c_p]),
     "wn_dequantize": (_c_i, [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i, _c_i, _c_p, _c_i, _c_p]),
+    "wn_tq_dequant": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i, _c_i, _c_p, _c_i, _c_p]),
+    "wn_dequantize_history": (_c_i, [
+        _c_p, _c_i64, _c_i64,                       # pages, page stride, head stride
+        _c_p, _c_i64, _c_i64,                       # norms, page stride, head stride
+        _c_p, _c_i, _c_i, _c_i,                     # table row, L, Hkv, S
+        _c_p, _c_p, _c_i, _c_i,                     # centroids, Pi, bw, D
+        _c_p, _c_i, _c_p]),                         # out, out dtype, stream
 }
 
 

@@ -221,14 +221,29 @@ def select_decode_backend(query: torch.Tensor, kv, requested: str) -> str:
 
 
 def dequantize_history(kv: pa.PackedKV, pages, norms, quant, b: int, dtype) -> torch.Tensor:
-    """(1, Hkv, L, D) reconstruction of sequence b on the GPU (packed_backend.py:192-208)."""
+    """(1, Hkv, L, D) reconstruction of sequence b on the GPU (packed_backend.py:192-208).
+
+    head_dim 128: one fused HIP kernel (``wn_dequantize_history``) reads the pool
+    pages through the page table, so nothing is gathered or unpacked first."""
     L = int(kv.seq_lens_host[b]) if kv.seq_lens_host is not None else int(kv.seq_lens[b])
     S = kv.page_size
+    D = kv.head_dim
+    if D == 128 and pages.stride(-1) == 1 and pages.stride(-2) == pages.shape[-1] and norms.stride(-1) == 1:
+        Hkv = pages.shape[1]
+        out = torch.empty(1, Hkv, L, D, dtype=dtype if dtype in _lib.DTYPE_CODE else torch.float32,
+                          device=pages.device)
+        if L == 0:
+            return out.to(dtype)
+        with torch.cuda.device(pages.device):
+            _lib.call("wn_dequantize_history", _lib.ptr(pages), pages.stride(0), pages.stride(1),
+                      _lib.ptr(norms), norms.stride(0), norms.stride(1), _lib.ptr(kv.page_table[b]), L, Hkv, S,
+                      _lib.ptr(quant.centroids), _lib.ptr(quant.Pi), quant.bit_width, D, _lib.ptr(out),
+                      _lib.DTYPE_CODE[out.dtype], _lib.stream_of(pages.device))
+        return out.to(dtype)
     table = kv.page_table_host if kv.page_table_host is not None else kv.page_table.cpu()
     ids = table[b, :(L + S - 1) // S].long().to(pages.device)
     rows = pages[ids].permute(1, 0, 2, 3).reshape(pages.shape[1], -1, pages.shape[3])[:, :L].contiguous()
     nrm = norms[ids].permute(1, 0, 2).reshape(norms.shape[1], -1)[:, :L].contiguous()
-    D = kv.head_dim
     codes = unpack(rows, quant.bit_width, D).contiguous()
     out = torch.empty(1, rows.shape[0], L, D, dtype=dtype if dtype in _lib.DTYPE_CODE else torch.float32,
                       device=rows.device)
