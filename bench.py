@@ -299,7 +299,8 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
             "codes_checked": vectors * D}
 
 
-def dequant_bench(dev, bws=(4, 6), reps: int = 50, check_rows: int = 2048, cpu_rows: int = 32768):
+def dequant_bench(dev, bws=(4, 6), reps: int = 50, check_rows: int = 2048, cpu_rows: int = 32768,
+                  fast: bool = False):
     """The fused history dequantization (``wn_tq_dequant``) at the shape the reference
     publishes its dequant numbers for: N = 1,048,576 vectors (B16 x H4 x L16384), D 128,
     bf16 out (``turboquant_kv/README.md:203-204``, ``results/phaseC_kernel_tf32.json``).
@@ -328,7 +329,7 @@ def dequant_bench(dev, bws=(4, 6), reps: int = 50, check_rows: int = 2048, cpu_r
         out = torch.empty(B, H, L, D, dtype=torch.bfloat16, device=dev)
 
         def call():
-            tq_dequant(packed, norms, tq.centroids, tq.Pi, bw, D, out=out)
+            tq_dequant(packed, norms, tq.centroids, tq.Pi, bw, D, out=out, allow_tf32=fast)
 
         for _ in range(5):
             call()
@@ -349,7 +350,7 @@ def dequant_bench(dev, bws=(4, 6), reps: int = 50, check_rows: int = 2048, cpu_r
         got = out.view(N, D)[:check_rows].cpu().double()
         err = (got - ref).abs().max().item()
         ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp(min=1e-30))) - 7)
-        ok = bool(((got - ref).abs() <= ulp + 2e-5 * ref.abs().max()).all())
+        ok = bool(((got - ref).abs() <= ulp + (2e-3 if fast else 2e-5) * ref.abs().max()).all())
         # CPU restatement, bounded sample
         c32, pi32 = tq.centroids.cpu(), tq.Pi.cpu()
         pcs = torch.from_numpy(opk.unpack(packed.view(N, nb)[:cpu_rows].cpu().numpy(), bw, D)).long()
@@ -357,7 +358,7 @@ def dequant_bench(dev, bws=(4, 6), reps: int = 50, check_rows: int = 2048, cpu_r
         t0 = time.perf_counter()
         _ = ((c32[pcs] @ pi32) * ns[:, None]).bfloat16()
         cpu_us = (time.perf_counter() - t0) * 1e6 * N / cpu_rows
-        res[f"{bw}bit"] = {"us_per_call": us, "vectors": N, "GBps": moved / (us * 1e-6) / 1e9,
+        res[f"{bw}bit" + ("_allow_tf32" if fast else "")] = {"us_per_call": us, "vectors": N, "GBps": moved / (us * 1e-6) / 1e9,
                            "frac_of_8TBps": moved / (us * 1e-6) / 8e12, "bytes_per_call": moved,
                            "max_abs_err_vs_f64": err, "within_bf16_step": ok,
                            "cpu_us_per_call": cpu_us, "cpu_sample_rows": cpu_rows, "cpu_threads": torch.get_num_threads(),
@@ -531,7 +532,7 @@ def main(argv=None):
         log(f"copy peak: {cp}")
 
     app = append_bench(c, lens, kvs[0].page_table_host, quants, dev) if args.append == "on" else None
-    deq = dequant_bench(dev) if args.dequant == "on" else None
+    deq = {**dequant_bench(dev), **dequant_bench(dev, fast=True)} if args.dequant == "on" else None
     if app:
         log(f"append: {app}")
     traffic = hbm_traffic(args.config, scan_kernel_name(c)) if args.traffic == "on" else None

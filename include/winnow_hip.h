@@ -151,23 +151,27 @@ int wn_dequantize(const uint8_t* codes, const uint16_t* norms, int64_t rows,
  * fp16 norm at norms + p * plane_rows + t, so a (..., MAXLEN, NB) cache buffer
  * sliced to its first L positions needs no copy (plane_rows = MAXLEN).
  * out (planes * L, D) contiguous of out_dtype (fp32, bf16 or fp16):
- * out[r] = (centroids[codes(r)] Pi) * norm(r). head_dim 128. */
+ * out[r] = (centroids[codes(r)] Pi) * norm(r). fast = 0: the rotation at
+ * near-fp32 accuracy (error below 2^-16 per term); fast = 1: one fp16 product
+ * per term (2^-11, the reference's allow_tf32). head_dim 128; packed and out
+ * 16-byte aligned. */
 int wn_tq_dequant(const uint8_t* packed, const uint16_t* norms, int64_t planes, int64_t L,
                   int64_t plane_rows, const float* centroids, const float* pi, int bw, int D,
-                  void* out, int out_dtype, void* stream);
+                  void* out, int out_dtype, int fast, void* stream);
 
 /* The dequantized history of one sequence straight from pool pages (replaces the
  * gather + unpack + dequantize of packed_backend.py:192-208 dequantize_history).
  * Position t < L of kv head h reads page table_row[t / S], slot t % S, at
  * pages + page * page_stride + h * head_stride + slot * (D*bw/8) (bytes) and its
  * norm at norms + page * norm_page_stride + h * norm_head_stride + slot
- * (elements). out (Hkv, L, D) contiguous of out_dtype. head_dim 128, S a power
- * of two. */
+ * (elements). out (Hkv, L, D) contiguous of out_dtype; fast as for
+ * wn_tq_dequant. head_dim 128, S a power of two, pages, their strides and out
+ * 16-byte aligned. */
 int wn_dequantize_history(const uint8_t* pages, int64_t page_stride, int64_t head_stride,
                           const uint16_t* norms, int64_t norm_page_stride, int64_t norm_head_stride,
                           const int32_t* table_row, int L, int Hkv, int S,
                           const float* centroids, const float* pi, int bw, int D,
-                          void* out, int out_dtype, void* stream);
+                          void* out, int out_dtype, int fast, void* stream);
 
 #ifdef __cplusplus
 }

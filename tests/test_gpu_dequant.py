@@ -58,6 +58,21 @@ def test_tq_dequant_matches_the_closed_form(bw):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("bw", [4, 6])
+def test_tq_dequant_fast_mode_stays_in_the_tf32_class(bw):
+    """allow_tf32=True: one fp16 product per term, within 2e-3 of the largest output
+    (the reference documents its tf32 path as faster and measurably less accurate)."""
+    from winnow_amd.kernel import tq_dequant
+    D = 128
+    packed, n16, ref, tq = _rows(bw, D, (2, 4, 77), 400 + bw)
+    out = torch.empty(2, 4, 77, D, device=DEV)
+    tq_dequant(packed.to(DEV), n16.to(DEV), tq.centroids.to(DEV), tq.Pi.to(DEV), bw, D, out=out, allow_tf32=True)
+    err = (out.cpu().double() - ref).abs().max().item()
+    assert err <= 2e-3 * ref.abs().max().item(), err
+    assert err > 0.0
+
+
+@pytest.mark.gpu
 def test_tq_dequant_reads_a_sliced_cache_buffer():
     """A (B, H, MAXLEN, NB) buffer sliced to its first L positions is read in place."""
     from winnow_amd.kernel import tq_dequant

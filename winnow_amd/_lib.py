@@ -57,13 +57,13 @@ SIGNATURES = {
     "wn_pack": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_p, _c_p]),
     "wn_unpack": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_p, _c_p]),
     "wn_dequantize": (_c_i, [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i, _c_i, _c_p, _c_i, _c_p]),
-    "wn_tq_dequant": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i, _c_i, _c_p, _c_i, _c_p]),
+    "wn_tq_dequant": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i, _c_i, _c_p, _c_i, _c_i, _c_p]),
     "wn_dequantize_history": (_c_i, [
         _c_p, _c_i64, _c_i64,                       # pages, page stride, head stride
         _c_p, _c_i64, _c_i64,                       # norms, page stride, head stride
         _c_p, _c_i, _c_i, _c_i,                     # table row, L, Hkv, S
         _c_p, _c_p, _c_i, _c_i,                     # centroids, Pi, bw, D
-        _c_p, _c_i, _c_p]),                         # out, out dtype, stream
+        _c_p, _c_i, _c_i, _c_p]),                   # out, out dtype, fast, stream
 }
 
 

@@ -9,16 +9,21 @@
 // MFMA would make it compute-bound (2 * 128 FLOP per output byte pair), so every
 // operand x is carried as a bf16 pair hi + lo (hi = x rounded, lo = x - hi rounded)
 // and the product as hi*hi + hi*lo + lo*hi with v_mfma_f32_16x16x32_bf16 (lo*lo is
-// below 2^-16 of the product; the output is rounded to bf16 anyway).
+// below 2^-16 of the product; the output is rounded to bf16 anyway). The fast mode
+// (the reference's allow_tf32) uses one fp16 product instead: 2^-11 per term, the
+// class of tf32's 10-bit mantissa.
 //
 // A persistent work-group of four waves stages Pi^T as bf16 hi and lo planes in LDS
 // once; each wave then takes passes of 32 rows (two 16-row tiles) and computes the
 // transposed product out^T = Pi^T y^T, so that a lane ends with four consecutive
 // output dims of one row:
-//   A  (output-dim tile t, k-step s): lane l holds Pi[32s + 8(l/16) .. +8][16t + l % 16],
+// The reduction order over the 128 input dims is permuted so that lane group
+// G = l/16 covers dims 32G .. 32G+31 over the four k-steps (k-step s: dims
+// 32G + 8s .. +8): a lane's codes are then one contiguous 4*bw-byte load per row.
+//   A  (output-dim tile t, k-step s): lane l holds Pi[32G + 8s .. +8][16t + l % 16],
 //      one 16-byte LDS read from the transposed plane (padded rows, conflict free);
 //   B  (row tile, k-step s): lane l holds the codebook values of row l % 16 at dims
-//      32s + 8(l/16) .. +8, looked up from a byte-indexed pair table for 4-bit codes
+//      32G + 8s .. +8, looked up from a byte-indexed pair table for 4-bit codes
 //      (one entry = hi or lo of the two codes of a byte) or per code;
 //   D  lane l holds output dims 16t + 4(l/16) .. +3 of row l % 16; the norm rescale
 //      and the cast happen on the way out, four values in one 8- or 16-byte store.
@@ -29,6 +34,7 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -55,6 +61,9 @@ struct DqArgs {
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+  return uint32_t(f32_to_f16(a)) | (uint32_t(f32_to_f16(b)) << 16);
+}
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
@@ -75,31 +84,50 @@ __device__ __forceinline__ void row_src(const DqArgs& a, int64_t r, const uint8_
   }
 }
 
-// The BW bytes holding codes 8q..8q+7 of a row (LSB-first), as little-endian words.
+// The 4*BW bytes (BW words) holding codes 32g..32g+31 of a row, LSB-first. Rows are
+// 16*BW bytes and 16-byte aligned (checked on the host), so the words are aligned.
 template <int BW>
-__device__ __forceinline__ void load_codes8(const uint8_t* row, int q, uint32_t (&w)[2]) {
-  const uint8_t* p = row + BW * q;
-  if constexpr (BW == 4) {
-    w[0] = *reinterpret_cast<const uint32_t*>(p);
-    w[1] = 0;
-  } else if constexpr (BW == 8) {
-    const uint2 x = *reinterpret_cast<const uint2*>(p);
-    w[0] = x.x;
-    w[1] = x.y;
-  } else if constexpr (BW == 2) {
-    w[0] = *reinterpret_cast<const uint16_t*>(p);
-    w[1] = 0;
-  } else {  // 3, 5, 6: byte-aligned groups of BW bytes
-    uint32_t w0 = 0, w1 = 0;
+__device__ __forceinline__ void load_codes32(const uint8_t* row, int g, uint32_t (&w)[BW]) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 4 * BW * g);
+  if constexpr (BW % 4 == 0) {
 #pragma unroll
-    for (int i = 0; i < BW; ++i) {
-      const uint32_t b = p[i];
-      if (i < 4) w0 |= b << (8 * i);
-      else w1 |= b << (8 * (i - 4));
+    for (int i = 0; i < BW / 4; ++i) {
+      const uint4 x = reinterpret_cast<const uint4*>(p)[i];
+      w[4 * i] = x.x;
+      w[4 * i + 1] = x.y;
+      w[4 * i + 2] = x.z;
+      w[4 * i + 3] = x.w;
     }
-    w[0] = w0;
-    w[1] = w1;
+  } else if constexpr (BW % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < BW / 2; ++i) {
+      const uint2 x = reinterpret_cast<const uint2*>(p)[i];
+      w[2 * i] = x.x;
+      w[2 * i + 1] = x.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < BW; ++i) w[i] = p[i];
   }
+}
+
+// Codes 8s..8s+7 of the 32 in w (k-step s) as two little-endian words: their
+// 8*BW bits starting at bit 8*BW*s.
+template <int BW>
+__device__ __forceinline__ void step_codes(const uint32_t (&w)[BW], int s, uint32_t (&c)[2]) {
+  const int bit = 8 * BW * s, wi = bit >> 5, sh = bit & 31;
+  uint32_t lo = w[wi] >> sh;
+  if (sh && wi + 1 < BW) lo |= w[wi + 1] << (32 - sh);
+  uint32_t hi = 0;
+  if (BW > 4) {
+    const int b2 = bit + 32, w2 = b2 >> 5, s2 = b2 & 31;
+    if (w2 < BW) {
+      hi = w[w2] >> s2;
+      if (s2 && w2 + 1 < BW) hi |= w[w2 + 1] << (32 - s2);
+    }
+  }
+  c[0] = lo;
+  c[1] = hi;
 }
 
 // Codebook of BW-bit codes in LDS as bf16 hi / lo: for 4-bit a pair table (entry b
@@ -112,23 +140,23 @@ struct DqTab {
   uint32_t lo[BW == 4 ? 256 : (1 << BW) / 2 + 1];
 };
 
-template <int BW>
+// Fast mode: hi holds fp16 values and lo is unused.
+template <int BW, bool FAST>
 __device__ __forceinline__ void stage_dq_tab(const float* cb, DqTab<BW>& t, int tid) {
-  if constexpr (BW == 4) {
-    for (int b = tid; b < 256; b += kDqWaves * 64) {
-      const float x0 = cb[b & 15], x1 = cb[b >> 4];
-      const uint32_t h = pack_bf16(x0, x1);
-      t.hi[b] = h;
-      t.lo[b] = pack_bf16(x0 - bf16_lo(h), x1 - bf16_hi(h));
-    }
-  } else {
-    constexpr int L = 1 << BW;
-    for (int i = tid; i < (L + 1) / 2; i += kDqWaves * 64) {
-      const float x0 = cb[2 * i], x1 = 2 * i + 1 < L ? cb[2 * i + 1] : 0.f;
+  auto put = [&](int i, float x0, float x1) {
+    if constexpr (FAST) {
+      t.hi[i] = pack_f16(x0, x1);
+    } else {
       const uint32_t h = pack_bf16(x0, x1);
       t.hi[i] = h;
       t.lo[i] = pack_bf16(x0 - bf16_lo(h), x1 - bf16_hi(h));
     }
+  };
+  if constexpr (BW == 4) {
+    for (int b = tid; b < 256; b += kDqWaves * 64) put(b, cb[b & 15], cb[b >> 4]);
+  } else {
+    constexpr int L = 1 << BW;
+    for (int i = tid; i < (L + 1) / 2; i += kDqWaves * 64) put(i, cb[2 * i], 2 * i + 1 < L ? cb[2 * i + 1] : 0.f);
   }
 }
 
@@ -138,8 +166,8 @@ __device__ __forceinline__ uint32_t half_of(const uint32_t* t, uint32_t c) {
   return (c & 1u) ? (w >> 16) : (w & 0xffffu);
 }
 
-// MFMA operands of 8 codes (little-endian words w): hi and lo bf16 of their values.
-template <int BW>
+// MFMA operands of 8 codes (little-endian words w): hi and lo of their values.
+template <int BW, bool FAST>
 __device__ __forceinline__ void codes_to_a(const uint32_t (&w)[2], const DqTab<BW>& t, s16x8& ah, s16x8& al) {
   uint32_t h[4], l[4];
   if constexpr (BW == 4) {
@@ -147,7 +175,7 @@ __device__ __forceinline__ void codes_to_a(const uint32_t (&w)[2], const DqTab<B
     for (int j = 0; j < 4; ++j) {
       const uint32_t b = (w[0] >> (8 * j)) & 0xffu;
       h[j] = t.hi[b];
-      l[j] = t.lo[b];
+      l[j] = FAST ? 0u : t.lo[b];
     }
   } else {
     uint32_t c[8];
@@ -161,7 +189,7 @@ __device__ __forceinline__ void codes_to_a(const uint32_t (&w)[2], const DqTab<B
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       h[j] = half_of(t.hi, c[2 * j]) | (half_of(t.hi, c[2 * j + 1]) << 16);
-      l[j] = half_of(t.lo, c[2 * j]) | (half_of(t.lo, c[2 * j + 1]) << 16);
+      l[j] = FAST ? 0u : half_of(t.lo, c[2 * j]) | (half_of(t.lo, c[2 * j + 1]) << 16);
     }
   }
   ah = __builtin_bit_cast(s16x8, make_uint4(h[0], h[1], h[2], h[3]));
@@ -181,43 +209,57 @@ __device__ __forceinline__ void store4(void* out, int64_t i, int dtype, f32x4 v)
   }
 }
 
-template <int BW>
+template <int BW, bool FAST>
 __global__ __launch_bounds__(kDqWaves * 64) void tq_dequant_kernel(DqArgs a) {
-  constexpr int D = kDqD, NB = D * BW / 8;
-  __shared__ __align__(16) uint16_t pit[2][D * kPiRow];  // Pi^T, bf16 hi and lo planes
+  constexpr int D = kDqD, NB = D * BW / 8, PLANES = FAST ? 1 : 2;
+  __shared__ __align__(16) uint16_t pit[PLANES][D * kPiRow];  // Pi^T: bf16 hi and lo, or fp16
   __shared__ DqTab<BW> tab;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Pi^T planes: pit[h][n * kPiRow + k] = split(Pi[k][n])
   for (int i = tid; i < D * D / 2; i += kDqWaves * 64) {
     const int k = i / (D / 2), n2 = 2 * (i % (D / 2));  // two columns of row k
     const float2 x = *reinterpret_cast<const float2*>(a.pi + k * D + n2);
-    const uint32_t h = pack_bf16(x.x, x.y);
-    const uint32_t l = pack_bf16(x.x - bf16_lo(h), x.y - bf16_hi(h));
-    pit[0][n2 * kPiRow + k] = uint16_t(h & 0xffffu);
-    pit[0][(n2 + 1) * kPiRow + k] = uint16_t(h >> 16);
-    pit[1][n2 * kPiRow + k] = uint16_t(l & 0xffffu);
-    pit[1][(n2 + 1) * kPiRow + k] = uint16_t(l >> 16);
+    if constexpr (FAST) {
+      const uint32_t h = pack_f16(x.x, x.y);
+      pit[0][n2 * kPiRow + k] = uint16_t(h & 0xffffu);
+      pit[0][(n2 + 1) * kPiRow + k] = uint16_t(h >> 16);
+    } else {
+      const uint32_t h = pack_bf16(x.x, x.y);
+      const uint32_t l = pack_bf16(x.x - bf16_lo(h), x.y - bf16_hi(h));
+      pit[0][n2 * kPiRow + k] = uint16_t(h & 0xffffu);
+      pit[0][(n2 + 1) * kPiRow + k] = uint16_t(h >> 16);
+      pit[PLANES - 1][n2 * kPiRow + k] = uint16_t(l & 0xffffu);
+      pit[PLANES - 1][(n2 + 1) * kPiRow + k] = uint16_t(l >> 16);
+    }
   }
-  stage_dq_tab<BW>(a.cb, tab, tid);
+  stage_dq_tab<BW, FAST>(a.cb, tab, tid);
   __syncthreads();
 
   const int g = lane >> 4, c16 = lane & 15;
-  const int64_t passes = (a.N + 31) / 32;
-  for (int64_t pass = int64_t(blockIdx.x) * kDqWaves + wave; pass < passes;
-       pass += int64_t(gridDim.x) * kDqWaves) {
-    const int64_t r0 = pass * 32;
-    // codes of row r0 + 16 rt + c16 (this lane's A rows) and norms of the D rows
-    uint32_t cw[2][4][2];
-    float nv[2];
+  const int64_t passes = (a.N + 31) / 32, stride = int64_t(gridDim.x) * kDqWaves;
+  // codes 32g .. 32g+31 of row r0 + 16 rt + c16 and that row's norm, for a pass;
+  // rows past N read row N - 1, so the loads of the next pass are unconditional and
+  // the compiler's waits stay one pass behind
+  auto load_pass = [&](int64_t pass, uint32_t (&cw)[2][BW], uint16_t (&nh)[2]) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const uint8_t* p;
       const uint16_t* n;
-      row_src<NB>(a, r0 + 16 * rt + c16, p, n);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) load_codes8<BW>(p, 4 * s + g, cw[rt][s]);
-      nv[rt] = f16_to_f32(*n);
+      row_src<NB>(a, pass * 32 + 16 * rt + c16, p, n);
+      load_codes32<BW>(p, g, cw[rt]);
+      nh[rt] = *n;
     }
+  };
+  int64_t pass = int64_t(blockIdx.x) * kDqWaves + wave;
+  if (pass >= passes) return;
+  uint32_t cw[2][BW];
+  uint16_t nh[2];
+  load_pass(pass, cw, nh);
+  for (; pass < passes; pass += stride) {
+    uint32_t cn[2][BW];
+    uint16_t nn[2];
+    load_pass(pass + stride, cn, nn);  // the next pass's codes land while this one computes
+    const int64_t r0 = pass * 32;
     f32x4 acc[2][8];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
@@ -227,55 +269,75 @@ __global__ __launch_bounds__(kDqWaves * 64) void tq_dequant_kernel(DqArgs a) {
     for (int s = 0; s < 4; ++s) {
       s16x8 yh[2], yl[2];
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) codes_to_a<BW>(cw[rt][s], tab, yh[rt], yl[rt]);
+      for (int rt = 0; rt < 2; ++rt) {
+        uint32_t cs[2];
+        step_codes<BW>(cw[rt], s, cs);
+        codes_to_a<BW, FAST>(cs, tab, yh[rt], yl[rt]);
+      }
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
-        const int off = (16 * t + c16) * kPiRow + 32 * s + 8 * g;
+        const int off = (16 * t + c16) * kPiRow + 32 * g + 8 * s;
         const s16x8 ph = *reinterpret_cast<const s16x8*>(&pit[0][off]);
-        const s16x8 pl = *reinterpret_cast<const s16x8*>(&pit[1][off]);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
-          acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, yh[rt], acc[rt][t], 0, 0, 0);
-          acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, yh[rt], acc[rt][t], 0, 0, 0);
-          acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, yl[rt], acc[rt][t], 0, 0, 0);
+          if constexpr (FAST) {
+            acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ph),
+                                                               __builtin_bit_cast(f16x8, yh[rt]), acc[rt][t], 0, 0, 0);
+          } else {
+            const s16x8 pl = *reinterpret_cast<const s16x8*>(&pit[PLANES - 1][off]);
+            acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, yh[rt], acc[rt][t], 0, 0, 0);
+            acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, yh[rt], acc[rt][t], 0, 0, 0);
+            acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, yl[rt], acc[rt][t], 0, 0, 0);
+          }
         }
       }
     }
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const int64_t row = r0 + 16 * rt + c16;
+      const float nv = f16_to_f32(nh[rt]);
       if (row < a.N) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) store4(a.out, row * D + 16 * t + 4 * g, a.out_dtype, acc[rt][t] * nv[rt]);
+        for (int t = 0; t < 8; ++t) store4(a.out, row * D + 16 * t + 4 * g, a.out_dtype, acc[rt][t] * nv);
       }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      nh[rt] = nn[rt];
+#pragma unroll
+      for (int i = 0; i < BW; ++i) cw[rt][i] = cn[rt][i];
     }
   }
 }
 
 using DqFn = void (*)(DqArgs);
 
+template <bool FAST>
 DqFn pick_dq(int bw) {
   switch (bw) {
-    case 2: return tq_dequant_kernel<2>;
-    case 3: return tq_dequant_kernel<3>;
-    case 4: return tq_dequant_kernel<4>;
-    case 5: return tq_dequant_kernel<5>;
-    case 6: return tq_dequant_kernel<6>;
-    case 8: return tq_dequant_kernel<8>;
+    case 2: return tq_dequant_kernel<2, FAST>;
+    case 3: return tq_dequant_kernel<3, FAST>;
+    case 4: return tq_dequant_kernel<4, FAST>;
+    case 5: return tq_dequant_kernel<5, FAST>;
+    case 6: return tq_dequant_kernel<6, FAST>;
+    case 8: return tq_dequant_kernel<8, FAST>;
   }
   return nullptr;
 }
 
-int launch_dq(DqArgs& a, int bw, hipStream_t st, const char* what) {
+int launch_dq(DqArgs& a, int bw, int fast, hipStream_t st, const char* what) {
   if (a.N == 0) return WN_OK;
-  const DqFn fn = pick_dq(bw);
+  const DqFn fn = fast ? pick_dq<true>(bw) : pick_dq<false>(bw);
   WN_REQUIRE(fn, WN_E_UNSUPPORTED, "%s: bit width %d not compiled", what, bw);
   int dev = 0, cus = 0;
   (void)hipGetDevice(&dev);
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (cus <= 0) cus = 256;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDqWaves * 64, 0) != hipSuccess || per_cu < 1)
+    per_cu = 1;
   const int64_t want = (a.N + 32 * kDqWaves - 1) / (32 * kDqWaves);
-  const int64_t grid = want < 2 * int64_t(cus) ? want : 2 * int64_t(cus);
+  const int64_t grid = want < int64_t(per_cu) * cus ? want : int64_t(per_cu) * cus;
   hipLaunchKernelGGL(fn, dim3(unsigned(grid)), dim3(kDqWaves * 64), 0, st, a);
   return check_launch(what);
 }
@@ -287,7 +349,7 @@ using namespace wn;
 
 extern "C" int wn_tq_dequant(const uint8_t* packed, const uint16_t* norms, int64_t planes, int64_t L,
                              int64_t plane_rows, const float* centroids, const float* pi, int bw, int D, void* out,
-                             int out_dtype, void* stream) {
+                             int out_dtype, int fast, void* stream) {
   clear_error();
   WN_REQUIRE(D == kDqD, WN_E_UNSUPPORTED, "wn_tq_dequant: head_dim %d (128 only)", D);
   WN_REQUIRE(planes >= 0 && L >= 0 && plane_rows >= L, WN_E_INVALID,
@@ -297,6 +359,8 @@ extern "C" int wn_tq_dequant(const uint8_t* packed, const uint16_t* norms, int64
              "wn_tq_dequant: output dtype %d", out_dtype);
   if (planes == 0 || L == 0) return WN_OK;
   WN_REQUIRE(packed && norms && centroids && pi && out, WN_E_INVALID, "wn_tq_dequant: null pointer");
+  WN_REQUIRE(reinterpret_cast<uintptr_t>(packed) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+             WN_E_INVALID, "wn_tq_dequant: packed and out must be 16-byte aligned");
   DqArgs a{};
   a.packed = packed;
   a.norms = norms;
@@ -308,13 +372,14 @@ extern "C" int wn_tq_dequant(const uint8_t* packed, const uint16_t* norms, int64
   a.plane_rows = plane_rows;
   a.table = nullptr;
   a.out_dtype = out_dtype;
-  return launch_dq(a, bw, static_cast<hipStream_t>(stream), "wn_tq_dequant");
+  return launch_dq(a, bw, fast, static_cast<hipStream_t>(stream), "wn_tq_dequant");
 }
 
 extern "C" int wn_dequantize_history(const uint8_t* pages, int64_t page_stride, int64_t head_stride,
                                      const uint16_t* norms, int64_t norm_page_stride, int64_t norm_head_stride,
                                      const int32_t* table_row, int L, int Hkv, int S, const float* centroids,
-                                     const float* pi, int bw, int D, void* out, int out_dtype, void* stream) {
+                                     const float* pi, int bw, int D, void* out, int out_dtype, int fast,
+                                     void* stream) {
   clear_error();
   WN_REQUIRE(D == kDqD, WN_E_UNSUPPORTED, "wn_dequantize_history: head_dim %d (128 only)", D);
   WN_REQUIRE(L >= 0 && Hkv > 0 && S > 0 && (S & (S - 1)) == 0, WN_E_INVALID,
@@ -324,6 +389,9 @@ extern "C" int wn_dequantize_history(const uint8_t* pages, int64_t page_stride, 
   if (L == 0) return WN_OK;
   WN_REQUIRE(pages && norms && table_row && centroids && pi && out, WN_E_INVALID,
              "wn_dequantize_history: null pointer");
+  WN_REQUIRE(reinterpret_cast<uintptr_t>(pages) % 16 == 0 && page_stride % 16 == 0 && head_stride % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(out) % 16 == 0,
+             WN_E_INVALID, "wn_dequantize_history: pages, their strides and out must be 16-byte aligned");
   DqArgs a{};
   a.packed = pages;
   a.norms = norms;
@@ -340,5 +408,5 @@ extern "C" int wn_dequantize_history(const uint8_t* pages, int64_t page_stride, 
   a.nsp = norm_page_stride;
   a.nsh = norm_head_stride;
   a.out_dtype = out_dtype;
-  return launch_dq(a, bw, static_cast<hipStream_t>(stream), "wn_dequantize_history");
+  return launch_dq(a, bw, fast, static_cast<hipStream_t>(stream), "wn_dequantize_history");
 }

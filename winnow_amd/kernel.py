@@ -6,9 +6,10 @@ gathers their centroids, applies the inverse rotation ``y @ Pi`` and the norm, a
 writes the result once in ``out``'s dtype (bf16 by default) -- one HIP kernel
 (``wn_tq_dequant``) on the matrix cores. Like the reference it reads a
 ``(..., MAXLEN, NB)`` cache buffer sliced to its first ``L`` positions in place
-(``kernel.py:46-51``). The reference's schedule keywords (``block_n``, ``allow_tf32``,
-``num_warps``, ``num_stages``) are accepted and ignored: the rotation always runs at
-near-fp32 accuracy.
+(``kernel.py:46-51``). ``allow_tf32`` keeps its meaning: False (the default) runs the
+rotation at near-fp32 accuracy, True trades it for speed (one fp16 product per term,
+2^-11 relative, the class of tf32). The other schedule keywords (``block_n``,
+``num_warps``, ``num_stages``) are accepted and ignored.
 """
 from __future__ import annotations
 
@@ -38,7 +39,7 @@ def tq_dequant(packed: torch.Tensor, norms: torch.Tensor, centroids: torch.Tenso
                bit_width: int, head_dim: int, out: torch.Tensor | None = None, block_n: int = 64,
                allow_tf32: bool = False, num_warps: int = 4, num_stages: int = 2) -> torch.Tensor:
     """``packed`` (..., NB) uint8 and ``norms`` (...) -> (..., head_dim) in ``out``'s dtype (kernel.py:78-115)."""
-    del block_n, allow_tf32, num_warps, num_stages  # schedule keywords of the Triton kernel
+    del block_n, num_warps, num_stages  # schedule keywords of the Triton kernel
     if not _lib.is_hip(packed):
         raise UnsupportedDevice(f"tq_dequant: tensor on {packed.device}, a HIP device is required")
     if bit_width not in SUPPORTED:
@@ -80,7 +81,7 @@ def tq_dequant(packed: torch.Tensor, norms: torch.Tensor, centroids: torch.Tenso
     with torch.cuda.device(packed.device):
         _lib.call("wn_tq_dequant", _lib.ptr(packed), _lib.ptr(norms), N // L, L, prow,
                   _lib.ptr(centroids.contiguous()), _lib.ptr(Pi.contiguous()), bit_width, head_dim,
-                  _lib.ptr(dst), _lib.DTYPE_CODE[dst.dtype], _lib.stream_of(packed.device))
+                  _lib.ptr(dst), _lib.DTYPE_CODE[dst.dtype], 1 if allow_tf32 else 0, _lib.stream_of(packed.device))
     if dst is not out:
         out.copy_(dst)
     return out

@@ -238,7 +238,7 @@ def dequantize_history(kv: pa.PackedKV, pages, norms, quant, b: int, dtype) -> t
             _lib.call("wn_dequantize_history", _lib.ptr(pages), pages.stride(0), pages.stride(1),
                       _lib.ptr(norms), norms.stride(0), norms.stride(1), _lib.ptr(kv.page_table[b]), L, Hkv, S,
                       _lib.ptr(quant.centroids), _lib.ptr(quant.Pi), quant.bit_width, D, _lib.ptr(out),
-                      _lib.DTYPE_CODE[out.dtype], _lib.stream_of(pages.device))
+                      _lib.DTYPE_CODE[out.dtype], 0, _lib.stream_of(pages.device))
         return out.to(dtype)
     table = kv.page_table_host if kv.page_table_host is not None else kv.page_table.cpu()
     ids = table[b, :(L + S - 1) // S].long().to(pages.device)
