@@ -20,13 +20,15 @@
 // The reduction order over the 128 input dims is permuted so that lane group
 // G = l/16 covers dims 32G .. 32G+31 over the four k-steps (k-step s: dims
 // 32G + 8s .. +8): a lane's codes are then one contiguous 4*bw-byte load per row.
-//   A  (output-dim tile t, k-step s): lane l holds Pi[32G + 8s .. +8][16t + l % 16],
+//   A  (output-dim tile t, k-step s): lane l holds Pi[32G + 8s .. +8][n] for the dim n
+//      of Pi^T row 16t + l % 16,
 //      one 16-byte LDS read from the transposed plane (padded rows, conflict free);
 //   B  (row tile, k-step s): lane l holds the codebook values of row l % 16 at dims
 //      32G + 8s .. +8, looked up from a byte-indexed pair table for 4-bit codes
 //      (one entry = hi or lo of the two codes of a byte) or per code;
-//   D  lane l holds output dims 16t + 4(l/16) .. +3 of row l % 16; the norm rescale
-//      and the cast happen on the way out, four values in one 8- or 16-byte store.
+//   D  lane l holds four output dims of row l % 16 per tile; the Pi^T rows are
+//      ordered so that tiles 2a and 2a+1 give it dims 32a + 8(l/16) .. +7, and the
+//      norm rescale and the cast happen on the way out, eight values per 16-byte store.
 #include "wn_common.h"
 
 namespace wn {
@@ -196,17 +198,28 @@ __device__ __forceinline__ void codes_to_a(const uint32_t (&w)[2], const DqTab<B
   al = __builtin_bit_cast(s16x8, make_uint4(l[0], l[1], l[2], l[3]));
 }
 
-// Four consecutive output elements at index i (a multiple of 4) in one store.
-__device__ __forceinline__ void store4(void* out, int64_t i, int dtype, f32x4 v) {
+// Eight consecutive output elements at index i (a multiple of 8) in one 16-byte
+// store (two for fp32).
+__device__ __forceinline__ void store8(void* out, int64_t i, int dtype, f32x4 u, f32x4 v) {
   if (dtype == WN_F32) {
-    *reinterpret_cast<float4*>(static_cast<float*>(out) + i) = make_float4(v[0], v[1], v[2], v[3]);
+    float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + i);
+    o[0] = make_float4(u[0], u[1], u[2], u[3]);
+    o[1] = make_float4(v[0], v[1], v[2], v[3]);
   } else if (dtype == WN_BF16) {
-    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + i) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + i) =
+        make_uint4(pack_bf16(u[0], u[1]), pack_bf16(u[2], u[3]), pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
   } else {
-    const uint32_t lo = uint32_t(f32_to_f16(v[0])) | (uint32_t(f32_to_f16(v[1])) << 16);
-    const uint32_t hi = uint32_t(f32_to_f16(v[2])) | (uint32_t(f32_to_f16(v[3])) << 16);
-    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + i) = make_uint2(lo, hi);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + i) =
+        make_uint4(pack_f16(u[0], u[1]), pack_f16(u[2], u[3]), pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
   }
+}
+
+// LDS row of output dim d in the Pi^T planes. Row 16t + 4g + j of output tile t
+// lands in lane group g, element j; placing dim d = 32a + 8g + 4b + j at tile 2a + b
+// gives lane group g the dims 32a + 8g .. +7 of each a: four 16-byte stores per row,
+// the four lane groups of a row covering 64 contiguous bytes per store.
+__device__ __forceinline__ int pit_row(int d) {
+  return (d & ~31) | (((d >> 2) & 1) << 4) | (((d >> 3) & 3) << 2) | (d & 3);
 }
 
 template <int BW, bool FAST>
@@ -215,21 +228,22 @@ __global__ __launch_bounds__(kDqWaves * 64) void tq_dequant_kernel(DqArgs a) {
   __shared__ __align__(16) uint16_t pit[PLANES][D * kPiRow];  // Pi^T: bf16 hi and lo, or fp16
   __shared__ DqTab<BW> tab;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // Pi^T planes: pit[h][n * kPiRow + k] = split(Pi[k][n])
+  // Pi^T planes: pit[h][pit_row(n) * kPiRow + k] = split(Pi[k][n])
   for (int i = tid; i < D * D / 2; i += kDqWaves * 64) {
     const int k = i / (D / 2), n2 = 2 * (i % (D / 2));  // two columns of row k
     const float2 x = *reinterpret_cast<const float2*>(a.pi + k * D + n2);
+    const int m = pit_row(n2);  // n2 even: dims n2, n2 + 1 sit in rows m, m + 1
     if constexpr (FAST) {
       const uint32_t h = pack_f16(x.x, x.y);
-      pit[0][n2 * kPiRow + k] = uint16_t(h & 0xffffu);
-      pit[0][(n2 + 1) * kPiRow + k] = uint16_t(h >> 16);
+      pit[0][m * kPiRow + k] = uint16_t(h & 0xffffu);
+      pit[0][(m + 1) * kPiRow + k] = uint16_t(h >> 16);
     } else {
       const uint32_t h = pack_bf16(x.x, x.y);
       const uint32_t l = pack_bf16(x.x - bf16_lo(h), x.y - bf16_hi(h));
-      pit[0][n2 * kPiRow + k] = uint16_t(h & 0xffffu);
-      pit[0][(n2 + 1) * kPiRow + k] = uint16_t(h >> 16);
-      pit[PLANES - 1][n2 * kPiRow + k] = uint16_t(l & 0xffffu);
-      pit[PLANES - 1][(n2 + 1) * kPiRow + k] = uint16_t(l >> 16);
+      pit[0][m * kPiRow + k] = uint16_t(h & 0xffffu);
+      pit[0][(m + 1) * kPiRow + k] = uint16_t(h >> 16);
+      pit[PLANES - 1][m * kPiRow + k] = uint16_t(l & 0xffffu);
+      pit[PLANES - 1][(m + 1) * kPiRow + k] = uint16_t(l >> 16);
     }
   }
   stage_dq_tab<BW, FAST>(a.cb, tab, tid);
@@ -298,7 +312,8 @@ __global__ __launch_bounds__(kDqWaves * 64) void tq_dequant_kernel(DqArgs a) {
       const float nv = f16_to_f32(nh[rt]);
       if (row < a.N) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) store4(a.out, row * D + 16 * t + 4 * g, a.out_dtype, acc[rt][t] * nv);
+        for (int c = 0; c < 4; ++c)
+          store8(a.out, row * D + 32 * c + 8 * g, a.out_dtype, acc[rt][2 * c] * nv, acc[rt][2 * c + 1] * nv);
       }
     }
 #pragma unroll
