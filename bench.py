@@ -307,7 +307,7 @@ def dequant_bench(dev, bws=(4, 6), reps: int = 50, check_rows: int = 2048, cpu_r
 
     Random packed bytes are valid codes at every width. Bytes per vector: NB packed +
     2 norm read, 2 D written. Timed with hipEvents over ``reps`` calls; the first
-    ``check_rows`` rows are checked against the float64 closed form, and the CPU
+    ``check_rows`` / 2 and the last ``check_rows`` / 2 rows are checked against the float64 closed form, and the CPU
     restatement (torch fp32 ``centroids[idx] @ Pi * n``) is timed on ``cpu_rows`` rows
     and scaled to N.
     """
@@ -342,12 +342,14 @@ def dequant_bench(dev, bws=(4, 6), reps: int = 50, check_rows: int = 2048, cpu_r
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) / reps * 1e3
         moved = N * (nb + 2 + 2 * D)
-        # float64 check of the first rows
-        pc = packed.view(N, nb)[:check_rows].cpu().numpy()
+        # float64 check of the first and the last rows (the first and the last pass of
+        # every wave's pipeline)
+        rows = torch.cat([torch.arange(check_rows // 2), torch.arange(N - check_rows // 2, N)]).to(dev)
+        pc = packed.view(N, nb)[rows].cpu().numpy()
         idx = torch.from_numpy(opk.unpack(pc, bw, D)).long()
         c64, pi64 = tq.centroids.cpu().double(), tq.Pi.cpu().double()
-        ref = (c64[idx] @ pi64) * norms.view(N)[:check_rows].cpu().double()[:, None]
-        got = out.view(N, D)[:check_rows].cpu().double()
+        ref = (c64[idx] @ pi64) * norms.view(N)[rows].cpu().double()[:, None]
+        got = out.view(N, D)[rows].cpu().double()
         err = (got - ref).abs().max().item()
         ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp(min=1e-30))) - 7)
         ok = bool(((got - ref).abs() <= ulp + (2e-3 if fast else 2e-5) * ref.abs().max()).all())

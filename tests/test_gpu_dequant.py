@@ -73,6 +73,33 @@ def test_tq_dequant_fast_mode_stays_in_the_tf32_class(bw):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("bw,shape", [(4, (1, 1, 5)), (3, (1,)), (4, (4, 3, 17011)), (3, (3, 2, 23459))])
+def test_tq_dequant_short_and_multi_pass_inputs(bw, shape):
+    """Fewer rows than one 32-row pass, and more rows than the persistent grid covers
+    in one pass per wave (up to 512 work-groups x 4 waves x 32 rows = 65,536), so every
+    wave runs its pipeline over several passes; the last pass is partial. Checked on
+    the first and last rows and a seeded sample in between."""
+    from winnow_amd.kernel import tq_dequant
+    D = 128
+    tq = oracle_quantizer(bw, D, 42)
+    g = torch.Generator().manual_seed(11 + bw)
+    N = int(np.prod(shape))
+    nb = D * bw // 8
+    packed = torch.randint(0, 256, (*shape, nb), dtype=torch.uint8, generator=g)
+    n16 = (torch.rand(*shape, generator=g) * 8 + 0.5).half()
+    out = torch.empty(*shape, D, device=DEV)
+    tq_dequant(packed.to(DEV), n16.to(DEV), tq.centroids.to(DEV), tq.Pi.to(DEV), bw, D, out=out)
+    rows = torch.unique(torch.cat([torch.arange(min(N, 2048)), torch.arange(max(0, N - 2048), N),
+                                   torch.randint(0, N, (4096,), generator=g)]))
+    pk = packed.reshape(N, nb)[rows].numpy()
+    idx = torch.from_numpy(opk.unpack(pk, bw, D)).long()
+    ref = (tq.centroids.double()[idx] @ tq.Pi.double()) * n16.reshape(N)[rows].double()[:, None]
+    got = out.reshape(N, D)[rows.to(DEV)].cpu().double()
+    err = (got - ref).abs().max().item()
+    assert err <= 2e-5 * ref.abs().max().item(), err
+
+
+@pytest.mark.gpu
 def test_tq_dequant_reads_a_sliced_cache_buffer():
     """A (B, H, MAXLEN, NB) buffer sliced to its first L positions is read in place."""
     from winnow_amd.kernel import tq_dequant

@@ -42,6 +42,7 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kDqD = 128;
 constexpr int kDqWaves = 4;
+constexpr int kDqTU = 2;  // output tiles per MFMA group
 constexpr int kPiRow = 136;  // bf16 per row of a Pi^T plane: 128 + 8 pad (272 B rows)
 
 struct DqArgs {
@@ -50,14 +51,15 @@ struct DqArgs {
   const float* pi;        // (D, D) fp32
   const float* cb;        // 2^bw fp32 centroids
   void* out;              // (N, D), row r at r * D
-  int64_t N;              // rows
+  int64_t N;              // rows (< 2^31, checked on the host)
   int64_t L;              // rows per plane (plane = r / L, position t = r % L)
+  uint32_t lm;            // r / L = (h + ((r - h) >> ls1)) >> ls2, h = umulhi(r, lm)
+  int ls1, ls2;
   int64_t plane_rows;     // strided mode: rows between consecutive planes in `packed`/`norms`
   const int32_t* table;   // paged mode (not null): page of position t is table[t >> log2S]
   int log2S;
   int64_t psp, psh;       // paged: packed page / plane strides, bytes
   int64_t nsp, nsh;       // paged: norm page / plane strides, elements
-  int out_dtype;
 };
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
@@ -69,18 +71,36 @@ __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
-// Source of row r (clamped to a valid row; the caller masks the stores).
-template <int NB>
-__device__ __forceinline__ void row_src(const DqArgs& a, int64_t r, const uint8_t*& p, const uint16_t*& n) {
-  r = r < a.N ? r : a.N - 1;
-  const int64_t plane = r / a.L, t = r - plane * a.L;
-  if (a.table) {
-    const int64_t page = a.table[t >> a.log2S];
-    const int64_t slot = t & ((int64_t(1) << a.log2S) - 1);
+// Plane and position of row r, clamped to a valid row (the caller masks the stores).
+// The plane index is a multiply-high by the host's magic number for L (exact for every
+// 32-bit r; Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, Figure 4.1).
+__device__ __forceinline__ void row_pos(const DqArgs& a, int64_t r, uint32_t& plane, uint32_t& t) {
+  const uint32_t r32 = uint32_t(r < a.N ? r : a.N - 1);
+  const uint32_t h = __umulhi(r32, a.lm);
+  plane = (h + ((r32 - h) >> a.ls1)) >> a.ls2;
+  t = r32 - plane * uint32_t(a.L);
+}
+
+// Paged mode: the page holding row r.
+__device__ __forceinline__ int32_t row_page(const DqArgs& a, int64_t r) {
+  uint32_t plane, t;
+  row_pos(a, r, plane, t);
+  return a.table[t >> a.log2S];
+}
+
+// Codes and norm of row r; in paged mode `page` is row_page(a, r).
+template <int NB, bool PAGED>
+__device__ __forceinline__ void row_src(const DqArgs& a, int64_t r, int32_t page, const uint8_t*& p,
+                                        const uint16_t*& n) {
+  uint32_t plane, t;
+  row_pos(a, r, plane, t);
+  if constexpr (PAGED) {
+    const int64_t slot = t & ((1u << a.log2S) - 1u);
     p = a.packed + page * a.psp + plane * a.psh + slot * NB;
     n = a.norms + page * a.nsp + plane * a.nsh + slot;
   } else {
-    const int64_t src = plane * a.plane_rows + t;
+    const int64_t src = int64_t(plane) * a.plane_rows + t;
     p = a.packed + src * NB;
     n = a.norms + src;
   }
@@ -200,12 +220,13 @@ __device__ __forceinline__ void codes_to_a(const uint32_t (&w)[2], const DqTab<B
 
 // Eight consecutive output elements at index i (a multiple of 8) in one 16-byte
 // store (two for fp32).
-__device__ __forceinline__ void store8(void* out, int64_t i, int dtype, f32x4 u, f32x4 v) {
-  if (dtype == WN_F32) {
+template <int OUT>
+__device__ __forceinline__ void store8(void* out, int64_t i, f32x4 u, f32x4 v) {
+  if constexpr (OUT == WN_F32) {
     float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + i);
     o[0] = make_float4(u[0], u[1], u[2], u[3]);
     o[1] = make_float4(v[0], v[1], v[2], v[3]);
-  } else if (dtype == WN_BF16) {
+  } else if constexpr (OUT == WN_BF16) {
     *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + i) =
         make_uint4(pack_bf16(u[0], u[1]), pack_bf16(u[2], u[3]), pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
   } else {
@@ -222,8 +243,8 @@ __device__ __forceinline__ int pit_row(int d) {
   return (d & ~31) | (((d >> 2) & 1) << 4) | (((d >> 3) & 3) << 2) | (d & 3);
 }
 
-template <int BW, bool FAST>
-__global__ __launch_bounds__(kDqWaves * 64) void tq_dequant_kernel(DqArgs a) {
+template <int BW, bool FAST, int OUT, bool PAGED>
+__global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void tq_dequant_kernel(DqArgs a) {
   constexpr int D = kDqD, NB = D * BW / 8, PLANES = FAST ? 1 : 2;
   __shared__ __align__(16) uint16_t pit[PLANES][D * kPiRow];  // Pi^T: bf16 hi and lo, or fp16
   __shared__ DqTab<BW> tab;
@@ -251,36 +272,42 @@ __global__ __launch_bounds__(kDqWaves * 64) void tq_dequant_kernel(DqArgs a) {
 
   const int g = lane >> 4, c16 = lane & 15;
   const int64_t passes = (a.N + 31) / 32, stride = int64_t(gridDim.x) * kDqWaves;
-  // codes 32g .. 32g+31 of row r0 + 16 rt + c16 and that row's norm, for a pass;
-  // rows past N read row N - 1, so the loads of the next pass are unconditional and
-  // the compiler's waits stay one pass behind
-  auto load_pass = [&](int64_t pass, uint32_t (&cw)[2][BW], uint16_t (&nh)[2]) {
+  // Loads and stores share one in-order counter (vmcnt), so a wait for a load also
+  // waits for every store issued before it. The pipeline is laid out so that no wait
+  // covers the stores of the pass just finished:
+  //  - two code buffers alternate (no register copies, which the compiler would make
+  //    wait for the loads that fill them), the next pass's codes are loaded before
+  //    this pass's stores, and paged mode loads page ids one more pass ahead;
+  //  - the first pass is peeled, so that the loop is entered, like its back edge,
+  //    with stores after the last loads;
+  //  - no store is conditional: rows past N read row N - 1 (every load is in
+  //    bounds) and store to row N - 1, the same bits that row's own lane writes
+  //    (equal inputs, equal MFMA column), so no path skips the stores.
+  auto page_ids = [&](int64_t pass, int32_t (&pg)[2]) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) pg[rt] = PAGED ? row_page(a, pass * 32 + 16 * rt + c16) : 0;
+  };
+  // codes 32g .. 32g+31 of row r0 + 16 rt + c16 and that row's norm
+  auto load_pass = [&](int64_t pass, const int32_t (&pg)[2], uint32_t (&cw)[2][BW], uint32_t (&nh)[2]) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const uint8_t* p;
       const uint16_t* n;
-      row_src<NB>(a, pass * 32 + 16 * rt + c16, p, n);
+      row_src<NB, PAGED>(a, pass * 32 + 16 * rt + c16, pg[rt], p, n);
       load_codes32<BW>(p, g, cw[rt]);
       nh[rt] = *n;
     }
   };
-  int64_t pass = int64_t(blockIdx.x) * kDqWaves + wave;
-  if (pass >= passes) return;
-  uint32_t cw[2][BW];
-  uint16_t nh[2];
-  load_pass(pass, cw, nh);
-  for (; pass < passes; pass += stride) {
-    uint32_t cn[2][BW];
-    uint16_t nn[2];
-    load_pass(pass + stride, cn, nn);  // the next pass's codes land while this one computes
-    const int64_t r0 = pass * 32;
-    f32x4 acc[2][8];
+  auto compute_pass = [&](const uint32_t (&cw)[2][BW], f32x4 (&acc)[2][8]) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
       for (int t = 0; t < 8; ++t) acc[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
+      // keeps the scheduler from hoisting the LDS reads of later k-steps (register
+      // pressure past two waves per SIMD)
+      __builtin_amdgcn_sched_barrier(0);
       s16x8 yh[2], yl[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
@@ -288,61 +315,125 @@ __global__ __launch_bounds__(kDqWaves * 64) void tq_dequant_kernel(DqArgs a) {
         step_codes<BW>(cw[rt], s, cs);
         codes_to_a<BW, FAST>(cs, tab, yh[rt], yl[rt]);
       }
+      // kDqTU output tiles at a time, each product type over all of them before the
+      // next, so that the three updates of an accumulator are 2 * kDqTU MFMAs apart
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int off = (16 * t + c16) * kPiRow + 32 * g + 8 * s;
-        const s16x8 ph = *reinterpret_cast<const s16x8*>(&pit[0][off]);
+      for (int t0 = 0; t0 < 8; t0 += kDqTU) {
+        s16x8 ph[kDqTU], pl[kDqTU];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          if constexpr (FAST) {
-            acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ph),
-                                                               __builtin_bit_cast(f16x8, yh[rt]), acc[rt][t], 0, 0, 0);
-          } else {
-            const s16x8 pl = *reinterpret_cast<const s16x8*>(&pit[PLANES - 1][off]);
-            acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, yh[rt], acc[rt][t], 0, 0, 0);
-            acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, yh[rt], acc[rt][t], 0, 0, 0);
-            acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, yl[rt], acc[rt][t], 0, 0, 0);
-          }
+        for (int u = 0; u < kDqTU; ++u) {
+          const int off = (16 * (t0 + u) + c16) * kPiRow + 32 * g + 8 * s;
+          ph[u] = *reinterpret_cast<const s16x8*>(&pit[0][off]);
+          if constexpr (!FAST) pl[u] = *reinterpret_cast<const s16x8*>(&pit[PLANES - 1][off]);
+        }
+        if constexpr (FAST) {
+#pragma unroll
+          for (int u = 0; u < kDqTU; ++u)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+              acc[rt][t0 + u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  __builtin_bit_cast(f16x8, ph[u]), __builtin_bit_cast(f16x8, yh[rt]), acc[rt][t0 + u], 0, 0, 0);
+        } else {
+#pragma unroll
+          for (int u = 0; u < kDqTU; ++u)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+              acc[rt][t0 + u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[u], yh[rt], acc[rt][t0 + u], 0, 0, 0);
+#pragma unroll
+          for (int u = 0; u < kDqTU; ++u)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+              acc[rt][t0 + u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl[u], yh[rt], acc[rt][t0 + u], 0, 0, 0);
+#pragma unroll
+          for (int u = 0; u < kDqTU; ++u)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+              acc[rt][t0 + u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[u], yl[rt], acc[rt][t0 + u], 0, 0, 0);
         }
       }
     }
+  };
+  auto store_pass = [&](int64_t pass, const uint32_t (&nh)[2], const f32x4 (&acc)[2][8]) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      const int64_t row = r0 + 16 * rt + c16;
-      const float nv = f16_to_f32(nh[rt]);
-      if (row < a.N) {
+      int64_t row = pass * 32 + 16 * rt + c16;
+      row = row < a.N ? row : a.N - 1;
+      const float nv = f16_to_f32(uint16_t(nh[rt]));
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          store8(a.out, row * D + 32 * c + 8 * g, a.out_dtype, acc[rt][2 * c] * nv, acc[rt][2 * c + 1] * nv);
-      }
+      for (int c = 0; c < 4; ++c)
+        store8<OUT>(a.out, row * D + 32 * c + 8 * g, acc[rt][2 * c] * nv, acc[rt][2 * c + 1] * nv);
     }
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      nh[rt] = nn[rt];
-#pragma unroll
-      for (int i = 0; i < BW; ++i) cw[rt][i] = cn[rt][i];
-    }
+  };
+  // One pass: page ids two passes ahead, codes of the next pass, then this pass.
+  auto half = [&](int64_t pass, const uint32_t (&cur)[2][BW], const uint32_t (&ncur)[2], uint32_t (&nxt)[2][BW],
+                  uint32_t (&nnxt)[2], const int32_t (&pg_nxt)[2], int32_t (&pg_after)[2]) {
+    page_ids(pass + 2 * stride, pg_after);
+    load_pass(pass + stride, pg_nxt, nxt, nnxt);
+    f32x4 acc[2][8];
+    compute_pass(cur, acc);
+    store_pass(pass, ncur, acc);
+  };
+
+  int64_t pass = int64_t(blockIdx.x) * kDqWaves + wave;
+  if (pass >= passes) return;
+  uint32_t b0[2][BW], b1[2][BW];
+  uint32_t n0[2], n1[2];  // fp16 bits, one register each (a packed pair would wait for both loads)
+  int32_t pa[2], pb[2];
+  page_ids(pass, pa);
+  load_pass(pass, pa, b0, n0);
+  page_ids(pass + stride, pb);
+  half(pass, b0, n0, b1, n1, pb, pa);
+  pass += stride;
+  // here b1 holds this pass's codes and pa the pages of the pass after it
+  while (pass < passes) {
+    half(pass, b1, n1, b0, n0, pa, pb);
+    pass += stride;
+    if (pass >= passes) break;
+    half(pass, b0, n0, b1, n1, pb, pa);
+    pass += stride;
   }
 }
 
 using DqFn = void (*)(DqArgs);
 
-template <bool FAST>
+template <bool FAST, int OUT, bool PAGED>
 DqFn pick_dq(int bw) {
   switch (bw) {
-    case 2: return tq_dequant_kernel<2, FAST>;
-    case 3: return tq_dequant_kernel<3, FAST>;
-    case 4: return tq_dequant_kernel<4, FAST>;
-    case 5: return tq_dequant_kernel<5, FAST>;
-    case 6: return tq_dequant_kernel<6, FAST>;
-    case 8: return tq_dequant_kernel<8, FAST>;
+    case 2: return tq_dequant_kernel<2, FAST, OUT, PAGED>;
+    case 3: return tq_dequant_kernel<3, FAST, OUT, PAGED>;
+    case 4: return tq_dequant_kernel<4, FAST, OUT, PAGED>;
+    case 5: return tq_dequant_kernel<5, FAST, OUT, PAGED>;
+    case 6: return tq_dequant_kernel<6, FAST, OUT, PAGED>;
+    case 8: return tq_dequant_kernel<8, FAST, OUT, PAGED>;
   }
   return nullptr;
 }
 
-int launch_dq(DqArgs& a, int bw, int fast, hipStream_t st, const char* what) {
+template <int OUT>
+DqFn pick_dq_out(int bw, int fast, bool paged) {
+  if (paged) return fast ? pick_dq<true, OUT, true>(bw) : pick_dq<false, OUT, true>(bw);
+  return fast ? pick_dq<true, OUT, false>(bw) : pick_dq<false, OUT, false>(bw);
+}
+
+// Magic number of r / L for every r < 2^32 (Granlund and Montgomery, Figure 4.1).
+void set_plane_divisor(DqArgs& a) {
+  const uint64_t d = uint64_t(a.L);
+  int l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  a.lm = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
+  a.ls1 = l < 1 ? l : 1;
+  a.ls2 = l > 1 ? l - 1 : 0;
+}
+
+int launch_dq(DqArgs& a, int bw, int fast, int out_dtype, hipStream_t st, const char* what) {
   if (a.N == 0) return WN_OK;
-  const DqFn fn = fast ? pick_dq<true>(bw) : pick_dq<false>(bw);
+  WN_REQUIRE(a.N < (int64_t(1) << 31) && a.L < (int64_t(1) << 31), WN_E_INVALID, "%s: %lld rows (2^31 max)", what,
+             (long long)a.N);
+  set_plane_divisor(a);
+  const bool paged = a.table != nullptr;
+  const DqFn fn = out_dtype == WN_F32    ? pick_dq_out<WN_F32>(bw, fast, paged)
+                  : out_dtype == WN_BF16 ? pick_dq_out<WN_BF16>(bw, fast, paged)
+                                         : pick_dq_out<WN_F16>(bw, fast, paged);
   WN_REQUIRE(fn, WN_E_UNSUPPORTED, "%s: bit width %d not compiled", what, bw);
   int dev = 0, cus = 0;
   (void)hipGetDevice(&dev);
@@ -386,8 +477,7 @@ extern "C" int wn_tq_dequant(const uint8_t* packed, const uint16_t* norms, int64
   a.L = L;
   a.plane_rows = plane_rows;
   a.table = nullptr;
-  a.out_dtype = out_dtype;
-  return launch_dq(a, bw, fast, static_cast<hipStream_t>(stream), "wn_tq_dequant");
+  return launch_dq(a, bw, fast, out_dtype, static_cast<hipStream_t>(stream), "wn_tq_dequant");
 }
 
 extern "C" int wn_dequantize_history(const uint8_t* pages, int64_t page_stride, int64_t head_stride,
@@ -422,6 +512,5 @@ extern "C" int wn_dequantize_history(const uint8_t* pages, int64_t page_stride, 
   a.psh = head_stride;
   a.nsp = norm_page_stride;
   a.nsh = norm_head_stride;
-  a.out_dtype = out_dtype;
-  return launch_dq(a, bw, fast, static_cast<hipStream_t>(stream), "wn_dequantize_history");
+  return launch_dq(a, bw, fast, out_dtype, static_cast<hipStream_t>(stream), "wn_dequantize_history");
 }
