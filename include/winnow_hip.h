@@ -27,6 +27,11 @@
  *   wn_pack / wn_unpack      turboquant_kv/packing.py:37-89
  *   wn_dequantize            turboquant_kv/cache.py:117-131
  *                            (TurboQuantMSE.dequantize_into)
+ *   wn_tq_dequant            turboquant_kv/kernel.py:78-115, csrc/tq_dequant.cu:186-215
+ *   wn_dequantize_history    turboquant_kv/packed_backend.py:192-208
+ *   wn_dense_decode_attention turboquant_kv/packed_attention_triton.py:190-201
+ *                            (dense_decode_attention, the matched unquantized
+ *                            baseline; DENSE branch of the kernel :101-127)
  */
 #ifndef WINNOW_HIP_H
 #define WINNOW_HIP_H
@@ -38,7 +43,7 @@
 extern "C" {
 #endif
 
-#define WN_ABI_VERSION 3
+#define WN_ABI_VERSION 4
 
 /* element types of floating-point tensors crossing the ABI */
 enum { WN_F32 = 0, WN_F16 = 1, WN_BF16 = 2 };
@@ -172,6 +177,33 @@ int wn_dequantize_history(const uint8_t* pages, int64_t page_stride, int64_t hea
                           const int32_t* table_row, int L, int Hkv, int S,
                           const float* centroids, const float* pi, int bw, int D,
                           void* out, int out_dtype, int fast, void* stream);
+
+/* Plan of wn_dense_decode_attention (as wn_decode_plan: requested_splits > 0 gives
+ * the reference's cdiv split of max_pages; 0 a balanced plan of persistent waves,
+ * pages_per_split = 0). page_dtype WN_BF16 or WN_F16. */
+int wn_dense_decode_plan(int B, int Hq, int Hkv, int D, int S, int page_dtype, int max_pages,
+                         int requested_splits, int* pages_per_split, int* num_splits);
+
+/* Decode attention over unquantized paged K/V (replaces dense_decode_attention,
+ * turboquant_kv/packed_attention_triton.py:190-201): pages (P, Hkv, S, D) of
+ * page_dtype (bf16 or fp16), the (S, D) rows of one (page, head) contiguous,
+ * strides in bytes; page_table, seq_lens, q, out, the scratch (sized by
+ * wn_decode_workspace_bytes with this plan) and the events as for
+ * wn_decode_attention. head_dim 128, n_rep <= 16, S a power of two >= 16, pages
+ * and their strides 16-byte aligned. Scores and the value sum carry fp32
+ * accuracy (q and the probabilities as 16-bit hi + lo pairs against exact
+ * 16-bit K and V). */
+int wn_dense_decode_attention(
+    const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+    const void* k_pages, int64_t k_stride_p, int64_t k_stride_h,
+    const void* v_pages, int64_t v_stride_p, int64_t v_stride_h, int page_dtype,
+    const int32_t* page_table, int64_t table_stride_b,
+    const int32_t* seq_lens,
+    void* out, int out_dtype,
+    void* workspace, int64_t workspace_bytes,
+    int B, int Hq, int Hkv, int D, int S, int max_pages,
+    float scale, int pages_per_split, int num_splits,
+    void* stream, void* ev_begin, void* ev_end);
 
 #ifdef __cplusplus
 }

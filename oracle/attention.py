@@ -11,10 +11,18 @@ CPU (torch fp32) restatement of ``turboquant_kv/packed_attention.py``:
 * ``pages_from_dense``                packed_attention.py:341-377
 * ``reconstruct_attention_f64``       float64 variant used for relative-L2 reports
   (the float64 operator check of model_contract.py:158-221)
+* ``dense_paged_attention_f64``       attention over unquantized paged K/V in float64:
+  the page gather + offset-causal softmax of packed_backend.py:229-246 (``_dense_sdpa``),
+  which the dense decode (packed_attention_triton.py:190-201) must match
 
 The algebraic pieces (``kv_head_for``, ``rotate_query``, ``rotate_output``,
 ``_online_update``, ``merge_partials``) are module attributes so tests can plant
 the reference's seven mutants here, on the CPU, and prove the checks catch them.
+
+``dense_paged_attention_f64`` is pinned against torch's scaled_dot_product_attention
+over the contiguous K/V the pages were scattered from (no paging on that side),
+with ragged, empty and one-token sequences, shuffled tables and GQA groups, and
+against planted paging mistakes.
 
 Pinned by (``tests/test_oracle_attention.py``): the three implementations agree
 with each other and with an unquantized softmax attention over the dequantized
@@ -294,6 +302,33 @@ def reconstruct_attention_f64(q: torch.Tensor, kv, scale: float) -> torch.Tensor
         v = (cv @ kv.v_quant.Pi.double()) * nv.double()[..., None]
         heads = torch.arange(Hq) // n_rep
         s = (q[b].double() @ k[heads].transpose(-1, -2)) * scale
+        out[b] = torch.softmax(s, -1) @ v[heads]
+    return out
+
+
+def dense_paged_attention_f64(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                              page_table: torch.Tensor, seq_lens: torch.Tensor, scale: float) -> torch.Tensor:
+    """q (B, Hq, Q, D) over pages (P, Hkv, S, D) -> (B, Hq, Q, D) float64.
+
+    Per sequence (packed_backend.py:229-246): gather its first ceil(L/S) pages, keep
+    L rows, query i sees keys j <= L - Q + i, head h reads kv head h // n_rep; a
+    sequence without tokens gives zeros.
+    """
+    B, Hq, Q, D = q.shape
+    P, Hkv, S, _ = k_pages.shape
+    n_rep = Hq // Hkv
+    out = torch.zeros(B, Hq, Q, D, dtype=torch.float64)
+    for b in range(B):
+        L = int(seq_lens[b])
+        if L == 0:
+            continue
+        ids = page_table[b, :(L + S - 1) // S].long()
+        hist = lambda pg: pg[ids].double().permute(1, 0, 2, 3).reshape(Hkv, -1, D)[:, :L]  # noqa: E731
+        k, v = hist(k_pages), hist(v_pages)
+        heads = torch.arange(Hq) // n_rep
+        s = (q[b].double() @ k[heads].transpose(-1, -2)) * scale                  # (Hq, Q, L)
+        visible = torch.arange(L)[None, :] <= (L - Q + torch.arange(Q))[:, None]  # (Q, L)
+        s = s.masked_fill(~visible, float("-inf"))
         out[b] = torch.softmax(s, -1) @ v[heads]
     return out
 

@@ -34,7 +34,8 @@ def test_header_declares_the_expected_entry_points():
     names = declared_symbols()
     for must in ("wn_abi_version", "wn_last_error", "wn_decode_plan", "wn_decode_workspace_bytes",
                  "wn_decode_attention", "wn_append_kv", "wn_quantize", "wn_pack", "wn_unpack",
-                 "wn_dequantize", "wn_tq_dequant", "wn_dequantize_history"):
+                 "wn_dequantize", "wn_tq_dequant", "wn_dequantize_history", "wn_dense_decode_plan",
+                 "wn_dense_decode_attention"):
         assert must in names
 
 
@@ -46,7 +47,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.wn_abi_version() == 3
+    assert lib.wn_abi_version() == 4
     assert isinstance(lib.wn_last_error(), bytes)
 
 

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libwinnow_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 WN_F32, WN_F16, WN_BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: WN_F32, torch.float16: WN_F16, torch.bfloat16: WN_BF16}
@@ -58,6 +58,17 @@ SIGNATURES = {
     "wn_unpack": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_p, _c_p]),
     "wn_dequantize": (_c_i, [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i, _c_i, _c_p, _c_i, _c_p]),
     "wn_tq_dequant": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i, _c_i, _c_p, _c_i, _c_i, _c_p]),
+    "wn_dense_decode_plan": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,
+                                    ctypes.POINTER(_c_i), ctypes.POINTER(_c_i)]),
+    "wn_dense_decode_attention": (_c_i, [
+        _c_p, _c_i, _c_i64, _c_i64,                 # q, dtype, strides
+        _c_p, _c_i64, _c_i64,                       # k pages, strides (bytes)
+        _c_p, _c_i64, _c_i64, _c_i,                 # v pages, strides, page dtype
+        _c_p, _c_i64, _c_p,                         # table, stride, seq_lens
+        _c_p, _c_i, _c_p, _c_i64,                   # out, out dtype, workspace
+        _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,         # B Hq Hkv D S max_pages
+        _c_f, _c_i, _c_i,                           # scale, pages_per_split, num_splits
+        _c_p, _c_p, _c_p]),                         # stream, ev_begin, ev_end
     "wn_dequantize_history": (_c_i, [
         _c_p, _c_i64, _c_i64,                       # pages, page stride, head stride
         _c_p, _c_i64, _c_i64,                       # norms, page stride, head stride

@@ -125,6 +125,16 @@ __global__ __launch_bounds__(256) void rotate_q_kernel(RotArgs a) {
   const int kvh = blockIdx.x, b = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
   if (a.chunk_prefix && kvh == 0 && b == 0 && z == 0) chunk_prefix_block(a.seq_lens, a.B, a.chunk_prefix);
   if (z == 0 && tid == 0) a.unit_meta[b * a.Hkv + kvh] = make_int2(0, 0);
+  if (!a.pi_k) {  // no rotation (dense pages): q_rot = scale * q
+    float* out = a.q_rot + (int64_t(b) * a.Hkv + kvh) * NREP * D + z * JQ;
+    for (int i = tid; i < NREP * JQ; i += 256) {
+      const int h = i / JQ, j = i % JQ;
+      out[h * D + j] =
+          h < a.n_rep ? a.scale * load_elem(a.q, b * a.qsb + int64_t(kvh * a.n_rep + h) * a.qsh + z * JQ + j, a.q_dtype)
+                      : 0.f;
+    }
+    return;
+  }
   const float4* src = reinterpret_cast<const float4*>(a.pi_k + z * JQ * D);
   for (int i = tid; i < JQ * D / 4; i += 256) {
     const float4 v = src[i];
@@ -350,9 +360,11 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
   __shared__ float av[D];
   const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
   const int lane = d & 63;
-  float pc[D];  // column d of Pi_V
+  float pc[D];  // column d of Pi_V (none: no output rotation, dense pages)
+  if (a.pi_v) {
 #pragma unroll
-  for (int k = 0; k < D; ++k) pc[k] = a.pi_v[k * D + d];
+    for (int k = 0; k < D; ++k) pc[k] = a.pi_v[k * D + d];
+  }
   const int2 meta = a.unit_meta[b * a.Hkv + kvh];
   const int64_t r0 = meta.x;
   const int n = meta.y;
@@ -393,8 +405,12 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
   __syncthreads();
   // out_j = sum_k a_k Pi_V[k, j]; (a / l) Pi_V == (a Pi_V) / l up to rounding
   float o = 0.f;
+  if (a.pi_v) {
 #pragma unroll
-  for (int k = 0; k < D; ++k) o = fmaf(av[k], pc[k], o);
+    for (int k = 0; k < D; ++k) o = fmaf(av[k], pc[k], o);
+  } else {
+    o = av[d];
+  }
   store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + d, a.out_dtype, o);
 }
 
@@ -662,6 +678,7 @@ extern "C" int wn_decode_attention(
   da.pages_per_split = pages_per_split;
   da.num_splits = num_splits;
   da.balanced = balanced ? 1 : 0;
+  da.qrows = max(sk.nrep, 1);
   // the row scan numbers its waves across work-groups of sk.wpb waves
   const int64_t waves = balanced ? int64_t(num_splits) : int64_t(num_splits) * Hkv * B;
   const dim3 grid = sk.rows ? dim3(unsigned((waves + sk.wpb - 1) / sk.wpb)) : dim3(num_splits, Hkv, B);
@@ -675,4 +692,112 @@ extern "C" int wn_decode_attention(
   else
     hipLaunchKernelGGL(merge_kernel<64>, dim3(n_rep, Hkv, B), dim3(64), 0, st, ma);
   return check_launch("wn_decode_attention");
+}
+
+// ---------------------------------------------------------------- dense pages
+
+extern "C" int wn_dense_decode_plan(int B, int Hq, int Hkv, int D, int S, int page_dtype, int max_pages,
+                                    int requested_splits, int* pages_per_split, int* num_splits) {
+  using namespace wn;
+  clear_error();
+  WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && max_pages >= 0, WN_E_INVALID,
+             "wn_dense_decode_plan: bad sizes B=%d Hq=%d Hkv=%d max_pages=%d", B, Hq, Hkv, max_pages);
+  WN_REQUIRE(pages_per_split && num_splits, WN_E_INVALID, "wn_dense_decode_plan: null output");
+  (void)D;
+  (void)S;
+  const int mp = max_pages > 0 ? max_pages : 1;
+  if (requested_splits > 0) {  // packed_attention_triton.py:211-216, as for packed pages
+    const int ns = requested_splits < mp ? requested_splits : mp;
+    *num_splits = ns;
+    *pages_per_split = (mp + ns - 1) / ns;
+    return WN_OK;
+  }
+  const SplitKernel sk = pick_dense_scan(page_dtype);
+  WN_REQUIRE(sk.fn, WN_E_UNSUPPORTED, "wn_dense_decode_plan: page dtype %d (bf16 or fp16)", page_dtype);
+  const int w = resident_waves(sk);
+  WN_REQUIRE(w > 0, WN_E_LAUNCH, "wn_dense_decode_plan: cannot query the device occupancy");
+  *pages_per_split = 0;
+  *num_splits = w;
+  return WN_OK;
+}
+
+extern "C" int wn_dense_decode_attention(
+    const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+    const void* k_pages, int64_t k_stride_p, int64_t k_stride_h,
+    const void* v_pages, int64_t v_stride_p, int64_t v_stride_h, int page_dtype,
+    const int32_t* page_table, int64_t table_stride_b, const int32_t* seq_lens,
+    void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
+    int B, int Hq, int Hkv, int D, int S, int max_pages, float scale, int pages_per_split, int num_splits,
+    void* stream, void* ev_begin, void* ev_end) {
+  using namespace wn;
+  clear_error();
+  WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, WN_E_INVALID,
+             "dense decode: need B>=0, Hq%%Hkv==0 (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
+  const int n_rep = Hq / Hkv;
+  WN_REQUIRE(n_rep <= 16, WN_E_UNSUPPORTED, "dense decode: n_rep=%d > 16 not compiled", n_rep);
+  WN_REQUIRE(D == 128, WN_E_UNSUPPORTED, "dense decode: head_dim %d not compiled (128)", D);
+  WN_REQUIRE(is_pow2(S) && S >= 16, WN_E_UNSUPPORTED, "dense decode: page size %d (a power of two >= 16)", S);
+  WN_REQUIRE(q_dtype >= WN_F32 && q_dtype <= WN_BF16 && out_dtype >= WN_F32 && out_dtype <= WN_BF16,
+             WN_E_INVALID, "dense decode: dtype codes %d/%d", q_dtype, out_dtype);
+  const SplitKernel sk = pick_dense_scan(page_dtype);
+  WN_REQUIRE(sk.fn, WN_E_UNSUPPORTED, "dense decode: page dtype %d (bf16 or fp16)", page_dtype);
+  const bool balanced = pages_per_split == 0;
+  WN_REQUIRE(num_splits > 0 && pages_per_split >= 0 &&
+                 (balanced || int64_t(pages_per_split) * num_splits >= int64_t(max_pages)),
+             WN_E_INVALID, "dense decode: plan %d x %d does not cover %d pages", num_splits, pages_per_split,
+             max_pages);
+  if (B == 0) return WN_OK;
+  WN_REQUIRE(q && k_pages && v_pages && page_table && seq_lens && out, WN_E_INVALID, "dense decode: null operand");
+  WN_REQUIRE(aligned(k_pages, 16) && aligned(v_pages, 16) && k_stride_p % 16 == 0 && k_stride_h % 16 == 0 &&
+                 v_stride_p % 16 == 0 && v_stride_h % 16 == 0,
+             WN_E_INVALID, "dense decode: pages need 16-byte aligned bases and strides");
+  WN_REQUIRE(k_stride_h >= int64_t(S) * D * 2 && v_stride_h >= int64_t(S) * D * 2, WN_E_INVALID,
+             "dense decode: head stride smaller than one (S, D) page block");
+  RotFn rot = pick_rot<128>(pad_nrep(n_rep));
+  WN_REQUIRE(rot, WN_E_UNSUPPORTED, "dense decode: n_rep=%d", n_rep);
+
+  const WsLayout lay = ws_layout(B, Hq, Hkv, D, pages_per_split, num_splits);
+  WN_REQUIRE(workspace && workspace_bytes >= lay.total && aligned(workspace, 256), WN_E_WORKSPACE,
+             "dense decode: workspace needs %lld bytes, 256-aligned (got %lld)", (long long)lay.total,
+             (long long)workspace_bytes);
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int32_t* prefix = balanced ? reinterpret_cast<int32_t*>(ws + lay.prefix) : nullptr;
+  int2* meta = reinterpret_cast<int2*>(ws + lay.meta);
+  // scores in log2 units: q_rot = scale * log2(e) * q, no rotation
+  RotArgs ra{q, q_stride_b, q_stride_h, nullptr, reinterpret_cast<float*>(ws + lay.qrot), seq_lens, prefix, meta,
+             float(double(scale) * 1.4426950408889634), B, Hkv, n_rep, q_dtype};
+  hipLaunchKernelGGL(rot, dim3(Hkv, B, 4), dim3(256), 0, st, ra);
+
+  DecodeArgs da{};
+  da.q_rot = ra.q_rot;
+  da.k_pages = static_cast<const uint8_t*>(k_pages);
+  da.v_pages = static_cast<const uint8_t*>(v_pages);
+  da.table = page_table;
+  da.seq_lens = seq_lens;
+  da.part_acc = reinterpret_cast<float*>(ws + lay.acc);
+  da.part_ml = reinterpret_cast<float*>(ws + lay.ml);
+  da.ksp = k_stride_p;
+  da.ksh = k_stride_h;
+  da.vsp = v_stride_p;
+  da.vsh = v_stride_h;
+  da.tsb = table_stride_b;
+  da.chunk_prefix = prefix;
+  da.unit_meta = meta;
+  da.B = B;
+  da.Hkv = Hkv;
+  da.n_rep = n_rep;
+  da.log2S = ilog2(S);
+  da.pages_per_split = pages_per_split;
+  da.num_splits = num_splits;
+  da.balanced = balanced ? 1 : 0;
+  da.qrows = pad_nrep(n_rep);
+  const int64_t waves = balanced ? int64_t(num_splits) : int64_t(num_splits) * Hkv * B;
+  if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
+  hipLaunchKernelGGL(sk.fn, dim3(unsigned((waves + sk.wpb - 1) / sk.wpb)), dim3(sk.block), 0, st, da);
+  if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
+
+  MergeArgs ma{da.part_acc, da.part_ml, nullptr, meta, out, out_dtype, Hq, Hkv, n_rep, 1};
+  hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep, Hkv, B), dim3(128), 0, st, ma);
+  return check_launch("wn_dense_decode_attention");
 }

@@ -24,6 +24,7 @@ struct DecodeArgs {
   int2* unit_meta;              // (B*Hkv): first partial row and partial count of each (sequence, kv head)
   int B, Hkv, n_rep, log2S, pages_per_split, num_splits;
   int balanced;  // 1: persistent waves share the flattened chunk space (pages_per_split unused)
+  int qrows;     // rows of q_rot per kv head
 };
 
 using SplitFn = void (*)(DecodeArgs);
@@ -43,5 +44,10 @@ struct SplitKernel {
 // splits or balanced persistent waves), or an empty SplitKernel when
 // (bw_k, bw_v, n_rep) is not compiled.
 SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep);
+
+// Dense-page scan (bf16 or fp16 pages of head_dim 128, up to 16 query heads per kv
+// head, page size >= 16) on the row scan's work plan, or an empty SplitKernel for
+// another page dtype.
+SplitKernel pick_dense_scan(int page_dtype);
 
 }  // namespace wn

@@ -296,3 +296,89 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
             float(scale), pps, ns,
             _lib.stream_of(q.device), ev0, ev1)
     return out
+
+
+DENSE_PAGE_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def dense_plan_for(q: torch.Tensor, kv: DenseKV, num_splits: int | None = None):
+    """(pages_per_split, num_splits) of the dense decode for this query and handle
+    (wn_dense_decode_plan): a balanced plan of persistent waves unless ``num_splits``."""
+    B, Hq, _, D = q.shape
+    pps, ns = ctypes.c_int(0), ctypes.c_int(0)
+    with torch.cuda.device(q.device):
+        _lib.call("wn_dense_decode_plan", B, Hq, kv.num_kv_heads, D, kv.page_size,
+                  _lib.DTYPE_CODE[kv.k_pages.dtype], kv.page_table.shape[1], int(num_splits or 0),
+                  ctypes.byref(pps), ctypes.byref(ns))
+    return pps.value, ns.value
+
+
+def dense_decode_attention(q: torch.Tensor, kv: DenseKV, scale: float, *,
+                           num_splits: int | None = None, allow_tf32: bool = False,
+                           num_warps: int = 4, num_stages: int = 2, pages_per_iter: int = 1,
+                           out_dtype: torch.dtype | None = None,
+                           workspace: torch.Tensor | None = None,
+                           timing_events=None) -> torch.Tensor:
+    """Unquantized paged decode on the packed decode's schedule, the matched baseline
+    (packed_attention_triton.py:190-201): q (B, Hq, 1, D) -> (B, Hq, 1, D) in q.dtype.
+
+    Pages (P, Hkv, S, D) bf16 or fp16. Errors before any launch, as the reference's
+    (``UnsupportedLayout``): a query of more than one token or off the GPU, a page size
+    or head dim that is not a power of two, non-unit element stride, K and V strides
+    that differ; and what this build does not compile (head_dim other than 128, page
+    size below 16, more than 16 query heads per kv head, fp32 pages). The schedule
+    keywords behave as in ``packed_decode_attention``.
+    """
+    del allow_tf32, num_warps, num_stages
+    if pages_per_iter < 1 or pages_per_iter & (pages_per_iter - 1):
+        raise UnsupportedLayout("pages_per_iter must be a power of two >= 1")
+    if q.dim() != 4 or q.shape[2] != 1 or not _lib.is_hip(q):
+        raise UnsupportedLayout("dense kernel: HIP decode only (one query token, tensors on the GPU)")
+    if not _pow2(kv.page_size) or not _pow2(kv.head_dim) or kv.k_pages.stride(-1) != 1 \
+            or kv.v_pages.stride() != kv.k_pages.stride():
+        raise UnsupportedLayout("dense kernel: unsupported page layout")
+    B, Hq, _, D = q.shape
+    Hkv = kv.num_kv_heads
+    if D != 128 or kv.head_dim != D or kv.k_pages.shape[-1] != D:
+        raise UnsupportedLayout(f"dense kernel: head_dim {D} (128 compiled)")
+    if Hq % Hkv or Hq // Hkv > MAX_N_REP:
+        raise UnsupportedLayout(f"dense kernel: {Hq} query heads over {Hkv} kv heads")
+    if kv.page_size < 16:
+        raise UnsupportedLayout(f"dense kernel: page size {kv.page_size} (>= 16 compiled)")
+    if kv.k_pages.dtype not in DENSE_PAGE_DTYPES or kv.v_pages.dtype != kv.k_pages.dtype:
+        raise UnsupportedLayout(f"dense kernel: pages {kv.k_pages.dtype}/{kv.v_pages.dtype} (bf16 or fp16)")
+    if kv.k_pages.stride(-2) != D:
+        raise UnsupportedLayout("dense kernel: the rows of a (page, head) block must be contiguous")
+    if kv.page_table.dtype != torch.int32 or kv.seq_lens.dtype != torch.int32 \
+            or kv.page_table.stride(-1) != 1 or not kv.seq_lens.is_contiguous():
+        raise UnsupportedLayout("dense kernel: page_table and seq_lens must be contiguous int32")
+    for t in (kv.k_pages, kv.v_pages, kv.page_table, kv.seq_lens):
+        if t.device != q.device:
+            raise UnsupportedLayout(f"dense kernel: operand on {t.device}, query on {q.device}")
+    max_pages = kv.page_table.shape[1]
+    pps, ns = dense_plan_for(q, kv, num_splits)
+    out_dtype = out_dtype or q.dtype
+    if out_dtype not in _lib.DTYPE_CODE:
+        raise UnsupportedLayout(f"output dtype {out_dtype} is not supported")
+    out = torch.empty(B, Hq, 1, D, dtype=out_dtype, device=q.device)
+    need = workspace_bytes(B, Hq, Hkv, D, pps, ns)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    elif workspace.numel() * workspace.element_size() < need or workspace.device != q.device:
+        raise UnsupportedLayout(f"workspace needs {need} bytes on {q.device}")
+    ev0, ev1 = timing_events or (None, None)
+    qv = q[:, :, 0]
+    es = kv.k_pages.element_size()
+    with torch.cuda.device(q.device):
+        _lib.call(
+            "wn_dense_decode_attention",
+            _lib.ptr(qv), _lib.DTYPE_CODE[q.dtype], qv.stride(0), qv.stride(1),
+            _lib.ptr(kv.k_pages), kv.k_pages.stride(0) * es, kv.k_pages.stride(1) * es,
+            _lib.ptr(kv.v_pages), kv.v_pages.stride(0) * es, kv.v_pages.stride(1) * es,
+            _lib.DTYPE_CODE[kv.k_pages.dtype],
+            _lib.ptr(kv.page_table), kv.page_table.stride(0), _lib.ptr(kv.seq_lens),
+            _lib.ptr(out), _lib.DTYPE_CODE[out_dtype],
+            _lib.ptr(workspace), workspace.numel() * workspace.element_size(),
+            B, Hq, Hkv, D, kv.page_size, max_pages, float(scale), pps, ns,
+            _lib.stream_of(q.device), ev0, ev1)
+    return out
