@@ -191,7 +191,7 @@ def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
             cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "run", "--",
                    sys.executable, str(ROOT / "bench.py"), "--config", str(cfg), "--steps", "3", "--warmup", "1",
                    "--settle", "0", "--parity", "off", "--cpu-baseline", "off", "--traffic", "off", "--append", "off",
-                   "--dequant", "off",
+                   "--dequant", "off", "--dense", "off",
                    "--copy-peak", "on"]
             try:
                 subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
@@ -219,6 +219,78 @@ def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
                             "bytes_per_launch": statistics.fmean(scan) * 1024 * factor}
     out["bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
     return out
+
+
+def dense_bench(c, lens, q, dev, steps: int = 30, warmup: int = 5, copies: int = 2, check_len: int = 2048):
+    """The matched unquantized baseline (dense_decode_attention, packed_attention_triton.py:190-201;
+    the reference's ``dense_paged`` arm, bench_packed_attention.py:101-117) at the same
+    batch, heads, lengths, page size and query: bf16 pages (P, Hkv, S, D), ~N(0, 1),
+    contiguous tables, ``copies`` pools rotated between steps as for the packed step.
+
+    Bytes per step: sum(L) * Hkv * 2 * D * 2 (K and V rows, the reference's dense
+    traffic model, bench_packed_attention.py:99). The scan kernel is timed with HIP
+    events on its stream, the step with events around the calls. Parity: two
+    sequences cut to ``check_len`` tokens against the float64 oracle on the same pages.
+    """
+    import torch
+    from oracle import attention as oa
+    from winnow_amd import packed_attention as pa
+
+    B, Hkv, D, S = len(lens), c["Hkv"], c["D"], c["S"]
+    need = [(L + S - 1) // S for L in lens]
+    P = sum(need)
+    table = torch.full((B, max(need)), -1, dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        table[b, :need[b]] = torch.arange(off, off + need[b], dtype=torch.int32)
+        off += need[b]
+    dtable, dl = table.to(dev), torch.tensor(lens, dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(99)
+    kvs = []
+    for _ in range(copies):
+        kp = torch.randn(P, Hkv, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+        vp = torch.randn(P, Hkv, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+        kvs.append(pa.DenseKV(kp, vp, dtable, dl, D))
+    scale = 1.0 / math.sqrt(D)
+    pps, ns = pa.dense_plan_for(q, kvs[0])
+    ws = torch.empty(pa.workspace_bytes(B, q.shape[1], Hkv, D, pps, ns), dtype=torch.uint8, device=dev)
+    for i in range(warmup):
+        pa.dense_decode_attention(q, kvs[i % copies], scale, workspace=ws)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in evs:
+        e0.record()
+        e1.record()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        e0, e1 = evs[i]
+        pa.dense_decode_attention(q, kvs[i % copies], scale, workspace=ws,
+                                  timing_events=(ctypes.c_void_p(e0.cuda_event), ctypes.c_void_p(e1.cuda_event)))
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    kern_ms = statistics.fmean(e0.elapsed_time(e1) for e0, e1 in evs)
+    nbytes = sum(lens) * Hkv * 2 * D * 2
+    # parity on two sequences cut to check_len tokens (same pages, shorter seq_lens)
+    seqs = [0, B - 1]
+    cut = torch.tensor([min(check_len, lens[b]) for b in seqs], dtype=torch.int32)
+    kv0 = kvs[0]
+    sub = pa.DenseKV(kv0.k_pages, kv0.v_pages, dtable[seqs], cut.to(dev), D)
+    got = pa.dense_decode_attention(q[seqs], sub, scale, out_dtype=torch.float32).cpu()
+    used = torch.unique(table[seqs, :(check_len + S - 1) // S].flatten()).long()
+    kpc = torch.zeros(P, Hkv, S, D, dtype=torch.bfloat16)
+    vpc = torch.zeros(P, Hkv, S, D, dtype=torch.bfloat16)
+    kpc[used], vpc[used] = kv0.k_pages[used.to(dev)].cpu(), kv0.v_pages[used.to(dev)].cpu()
+    ref = oa.dense_paged_attention_f64(q[seqs].float().cpu(), kpc, vpc, table[seqs], cut, scale)
+    err = (got.double() - ref).abs().max().item()
+    del kvs, ws
+    torch.cuda.empty_cache()
+    return {"us_per_step": ms * 1e3, "scan_kernel_us": kern_ms * 1e3, "bytes_per_step": nbytes,
+            "scan_GBps": nbytes / (kern_ms * 1e-3) / 1e9, "scan_frac_of_8TBps": nbytes / (kern_ms * 1e-3) / 8e12,
+            "tokens_per_s": B / (ms * 1e-3), "page_dtype": "bf16", "splits": ns, "pages_per_split": pps,
+            "parity_max_abs_err_vs_f64": err, "parity_within_2e-3_1e-3": bool(
+                torch.allclose(got.double(), ref, atol=2e-3, rtol=1e-3))}
 
 
 def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
@@ -476,6 +548,8 @@ def main(argv=None):
                          "(N = 1,048,576 vectors, 4- and 6-bit)")
     ap.add_argument("--dequant-only", action="store_true",
                     help="run only the dequantization timing and print its JSON (for profiling that kernel)")
+    ap.add_argument("--dense", choices=["on", "off"], default="on",
+                    help="time the matched unquantized paged decode (bf16 pages) on the same shape")
     ap.add_argument("--append", choices=["on", "off"], default="on",
                     help="time the quantize+pack append of 16 new tokens per sequence (BASELINE config 3)")
     ap.add_argument("--traffic", choices=["on", "off"], default="on",
@@ -554,6 +628,12 @@ def main(argv=None):
     if cp:
         log(f"copy peak: {cp}")
 
+    dense = None
+    if args.dense == "on":
+        dense = dense_bench(c, lens, q, dev)
+        dense["packed_speedup_per_step"] = dense["us_per_step"] / (ms * 1e3)
+        dense["packed_speedup_scan"] = dense["scan_kernel_us"] / (kern_ms * 1e3)
+        log(f"dense: {dense}")
     app = append_bench(c, lens, kvs[0].page_table_host, quants, dev) if args.append == "on" else None
     deq = {**dequant_bench(dev), **dequant_bench(dev, fast=True)} if args.dequant == "on" else None
     if app:
@@ -600,6 +680,7 @@ def main(argv=None):
                      "copy_peak_GBps": cp["GBps"] if cp else None,
                      "frac_of_copy_peak": achieved / cp["GBps"] if cp else None},
         "cpu_baseline": cpu,
+        "dense_baseline": dense,
         "append": app,
         "dequant": deq,
         "parity": par,
