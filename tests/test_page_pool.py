@@ -219,6 +219,13 @@ def test_decode_dispatch_has_no_host_fallback():
         pb.select_decode_backend(q, kv, "no_such_backend")
     with pytest.raises(pa.UnsupportedLayout):
         pa.packed_decode_attention(q, kv, 1.0)      # host tensors never reach a kernel
+    dense = pa.DenseKV(torch.zeros(2, 2, 16, 128, dtype=torch.bfloat16), torch.zeros(2, 2, 16, 128, dtype=torch.bfloat16),
+                       torch.zeros(1, 2, dtype=torch.int32), torch.tensor([20], dtype=torch.int32), 128)
+    qd = torch.zeros(1, 4, 1, 128)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        pb.select_decode_backend(qd, dense, "auto")
+    with pytest.raises(ValueError):
+        pb.select_decode_backend(qd, dense, "hip_packed")
 
 
 def test_unsupported_models_are_rejected():

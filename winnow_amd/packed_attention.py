@@ -301,6 +301,17 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
 DENSE_PAGE_DTYPES = (torch.bfloat16, torch.float16)
 
 
+def dense_supported(q: torch.Tensor, kv: DenseKV) -> bool:
+    """Whether ``dense_decode_attention`` compiles this shape (head_dim 128, page size
+    >= 16 and a power of two, bf16/fp16 pages with contiguous rows, <= 16 query heads
+    per kv head, one query token)."""
+    return (q.dim() == 4 and q.shape[2] == 1 and q.shape[-1] == 128 and kv.head_dim == 128
+            and kv.k_pages.dtype in DENSE_PAGE_DTYPES and kv.v_pages.dtype == kv.k_pages.dtype
+            and kv.page_size >= 16 and _pow2(kv.page_size) and kv.k_pages.stride(-1) == 1
+            and kv.k_pages.stride(-2) == 128 and kv.v_pages.stride() == kv.k_pages.stride()
+            and q.shape[1] % kv.num_kv_heads == 0 and q.shape[1] // kv.num_kv_heads <= MAX_N_REP)
+
+
 def dense_plan_for(q: torch.Tensor, kv: DenseKV, num_splits: int | None = None):
     """(pages_per_split, num_splits) of the dense decode for this query and handle
     (wn_dense_decode_plan): a balanced plan of persistent waves unless ``num_splits``."""

@@ -9,8 +9,9 @@ Drop-in for ``turboquant_kv/packed_backend.py``:
   happens on the device, so unlike the reference there is no per-layer
   device-to-host copy of the table (packed_backend.py:144).
 * ``winnow_packed_attention`` (packed_backend.py:260-290) serves decode with the
-  HIP operator and a prefill chunk by dequantizing the sequence's history on the
-  GPU and calling SDPA (packed_backend.py:192-226).
+  HIP operator (packed pages) or the HIP dense kernel (unquantized pages), and a
+  prefill chunk by dequantizing the sequence's history on the GPU and calling SDPA
+  (packed_backend.py:192-226).
 * ``make_pool``, ``quantizers_for``, ``select_decode_backend``, ``BACKEND_COUNTS``
   keep the reference's names and meaning. There is no host fallback: a decode on
   a non-HIP tensor raises.
@@ -30,7 +31,7 @@ from winnow_amd.quantizer import get_quantizer
 
 ATTN_NAME = "winnow_packed"
 SUPPORTED_ARCH = ("Qwen2ForCausalLM",)
-DECODE_BACKENDS = ("hip_packed", "reconstruct_sdpa")
+DECODE_BACKENDS = ("hip_packed", "reconstruct_sdpa", "hip_dense", "dense_sdpa")
 
 # How many attention calls each backend served (packed_backend.py:38-40).
 BACKEND_COUNTS: Counter = Counter()
@@ -208,8 +209,17 @@ def append_kv(k: torch.Tensor, v: torch.Tensor | None, k_tq, v_tq,
 def select_decode_backend(query: torch.Tensor, kv, requested: str) -> str:
     """Which operator serves a decode step; unsupported requests fail loudly (packed_backend.py:173-189)."""
     if isinstance(kv, pa.DenseKV):
-        if requested not in ("auto", "dense_sdpa"):
+        # packed_backend.py:175-179: the dense kernel where it runs, else dense SDPA
+        if requested == "dense_sdpa":
+            return requested
+        if requested not in ("auto", "triton_dense", "hip_dense"):
             raise ValueError(f"backend {requested!r} does not read dense pages")
+        if not _lib.is_hip(query):
+            raise RuntimeError("the dense decode operator needs a HIP device; there is no host fallback")
+        if pa.dense_supported(query, kv):
+            return "hip_dense"
+        if requested == "hip_dense":
+            raise ValueError("hip_dense does not compile this shape (head_dim 128, bf16/fp16 pages, S >= 16)")
         return "dense_sdpa"
     if requested in ("auto", "triton_packed", "hip_packed"):
         if not _lib.is_hip(query):
@@ -307,8 +317,14 @@ def winnow_packed_attention(module, query, key, value, attention_mask, dropout: 
                                       scaling=scaling, **kwargs)
     Q = query.shape[2]
     if isinstance(key, pa.DenseKV):
-        BACKEND_COUNTS[("prefill_" if Q > 1 else "") + "dense_sdpa"] += 1
-        return _dense_sdpa(query, key, scaling).transpose(1, 2).contiguous(), None
+        if Q > 1:
+            BACKEND_COUNTS["prefill_dense_sdpa"] += 1
+            return _dense_sdpa(query, key, scaling).transpose(1, 2).contiguous(), None
+        backend = select_decode_backend(query, key, getattr(key, "decode_backend", "auto"))
+        BACKEND_COUNTS[backend] += 1
+        out = (pa.dense_decode_attention(query, key, scaling) if backend == "hip_dense"
+               else _dense_sdpa(query, key, scaling))
+        return out.transpose(1, 2).contiguous(), None
     if Q > 1:
         BACKEND_COUNTS["prefill_reconstruct_sdpa"] += 1
         out = _reconstruct_sdpa(query, key, scaling)
