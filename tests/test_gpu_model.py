@@ -27,21 +27,13 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def model():
-    from transformers import Qwen2Config, Qwen2ForCausalLM
-    from winnow_amd import packed_backend as pb
-    torch.manual_seed(0)
-    cfg = Qwen2Config(vocab_size=128, hidden_size=512, intermediate_size=512, num_hidden_layers=2,
-                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=512,
-                      initializer_range=0.25, architectures=["Qwen2ForCausalLM"])
-    m = Qwen2ForCausalLM(cfg).eval().to(DEV)
-    pb.register()
-    return m
+    from tiny_qwen import tiny_qwen
+    return tiny_qwen(DEV)
 
 
-def _prompts(n, seed=1, lo=5, hi=70):
-    g = torch.Generator().manual_seed(seed)
-    return [torch.randint(0, 128, (int(torch.randint(lo, hi, (1,), generator=g)),), generator=g).tolist()
-            for _ in range(n)]
+def _prompts(n, seed=1):
+    from tiny_qwen import prompts
+    return prompts(n, seed)
 
 
 @torch.no_grad()
