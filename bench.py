@@ -560,7 +560,8 @@ def main(argv=None):
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); the "
-              f"decode path has no collective, see DESIGN.md for how it would shard", file=sys.stderr)
+              f"decode path has no collective: it would shard on the kv-head axis, one GPU's share "
+              f"being this measurement", file=sys.stderr)
         return 2
 
     import torch
