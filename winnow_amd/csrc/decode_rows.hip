@@ -88,10 +88,19 @@ __device__ __forceinline__ uint32_t put_byte1(uint32_t r, uint32_t x) {
 
 constexpr int kPairTableBytes = 256 * 32 * 8;  // 256 byte values x 32 lanes x float2
 
-// LDS bytes the codebook of BW-bit codes occupies: the replicated pair table for
-// 4-bit codes, else the plain 2^BW-entry table (padded to 16 bytes).
+// Widths read two codes per LDS access from a plain (not replicated) pair table of
+// 2^(2 BW) entries: 2, 3, 5 and 6 bits (128 B to 32 KB). 4-bit codes have the
+// replicated byte table; 8-bit pairs would need 512 KB.
 template <int BW>
-constexpr int table_bytes() { return BW == 4 ? kPairTableBytes : (4 << BW) < 16 ? 16 : (4 << BW); }
+constexpr bool pair_coded() { return BW == 2 || BW == 3 || BW == 5 || BW == 6; }
+
+// LDS bytes the codebook of BW-bit codes occupies: the replicated pair table for
+// 4-bit codes, the pair table of pair_coded widths, else the plain 2^BW-entry table
+// (padded to 16 bytes).
+template <int BW>
+constexpr int table_bytes() {
+  return BW == 4 ? kPairTableBytes : pair_coded<BW>() ? (8 << (2 * BW)) : (4 << BW) < 16 ? 16 : (4 << BW);
+}
 
 // A codebook in LDS as one lane reads it.
 template <int BW>
@@ -111,7 +120,9 @@ struct Tab<4> {
 
 // Stages a codebook into LDS at `dst` with all `nthr` threads of the work-group:
 // the replicated pair table for 4-bit codes (entry (b, r) at byte 256*b + 8*r holds
-// (c[b & 15], c[b >> 4])), else the plain table.
+// (c[b & 15], c[b >> 4])), the pair table of pair_coded widths (entry i holds
+// (c[i mod 2^BW], c[i >> BW]): two consecutive codes, LSB first, read as one
+// 2*BW-bit index), else the plain table.
 template <int BW>
 __device__ __forceinline__ void stage_table(const float* cb, char* dst, int tid, int nthr) {
   if constexpr (BW == 4) {
@@ -120,6 +131,9 @@ __device__ __forceinline__ void stage_table(const float* cb, char* dst, int tid,
       const int b = i >> 5;
       t[i] = make_float2(cb[b & 15], cb[b >> 4]);
     }
+  } else if constexpr (pair_coded<BW>()) {
+    float2* t = reinterpret_cast<float2*>(dst);
+    for (int i = tid; i < (1 << (2 * BW)); i += nthr) t[i] = make_float2(cb[i & ((1 << BW) - 1)], cb[i >> BW]);
   } else {
     float* t = reinterpret_cast<float*>(dst);
     for (int i = tid; i < (1 << BW); i += nthr) t[i] = cb[i];
@@ -128,7 +142,8 @@ __device__ __forceinline__ void stage_table(const float* cb, char* dst, int tid,
 
 // Codebook values of the 8 codes starting at bit BIT0 of the word array (LSB-first,
 // BW bits each) into v[0..7]: one SDWA move and one 8-byte LDS read per two 4-bit
-// codes; other widths extract each code and read the plain table.
+// codes; one 2*BW-bit extract and one 8-byte read per two codes of a pair_coded
+// width; 8-bit codes are read one by one from the plain table.
 template <int BW, int BIT0, int NW>
 __device__ __forceinline__ void lookup8(const uint32_t (&w)[NW], Tab<BW>& tab, float (&v)[8]) {
   if constexpr (BW == 4) {
@@ -137,6 +152,16 @@ __device__ __forceinline__ void lookup8(const uint32_t (&w)[NW], Tab<BW>& tab, f
       constexpr int k = decltype(kc)::value;
       tab.r[k] = put_byte1<k>(tab.r[k], w[BIT0 / 32]);
       const float2 e = *reinterpret_cast<const float2*>(tab.lds + tab.r[k]);
+      v[2 * k] = e.x;
+      v[2 * k + 1] = e.y;
+    });
+  } else if constexpr (pair_coded<BW>()) {
+    static_for<0, 4>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      constexpr int bit = BIT0 + 2 * BW * k, wi = bit >> 5, sh = bit & 31;
+      uint32_t x = w[wi] >> sh;
+      if constexpr (sh + 2 * BW > 32) x |= w[wi + 1] << (32 - sh);
+      const float2 e = reinterpret_cast<const float2*>(tab.t)[x & ((1u << (2 * BW)) - 1u)];
       v[2 * k] = e.x;
       v[2 * k + 1] = e.y;
     });
