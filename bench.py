@@ -132,7 +132,8 @@ def scan_kernel_name(c) -> str:
     """Symbol of the page-scan kernel wn_decode_attention launches for this shape."""
     scan = os.environ.get("WN_DECODE_SCAN", "rows") or "rows"
     n_rep = c["Hq"] // c["Hkv"]
-    if c["D"] == 128 and n_rep <= 8 and c["S"] >= 16 and scan != "valu":
+    fits = n_rep <= 8 or (n_rep <= 16 and n_rep % 2 == 0)   # even n_rep > 8: two virtual heads per kv head
+    if c["D"] == 128 and fits and c["S"] >= 16 and scan != "valu":
         return "decode_rows_kernel"
     return "decode_split_kernel"
 

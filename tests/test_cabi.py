@@ -59,7 +59,8 @@ def test_plan_reference_semantics(lib):
     assert decode_plan(2, 8, 4, 128, 16, 4, 4, 0, 1) == (1, 1)
     # automatic plans for shapes the vector-ALU scan serves (no device query): fixed
     # splits covering the table
-    for B, Hq, Hkv, D, mp in ((16, 128, 8, 128, 2048), (4, 128, 8, 128, 8192), (64, 8, 8, 64, 4096),
+    # (odd n_rep above 8 and head_dim 64; even n_rep up to 16 runs on the row scan)
+    for B, Hq, Hkv, D, mp in ((16, 72, 8, 128, 2048), (4, 88, 8, 128, 8192), (64, 8, 8, 64, 4096),
                               (1, 16, 1, 64, 64), (1, 1, 1, 64, 1)):
         pps, ns = decode_plan(B, Hq, Hkv, D, 16, 4, 4, mp)
         assert pps * ns >= mp and pps >= 1 and ns >= 1

@@ -53,9 +53,11 @@ def test_kernel_matches_oracle(name, B, Hq, Hkv, D, lens, S, bw, qs, splits):
 
 
 @pytest.mark.parametrize("bwk,bwv,Hq,Hkv", [(6, 6, 32, 8), (4, 6, 64, 8), (2, 2, 16, 4), (5, 5, 8, 4),
-                                             (6, 4, 32, 8), (4, 8, 32, 8), (4, 4, 32, 2), (4, 4, 32, 16)])
+                                             (6, 4, 32, 8), (4, 8, 32, 8), (4, 4, 32, 2), (4, 4, 32, 16),
+                                             (4, 4, 24, 2), (6, 6, 40, 4), (4, 6, 28, 2)])
 def test_widths_and_groups(bwk, bwv, Hq, Hkv):
-    """Every compiled width pair and GQA group size (n_rep 1..16), ragged lengths, S=16."""
+    """Every compiled width pair and GQA group size (n_rep 1..16; 10, 12, 14 and 16 run
+    the row scan as two virtual kv heads per kv head), ragged lengths, S=16."""
     print(f"widths {bwk}/{bwv} Hq={Hq} Hkv={Hkv}", flush=True)
     lens = (0, 1, 15, 16, 17, 333, 1024)
     q, kv = build(300 + bwk * 10 + bwv, len(lens), Hq, Hkv, 128, lens, 16, bwk, bw_v=bwv)

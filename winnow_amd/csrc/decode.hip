@@ -479,11 +479,18 @@ int pad_nrep(int n_rep) {
   return p;
 }
 
-// The scan wn_decode_attention runs for this shape.
+// The scan wn_decode_attention runs for this shape. An even n_rep of 10..16 runs on
+// the row scan as twice the kv heads with n_rep / 2 query heads each (kvshift 1):
+// q_rot rows, partial rows and output heads are laid out alike in both views, and
+// only the scan's page and norm addresses map a virtual head back to its kv head.
 SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v) {
   SplitKernel sk;
   const int n_rep = Hq / Hkv;
-  if (D == 128 && n_rep <= 8 && S >= 16 && rows_allowed()) sk = pick_split_rows(bw_k, bw_v, n_rep);
+  const int shift = (n_rep > 8 && n_rep <= 16 && n_rep % 2 == 0) ? 1 : 0;
+  if (D == 128 && (n_rep >> shift) <= 8 && S >= 16 && rows_allowed()) {
+    sk = pick_split_rows(bw_k, bw_v, n_rep >> shift);
+    sk.kvshift = shift;
+  }
   if (!sk.fn) {
     const int nrp = pad_nrep(n_rep);
     sk.fn = D == 128 ? pick_split<128>(bw_k, bw_v, nrp) : pick_split<64>(bw_k, bw_v, nrp);
@@ -529,7 +536,8 @@ WsLayout ws_layout(int B, int Hq, int Hkv, int D, int pages_per_split, int num_s
   l.qrot = 0;
   l.prefix = align256(int64_t(B) * Hkv * nrp * D * 4);
   l.meta = l.prefix + align256(int64_t(B + 1) * 4);
-  l.acc = l.meta + align256(int64_t(B) * Hkv * 8);
+  // unit_meta: one per kv head, or per virtual head when n_rep > 8 (choose_scan)
+  l.acc = l.meta + align256(int64_t(B) * Hkv * (n_rep > 8 ? 2 : 1) * 8);
   l.ml = l.acc + align256(rows * n_rep * D * 4);
   l.total = l.ml + align256(rows * n_rep * 2 * 4);
   return l;
@@ -644,9 +652,11 @@ extern "C" int wn_decode_attention(
   // the matrix-core scan keeps scores in log2 units: fold log2(e) into q_rot
   const float q_scale = sk.log2_units ? float(double(scale) * 1.4426950408889634) : scale;
   int2* meta = reinterpret_cast<int2*>(ws + lay.meta);
+  // from here on the kv heads are the scan's (virtual) ones
+  const int Hkv_s = Hkv << sk.kvshift, n_rep_s = n_rep >> sk.kvshift;
   RotArgs ra{q, q_stride_b, q_stride_h, pi_k, reinterpret_cast<float*>(ws + lay.qrot), seq_lens, prefix, meta,
-             q_scale, B, Hkv, n_rep, q_dtype};
-  hipLaunchKernelGGL(rot, dim3(Hkv, B, 4), dim3(256), 0, st, ra);
+             q_scale, B, Hkv_s, n_rep_s, q_dtype};
+  hipLaunchKernelGGL(rot, dim3(Hkv_s, B, 4), dim3(256), 0, st, ra);
 
   DecodeArgs da;
   da.q_rot = ra.q_rot;
@@ -672,25 +682,26 @@ extern "C" int wn_decode_attention(
   da.chunk_prefix = prefix;
   da.unit_meta = meta;
   da.B = B;
-  da.Hkv = Hkv;
-  da.n_rep = n_rep;
+  da.Hkv = Hkv_s;
+  da.n_rep = n_rep_s;
   da.log2S = ilog2(S);
   da.pages_per_split = pages_per_split;
   da.num_splits = num_splits;
   da.balanced = balanced ? 1 : 0;
   da.qrows = max(sk.nrep, 1);
+  da.kvshift = sk.kvshift;
   // the row scan numbers its waves across work-groups of sk.wpb waves
-  const int64_t waves = balanced ? int64_t(num_splits) : int64_t(num_splits) * Hkv * B;
-  const dim3 grid = sk.rows ? dim3(unsigned((waves + sk.wpb - 1) / sk.wpb)) : dim3(num_splits, Hkv, B);
+  const int64_t waves = balanced ? int64_t(num_splits) : int64_t(num_splits) * Hkv_s * B;
+  const dim3 grid = sk.rows ? dim3(unsigned((waves + sk.wpb - 1) / sk.wpb)) : dim3(num_splits, Hkv_s, B);
   if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
   hipLaunchKernelGGL(sk.fn, grid, dim3(sk.block), 0, st, da);
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
-  MergeArgs ma{da.part_acc, da.part_ml, pi_v, meta, out, out_dtype, Hq, Hkv, n_rep, sk.log2_units ? 1 : 0};
+  MergeArgs ma{da.part_acc, da.part_ml, pi_v, meta, out, out_dtype, Hq, Hkv_s, n_rep_s, sk.log2_units ? 1 : 0};
   if (D == 128)
-    hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep, Hkv, B), dim3(128), 0, st, ma);
+    hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep_s, Hkv_s, B), dim3(128), 0, st, ma);
   else
-    hipLaunchKernelGGL(merge_kernel<64>, dim3(n_rep, Hkv, B), dim3(64), 0, st, ma);
+    hipLaunchKernelGGL(merge_kernel<64>, dim3(n_rep_s, Hkv_s, B), dim3(64), 0, st, ma);
   return check_launch("wn_decode_attention");
 }
 

@@ -252,7 +252,7 @@ __device__ __forceinline__ void load_k(const DecodeArgs& a, int kvh, int lane, i
                                        RowBuf<BWK, BWV>& r) {
   constexpr int NBK = 16 * BWK, KW = RowBuf<BWK, BWV>::KW;
   const int slot = (c0 + lane) & ((1 << a.log2S) - 1);
-  const uint8_t* krow = a.k_pages + int64_t(pid_lane) * a.ksp + kvh * a.ksh + slot * NBK;
+  const uint8_t* krow = a.k_pages + int64_t(pid_lane) * a.ksp + (kvh >> a.kvshift) * a.ksh + slot * NBK;
 #pragma unroll
   for (int i = 0; i < NBK / 16; ++i) {
     const uint4 x = reinterpret_cast<const uint4*>(krow)[i];
@@ -261,8 +261,8 @@ __device__ __forceinline__ void load_k(const DecodeArgs& a, int kvh, int lane, i
     r.w[4 * i + 2] = x.z;
     r.w[4 * i + 3] = x.w;
   }
-  r.w[KW] = a.k_norms[int64_t(pid_lane) * a.knp + kvh * a.knh + slot];
-  r.w[KW + 1] = a.v_norms[int64_t(pid_lane) * a.vnp + kvh * a.vnh + slot];
+  r.w[KW] = a.k_norms[int64_t(pid_lane) * a.knp + (kvh >> a.kvshift) * a.knh + slot];
+  r.w[KW + 1] = a.v_norms[int64_t(pid_lane) * a.vnp + (kvh >> a.kvshift) * a.vnh + slot];
 }
 
 // V side of chunk [c0, c0+64): for every token quad q the BWV bytes of codes
@@ -279,7 +279,7 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, i
   static_for<0, 4>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     const int pid_j = __builtin_amdgcn_readlane(pid_lane, 16 * j);
-    const uint8_t* vj = a.v_pages + int64_t(pid_j) * a.vsp + kvh * a.vsh + ((c0 + 16 * j) & smask) * NBV + lane_off;
+    const uint8_t* vj = a.v_pages + int64_t(pid_j) * a.vsp + (kvh >> a.kvshift) * a.vsh + ((c0 + 16 * j) & smask) * NBV + lane_off;
     static_for<0, 4>([&](auto qc) {
       constexpr int qq = decltype(qc)::value;
       uint32_t t[VW];

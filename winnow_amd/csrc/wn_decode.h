@@ -25,6 +25,7 @@ struct DecodeArgs {
   int B, Hkv, n_rep, log2S, pages_per_split, num_splits;
   int balanced;  // 1: persistent waves share the flattened chunk space (pages_per_split unused)
   int qrows;     // rows of q_rot per kv head
+  int kvshift;   // the pages of (virtual) kv head h are those of kv head h >> kvshift
 };
 
 using SplitFn = void (*)(DecodeArgs);
@@ -36,6 +37,7 @@ struct SplitKernel {
   int nrep = 0;   // query-head rows per kv head the kernel reads from q_rot
   bool log2_units = false;  // scores/maxima in log2 units (q_rot scaled by log2 e)
   bool rows = false;        // the row-per-lane matrix-core scan (balanced plans allowed)
+  int kvshift = 0;          // 1: each kv head runs as two virtual heads of n_rep / 2 query heads
 };
 
 // Row-per-lane matrix-core page scan for head_dim 128, power-of-two page sizes
