@@ -68,7 +68,8 @@ const char* wn_last_error(void);
  * reference's num_splits, packed_attention_triton.py:211-216): *pages_per_split
  * = cdiv(max_pages, splits), one partial per (sequence, kv head, split).
  * requested_splits == 0 lets the library choose. Where the row-per-lane
- * matrix-core scan applies (head_dim 128, <= 8 query heads per kv head, page
+ * matrix-core scan applies (head_dim 128, <= 8 query heads per kv head or an
+ * even number up to 16, page
  * size >= 16) the plan is balanced: *pages_per_split = 0 and *num_splits = the
  * number of resident waves on the current device, which then share the
  * flattened (sequence, kv head, 64-token chunk) space equally, ragged batches

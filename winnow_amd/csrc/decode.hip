@@ -5,7 +5,8 @@
 //                        one block also writes the per-sequence chunk prefix the
 //                        balanced scan partitions by
 //   2. page scan         the row-per-lane matrix-core scan (decode_rows.hip) where
-//                        it applies (head_dim 128, <= 8 query heads per kv head),
+//                        it applies (head_dim 128, <= 8 query heads per kv head
+//                        or an even number up to 16),
 //                        else decode_split_kernel below: one work-group per
 //                        (split, kv head, sequence), score phase (lane = token),
 //                        online softmax, value phase (16 lanes per token row),

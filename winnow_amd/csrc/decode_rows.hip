@@ -1,6 +1,7 @@
 // Row-per-lane matrix-core page scan of the packed decode attention (head_dim 128,
-// power-of-two page size >= 16, up to eight query heads per kv head in one or two
-// groups of four), gfx950.
+// power-of-two page size >= 16, up to eight query heads per (virtual) kv head in one
+// or two groups of four; the host runs an even n_rep of 10..16 as two virtual kv
+// heads per kv head, kvshift), gfx950.
 //
 // Waves are independent of each other; the waves of a work-group only share the
 // codebook tables staged in LDS. With fixed splits a wave owns a range of pages of
