@@ -88,3 +88,31 @@ def test_argument_errors_are_reported_not_fatal(lib):
     # empty work is a successful no-op and clears the error
     _lib.call("wn_pack", None, 0, 128, 4, None, None)
     assert lib.wn_last_error() == b""
+
+
+def test_dequant_and_dense_entry_points_reject_before_any_launch(lib):
+    """Argument errors of the newer entry points come back as codes with a message,
+    before anything touches a device (no GPU here)."""
+    from winnow_amd import _lib
+    with pytest.raises(_lib.WinnowHipError, match="head_dim"):          # 64 is not compiled
+        _lib.call("wn_tq_dequant", None, None, 1, 4, 4, None, None, 4, 64, None, 0, 0, None)
+    with pytest.raises(_lib.WinnowHipError, match="bad sizes"):         # plane_rows < L
+        _lib.call("wn_tq_dequant", None, None, 1, 4, 3, None, None, 4, 128, None, 0, 0, None)
+    with pytest.raises(_lib.WinnowHipError, match="output dtype"):
+        _lib.call("wn_tq_dequant", None, None, 1, 4, 4, None, None, 4, 128, None, 9, 0, None)
+    with pytest.raises(_lib.WinnowHipError, match="null pointer"):
+        _lib.call("wn_tq_dequant", None, None, 1, 4, 4, None, None, 4, 128, None, 0, 0, None)
+    with pytest.raises(_lib.WinnowHipError, match="S=12"):              # S must be a power of two
+        _lib.call("wn_dequantize_history", None, 0, 0, None, 0, 0, None, 5, 2, 12, None, None, 4, 128,
+                  None, 0, 0, None)
+    dense = ("wn_dense_decode_attention", None, _lib.WN_BF16 if hasattr(_lib, "WN_BF16") else 2, 0, 0,
+             None, 0, 0, None, 0, 0)
+    with pytest.raises(_lib.WinnowHipError, match="n_rep"):             # 17 query heads per kv head
+        _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 1, 17, 1, 128, 16, 1, 1.0, 0, 1, None, None, None)
+    with pytest.raises(_lib.WinnowHipError, match="page dtype"):        # fp32 pages
+        _lib.call(*dense, 0, None, 0, None, None, 0, None, 0, 1, 4, 1, 128, 16, 1, 1.0, 0, 1, None, None, None)
+    with pytest.raises(_lib.WinnowHipError, match="page size"):
+        _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 1, 4, 1, 128, 8, 1, 1.0, 0, 1, None, None, None)
+    # no sequences: a successful no-op
+    _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 0, 4, 1, 128, 16, 1, 1.0, 0, 1, None, None, None)
+    assert lib.wn_last_error() == b""
