@@ -190,7 +190,7 @@ int wn_dense_decode_plan(int B, int Hq, int Hkv, int D, int S, int page_dtype, i
  * page_dtype (bf16 or fp16), the (S, D) rows of one (page, head) contiguous,
  * strides in bytes; page_table, seq_lens, q, out, the scratch (sized by
  * wn_decode_workspace_bytes with this plan) and the events as for
- * wn_decode_attention. head_dim 128, n_rep <= 16, S a power of two >= 16, pages
+ * wn_decode_attention. head_dim 64 or 128, n_rep <= 16, S a power of two >= 16, pages
  * and their strides 16-byte aligned. Scores and the value sum carry fp32
  * accuracy (q and the probabilities as 16-bit hi + lo pairs against exact
  * 16-bit K and V). */

@@ -6,8 +6,8 @@ SDPA over contiguous K/V) on the same bf16 / fp16 page values, at the tolerance 
 the packed decode: fp32 output within 2e-3 abs / 1e-3 rel. The case matrix: the
 reference's own test case (test_packed_attention_triton.py:153-173: B 3, Hq 28, Hkv
 4, lengths 33 / 0 / 70, shuffled tables, splits 1, 2, 3), every n_rep class up to
-16, page sizes 16 / 32 / 64, ragged lengths including 0, 1, 15, 16, 17, fp16 pages,
-bf16 output, long contexts, and the rejections.
+16, page sizes 16 / 32 / 64, ragged lengths including 0, 1, 15, 16, 17, head_dim 64
+and 128, fp16 pages, bf16 output, long contexts, and the rejections.
 """
 from __future__ import annotations
 
@@ -63,6 +63,21 @@ def test_dense_head_groups_and_page_sizes(Hq, Hkv, S):
     got = _run(q, kp, vp, table, sl, scale, out_dtype=torch.float32).cpu()
     ref = oa.dense_paged_attention_f64(q, kp, vp, table, sl, scale)
     assert torch.allclose(got.double(), ref, atol=ATOL, rtol=RTOL), (got.double() - ref).abs().max()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Hq,Hkv,S", [(8, 2, 16), (16, 1, 32), (14, 2, 64)])
+def test_dense_head_dim_64(Hq, Hkv, S):
+    lens = (0, 1, 17, 333, 1024)
+    kp, vp, table, sl = _pages(80 + Hq + S, lens, Hkv, S, D=64)
+    q = torch.randn(len(lens), Hq, 1, 64, generator=torch.Generator().manual_seed(Hq + S))
+    scale = 64 ** -0.5
+    got = _run(q, kp, vp, table, sl, scale, out_dtype=torch.float32).cpu()
+    ref = oa.dense_paged_attention_f64(q, kp, vp, table, sl, scale)
+    assert torch.allclose(got.double(), ref, atol=ATOL, rtol=RTOL), (got.double() - ref).abs().max()
+    for s in (1, 3):
+        got_s = _run(q, kp, vp, table, sl, scale, num_splits=s, out_dtype=torch.float32).cpu()
+        assert torch.allclose(got_s.double(), ref, atol=ATOL, rtol=RTOL)
 
 
 @pytest.mark.gpu

@@ -715,7 +715,6 @@ extern "C" int wn_dense_decode_plan(int B, int Hq, int Hkv, int D, int S, int pa
   WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && max_pages >= 0, WN_E_INVALID,
              "wn_dense_decode_plan: bad sizes B=%d Hq=%d Hkv=%d max_pages=%d", B, Hq, Hkv, max_pages);
   WN_REQUIRE(pages_per_split && num_splits, WN_E_INVALID, "wn_dense_decode_plan: null output");
-  (void)D;
   (void)S;
   const int mp = max_pages > 0 ? max_pages : 1;
   if (requested_splits > 0) {  // packed_attention_triton.py:211-216, as for packed pages
@@ -724,8 +723,9 @@ extern "C" int wn_dense_decode_plan(int B, int Hq, int Hkv, int D, int S, int pa
     *pages_per_split = (mp + ns - 1) / ns;
     return WN_OK;
   }
-  const SplitKernel sk = pick_dense_scan(page_dtype);
-  WN_REQUIRE(sk.fn, WN_E_UNSUPPORTED, "wn_dense_decode_plan: page dtype %d (bf16 or fp16)", page_dtype);
+  const SplitKernel sk = pick_dense_scan(page_dtype, D);
+  WN_REQUIRE(sk.fn, WN_E_UNSUPPORTED, "wn_dense_decode_plan: page dtype %d (bf16 or fp16), head_dim %d (64, 128)",
+             page_dtype, D);
   const int w = resident_waves(sk);
   WN_REQUIRE(w > 0, WN_E_LAUNCH, "wn_dense_decode_plan: cannot query the device occupancy");
   *pages_per_split = 0;
@@ -747,11 +747,11 @@ extern "C" int wn_dense_decode_attention(
              "dense decode: need B>=0, Hq%%Hkv==0 (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
   const int n_rep = Hq / Hkv;
   WN_REQUIRE(n_rep <= 16, WN_E_UNSUPPORTED, "dense decode: n_rep=%d > 16 not compiled", n_rep);
-  WN_REQUIRE(D == 128, WN_E_UNSUPPORTED, "dense decode: head_dim %d not compiled (128)", D);
+  WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "dense decode: head_dim %d not compiled (64, 128)", D);
   WN_REQUIRE(is_pow2(S) && S >= 16, WN_E_UNSUPPORTED, "dense decode: page size %d (a power of two >= 16)", S);
   WN_REQUIRE(q_dtype >= WN_F32 && q_dtype <= WN_BF16 && out_dtype >= WN_F32 && out_dtype <= WN_BF16,
              WN_E_INVALID, "dense decode: dtype codes %d/%d", q_dtype, out_dtype);
-  const SplitKernel sk = pick_dense_scan(page_dtype);
+  const SplitKernel sk = pick_dense_scan(page_dtype, D);
   WN_REQUIRE(sk.fn, WN_E_UNSUPPORTED, "dense decode: page dtype %d (bf16 or fp16)", page_dtype);
   const bool balanced = pages_per_split == 0;
   WN_REQUIRE(num_splits > 0 && pages_per_split >= 0 &&
@@ -765,7 +765,7 @@ extern "C" int wn_dense_decode_attention(
              WN_E_INVALID, "dense decode: pages need 16-byte aligned bases and strides");
   WN_REQUIRE(k_stride_h >= int64_t(S) * D * 2 && v_stride_h >= int64_t(S) * D * 2, WN_E_INVALID,
              "dense decode: head stride smaller than one (S, D) page block");
-  RotFn rot = pick_rot<128>(pad_nrep(n_rep));
+  RotFn rot = D == 128 ? pick_rot<128>(pad_nrep(n_rep)) : pick_rot<64>(pad_nrep(n_rep));
   WN_REQUIRE(rot, WN_E_UNSUPPORTED, "dense decode: n_rep=%d", n_rep);
 
   const WsLayout lay = ws_layout(B, Hq, Hkv, D, pages_per_split, num_splits);
@@ -810,6 +810,9 @@ extern "C" int wn_dense_decode_attention(
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
   MergeArgs ma{da.part_acc, da.part_ml, nullptr, meta, out, out_dtype, Hq, Hkv, n_rep, 1};
-  hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep, Hkv, B), dim3(128), 0, st, ma);
+  if (D == 128)
+    hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep, Hkv, B), dim3(128), 0, st, ma);
+  else
+    hipLaunchKernelGGL(merge_kernel<64>, dim3(n_rep, Hkv, B), dim3(64), 0, st, ma);
   return check_launch("wn_dense_decode_attention");
 }

@@ -5,15 +5,15 @@
 // balanced persistent waves over 64-token chunks, the same (acc, m, l) partials and
 // the same merge (no output rotation). Only the page scan differs.
 //
-// Pages are (P, Hkv, S, 128) bf16 or fp16, each (page, kv head) block S contiguous
-// rows of 256 bytes. A wave walks its tokens in 16-token tiles, one page slice each:
+// Pages are (P, Hkv, S, D) bf16 or fp16 with D 64 or 128, each (page, kv head) block
+// S contiguous rows of 2D bytes. A wave walks its tokens in 16-token tiles, one page slice each:
 //
-//   scores  lane l loads row l % 16 of the tile, bytes 64G .. 64G+63 (G = l / 16), of
-//           K and of V: 1 KB contiguous per load instruction. s^T = K q^T runs on
-//           v_mfma_f32_16x16x32_{bf16,f16}: A = K with the reduction order over the
-//           128 dims permuted so that lane group G covers dims 32G .. 32G+31 (k-step s:
-//           32G + 8s .. +8, exactly the 16 bytes the lane loaded), B = q^T with the
-//           same order, query heads padded to 16. q is a hi + lo pair in the page's
+//   scores  lane l loads row l % 16 of the tile, bytes (D/2)G .. (D/2)(G+1) - 1
+//           (G = l / 16), of K and of V: 16 rows x 2D bytes contiguous per tile.
+//           s^T = K q^T runs on v_mfma_f32_16x16x32_{bf16,f16}: A = K with the
+//           reduction order over the D dims permuted so that lane group G covers dims
+//           (D/4)G .. (D/4)(G+1) - 1 (k-step s: (D/4)G + 8s .. +8, 16 bytes the lane
+//           loaded), B = q^T with the same order, query heads padded to 16. q is a hi + lo pair in the page's
 //           16-bit type (K is exact in it), so scores carry fp32 accuracy. Lane l ends
 //           with the scores of head l % 16 for tokens 4G .. 4G+3.
 //   softmax per head in log2 units with a lazy maximum (it moves, rescaling the
@@ -36,9 +36,12 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kDenseWpb = 4;           // independent waves per work-group
-constexpr int kVRow = 264;             // bytes per row of the V tile: 256 + 8, so that rows 4 apart
-                                       // start 8 banks apart (the transposed reads are conflict free)
-constexpr int kVTile = 16 * kVRow;     // bytes of one wave's tile
+// Bytes per row of a wave's V tile: 2D + 8, so that rows 4 apart start 8 banks apart
+// (the transposed reads are conflict free for D = 64 and 128), and of the tile.
+template <int D>
+constexpr int vrow() { return 2 * D + 8; }
+template <int D>
+constexpr int vtile() { return 16 * vrow<D>(); }
 constexpr float kDenseRescale = 8.0f;  // log2 units
 
 // Two values in the page's 16-bit type (round to nearest even), low half first.
@@ -83,26 +86,28 @@ __device__ __forceinline__ f32x4 mma16(const uint2& a, const uint2& b, f32x4 c) 
                                                      0, 0, 0);
 }
 
+template <int NT>
 struct DenseState {
-  f32x4 acc[8];  // acc[T][j] = O[head 4G + j][dim 16T + l % 16]
+  f32x4 acc[NT];  // acc[T][j] = O[head 4G + j][dim 16T + l % 16]
   float m;       // running maximum of head l % 16 (equal in its four lanes), log2 units
   float l;       // this lane's share of head l % 16's sum
 };
 
 // Scans tokens [t_lo, t_hi) of (sequence b, kv head kvh), t_lo a multiple of 16, and
-// writes one partial at row prow.
-template <bool F16>
+// writes one partial at row prow. Lane group g covers dims (D/4)g .. (D/4)g + D/4 - 1:
+// NS = D/32 k-steps of 8 dims, NT = D/16 output tiles.
+template <bool F16, int D>
 __device__ __forceinline__ void dense_range(const DecodeArgs& a, int b, int kvh, int t_lo, int t_hi, int64_t prow,
                                             int lane, char* vt) {
-  constexpr int D = 128;
+  constexpr int NS = D / 32, NT = D / 16, LB = D / 2, VR = vrow<D>();
   const int h = lane & 15, g = lane >> 4;
-  // B operand of the scores: q^T rows 32g + 8s .. +8 of head h, hi and lo
-  uint4 qh[4], ql[4];
+  // B operand of the scores: q^T rows (D/4)g + 8s .. +8 of head h, hi and lo
+  uint4 qh[NS], ql[NS];
   {
     const bool live = h < a.n_rep;
-    const float* qp = a.q_rot + ((int64_t(b) * a.Hkv + kvh) * a.qrows + (live ? h : 0)) * D + 32 * g;
+    const float* qp = a.q_rot + ((int64_t(b) * a.Hkv + kvh) * a.qrows + (live ? h : 0)) * D + (D / 4) * g;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < NS; ++s) {
       uint32_t hw[4], lw[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -115,43 +120,43 @@ __device__ __forceinline__ void dense_range(const DecodeArgs& a, int b, int kvh,
   }
   const int smask = (1 << a.log2S) - 1;
   const int32_t* trow = a.table + b * a.tsb;
-  const uint8_t* kb = a.k_pages + kvh * a.ksh + 64 * g;
-  const uint8_t* vb = a.v_pages + kvh * a.vsh + 64 * g;
+  const uint8_t* kb = a.k_pages + kvh * a.ksh + LB * g;
+  const uint8_t* vb = a.v_pages + kvh * a.vsh + LB * g;
   const int nsub = (t_hi - t_lo + 15) >> 4;
   // page of tile u (clamped to the last tile, which is then read again)
   auto pid_of = [&](int u) { return trow[(t_lo + 16 * min(u, nsub - 1)) >> a.log2S]; };
   // row h of tile u (tokens past t_hi are rows of the same page, masked later)
-  auto load = [&](int u, int pid, uint4 (&k)[4], uint4 (&v)[4]) {
+  auto load = [&](int u, int pid, uint4 (&k)[NS], uint4 (&v)[NS]) {
     const int64_t slot = (t_lo + 16 * min(u, nsub - 1) + h) & smask;
     const uint4* kp = reinterpret_cast<const uint4*>(kb + pid * a.ksp + slot * (2 * D));
     const uint4* vp = reinterpret_cast<const uint4*>(vb + pid * a.vsp + slot * (2 * D));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) k[i] = kp[i];
+    for (int i = 0; i < NS; ++i) k[i] = kp[i];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = vp[i];
+    for (int i = 0; i < NS; ++i) v[i] = vp[i];
   };
 
-  DenseState st;
+  DenseState<NT> st;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) st.acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < NT; ++t) st.acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   st.m = -INFINITY;
   st.l = 0.f;
 
-  auto compute = [&](int u, const uint4 (&k)[4], const uint4 (&v)[4]) {
+  auto compute = [&](int u, const uint4 (&k)[NS], const uint4 (&v)[NS]) {
     const int c0 = t_lo + 16 * u;
     // V rows into the tile (the previous tile's reads are done first)
     wave_lds_sync();
     {
-      char* row = vt + h * kVRow + 64 * g;
+      char* row = vt + h * VR + LB * g;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < NS; ++i) {
         *reinterpret_cast<uint2*>(row + 16 * i) = make_uint2(v[i].x, v[i].y);
         *reinterpret_cast<uint2*>(row + 16 * i + 8) = make_uint2(v[i].z, v[i].w);
       }
     }
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < NS; ++s) {
       sc = mma32<F16>(k[s], qh[s], sc);
       sc = mma32<F16>(k[s], ql[s], sc);
     }
@@ -174,7 +179,7 @@ __device__ __forceinline__ void dense_range(const DecodeArgs& a, int b, int kvh,
       for (int j = 0; j < 4; ++j) {
         const float aj = __shfl(alpha, 4 * g + j, 64);  // lane 4g + j holds head 4g + j
 #pragma unroll
-        for (int t = 0; t < 8; ++t) st.acc[t][j] *= aj;
+        for (int t = 0; t < NT; ++t) st.acc[t][j] *= aj;
       }
     }
     float p[4];
@@ -188,12 +193,12 @@ __device__ __forceinline__ void dense_range(const DecodeArgs& a, int b, int kvh,
     split2<F16>(p[2], p[3], ph1, pl1);
     const uint2 ph = make_uint2(ph0, ph1), pl = make_uint2(pl0, pl1);
     wave_lds_sync();  // the tile is written
-    const uint16_t* col = reinterpret_cast<const uint16_t*>(vt + 4 * g * kVRow) + h;
+    const uint16_t* col = reinterpret_cast<const uint16_t*>(vt + 4 * g * VR) + h;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < NT; ++t) {
       const uint16_t* c = col + 16 * t;
-      const uint2 vbk = make_uint2(uint32_t(c[0]) | (uint32_t(c[kVRow / 2]) << 16),
-                                   uint32_t(c[kVRow]) | (uint32_t(c[3 * kVRow / 2]) << 16));
+      const uint2 vbk = make_uint2(uint32_t(c[0]) | (uint32_t(c[VR / 2]) << 16),
+                                   uint32_t(c[VR]) | (uint32_t(c[3 * VR / 2]) << 16));
       st.acc[t] = mma16<F16>(ph, vbk, st.acc[t]);
       st.acc[t] = mma16<F16>(pl, vbk, st.acc[t]);
     }
@@ -201,7 +206,7 @@ __device__ __forceinline__ void dense_range(const DecodeArgs& a, int b, int kvh,
 
   // Two tile buffers alternate; the next tile loads while this one computes, page
   // ids one tile further ahead.
-  uint4 ka[4], va[4], kn[4], vn[4];
+  uint4 ka[NS], va[NS], kn[NS], vn[NS];
   load(0, pid_of(0), ka, va);
   int pid1 = pid_of(1);
   for (int u = 0; u < nsub; u += 2) {
@@ -225,7 +230,7 @@ __device__ __forceinline__ void dense_range(const DecodeArgs& a, int b, int kvh,
     if (head < a.n_rep) {
       float* dst = a.part_acc + (row0 + head) * D + h;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) dst[16 * t] = st.acc[t][j];
+      for (int t = 0; t < NT; ++t) dst[16 * t] = st.acc[t][j];
     }
   }
   if (g == 0 && h < a.n_rep) {
@@ -244,13 +249,13 @@ __device__ __forceinline__ int dense_xcd_major(int p, int n) {
 // head, sequence) per wave; or balanced, the waves sharing the flattened
 // (sequence, kv head, 64-token chunk) space equally, one partial per (sequence, kv
 // head) a wave touches, at row w + b*Hkv + kvh, and unit_meta for the merge.
-template <bool F16>
+template <bool F16, int D>
 __global__ __launch_bounds__(64 * kDenseWpb) void dense_scan_kernel(DecodeArgs a) {
-  __shared__ __align__(16) char lds[kDenseWpb * kVTile];
+  __shared__ __align__(16) char lds[kDenseWpb * vtile<D>()];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t w = int64_t(dense_xcd_major(blockIdx.x, gridDim.x)) * kDenseWpb + wig;
-  char* vt = lds + wig * kVTile;
+  char* vt = lds + wig * vtile<D>();
 
   int b, kvh, t_lo, t_hi;
   int64_t prow;
@@ -312,7 +317,7 @@ __global__ __launch_bounds__(64 * kDenseWpb) void dense_scan_kernel(DecodeArgs a
       }
       s += c_hi - c_lo;
     }
-    dense_range<F16>(a, b, kvh, t_lo, t_hi, prow, lane, vt);
+    dense_range<F16, D>(a, b, kvh, t_lo, t_hi, prow, lane, vt);
     if (!a.balanced || s >= e) break;
     if (kvh + 1 == a.Hkv && c_hi == nb) ++b;
   }
@@ -320,10 +325,12 @@ __global__ __launch_bounds__(64 * kDenseWpb) void dense_scan_kernel(DecodeArgs a
 
 }  // namespace
 
-SplitKernel pick_dense_scan(int page_dtype) {
+SplitKernel pick_dense_scan(int page_dtype, int D) {
   SplitKernel k;
-  if (page_dtype == WN_BF16) k.fn = dense_scan_kernel<false>;
-  else if (page_dtype == WN_F16) k.fn = dense_scan_kernel<true>;
+  if (D == 128 && page_dtype == WN_BF16) k.fn = dense_scan_kernel<false, 128>;
+  else if (D == 128 && page_dtype == WN_F16) k.fn = dense_scan_kernel<true, 128>;
+  else if (D == 64 && page_dtype == WN_BF16) k.fn = dense_scan_kernel<false, 64>;
+  else if (D == 64 && page_dtype == WN_F16) k.fn = dense_scan_kernel<true, 64>;
   else return SplitKernel{};
   k.block = 64 * kDenseWpb;
   k.wpb = kDenseWpb;

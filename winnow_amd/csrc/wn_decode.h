@@ -47,9 +47,9 @@ struct SplitKernel {
 // (bw_k, bw_v, n_rep) is not compiled.
 SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep);
 
-// Dense-page scan (bf16 or fp16 pages of head_dim 128, up to 16 query heads per kv
-// head, page size >= 16) on the row scan's work plan, or an empty SplitKernel for
-// another page dtype.
-SplitKernel pick_dense_scan(int page_dtype);
+// Dense-page scan (bf16 or fp16 pages of head_dim 64 or 128, up to 16 query heads
+// per kv head, page size >= 16) on the row scan's work plan, or an empty SplitKernel
+// for another page dtype or head_dim.
+SplitKernel pick_dense_scan(int page_dtype, int D);
 
 }  // namespace wn

@@ -302,13 +302,14 @@ DENSE_PAGE_DTYPES = (torch.bfloat16, torch.float16)
 
 
 def dense_supported(q: torch.Tensor, kv: DenseKV) -> bool:
-    """Whether ``dense_decode_attention`` compiles this shape (head_dim 128, page size
-    >= 16 and a power of two, bf16/fp16 pages with contiguous rows, <= 16 query heads
-    per kv head, one query token)."""
-    return (q.dim() == 4 and q.shape[2] == 1 and q.shape[-1] == 128 and kv.head_dim == 128
+    """Whether ``dense_decode_attention`` compiles this shape (head_dim 64 or 128, page
+    size >= 16 and a power of two, bf16/fp16 pages with contiguous rows, <= 16 query
+    heads per kv head, one query token)."""
+    D = q.shape[-1]
+    return (q.dim() == 4 and q.shape[2] == 1 and D in (64, 128) and kv.head_dim == D
             and kv.k_pages.dtype in DENSE_PAGE_DTYPES and kv.v_pages.dtype == kv.k_pages.dtype
             and kv.page_size >= 16 and _pow2(kv.page_size) and kv.k_pages.stride(-1) == 1
-            and kv.k_pages.stride(-2) == 128 and kv.v_pages.stride() == kv.k_pages.stride()
+            and kv.k_pages.stride(-2) == D and kv.v_pages.stride() == kv.k_pages.stride()
             and q.shape[1] % kv.num_kv_heads == 0 and q.shape[1] // kv.num_kv_heads <= MAX_N_REP)
 
 
@@ -350,8 +351,8 @@ def dense_decode_attention(q: torch.Tensor, kv: DenseKV, scale: float, *,
         raise UnsupportedLayout("dense kernel: unsupported page layout")
     B, Hq, _, D = q.shape
     Hkv = kv.num_kv_heads
-    if D != 128 or kv.head_dim != D or kv.k_pages.shape[-1] != D:
-        raise UnsupportedLayout(f"dense kernel: head_dim {D} (128 compiled)")
+    if D not in (64, 128) or kv.head_dim != D or kv.k_pages.shape[-1] != D:
+        raise UnsupportedLayout(f"dense kernel: head_dim {D} (64 and 128 compiled)")
     if Hq % Hkv or Hq // Hkv > MAX_N_REP:
         raise UnsupportedLayout(f"dense kernel: {Hq} query heads over {Hkv} kv heads")
     if kv.page_size < 16:
