@@ -135,6 +135,24 @@ def test_dense_rejections():
         pa.dense_decode_attention(q.to(DEV), kv, 0.1)
 
 
+@pytest.mark.gpu
+def test_dense_rejects_bad_metadata_before_launch():
+    """A live page id outside the pool or a length beyond the table never reaches the
+    kernel; with ``check_ranges=False`` the same call on good metadata still runs."""
+    from winnow_amd import packed_attention as pa
+    kp, vp, table, sl = _pages(73, (20, 40), 2, 16, spare=0)
+    q = torch.randn(2, 4, 1, 128, generator=torch.Generator().manual_seed(5))
+    P = kp.shape[0]
+    for bad_table, bad_len, why in ((torch.tensor([[0, P, -1], [1, 2, 3]], dtype=torch.int32), sl, "sequence 0"),
+                                    (torch.tensor([[0, 4, -1], [1, -1, 3]], dtype=torch.int32), sl, "sequence 1"),
+                                    (table, torch.tensor([20, 49], dtype=torch.int32), "out of range")):
+        with pytest.raises(pa.UnsupportedLayout, match=why):
+            _run(q, kp, vp, bad_table, bad_len, 0.1)
+    got = _run(q, kp, vp, table, sl, 0.1, check_ranges=False, out_dtype=torch.float32).cpu()
+    ref = oa.dense_paged_attention_f64(q, kp, vp, table, sl, 0.1)
+    assert torch.allclose(got.double(), ref, atol=ATOL, rtol=RTOL)
+
+
 def test_dense_decode_has_no_host_path():
     from winnow_amd import packed_attention as pa
     kp, vp, table, sl = _pages(71, (20,), 2, 16)

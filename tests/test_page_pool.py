@@ -257,3 +257,21 @@ def test_paged_cache_builds_its_table_from_the_pool_and_refuses_stale_owners():
     gone = pb.PagedPackedCache(p, ["b"], [0], k_quant=None, v_quant=None, head_dim=8)
     with pytest.raises(StalePage):                  # released: holds nothing
         gone._prepare(1, torch.device("cpu"))
+
+
+def test_page_range_check_reads_only_live_slots():
+    """Slots past cdiv(len, S) may hold anything (-1 padding, stale ids); a live slot
+    outside [0, P) or a length beyond the table is an error."""
+    table = torch.tensor([[3, 1, -1, 99], [0, -1, -1, -1]], dtype=torch.int32)
+    pa.check_page_ranges(torch.tensor([17, 16], dtype=torch.int32), table, 4, 16)
+    pa.check_page_ranges(torch.tensor([0, 0], dtype=torch.int32), table, 4, 16)
+    with pytest.raises(pa.UnsupportedLayout, match="sequence 0"):
+        pa.check_page_ranges(torch.tensor([33, 16], dtype=torch.int32), table, 4, 16)
+    with pytest.raises(pa.UnsupportedLayout, match="sequence 1"):
+        pa.check_page_ranges(torch.tensor([17, 17], dtype=torch.int32), table, 4, 16)
+    with pytest.raises(pa.UnsupportedLayout, match="sequence 0"):
+        pa.check_page_ranges(torch.tensor([17, 16], dtype=torch.int32), table, 3, 16)
+    with pytest.raises(pa.UnsupportedLayout, match="out of range"):
+        pa.check_page_ranges(torch.tensor([65, 0], dtype=torch.int32), table, 4, 16)
+    with pytest.raises(pa.UnsupportedLayout, match="out of range"):
+        pa.check_page_ranges(torch.tensor([-1, 0], dtype=torch.int32), table, 4, 16)

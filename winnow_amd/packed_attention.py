@@ -165,17 +165,25 @@ def check_contract(q: torch.Tensor, kv: PackedKV, *, check_ranges: bool = True) 
         return
     lens = kv.seq_lens_host if kv.seq_lens_host is not None else kv.seq_lens
     table = kv.page_table_host if kv.page_table_host is not None else kv.page_table
-    lens = lens.to("cpu", torch.int64)
-    if (lens < 0).any() or (lens > kv.page_table.shape[1] * S).any():
+    check_page_ranges(lens, table, P, S)
+
+
+def check_page_ranges(seq_lens: torch.Tensor, page_table: torch.Tensor, num_pages: int,
+                      page_size: int) -> None:
+    """Every length fits the table and every page id a sequence reads (those below
+    cdiv(len, page_size)) lies in [0, num_pages): the scan kernels index pages with
+    these ids unchecked. Copies the two small tensors to the host."""
+    lens = seq_lens.to("cpu", torch.int64)
+    if (lens < 0).any() or (lens > page_table.shape[1] * page_size).any():
         raise UnsupportedLayout("seq_lens out of range for the page table")
-    used = (lens + S - 1) // S
-    table = table.to("cpu", torch.int64)
+    used = (lens + page_size - 1) // page_size
+    table = page_table.to("cpu", torch.int64)
     width = torch.arange(table.shape[1])[None, :]
     live = width < used[:, None]
-    bad = live & ((table < 0) | (table >= P))
+    bad = live & ((table < 0) | (table >= num_pages))
     if bad.any():
         b = int(bad.any(1).nonzero()[0])
-        raise UnsupportedLayout(f"sequence {b} references a page outside [0, {P})")
+        raise UnsupportedLayout(f"sequence {b} references a page outside [0, {num_pages})")
 
 
 def _pow2(x: int) -> bool:
@@ -330,6 +338,7 @@ def dense_decode_attention(q: torch.Tensor, kv: DenseKV, scale: float, *,
                            num_warps: int = 4, num_stages: int = 2, pages_per_iter: int = 1,
                            out_dtype: torch.dtype | None = None,
                            workspace: torch.Tensor | None = None,
+                           check_ranges: bool = True,
                            timing_events=None) -> torch.Tensor:
     """Unquantized paged decode on the packed decode's schedule, the matched baseline
     (packed_attention_triton.py:190-201): q (B, Hq, 1, D) -> (B, Hq, 1, D) in q.dtype.
@@ -337,9 +346,11 @@ def dense_decode_attention(q: torch.Tensor, kv: DenseKV, scale: float, *,
     Pages (P, Hkv, S, D) bf16 or fp16. Errors before any launch, as the reference's
     (``UnsupportedLayout``): a query of more than one token or off the GPU, a page size
     or head dim that is not a power of two, non-unit element stride, K and V strides
-    that differ; and what this build does not compile (head_dim other than 128, page
-    size below 16, more than 16 query heads per kv head, fp32 pages). The schedule
-    keywords behave as in ``packed_decode_attention``.
+    that differ; and what this build does not compile (head_dim other than 64 or 128,
+    page size below 16, more than 16 query heads per kv head, fp32 pages). A length
+    beyond the table or a live page id outside the pool is rejected too (a host copy
+    of the metadata; ``check_ranges=False`` skips it for callers that own the
+    metadata). The schedule keywords behave as in ``packed_decode_attention``.
     """
     del allow_tf32, num_warps, num_stages
     if pages_per_iter < 1 or pages_per_iter & (pages_per_iter - 1):
@@ -367,6 +378,12 @@ def dense_decode_attention(q: torch.Tensor, kv: DenseKV, scale: float, *,
     for t in (kv.k_pages, kv.v_pages, kv.page_table, kv.seq_lens):
         if t.device != q.device:
             raise UnsupportedLayout(f"dense kernel: operand on {t.device}, query on {q.device}")
+    if kv.page_table.dim() != 2 or kv.page_table.shape[0] != B or kv.seq_lens.shape != (B,):
+        raise UnsupportedLayout("dense kernel: page_table must be (B, max_pages) and seq_lens (B,)")
+    if kv.v_pages.shape != kv.k_pages.shape:
+        raise UnsupportedLayout("dense kernel: K and V pages differ in shape")
+    if check_ranges:
+        check_page_ranges(kv.seq_lens, kv.page_table, kv.k_pages.shape[0], kv.page_size)
     max_pages = kv.page_table.shape[1]
     pps, ns = dense_plan_for(q, kv, num_splits)
     out_dtype = out_dtype or q.dtype
