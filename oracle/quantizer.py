@@ -20,6 +20,10 @@ Pinned by (``tests/test_oracle_quantizer.py``):
 * ``quantize``: bucketize semantics on hand-built vectors that sit exactly on,
   just below and just above fp32 boundaries; zero vectors (norm clamps to
   1e-10, every code equals ``#{b < 0}``); the norm against a float64 norm.
+* The exact fp32 bits of ``Pi`` (seeds 42 and 43) and of every codebook
+  (2-8 bits): ``tests/golden/reference_constants.json``, written in the build
+  container by the reference's own ``TurboQuantMSE`` (``cache.py:84-106``),
+  checked by ``tests/test_golden.py``.
 """
 from __future__ import annotations
 

@@ -1,7 +1,10 @@
 """Golden fixtures of ``tests/golden`` (written by ``tests/golden/make_golden.py``).
 
 CPU: the oracle and the product's host-side quantizer construction reproduce the
-committed quantizer constants bit for bit, and the oracle reproduces BASELINE
+committed quantizer constants bit for bit, both the oracle-written
+``quantizer_constants.json`` and ``reference_constants.json``, which
+``tests/golden/make_reference_constants.py`` wrote from the reference's own
+``TurboQuantMSE`` (cache.py:84-106); and the oracle reproduces BASELINE
 config 1 (page bytes and norms by SHA-256, outputs to 1e-6).
 
 GPU: the HIP append of config 1's inputs gives the oracle's page bytes (under
@@ -79,6 +82,43 @@ def test_product_builds_the_same_constants(constants, bw):
     c, b = lloyd_max_gaussian(2 ** bw, sigma=1.0 / math.sqrt(128))
     assert _hex(torch.tensor(c, dtype=torch.float32)) == constants["codebooks"][str(bw)]["centroids"]
     assert _hex(torch.tensor(b[1:-1], dtype=torch.float32)) == constants["codebooks"][str(bw)]["boundaries"]
+
+
+@pytest.fixture(scope="module")
+def reference_constants():
+    return json.loads((GOLDEN / "reference_constants.json").read_text())
+
+
+def test_reference_constants_cover_the_oracle_fixture(constants, reference_constants):
+    """The fixture written from the reference's own TurboQuantMSE (cache.py:84-106) holds
+    the same seeds and widths as the oracle's, so the two tests below pin every one."""
+    assert reference_constants["head_dim"] == constants["head_dim"] == 128
+    assert set(reference_constants["pi_sha256"]) == set(constants["pi_sha256"]) == {"42", "43"}
+    assert set(reference_constants["codebooks"]) == set(constants["codebooks"])
+
+
+@pytest.mark.parametrize("seed", [42, 43])
+def test_oracle_rotation_matches_reference(reference_constants, seed):
+    """Pi = Q sign(diag R) of the seeded QR (cache.py:92-97), bit for bit as the reference built it."""
+    from winnow_amd.quantizer import seeded_rotation
+    want = reference_constants["pi_sha256"][str(seed)]
+    assert _sha(oracle_quantizer(4, 128, seed).Pi) == want
+    assert _sha(seeded_rotation(128, seed)) == want
+
+
+@pytest.mark.parametrize("bw", [2, 3, 4, 5, 6, 8])
+def test_codebooks_match_reference(reference_constants, bw):
+    """Lloyd-Max centroids and the interior boundaries (cache.py:62-82, 98-103), bit for bit."""
+    import math
+
+    from winnow_amd.quantizer import lloyd_max_gaussian
+    ref = reference_constants["codebooks"][str(bw)]
+    tq = oracle_quantizer(bw, 128, 42)
+    assert _hex(tq.centroids) == ref["centroids"]
+    assert _hex(tq.boundaries) == ref["boundaries"]
+    c, b = lloyd_max_gaussian(2 ** bw, sigma=1.0 / math.sqrt(128))
+    assert _hex(torch.tensor(c, dtype=torch.float32)) == ref["centroids"]
+    assert _hex(torch.tensor(b[1:-1], dtype=torch.float32)) == ref["boundaries"]
 
 
 def test_oracle_reproduces_config1(c1, oracle_c1):
