@@ -374,6 +374,12 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
   const float* ml = a.part_ml + 2 * (r0 * pstride + h);
   const float* acc = a.part_acc + (r0 * pstride + h) * D + d;
   float M = -INFINITY, num = 0.f, den = 0.f;
+  // every load of a batch is issued, clamped to the last partial; the extras weigh 0
+  float xv[kMergeBatch];
+  auto load_batch = [&](int first) {
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) xv[k] = acc[int64_t(min(first + k, n - 1)) * pstride * D];
+  };
   for (int s0 = 0; s0 < n; s0 += 64) {
     const int cnt = min(64, n - s0);
     float mk = -INFINITY, lk = 0.f;
@@ -382,6 +388,8 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
       mk = x.x;
       lk = x.y;
     }
+    // the first batch's acc rows travel with the (m, l) loads: they need only the range
+    if (s0 == 0) load_batch(0);
     const float Mn = fmaxf(M, wave_max(mk));
     // a partial that saw no key (m = -inf) and the lanes past the batch weigh 0
     const float wk = mk == -INFINITY ? 0.f : wexp(mk - Mn);
@@ -390,11 +398,7 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
     num *= r_old;
     M = Mn;
     for (int k0 = 0; k0 < cnt; k0 += kMergeBatch) {
-      // every load is issued, clamped to the last partial; the extras weigh 0
-      float xv[kMergeBatch];
-#pragma unroll
-      for (int k = 0; k < kMergeBatch; ++k)
-        xv[k] = acc[int64_t(min(s0 + k0 + k, n - 1)) * pstride * D];
+      if (s0 + k0 > 0) load_batch(s0 + k0);
 #pragma unroll
       for (int k = 0; k < kMergeBatch; ++k) {
         const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k0 + k));
