@@ -219,19 +219,23 @@ __device__ __forceinline__ void codes_to_a(const uint32_t (&w)[2], const DqTab<B
 }
 
 // Eight consecutive output elements at index i (a multiple of 8) in one 16-byte
-// store (two for fp32).
+// store (two for fp32). The 16-bit outputs are written once and never read back
+// by this kernel, so their stores are nontemporal (streamed past the caches): the
+// write-bound fast mode measured 104 -> 88 us (4-bit) and 108 -> 96 us (6-bit) per
+// 1M vectors, the compute-bound accurate mode unchanged.
 template <int OUT>
 __device__ __forceinline__ void store8(void* out, int64_t i, f32x4 u, f32x4 v) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   if constexpr (OUT == WN_F32) {
     float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + i);
     o[0] = make_float4(u[0], u[1], u[2], u[3]);
     o[1] = make_float4(v[0], v[1], v[2], v[3]);
   } else if constexpr (OUT == WN_BF16) {
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + i) =
-        make_uint4(pack_bf16(u[0], u[1]), pack_bf16(u[2], u[3]), pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+    const u32x4 w = {pack_bf16(u[0], u[1]), pack_bf16(u[2], u[3]), pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + i));
   } else {
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + i) =
-        make_uint4(pack_f16(u[0], u[1]), pack_f16(u[2], u[3]), pack_f16(v[0], v[1]), pack_f16(v[2], v[3]));
+    const u32x4 w = {pack_f16(u[0], u[1]), pack_f16(u[2], u[3]), pack_f16(v[0], v[1]), pack_f16(v[2], v[3])};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + i));
   }
 }
 
