@@ -95,7 +95,7 @@ def test_released_page_waits_for_its_fence():
 
 
 def test_mutant_reclaim_ignoring_fences_is_caught(monkeypatch):
-    monkeypatch.setattr(PagePool, "_event_done", lambda self, f: True)
+    monkeypatch.setattr(PagePool, "_fence_done", lambda self, f: True)
     ev = Pending()
     p = pool()
     p.ensure("a", 8)
@@ -120,17 +120,44 @@ def test_stale_refs_fail_after_request_id_reuse():
 
 
 def test_mutant_release_without_generation_bump_is_caught(monkeypatch):
-    real = PagePool.release
+    def no_bump(self, pages):
+        self._holder[pages] = -1
+    monkeypatch.setattr(PagePool, "_revoke", no_bump)
+    p = pool(pages=1)
+    old = p.ensure("a", 4)
+    p.release("a")
+    p.ensure("b", 4)
+    with pytest.raises(StalePage):                # another owner holds it now: still caught
+        p.validate("a", old)
+    p.release("b")
+    p.ensure("a", 4)
+    p.validate("a", old)                          # same owner again: only the generation could tell
 
-    def no_bump(self, owner, fence=None):
-        refs = list(self._held.get(owner, []))
-        n = real(self, owner, fence)
-        for r in refs:
-            self._gen[r.page] -= 1
-        return n
-    monkeypatch.setattr(PagePool, "release", no_bump)
-    p, old = _reuse()
-    p.validate("a", old)                          # the mutant lets the stale launch through
+
+def test_release_batches_pages_behind_one_fence():
+    evs = [Pending(), Pending()]
+    it = iter(evs)
+    p = pool(pages=6, fence=lambda: next(it))
+    p.ensure("a", 8)
+    p.ensure("b", 12)
+    assert [r.page for r in p.held("a")] == [0, 1] and [r.page for r in p.held("b")] == [2, 3, 4]
+    assert p.release("a") == 2 and p.release("b") == 3
+    assert p.stats() == {"free": 1, "pending": 5, "owned": 0, "requests": 0, "total": 6}
+    evs[1].fired = True                           # b's fence completes first
+    assert p.reclaim() == 3
+    assert [r.page for r in p.ensure("c", 16)] == [2, 3, 4, 5]   # lowest free pages first
+    evs[0].fired = True
+    assert p.reclaim() == 2 and p.stats()["free"] == 2
+
+
+def test_validate_rejects_foreign_and_out_of_range_refs():
+    p = pool(pages=4)
+    a = p.ensure("a", 4)
+    p.ensure("b", 4)
+    with pytest.raises(StalePage, match="current owner 'a'"):
+        p.validate("b", a)
+    with pytest.raises(StalePage, match="outside"):
+        p.validate("a", [type(a[0])(7, 0)])
 
 
 def test_concurrent_ensure_and_release_keep_the_page_count():
@@ -244,19 +271,35 @@ def test_paged_cache_builds_its_table_from_the_pool_and_refuses_stale_owners():
     p.ensure("a", 6)
     p.ensure("b", 3)
     cache = pb.PagedPackedCache(p, ["a", "b"], [5, 2], k_quant=None, v_quant=None, head_dim=8)
-    cache._prepare(1, torch.device("cpu"))
-    table = cache._table_host
-    assert table.shape == (2, 2)
-    assert table[0].tolist() == [r.page for r in p.held("a")]
-    assert table[1, 0] == p.held("b")[0].page and table[1, 1] == -1
-    assert cache._seq_host.tolist() == [6, 3]
+    meta = cache.begin(1, torch.device("cpu"))
+    assert meta.table_host.shape == (2, 2) and meta.table_host.dtype == torch.int32
+    assert meta.table_host[0].tolist() == [r.page for r in p.held("a")]
+    assert meta.table_host[1, 0] == p.held("b")[0].page and meta.table_host[1, 1] == -1
+    assert meta.seq_host.tolist() == [6, 3] and meta.start_host.tolist() == [5, 2]
+    assert torch.equal(meta.table, meta.table_host) and torch.equal(meta.seq, meta.seq_host)
     short = pb.PagedPackedCache(p, ["b"], [4], k_quant=None, v_quant=None, head_dim=8)
     with pytest.raises(StalePage):                  # 5 tokens need 2 pages, b holds 1
-        short._prepare(1, torch.device("cpu"))
+        short.begin(1, torch.device("cpu"))
     p.release("b")
     gone = pb.PagedPackedCache(p, ["b"], [0], k_quant=None, v_quant=None, head_dim=8)
     with pytest.raises(StalePage):                  # released: holds nothing
-        gone._prepare(1, torch.device("cpu"))
+        gone.begin(1, torch.device("cpu"))
+
+
+def test_append_range_check_reads_host_metadata():
+    """Positions past the table row or pages outside the pool are refused before launch
+    (the reference raises in its gather, packed_backend.py:144)."""
+    table = torch.tensor([[3, 1, -1], [0, -1, -1]], dtype=torch.int32)
+    pb._positions_in_range(torch.tensor([30, 10]), table, 2, 4, 16)         # b0: 30,31 on page 1
+    pb._positions_in_range(torch.tensor([0, 0]), table, 0, 4, 16)           # nothing appended
+    with pytest.raises(pa.UnsupportedLayout, match="sequence 1"):
+        pb._positions_in_range(torch.tensor([0, 15]), table, 2, 4, 16)      # b1: 16 needs column 1 (-1)
+    with pytest.raises(pa.UnsupportedLayout, match="outside its 3-page"):
+        pb._positions_in_range(torch.tensor([47, 0]), table, 2, 4, 16)      # 48 is past 3 pages
+    with pytest.raises(pa.UnsupportedLayout, match="outside"):
+        pb._positions_in_range(torch.tensor([0, 0]), table, 1, 3, 16)       # page 3 of a 3-page pool
+    with pytest.raises(pa.UnsupportedLayout):
+        pb._positions_in_range(torch.tensor([-1, 0]), table, 1, 4, 16)
 
 
 def test_page_range_check_reads_only_live_slots():

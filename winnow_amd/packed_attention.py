@@ -87,13 +87,19 @@ class PackedKV:
 
 @dataclass
 class DenseKV:
-    """Unquantized paged K/V: pages (P, Hkv, S, D) in the model dtype (packed_attention.py:95-111)."""
+    """Unquantized paged K/V: pages (P, Hkv, S, D) in the model dtype (packed_attention.py:95-111).
+
+    ``seq_lens_host`` / ``page_table_host`` are optional CPU mirrors, read by the range
+    checks in place of the device tensors, as on ``PackedKV``.
+    """
 
     k_pages: torch.Tensor
     v_pages: torch.Tensor
     page_table: torch.Tensor
     seq_lens: torch.Tensor
     head_dim: int
+    seq_lens_host: torch.Tensor | None = None
+    page_table_host: torch.Tensor | None = None
 
     @property
     def page_size(self) -> int:
@@ -254,7 +260,7 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
                             out_dtype: torch.dtype | None = None,
                             workspace: torch.Tensor | None = None,
                             check_ranges: bool = True,
-                            timing_events=None) -> torch.Tensor:
+                            timing_events=None, plan: tuple[int, int] | None = None) -> torch.Tensor:
     """q (B, Hq, 1, D) -> (B, Hq, 1, D) in q.dtype (packed_attention_triton.py:180-187).
 
     ``num_splits=None`` lets the library plan the split: persistent waves that
@@ -266,7 +272,10 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
     returns the fp32 result before the cast (for parity checks). ``workspace``
     is an optional caller-owned uint8 buffer of at least ``workspace_bytes``.
     ``timing_events`` is an optional pair of raw ``hipEvent_t`` handles recorded
-    around the page-scan kernel.
+    around the page-scan kernel. ``plan`` = ``(pages_per_split, num_splits)`` replaces
+    the library's plan: ``(0, w)`` is a balanced plan over ``w`` waves (each wave then
+    scans several chunks when the batch has more than ``w``), ``(p, n)`` with
+    ``p * n >= max_pages`` fixed splits.
     """
     del allow_tf32, num_warps, num_stages
     if pages_per_iter < 1 or pages_per_iter & (pages_per_iter - 1):
@@ -275,7 +284,7 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
     B, Hq, _, D = q.shape
     Hkv = kv.num_kv_heads
     max_pages = kv.page_table.shape[1]
-    pps, ns = plan_for(q, kv, num_splits)
+    pps, ns = plan if plan is not None else plan_for(q, kv, num_splits)
     out_dtype = out_dtype or q.dtype
     if out_dtype not in _lib.DTYPE_CODE:
         raise UnsupportedLayout(f"output dtype {out_dtype} is not supported")
@@ -339,7 +348,7 @@ def dense_decode_attention(q: torch.Tensor, kv: DenseKV, scale: float, *,
                            out_dtype: torch.dtype | None = None,
                            workspace: torch.Tensor | None = None,
                            check_ranges: bool = True,
-                           timing_events=None) -> torch.Tensor:
+                           timing_events=None, plan: tuple[int, int] | None = None) -> torch.Tensor:
     """Unquantized paged decode on the packed decode's schedule, the matched baseline
     (packed_attention_triton.py:190-201): q (B, Hq, 1, D) -> (B, Hq, 1, D) in q.dtype.
 
@@ -350,7 +359,7 @@ def dense_decode_attention(q: torch.Tensor, kv: DenseKV, scale: float, *,
     page size below 16, more than 16 query heads per kv head, fp32 pages). A length
     beyond the table or a live page id outside the pool is rejected too (a host copy
     of the metadata; ``check_ranges=False`` skips it for callers that own the
-    metadata). The schedule keywords behave as in ``packed_decode_attention``.
+    metadata). The schedule keywords and ``plan`` behave as in ``packed_decode_attention``.
     """
     del allow_tf32, num_warps, num_stages
     if pages_per_iter < 1 or pages_per_iter & (pages_per_iter - 1):
@@ -383,9 +392,11 @@ def dense_decode_attention(q: torch.Tensor, kv: DenseKV, scale: float, *,
     if kv.v_pages.shape != kv.k_pages.shape:
         raise UnsupportedLayout("dense kernel: K and V pages differ in shape")
     if check_ranges:
-        check_page_ranges(kv.seq_lens, kv.page_table, kv.k_pages.shape[0], kv.page_size)
+        check_page_ranges(kv.seq_lens if kv.seq_lens_host is None else kv.seq_lens_host,
+                          kv.page_table if kv.page_table_host is None else kv.page_table_host,
+                          kv.k_pages.shape[0], kv.page_size)
     max_pages = kv.page_table.shape[1]
-    pps, ns = dense_plan_for(q, kv, num_splits)
+    pps, ns = plan if plan is not None else dense_plan_for(q, kv, num_splits)
     out_dtype = out_dtype or q.dtype
     if out_dtype not in _lib.DTYPE_CODE:
         raise UnsupportedLayout(f"output dtype {out_dtype} is not supported")

@@ -1,20 +1,26 @@
-"""Model-side integration: the paged packed cache's append path and the decode dispatcher.
+"""Model-side integration: the paged packed cache's append path and the attention dispatcher.
 
-Drop-in for ``turboquant_kv/packed_backend.py``:
+Names, arguments and errors are those of ``turboquant_kv/packed_backend.py``
+(``UnsupportedModel``, ``check_model``, ``head_dim_of``, ``make_pool``,
+``quantizers_for``, ``PagedPackedCache``, ``select_decode_backend``,
+``dequantize_history``, ``winnow_packed_attention``, ``register``,
+``BACKEND_COUNTS``; packed_backend.py:38-303). How they run on MI355X:
 
-* ``PagedPackedCache.update`` (packed_backend.py:136-170) quantizes, bit-packs
-  and scatters the new K/V into the pool pages with ONE ``wn_append_kv`` launch
-  per layer (K and V together). Token i of sequence b goes to page
-  ``table[b, (L_b + i) // S]`` slot ``(L_b + i) % S``; the page-table lookup
-  happens on the device, so unlike the reference there is no per-layer
-  device-to-host copy of the table (packed_backend.py:144).
-* ``winnow_packed_attention`` (packed_backend.py:260-290) serves decode with the
-  HIP operator (packed pages) or the HIP dense kernel (unquantized pages), and a
-  prefill chunk by dequantizing the sequence's history on the GPU and calling SDPA
-  (packed_backend.py:192-226).
-* ``make_pool``, ``quantizers_for``, ``select_decode_backend``, ``BACKEND_COUNTS``
-  keep the reference's names and meaning. There is no host fallback: a decode on
-  a non-HIP tensor raises.
+* ``PagedPackedCache`` asks the pool once per forward for a ``PageTable`` (page
+  table, start positions and lengths, uploaded in one copy). Every layer then
+  appends K and V with ONE ``wn_append_kv`` launch: quantize, bit-pack and scatter
+  into the pool, the table lookup ``table[b, (L_b + i) // S]`` done on the device.
+  The reference copies the table back to the host in every layer
+  (packed_backend.py:144); nothing here reads device memory.
+* ``append_kv`` validates shapes, and that every position lands inside the table
+  and every page it names inside the pool, on host copies of the metadata before
+  the launch, raising ``UnsupportedLayout`` as the reference raises in its gather.
+* Decode (one query token) runs the HIP compressed-domain operator on packed pages,
+  the HIP dense operator on unquantized pages. A prefill chunk dequantizes the
+  batch's histories on the GPU (``wn_dequantize_history``) into one padded tensor
+  and runs ONE SDPA call with a per-sequence offset-causal mask (the reference loops
+  over sequences, packed_backend.py:210-246).
+* There is no host fallback: a decode on a non-HIP tensor raises.
 """
 from __future__ import annotations
 
@@ -26,14 +32,15 @@ import torch.nn.functional as F
 from winnow_amd import _lib
 from winnow_amd import packed_attention as pa
 from winnow_amd.packing import packed_bytes, unpack
-from winnow_amd.page_pool import PagePool, StalePage
+from winnow_amd.page_pool import PagePool, PageTable
 from winnow_amd.quantizer import get_quantizer
 
 ATTN_NAME = "winnow_packed"
 SUPPORTED_ARCH = ("Qwen2ForCausalLM",)
 DECODE_BACKENDS = ("hip_packed", "reconstruct_sdpa", "hip_dense", "dense_sdpa")
 
-# How many attention calls each backend served (packed_backend.py:38-40).
+# Attention calls served per backend (packed_backend.py:38-40); tests read it to see
+# which operator ran.
 BACKEND_COUNTS: Counter = Counter()
 
 
@@ -41,175 +48,241 @@ class UnsupportedModel(ValueError):
     pass
 
 
-def check_model(config, bit_width: int) -> None:
-    """Reject unsupported model configurations before load (packed_backend.py:58-68)."""
-    arch = (getattr(config, "architectures", None) or ["?"])[0]
-    if arch not in SUPPORTED_ARCH:
-        raise UnsupportedModel(f"{arch} is not a supported architecture {SUPPORTED_ARCH}")
-    if getattr(config, "use_sliding_window", False):
-        raise UnsupportedModel("sliding-window attention is not supported")
-    types = set(getattr(config, "layer_types", None) or ["full_attention"])
-    if types != {"full_attention"}:
-        raise UnsupportedModel(f"layer types {sorted(types)} are not all full attention")
-    packed_bytes(head_dim_of(config), bit_width)
-
-
 def head_dim_of(config) -> int:
     return getattr(config, "head_dim", None) or config.hidden_size // config.num_attention_heads
+
+
+# (what is wrong, test) pairs of the model contract (packed_backend.py:58-68)
+_MODEL_RULES = (
+    (lambda c: f"{_arch(c)} is not a supported architecture {SUPPORTED_ARCH}",
+     lambda c: _arch(c) not in SUPPORTED_ARCH),
+    (lambda c: "sliding-window attention is not supported",
+     lambda c: bool(getattr(c, "use_sliding_window", False))),
+    (lambda c: f"layer types {sorted(set(c.layer_types))} are not all full attention",
+     lambda c: any(t != "full_attention" for t in (getattr(c, "layer_types", None) or ()))),
+)
+
+
+def _arch(config) -> str:
+    return (getattr(config, "architectures", None) or ["?"])[0]
+
+
+def check_model(config, bit_width: int) -> None:
+    """Reject a model this path does not serve before it is loaded; ``ValueError`` when
+    ``head_dim * bit_width`` is not a whole number of bytes."""
+    for message, broken in _MODEL_RULES:
+        if broken(config):
+            raise UnsupportedModel(message(config))
+    packed_bytes(head_dim_of(config), bit_width)
 
 
 def make_pool(config, *, bit_width: int | None, num_pages: int, page_size: int, device,
               max_pages_per_request=None, fence_factory=None,
               dense_dtype: torch.dtype | None = None) -> PagePool:
-    """Packed pool at ``bit_width``, or with ``dense_dtype`` an unquantized pool (packed_backend.py:75-85)."""
+    """A pool for every layer of ``config``: packed at ``bit_width``, or unquantized rows
+    of ``dense_dtype`` (packed_backend.py:75-85)."""
     D = head_dim_of(config)
-    nb = D if dense_dtype is not None else packed_bytes(D, bit_width)
+    row = D if dense_dtype is not None else packed_bytes(D, bit_width)
     return PagePool(num_layers=config.num_hidden_layers, num_pages=num_pages,
-                    num_kv_heads=config.num_key_value_heads, page_size=page_size,
-                    nb_k=nb, nb_v=nb, device=device, max_pages_per_request=max_pages_per_request,
+                    num_kv_heads=config.num_key_value_heads, page_size=page_size, nb_k=row, nb_v=row,
+                    device=device, max_pages_per_request=max_pages_per_request,
                     fence_factory=fence_factory, dense_dtype=dense_dtype)
 
 
 def quantizers_for(config, bit_width: int, device, k_seed: int = 42, v_seed: int = 42):
-    """K and V quantizers; seed 42/42 by default, as the reference (packed_backend.py:298-303)."""
+    """The K and V quantizers; rotation seeds 42 and 42 by default (packed_backend.py:298-303)."""
     D = head_dim_of(config)
     return get_quantizer(bit_width, D, device, seed=k_seed), get_quantizer(bit_width, D, device, seed=v_seed)
 
 
-class PagedPackedCache:
-    """Duck-typed cache for one forward over a batch of pool-backed sequences.
+# ---------------------------------------------------------------------------- append
 
-    ``owners[b]`` is the request id whose pages hold sequence b and
-    ``lengths[b]`` the tokens already stored; every sequence appends the same n
-    tokens per forward; lengths advance after the last layer (packed_backend.py:88-112).
-    """
-
-    def __init__(self, pool: PagePool, owners, lengths, *, k_quant, v_quant,
-                 head_dim: int, decode_backend: str = "auto"):
-        self.pool = pool
-        self.owners = list(owners)
-        self.lengths = list(lengths)
-        self.kq, self.vq = k_quant, v_quant
-        self.head_dim = head_dim
-        self.decode_backend = decode_backend
-        self._table = self._table_host = self._seq = self._seq_host = self._start = None
-        self._refs = None
-
-    def get_seq_length(self, layer_idx: int = 0) -> int:
-        if len(set(self.lengths)) != 1:
-            raise RuntimeError("mixed lengths: pass explicit position_ids")
-        return self.lengths[0]
-
-    def _prepare(self, n: int, device) -> None:
-        """Once per forward: check ownership and reservation, build the table (packed_backend.py:114-133).
-
-        Never allocates pages: a forward racing a release must fail.
-        """
-        refs = [self.pool.held(o) for o in self.owners]
-        for o, r, L in zip(self.owners, refs, self.lengths):
-            if self.pool.pages_for(L + n) > len(r):
-                raise StalePage(f"{o} holds {len(r)} pages, needs {self.pool.pages_for(L + n)}")
-            self.pool.validate(o, r)
-        width = max(max(len(r) for r in refs), 1)
-        table = torch.full((len(refs), width), -1, dtype=torch.int32)
-        for b, r in enumerate(refs):
-            if r:
-                table[b, :len(r)] = torch.tensor([x.page for x in r], dtype=torch.int32)
-        self._refs = refs
-        self._table_host = table
-        self._seq_host = torch.tensor([L + n for L in self.lengths], dtype=torch.int32)
-        start = torch.tensor(self.lengths, dtype=torch.int32)
-        self._table = table.to(device, non_blocking=True)
-        self._seq = self._seq_host.to(device, non_blocking=True)
-        self._start = start.to(device, non_blocking=True)
-
-    @torch.no_grad()
-    def update(self, key_states, value_states, layer_idx, *args, **kwargs):
-        B, Hkv, n, D = key_states.shape
-        if B != len(self.owners):
-            raise RuntimeError(f"batch {B} != {len(self.owners)} owners")
-        if layer_idx == 0:
-            self._prepare(n, key_states.device)
-        S = self.pool.page_size
-        if self.pool.dense:
-            pos = torch.tensor([[L + i for i in range(n)] for L in self.lengths])
-            pids = torch.gather(self._table_host.long(), 1, pos // S).to(key_states.device)
-            slots = (pos % S).to(key_states.device)
-            for src, pages in ((key_states, self.pool.k_pages), (value_states, self.pool.v_pages)):
-                pages[layer_idx][pids, :, slots] = src.permute(0, 2, 1, 3).to(pages.dtype)
-            handle = pa.DenseKV(self.pool.k_pages[layer_idx], self.pool.v_pages[layer_idx],
-                                self._table, self._seq, D)
-        else:
-            append_kv(key_states, value_states, self.kq, self.vq,
-                      self.pool.k_pages[layer_idx], self.pool.v_pages[layer_idx],
-                      self.pool.k_norms[layer_idx], self.pool.v_norms[layer_idx],
-                      self._table, self._start)
-            handle = pa.PackedKV(
-                self.pool.k_pages[layer_idx], self.pool.k_norms[layer_idx],
-                self.pool.v_pages[layer_idx], self.pool.v_norms[layer_idx],
-                self._table, self._seq, pa.Quantizer.from_tq(self.kq), pa.Quantizer.from_tq(self.vq), D,
-                seq_lens_host=self._seq_host, page_table_host=self._table_host)
-        handle.decode_backend = self.decode_backend
-        if layer_idx == self.pool.num_layers - 1:
-            self.lengths = [L + n for L in self.lengths]
-        return handle, handle
+def _positions_in_range(start: torch.Tensor, table: torch.Tensor, n: int, num_pages: int,
+                        page_size: int) -> None:
+    """Every position start[b] + i (i < n) lies inside row b of the table and names a
+    page in [0, num_pages). Reads host tensors only."""
+    start = start.to(torch.int64)
+    width = table.shape[1]
+    if n == 0 or start.numel() == 0:
+        return
+    if (start < 0).any() or (start + n > width * page_size).any():
+        b = int(((start < 0) | (start + n > width * page_size)).nonzero()[0])
+        raise pa.UnsupportedLayout(f"append: sequence {b} writes positions {int(start[b])}.."
+                                   f"{int(start[b]) + n - 1} outside its {width}-page table row")
+    cols = torch.arange(width)[None, :]
+    first, last = start // page_size, (start + n - 1) // page_size
+    touched = (cols >= first[:, None]) & (cols <= last[:, None])
+    ids = table.to(torch.int64)
+    bad = touched & ((ids < 0) | (ids >= num_pages))
+    if bad.any():
+        b = int(bad.any(1).nonzero()[0])
+        raise pa.UnsupportedLayout(f"append: sequence {b} writes to a page outside [0, {num_pages})")
 
 
 @torch.no_grad()
 def append_kv(k: torch.Tensor, v: torch.Tensor | None, k_tq, v_tq,
               k_pages: torch.Tensor, v_pages: torch.Tensor | None,
               k_norms: torch.Tensor, v_norms: torch.Tensor | None,
-              page_table: torch.Tensor, start_pos: torch.Tensor) -> None:
-    """Quantize + pack + scatter (B, Hkv, n, D) K (and V) into one layer's pages, one launch.
+              page_table: torch.Tensor, start_pos: torch.Tensor, *,
+              page_table_host: torch.Tensor | None = None,
+              start_pos_host: torch.Tensor | None = None,
+              check_ranges: bool = True) -> None:
+    """Quantize, pack and scatter (B, Hkv, n, D) K (and V, unless ``v`` is None) into one
+    layer's pages in one launch; token i of sequence b lands at position
+    ``start_pos[b] + i``: page ``page_table[b, pos // S]``, slot ``pos % S``
+    (packed_backend.py:143-161).
 
-    Token i of sequence b lands at position ``start_pos[b] + i``.
+    Raises ``UnsupportedLayout`` before the launch for operands off the GPU or of the
+    wrong shape, and (``check_ranges``) for a position beyond the table row or a page
+    id outside the pool. The range check reads ``page_table_host`` /
+    ``start_pos_host`` when given, else copies the two small tensors to the host.
     """
-    for t in (k, k_pages, k_norms, page_table, start_pos):
-        if not _lib.is_hip(t):
-            raise pa.UnsupportedLayout("append_kv needs every operand on a HIP device")
+    operands = [k, k_pages, k_norms, page_table, start_pos] + ([v, v_pages, v_norms] if v is not None else [])
+    if any(t is None for t in operands):
+        raise pa.UnsupportedLayout("append: V needs its pages and norms")
+    if not all(_lib.is_hip(t) for t in operands) or len({t.device for t in operands}) != 1:
+        raise pa.UnsupportedLayout("append: every operand must be on one HIP device")
+    if k.dim() != 4:
+        raise pa.UnsupportedLayout(f"append: K must be (B, Hkv, n, D), got {tuple(k.shape)}")
     B, Hkv, n, D = k.shape
+    if v is not None and v.shape != k.shape:
+        raise pa.UnsupportedLayout(f"append: V {tuple(v.shape)} differs from K {tuple(k.shape)}")
     if k.dtype not in _lib.DTYPE_CODE:
         k = k.float()
     if v is not None and v.dtype != k.dtype:
         v = v.to(k.dtype)
-    for x in (k, v):
-        if x is not None and x.stride(-1) != 1:
-            raise pa.UnsupportedLayout("K/V states need a contiguous head_dim")
-    if page_table.dtype != torch.int32 or start_pos.dtype != torch.int32 or page_table.stride(-1) != 1:
-        raise pa.UnsupportedLayout("page_table / start_pos must be int32 with contiguous rows")
-    for pages, norms, tq in ((k_pages, k_norms, k_tq), (v_pages, v_norms, v_tq)):
-        if pages is None:
-            continue
-        if pages.shape[1:] != (Hkv, pages.shape[2], packed_bytes(D, tq.bit_width)) or \
-                pages.stride(-1) != 1 or pages.stride(-2) != pages.shape[-1] or norms.stride(-1) != 1:
-            raise pa.UnsupportedLayout("pages must be (P, Hkv, S, NB) with contiguous rows")
-    S = k_pages.shape[2]
-    dev = k.device
-    vv = v if v is not None else None
-    with torch.cuda.device(dev):
+    if k.stride(-1) != 1 or (v is not None and v.stride(-1) != 1):
+        raise pa.UnsupportedLayout("append: K/V need a contiguous head_dim")
+    if page_table.dtype != torch.int32 or page_table.dim() != 2 or page_table.shape[0] != B \
+            or page_table.stride(-1) != 1:
+        raise pa.UnsupportedLayout("append: page_table must be (B, max_pages) int32 with contiguous rows")
+    if start_pos.dtype != torch.int32 or start_pos.shape != (B,):
+        raise pa.UnsupportedLayout("append: start_pos must be (B,) int32")
+    P, S = k_pages.shape[0], k_pages.shape[2]
+    sides = [(k_pages, k_norms, k_tq)] + ([(v_pages, v_norms, v_tq)] if v is not None else [])
+    for pages, norms, tq in sides:
+        nb = packed_bytes(D, tq.bit_width)
+        if pages.dtype != torch.uint8 or pages.shape != (P, Hkv, S, nb) or pages.stride(-1) != 1 \
+                or pages.stride(-2) != nb:
+            raise pa.UnsupportedLayout(f"append: pages must be (P={P}, Hkv={Hkv}, S={S}, NB={nb}) uint8 "
+                                       f"with contiguous rows, got {tuple(pages.shape)}")
+        if norms.dtype != torch.float16 or norms.shape != (P, Hkv, S) or norms.stride(-1) != 1:
+            raise pa.UnsupportedLayout("append: norms must be (P, Hkv, S) fp16 with a contiguous slot axis")
+        if tq.Pi.shape != (D, D) or tq.Pi.device != k.device or tq.boundaries.numel() != 2 ** tq.bit_width - 1:
+            raise pa.UnsupportedLayout("append: quantizer does not match head_dim or device")
+    if check_ranges:
+        table = page_table_host if page_table_host is not None else page_table.cpu()
+        start = start_pos_host if start_pos_host is not None else start_pos.cpu()
+        _positions_in_range(start, table, n, P, S)
+    if B == 0 or n == 0:
+        return
+    has_v = v is not None
+    vv, vp, vn = (v, v_pages, v_norms) if has_v else (None, None, None)
+    with torch.cuda.device(k.device):
         _lib.call(
             "wn_append_kv",
             _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
-            _lib.ptr(vv), vv.stride(0) if vv is not None else 0, vv.stride(1) if vv is not None else 0,
-            vv.stride(2) if vv is not None else 0, _lib.DTYPE_CODE[k.dtype],
+            _lib.ptr(vv), *((vv.stride(0), vv.stride(1), vv.stride(2)) if has_v else (0, 0, 0)),
+            _lib.DTYPE_CODE[k.dtype],
             _lib.ptr(k_tq.Pi), _lib.ptr(k_tq.boundaries), k_tq.bit_width,
-            _lib.ptr(v_tq.Pi) if vv is not None else None,
-            _lib.ptr(v_tq.boundaries) if vv is not None else None,
-            v_tq.bit_width if vv is not None else 0,
+            _lib.ptr(v_tq.Pi) if has_v else None, _lib.ptr(v_tq.boundaries) if has_v else None,
+            v_tq.bit_width if has_v else 0,
             _lib.ptr(page_table), page_table.stride(0), _lib.ptr(start_pos),
             _lib.ptr(k_pages), k_pages.stride(0), k_pages.stride(1),
-            _lib.ptr(v_pages) if vv is not None else None,
-            v_pages.stride(0) if vv is not None else 0, v_pages.stride(1) if vv is not None else 0,
+            _lib.ptr(vp), *((vp.stride(0), vp.stride(1)) if has_v else (0, 0)),
             _lib.ptr(k_norms), k_norms.stride(0), k_norms.stride(1),
-            _lib.ptr(v_norms) if vv is not None else None,
-            v_norms.stride(0) if vv is not None else 0, v_norms.stride(1) if vv is not None else 0,
-            B, Hkv, n, D, S, k_pages.shape[0], page_table.shape[1], _lib.stream_of(dev))
+            _lib.ptr(vn), *((vn.stride(0), vn.stride(1)) if has_v else (0, 0)),
+            B, Hkv, n, D, S, P, page_table.shape[1], _lib.stream_of(k.device))
 
+
+def _append_dense_rows(src: torch.Tensor, pages: torch.Tensor, meta: PageTable) -> None:
+    """Unquantized append: row (page, h, slot) of a contiguous (P, Hkv, S, D) layer is
+    flat row (page * Hkv + h) * S + slot; the addresses are formed on the device."""
+    B, Hkv, n, D = src.shape
+    S = pages.shape[2]
+    dev = src.device
+    pos = meta.start.to(torch.int64)[:, None] + torch.arange(n, device=dev)[None, :]          # (B, n)
+    page = meta.table.to(torch.int64).gather(1, pos // S)                                       # (B, n)
+    heads = torch.arange(Hkv, device=dev)
+    rows = (page[:, :, None] * Hkv + heads[None, None, :]) * S + (pos % S)[:, :, None]           # (B, n, Hkv)
+    flat = pages.view(-1, D)
+    flat.index_copy_(0, rows.reshape(-1), src.permute(0, 2, 1, 3).reshape(-1, D).to(pages.dtype))
+
+
+class PagedPackedCache:
+    """Duck-typed transformers cache for one forward over pool-backed sequences.
+
+    ``owners[b]`` names the lease whose pages hold sequence b and ``lengths[b]`` the
+    tokens it already stores. A forward appends the same n tokens to every sequence
+    (n = 1 for a batched decode step, a chunk for a single-sequence prefill); the
+    lengths advance once the last layer has written (packed_backend.py:88-112).
+    """
+
+    def __init__(self, pool: PagePool, owners, lengths, *, k_quant, v_quant,
+                 head_dim: int, decode_backend: str = "auto"):
+        if len(owners) != len(lengths):
+            raise ValueError("one length per owner")
+        self.pool = pool
+        self.owners = list(owners)
+        self.lengths = [int(L) for L in lengths]
+        self.kq, self.vq = k_quant, v_quant
+        self.head_dim = head_dim
+        self.decode_backend = decode_backend
+        self.meta: PageTable | None = None
+
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        if any(L != self.lengths[0] for L in self.lengths):
+            raise RuntimeError("mixed lengths: pass explicit position_ids")
+        return self.lengths[0] if self.lengths else 0
+
+    def begin(self, n: int, device) -> PageTable:
+        """Page metadata of this forward: checked against the pool's leases (a short or
+        released lease raises ``StalePage``; pages are never granted here), range-checked
+        on the host, and uploaded to ``device`` in one copy."""
+        meta = self.pool.batch_table(self.owners, self.lengths, n)
+        _positions_in_range(meta.start_host, meta.table_host, n, self.pool.num_pages, self.pool.page_size)
+        self.meta = meta.to(device)
+        return self.meta
+
+    @torch.no_grad()
+    def update(self, key_states, value_states, layer_idx, *args, **kwargs):
+        B, Hkv, n, D = key_states.shape
+        if B != len(self.owners):
+            raise RuntimeError(f"batch {B} != {len(self.owners)} owners")
+        if layer_idx == 0 or self.meta is None:
+            self.begin(n, key_states.device)
+        meta, pool = self.meta, self.pool
+        if pool.dense:
+            _append_dense_rows(key_states, pool.k_pages[layer_idx], meta)
+            _append_dense_rows(value_states, pool.v_pages[layer_idx], meta)
+            handle = pa.DenseKV(pool.k_pages[layer_idx], pool.v_pages[layer_idx], meta.table, meta.seq, D,
+                                seq_lens_host=meta.seq_host, page_table_host=meta.table_host)
+        else:
+            append_kv(key_states, value_states, self.kq, self.vq,
+                      pool.k_pages[layer_idx], pool.v_pages[layer_idx],
+                      pool.k_norms[layer_idx], pool.v_norms[layer_idx],
+                      meta.table, meta.start, check_ranges=False)    # checked once in begin()
+            handle = pa.PackedKV(pool.k_pages[layer_idx], pool.k_norms[layer_idx],
+                                 pool.v_pages[layer_idx], pool.v_norms[layer_idx],
+                                 meta.table, meta.seq, pa.Quantizer.from_tq(self.kq),
+                                 pa.Quantizer.from_tq(self.vq), D,
+                                 seq_lens_host=meta.seq_host, page_table_host=meta.table_host)
+        handle.decode_backend = self.decode_backend
+        if layer_idx == pool.num_layers - 1:
+            self.lengths = meta.seq_host.tolist()
+        return handle, handle
+
+
+# ---------------------------------------------------------------------------- attention
 
 def select_decode_backend(query: torch.Tensor, kv, requested: str) -> str:
-    """Which operator serves a decode step; unsupported requests fail loudly (packed_backend.py:173-189)."""
+    """The operator that serves a one-token decode step (packed_backend.py:173-189).
+
+    Packed pages: ``auto`` (and the reference's ``triton_packed``) is the HIP operator;
+    ``reconstruct_sdpa`` is the dequantize-then-SDPA path. Dense pages: the HIP dense
+    operator where it compiles the shape, else dense SDPA. Requests that cannot be
+    served raise; nothing falls back to the host."""
     if isinstance(kv, pa.DenseKV):
-        # packed_backend.py:175-179: the dense kernel where it runs, else dense SDPA
         if requested == "dense_sdpa":
             return requested
         if requested not in ("auto", "triton_dense", "hip_dense"):
@@ -219,7 +292,7 @@ def select_decode_backend(query: torch.Tensor, kv, requested: str) -> str:
         if pa.dense_supported(query, kv):
             return "hip_dense"
         if requested == "hip_dense":
-            raise ValueError("hip_dense does not compile this shape (head_dim 128, bf16/fp16 pages, S >= 16)")
+            raise ValueError("hip_dense does not compile this shape (head_dim 64/128, fp32/bf16/fp16 pages, S >= 16)")
         return "dense_sdpa"
     if requested in ("auto", "triton_packed", "hip_packed"):
         if not _lib.is_hip(query):
@@ -230,112 +303,137 @@ def select_decode_backend(query: torch.Tensor, kv, requested: str) -> str:
     return requested
 
 
-def dequantize_history(kv: pa.PackedKV, pages, norms, quant, b: int, dtype) -> torch.Tensor:
-    """(1, Hkv, L, D) reconstruction of sequence b on the GPU (packed_backend.py:192-208).
+def _host_lens(kv) -> torch.Tensor:
+    return kv.seq_lens_host if kv.seq_lens_host is not None else kv.seq_lens.cpu()
 
-    head_dim 128: one fused HIP kernel (``wn_dequantize_history``) reads the pool
-    pages through the page table, so nothing is gathered or unpacked first."""
-    L = int(kv.seq_lens_host[b]) if kv.seq_lens_host is not None else int(kv.seq_lens[b])
-    S = kv.page_size
-    D = kv.head_dim
-    if D == 128 and pages.stride(-1) == 1 and pages.stride(-2) == pages.shape[-1] and norms.stride(-1) == 1:
-        Hkv = pages.shape[1]
-        out = torch.empty(1, Hkv, L, D, dtype=dtype if dtype in _lib.DTYPE_CODE else torch.float32,
-                          device=pages.device)
-        if L == 0:
-            return out.to(dtype)
-        with torch.cuda.device(pages.device):
+
+def _host_table(kv) -> torch.Tensor:
+    return kv.page_table_host if kv.page_table_host is not None else kv.page_table.cpu()
+
+
+def dequantize_history(kv: pa.PackedKV, pages, norms, quant, b: int, dtype) -> torch.Tensor:
+    """(1, Hkv, L, D) reconstruction of sequence b's history, on the GPU (packed_backend.py:192-208).
+
+    head_dim 128 with contiguous page rows: one ``wn_dequantize_history`` launch reads
+    the pool pages through the table row. Other shapes gather the rows, unpack and
+    dequantize with the standalone kernels."""
+    L = int(_host_lens(kv)[b])
+    S, D, Hkv = kv.page_size, kv.head_dim, pages.shape[1]
+    odt = dtype if dtype in _lib.DTYPE_CODE else torch.float32
+    out = torch.empty(1, Hkv, L, D, dtype=odt, device=pages.device)
+    if L == 0:
+        return out.to(dtype)
+    fused = D == 128 and pages.stride(-1) == 1 and pages.stride(-2) == pages.shape[-1] and norms.stride(-1) == 1
+    with torch.cuda.device(pages.device):
+        if fused:
             _lib.call("wn_dequantize_history", _lib.ptr(pages), pages.stride(0), pages.stride(1),
                       _lib.ptr(norms), norms.stride(0), norms.stride(1), _lib.ptr(kv.page_table[b]), L, Hkv, S,
                       _lib.ptr(quant.centroids), _lib.ptr(quant.Pi), quant.bit_width, D, _lib.ptr(out),
-                      _lib.DTYPE_CODE[out.dtype], 0, _lib.stream_of(pages.device))
-        return out.to(dtype)
-    table = kv.page_table_host if kv.page_table_host is not None else kv.page_table.cpu()
-    ids = table[b, :(L + S - 1) // S].long().to(pages.device)
-    rows = pages[ids].permute(1, 0, 2, 3).reshape(pages.shape[1], -1, pages.shape[3])[:, :L].contiguous()
-    nrm = norms[ids].permute(1, 0, 2).reshape(norms.shape[1], -1)[:, :L].contiguous()
-    codes = unpack(rows, quant.bit_width, D).contiguous()
-    out = torch.empty(1, rows.shape[0], L, D, dtype=dtype if dtype in _lib.DTYPE_CODE else torch.float32,
-                      device=rows.device)
-    with torch.cuda.device(rows.device):
-        _lib.call("wn_dequantize", _lib.ptr(codes), _lib.ptr(nrm), codes.numel() // D, _lib.ptr(quant.Pi),
-                  _lib.ptr(quant.centroids), quant.bit_width, D, _lib.ptr(out), _lib.DTYPE_CODE[out.dtype],
-                  _lib.stream_of(rows.device))
+                      _lib.DTYPE_CODE[odt], 0, _lib.stream_of(pages.device))
+        else:
+            ids = _host_table(kv)[b, :-(-L // S)].to(torch.int64).to(pages.device)
+            rows = pages[ids].transpose(0, 1).reshape(Hkv, -1, pages.shape[-1])[:, :L].contiguous()
+            nrm = norms[ids].transpose(0, 1).reshape(Hkv, -1)[:, :L].contiguous()
+            codes = unpack(rows, quant.bit_width, D).contiguous()
+            _lib.call("wn_dequantize", _lib.ptr(codes), _lib.ptr(nrm), Hkv * L, _lib.ptr(quant.Pi),
+                      _lib.ptr(quant.centroids), quant.bit_width, D, _lib.ptr(out), _lib.DTYPE_CODE[odt],
+                      _lib.stream_of(pages.device))
     return out.to(dtype)
 
 
+def _offset_causal(lens: torch.Tensor, Q: int, Lmax: int, device):
+    """(B, 1, Q, Lmax) mask: query i of a sequence of length L sees keys j <= L - Q + i,
+    and (B, 1, Q, 1) whether the row sees any key (packed_attention.py:200-205)."""
+    last = lens.to(torch.int64)[:, None] - Q + torch.arange(Q)[None, :]                         # (B, Q)
+    mask = torch.arange(Lmax)[None, None, :] <= last[:, :, None]
+    return mask[:, None].to(device), (last >= 0)[:, None, :, None].to(device)
+
+
+def _padded_sdpa(query, k, v, lens, scaling):
+    """One SDPA call over histories padded to the longest; rows without a key are 0."""
+    B, Hq, Q, _ = query.shape
+    mask, live = _offset_causal(lens, Q, k.shape[2], query.device)
+    out = F.scaled_dot_product_attention(query, k, v, attn_mask=mask, scale=scaling,
+                                         enable_gqa=Hq != k.shape[1])
+    return torch.where(live, out, torch.zeros((), dtype=out.dtype, device=out.device))
+
+
 def _reconstruct_sdpa(query, kv: pa.PackedKV, scaling):
-    """Per sequence: dequantize on the GPU, then SDPA with an offset causal mask (packed_backend.py:211-226)."""
+    """Dequantize every sequence's history on the GPU into one padded (B, Hkv, Lmax, D)
+    pair, then one offset-causal SDPA over the batch (packed_backend.py:211-226)."""
     B, Hq, Q, D = query.shape
-    out = torch.zeros(B, Hq, Q, D, dtype=query.dtype, device=query.device)
-    lens = kv.seq_lens_host if kv.seq_lens_host is not None else kv.seq_lens.cpu()
-    for b in range(B):
-        L = int(lens[b])
-        if L == 0:
-            continue
-        k = dequantize_history(kv, kv.k_pages, kv.k_norms, kv.k_quant, b, query.dtype)
-        v = dequantize_history(kv, kv.v_pages, kv.v_norms, kv.v_quant, b, query.dtype)
-        mask = torch.arange(L, device=query.device)[None, :] <= (
-            L - Q + torch.arange(Q, device=query.device))[:, None]
-        out[b] = F.scaled_dot_product_attention(query[b:b + 1], k, v, attn_mask=mask, scale=scaling,
-                                                enable_gqa=Hq != k.shape[1])[0]
-    return out
+    lens = _host_lens(kv).to(torch.int64)
+    Lmax = int(lens.max()) if B else 0
+    if Lmax == 0:
+        return torch.zeros(B, Hq, Q, D, dtype=query.dtype, device=query.device)
+    hist = []
+    for pages, norms, quant in ((kv.k_pages, kv.k_norms, kv.k_quant), (kv.v_pages, kv.v_norms, kv.v_quant)):
+        buf = torch.zeros(B, kv.num_kv_heads, Lmax, D, dtype=query.dtype, device=query.device)
+        for b in range(B):
+            if lens[b]:
+                buf[b, :, :int(lens[b])] = dequantize_history(kv, pages, norms, quant, b, query.dtype)[0]
+        hist.append(buf)
+    return _padded_sdpa(query, hist[0], hist[1], lens, scaling)
 
 
 def _dense_sdpa(query, kv: pa.DenseKV, scaling):
-    """Per sequence: gather unquantized pages, SDPA with an offset causal mask (packed_backend.py:229-245)."""
+    """Gather every sequence's unquantized rows into one padded (B, Hkv, Lmax, D) pair with
+    one indexed read per side, then one offset-causal SDPA (packed_backend.py:229-246)."""
     B, Hq, Q, D = query.shape
-    out = torch.zeros(B, Hq, Q, D, dtype=query.dtype, device=query.device)
+    lens = _host_lens(kv).to(torch.int64)
+    Lmax = int(lens.max()) if B else 0
+    if Lmax == 0:
+        return torch.zeros(B, Hq, Q, D, dtype=query.dtype, device=query.device)
     S = kv.page_size
-    lens = kv.seq_lens.cpu()
-    table = kv.page_table.cpu()
-    for b in range(B):
-        L = int(lens[b])
-        if L == 0:
-            continue
-        ids = table[b, :(L + S - 1) // S].long().to(query.device)
+    t = torch.arange(Lmax)
+    table = _host_table(kv).to(torch.int64)
+    page = table[:, t // S].clamp(min=0)                        # padding reads page 0; masked out
+    page = torch.where(t[None, :] < lens[:, None], page, torch.zeros_like(page)).to(query.device)
+    slot = (t % S).to(query.device)[None, :].expand(B, Lmax)
+    k = kv.k_pages[page, :, slot].permute(0, 2, 1, 3).to(query.dtype)         # (B, Hkv, Lmax, D)
+    v = kv.v_pages[page, :, slot].permute(0, 2, 1, 3).to(query.dtype)
+    return _padded_sdpa(query, k, v, lens, scaling)
 
-        def hist(p):
-            return p[ids].permute(1, 0, 2, 3).reshape(p.shape[1], -1, D)[None, :, :L].to(query.dtype)
 
-        mask = torch.arange(L, device=query.device)[None, :] <= (
-            L - Q + torch.arange(Q, device=query.device))[:, None]
-        out[b] = F.scaled_dot_product_attention(query[b:b + 1], hist(kv.k_pages), hist(kv.v_pages),
-                                                attn_mask=mask, scale=scaling,
-                                                enable_gqa=Hq != kv.num_kv_heads)[0]
-    return out
+def _hip_packed(query, kv, scaling):
+    return pa.packed_decode_attention(query, kv, scaling)
+
+
+def _hip_dense(query, kv, scaling):
+    return pa.dense_decode_attention(query, kv, scaling)
+
+
+_ROUTES = {
+    "hip_packed": _hip_packed,
+    "reconstruct_sdpa": _reconstruct_sdpa,
+    "prefill_reconstruct_sdpa": _reconstruct_sdpa,
+    "hip_dense": _hip_dense,
+    "dense_sdpa": _dense_sdpa,
+    "prefill_dense_sdpa": _dense_sdpa,
+}
+
+
+def _route(query, kv) -> str:
+    if query.shape[2] > 1:
+        return "prefill_dense_sdpa" if isinstance(kv, pa.DenseKV) else "prefill_reconstruct_sdpa"
+    return select_decode_backend(query, kv, getattr(kv, "decode_backend", "auto"))
 
 
 def winnow_packed_attention(module, query, key, value, attention_mask, dropout: float = 0.0,
                             scaling=None, **kwargs):
-    """``AttentionInterface`` entry point; returns ((B, Q, Hq, D), None) (packed_backend.py:260-290)."""
-    scaling = scaling if scaling is not None else query.shape[-1] ** -0.5
+    """``AttentionInterface`` entry point: ``(B, Q, Hq, D), None`` (packed_backend.py:260-290).
+
+    A cache handle as ``key`` routes by page kind and query length; plain tensors go to
+    transformers' SDPA, counted as ``native_sdpa``."""
+    scale = query.shape[-1] ** -0.5 if scaling is None else scaling
     if not isinstance(key, (pa.PackedKV, pa.DenseKV)):
         from transformers.integrations.sdpa_attention import sdpa_attention_forward
         BACKEND_COUNTS["native_sdpa"] += 1
         return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout,
-                                      scaling=scaling, **kwargs)
-    Q = query.shape[2]
-    if isinstance(key, pa.DenseKV):
-        if Q > 1:
-            BACKEND_COUNTS["prefill_dense_sdpa"] += 1
-            return _dense_sdpa(query, key, scaling).transpose(1, 2).contiguous(), None
-        backend = select_decode_backend(query, key, getattr(key, "decode_backend", "auto"))
-        BACKEND_COUNTS[backend] += 1
-        out = (pa.dense_decode_attention(query, key, scaling) if backend == "hip_dense"
-               else _dense_sdpa(query, key, scaling))
-        return out.transpose(1, 2).contiguous(), None
-    if Q > 1:
-        BACKEND_COUNTS["prefill_reconstruct_sdpa"] += 1
-        out = _reconstruct_sdpa(query, key, scaling)
-    else:
-        backend = select_decode_backend(query, key, getattr(key, "decode_backend", "auto"))
-        BACKEND_COUNTS[backend] += 1
-        if backend == "hip_packed":
-            out = pa.packed_decode_attention(query, key, scaling)
-        else:
-            out = _reconstruct_sdpa(query, key, scaling)
-    return out.transpose(1, 2).contiguous(), None
+                                      scaling=scale, **kwargs)
+    route = _route(query, key)
+    BACKEND_COUNTS[route] += 1
+    return _ROUTES[route](query, key, scale).transpose(1, 2).contiguous(), None
 
 
 def register() -> None:
