@@ -92,7 +92,11 @@ int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int pages_per_s
  *   q_rot = scale * q Pi_K^T; per key s = n_K (q_rot . c_K); online softmax
  *   over pages; a = sum p n_V c_V; out = (a / l) Pi_V. Rows with no key are 0.
  *   pages_per_split / num_splits come from wn_decode_plan (pages_per_split 0
- *   = balanced plan).
+ *   = balanced plan over num_splits waves; any num_splits >= 1 is valid).
+ *   Preconditions the device reads unchecked (the Python layer checks them on
+ *   host copies before the call): 0 <= seq_lens[b] <= max_pages * S, and every
+ *   page id a sequence reads, page_table[b, j] for j < cdiv(seq_lens[b], S), lies
+ *   in [0, P) of the pages the strides address.
  *   ev_begin / ev_end (hipEvent_t or NULL) are recorded on `stream` around
  *   the split-K page-scan kernel only, for in-situ timing of that kernel. */
 int wn_decode_attention(
@@ -119,8 +123,9 @@ int wn_decode_attention(
  *              page page_table[b, pos / S], slot pos % S
  *   per vector: n = max(||x||, 1e-10); y = (x / n) Pi^T; code = #{boundary < y};
  *   the packed row goes to pages, fp16(n) to norms. max_pages is the width of
- *   page_table; vectors whose position falls outside it, or whose page id is
- *   outside [0, num_pages), are not written. */
+ *   page_table. Callers must keep every position inside the table row and every
+ *   page id it names inside [0, num_pages) (the Python layer raises otherwise);
+ *   as a last guard the device skips, without writing, any vector that does not. */
 int wn_append_kv(
     const void* k, int64_t ks_b, int64_t ks_h, int64_t ks_n,
     const void* v, int64_t vs_b, int64_t vs_h, int64_t vs_n, int x_dtype,

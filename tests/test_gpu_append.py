@@ -84,60 +84,123 @@ def test_quantize_on_exact_boundaries():
     adjudicate_codes(x, codes, ocodes, oracle_quantizer(4, D, 42))
 
 
-@pytest.mark.parametrize("bw", [4, 6])
-def test_append_config3_shape(bw):
-    """BASELINE config 3 append: 16 new tokens per sequence, (16, 8, 16, 128) bf16, into shuffled pages."""
-    from winnow_amd import packed_backend as pb
-    B, Hkv, n, D, S = 16, 8, 16, 128, 16
-    g = torch.Generator().manual_seed(2)
-    prior = torch.randint(0, 200, (B,), generator=g)            # tokens already stored per sequence
+def _shuffled_pool(g, B, Hkv, n, D, S, bw, prior):
+    """Pages for ``prior[b] + n`` tokens per sequence in random order, full of random bytes."""
     P = int(sum((int(L) + n + S - 1) // S for L in prior)) + 5
     order = torch.randperm(P, generator=g)
-    width = max((int(L) + n + S - 1) // S for L in prior)
+    width = max((int(L) + n + S - 1) // S for L in prior) + 1
     table = torch.full((B, width), -1, dtype=torch.int32)
     nxt = 0
     for b in range(B):
         for t in range((int(prior[b]) + n + S - 1) // S):
             table[b, t] = int(order[nxt])
             nxt += 1
+    nb = opk.packed_bytes(D, bw)
+    pages = [torch.randint(0, 256, (P, Hkv, S, nb), dtype=torch.uint8, generator=g) for _ in range(2)]
+    norms = [torch.randn(P, Hkv, S, generator=g).half() for _ in range(2)]
+    return P, table, pages, norms
+
+
+def _compare_append(got, before, want, src, oq, table, prior, n, bw, D):
+    """Bytes outside the appended slots unchanged (always checked); inside them, the
+    oracle's bytes, or codes that differ only by adjudicated flips."""
+    S = got.shape[2]
+    pos = oapp.positions(prior, n)
+    pids, slots = oapp.locate(table, pos, S)
+    written = torch.zeros(got.shape[:3], dtype=torch.bool)
+    written[pids, :, slots] = True
+    assert torch.equal(got[~written], before[~written]), "bytes outside the appended slots changed"
+    if torch.equal(got, want):
+        return 0
+    gc = torch.from_numpy(opk.unpack(got.numpy(), bw, D))
+    wc = torch.from_numpy(opk.unpack(want.numpy(), bw, D))
+    return adjudicate_codes(src, gc[pids, :, slots].permute(0, 2, 1, 3), wc[pids, :, slots].permute(0, 2, 1, 3), oq)
+
+
+@pytest.mark.parametrize("bw", [4, 6])
+def test_append_config3_shape(bw):
+    """BASELINE config 3 append: 16 new tokens per sequence, (16, 8, 16, 128) bf16, into
+    shuffled pages holding random bytes; codes and norms against the pinned oracle scatter."""
+    from winnow_amd import packed_backend as pb
+    B, Hkv, n, D, S = 16, 8, 16, 128, 16
+    g = torch.Generator().manual_seed(2)
+    prior = torch.randint(0, 200, (B,), generator=g)            # tokens already stored per sequence
+    P, table, (kp0, vp0), (kn0, vn0) = _shuffled_pool(g, B, Hkv, n, D, S, bw, prior)
     k = torch.randn(B, Hkv, n, D, generator=g).bfloat16()
     v = torch.randn(B, Hkv, n, D, generator=g).bfloat16()
-    nb = opk.packed_bytes(D, bw)
-    ref_kp = torch.randint(0, 256, (P, Hkv, S, nb), dtype=torch.uint8, generator=g)   # pre-existing bytes
-    ref_vp = torch.randint(0, 256, (P, Hkv, S, nb), dtype=torch.uint8, generator=g)
-    ref_kn = torch.randn(P, Hkv, S, generator=g).half()
-    ref_vn = torch.randn(P, Hkv, S, generator=g).half()
     kq, vq = _q(bw, D, 42), _q(bw, D, 43)
-    dk, dv, dkn, dvn = (t.to(DEV) for t in (ref_kp, ref_vp, ref_kn, ref_vn))
+    dk, dv, dkn, dvn = (t.to(DEV) for t in (kp0, vp0, kn0, vn0))
     pb.append_kv(k.to(DEV), v.to(DEV), kq, vq, dk, dv, dkn, dvn, table.to(DEV),
                  prior.to(torch.int32).to(DEV))
     okq, ovq = oracle_quantizer(bw, D, 42), oracle_quantizer(bw, D, 43)
-    oapp.append(k, okq, ref_kp, ref_kn, table, prior.tolist())
-    oapp.append(v, ovq, ref_vp, ref_vn, table, prior.tolist())
-    for got, want, src, oq in ((dk, ref_kp, k, okq), (dv, ref_vp, v, ovq)):
+    want = [kp0.clone(), vp0.clone()]
+    wantn = [kn0.clone(), vn0.clone()]
+    oapp.append(k, okq, want[0], wantn[0], table, prior.tolist())
+    oapp.append(v, ovq, want[1], wantn[1], table, prior.tolist())
+    flips = 0
+    for got, before, w, src, oq in ((dk, kp0, want[0], k, okq), (dv, vp0, want[1], v, ovq)):
+        flips += _compare_append(got.cpu(), before, w, src, oq, table, prior.tolist(), n, bw, D)
+    print(f"config-3 append {bw} bits: {flips} adjudicated code flips", flush=True)
+    pos = oapp.positions(prior.tolist(), n)
+    pids, slots = oapp.locate(table, pos, S)
+    for got, before, w, src in ((dkn, kn0, wantn[0], k), (dvn, vn0, wantn[1], v)):
         got = got.cpu()
-        if not torch.equal(got, want):
-            # identical bytes except where an adjudicated code flip changed the packing
-            gc = torch.from_numpy(opk.unpack(got.numpy(), bw, D))
-            wc = torch.from_numpy(opk.unpack(want.numpy(), bw, D))
-            pos = torch.tensor([[int(L) + i for i in range(n)] for L in prior])
-            pids = torch.gather(table.long(), 1, pos // S)
-            slots = pos % S
-            sel_g = gc[pids, :, slots].permute(0, 2, 1, 3)
-            sel_w = wc[pids, :, slots].permute(0, 2, 1, 3)
-            adjudicate_codes(src, sel_g, sel_w, oq)
-            mask = torch.ones(P, Hkv, S, dtype=torch.bool)
-            mask[pids, :, slots] = False
-            assert torch.equal(got[mask], want[mask]), "bytes outside the appended slots changed"
-    for got, want, src in ((dkn, ref_kn, k), (dvn, ref_vn, v)):
-        got = got.cpu()
-        if not torch.equal(got.view(torch.int16), want.view(torch.int16)):
-            n32 = src.float().norm(dim=-1).clamp(min=1e-10)
-            pos = torch.tensor([[int(L) + i for i in range(n)] for L in prior])
-            pids = torch.gather(table.long(), 1, pos // S)
-            slots = pos % S
-            adjudicate_fp16_norms(n32.permute(0, 2, 1), n32.permute(0, 2, 1),
-                                  got[pids, :, slots], want[pids, :, slots])
+        written = torch.zeros(got.shape, dtype=torch.bool)
+        written[pids, :, slots] = True
+        assert torch.equal(got[~written].view(torch.int16), before[~written].view(torch.int16))
+        if not torch.equal(got.view(torch.int16), w.view(torch.int16)):
+            n32 = src.float().norm(dim=-1).clamp(min=1e-10).permute(0, 2, 1)
+            adjudicate_fp16_norms(n32, n32, got[pids, :, slots], w[pids, :, slots])
+
+
+def test_append_k_only_leaves_v_alone():
+    """v = None appends K alone (the C ABI's NULL V): K bytes as the oracle's, V pages and
+    norms untouched."""
+    from winnow_amd import packed_backend as pb
+    B, Hkv, n, D, S, bw = 3, 4, 5, 128, 16, 4
+    g = torch.Generator().manual_seed(21)
+    prior = torch.tensor([14, 0, 33])                           # starts mid-page, empty, mid-page
+    P, table, (kp0, vp0), (kn0, vn0) = _shuffled_pool(g, B, Hkv, n, D, S, bw, prior)
+    k = torch.randn(B, Hkv, n, D, generator=g)
+    kq = _q(bw, D, 42)
+    dk, dv, dkn, dvn = (t.to(DEV) for t in (kp0, vp0, kn0, vn0))
+    pb.append_kv(k.to(DEV), None, kq, None, dk, None, dkn, None, table.to(DEV), prior.to(torch.int32).to(DEV))
+    want, wantn = kp0.clone(), kn0.clone()
+    okq = oracle_quantizer(bw, D, 42)
+    oapp.append(k, okq, want, wantn, table, prior.tolist())
+    _compare_append(dk.cpu(), kp0, want, k, okq, table, prior.tolist(), n, bw, D)
+    assert torch.equal(dv.cpu(), vp0) and torch.equal(dvn.cpu().view(torch.int16), vn0.view(torch.int16))
+
+
+def test_append_rejects_before_launch():
+    """Positions past the table row, pages outside the pool and V of another shape are
+    refused before any launch, and the pool is left as it was (the reference raises in
+    its gather, packed_backend.py:144)."""
+    from winnow_amd import packed_attention as pa
+    from winnow_amd import packed_backend as pb
+    B, Hkv, n, D, S, bw = 2, 2, 4, 128, 16, 4
+    kq = _q(bw, D, 42)
+    P = 4
+    kp = torch.zeros(P, Hkv, S, 64, dtype=torch.uint8, device=DEV)
+    kn = torch.zeros(P, Hkv, S, dtype=torch.float16, device=DEV)
+    k = torch.randn(B, Hkv, n, D, device=DEV)
+    table = torch.tensor([[0, 1], [2, -1]], dtype=torch.int32)
+    ok = torch.tensor([10, 3], dtype=torch.int32)
+    pb.append_kv(k, k, kq, kq, kp, kp.clone(), kn, kn.clone(), table.to(DEV), ok.to(DEV))
+    for tab, start, why in ((table, torch.tensor([30, 3], dtype=torch.int32), "outside its 2-page"),
+                            (table, torch.tensor([0, 14], dtype=torch.int32), "sequence 1"),
+                            (torch.tensor([[0, 9], [2, -1]], dtype=torch.int32), ok + 4, "outside \\[0, 4\\)")):
+        snap = kp.clone()
+        with pytest.raises(pa.UnsupportedLayout, match=why):
+            pb.append_kv(k, None, kq, None, kp, None, kn, None, tab.to(DEV), start.to(DEV))
+        with pytest.raises(pa.UnsupportedLayout, match=why):      # same through host mirrors
+            pb.append_kv(k, None, kq, None, kp, None, kn, None, tab.to(DEV), start.to(DEV),
+                         page_table_host=tab, start_pos_host=start)
+        assert torch.equal(kp, snap)
+    with pytest.raises(pa.UnsupportedLayout, match="differs"):
+        pb.append_kv(k, k[:, :, :2], kq, kq, kp, kp.clone(), kn, kn.clone(), table.to(DEV), ok.to(DEV))
+    with pytest.raises(pa.UnsupportedLayout, match="norms"):
+        pb.append_kv(k, None, kq, None, kp, None, kn[:, :1], None, table.to(DEV), ok.to(DEV))
 
 
 def test_dequantize_matches_oracle_and_fp16_budget():

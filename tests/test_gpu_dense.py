@@ -158,3 +158,19 @@ def test_dense_decode_has_no_host_path():
     kp, vp, table, sl = _pages(71, (20,), 2, 16)
     with pytest.raises(pa.UnsupportedLayout):
         pa.dense_decode_attention(torch.randn(1, 4, 1, 128), pa.DenseKV(kp, vp, table, sl, 128), 0.1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("waves", [1, 5, 37])
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (64, 4)])
+def test_dense_balanced_plan_with_few_waves(waves, Hq, Hkv):
+    """The dense scan's balanced loop with each wave walking many chunks across
+    (sequence, kv head) boundaries and over zero-length sequences mid-share."""
+    lens = (0, 130, 0, 0, 64, 1, 700, 0, 65, 2000, 0)
+    kp, vp, table, sl = _pages(600 + waves + Hq, lens, Hkv, 16)
+    q = torch.randn(len(lens), Hq, 1, 128, generator=torch.Generator().manual_seed(waves))
+    scale = 128 ** -0.5
+    got = _run(q, kp, vp, table, sl, scale, plan=(0, waves), out_dtype=torch.float32).cpu()
+    ref = oa.dense_paged_attention_f64(q, kp, vp, table, sl, scale)
+    assert torch.allclose(got.double(), ref, atol=ATOL, rtol=RTOL), (got.double() - ref).abs().max()
+    assert bool((got[[0, 2, 3, 7, 10]] == 0).all())

@@ -494,7 +494,9 @@ SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v) {
   const int shift = (n_rep > 8 && n_rep <= 16 && n_rep % 2 == 0) ? 1 : 0;
   if (D == 128 && (n_rep >> shift) <= 8 && S >= 16 && rows_allowed()) {
     sk = pick_split_rows(bw_k, bw_v, n_rep >> shift);
-    sk.kvshift = shift;
+    // the virtual-head view exists only on the row scan; the VALU scan below reads
+    // physical kv heads
+    if (sk.fn) sk.kvshift = shift;
   }
   if (!sk.fn) {
     const int nrp = pad_nrep(n_rep);
