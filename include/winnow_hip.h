@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define WN_ABI_VERSION 4
+#define WN_ABI_VERSION 5
 
 /* element types of floating-point tensors crossing the ABI */
 enum { WN_F32 = 0, WN_F16 = 1, WN_BF16 = 2 };
@@ -111,6 +111,32 @@ int wn_decode_attention(
     const int32_t* seq_lens,
     void* out, int out_dtype,
     void* workspace, int64_t workspace_bytes,
+    int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
+    float scale, int pages_per_split, int num_splits,
+    void* stream, void* ev_begin, void* ev_end);
+
+/* Allocation-free variant of wn_decode_attention. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory, not even a
+ * workspace (code under HIP graph capture, serving loops that forbid
+ * allocation). Same arguments, meaning and result as wn_decode_attention without
+ * the workspace: the scratch is a static device array of WN_NOALLOC_SCRATCH_BYTES
+ * (32 MiB) that each GPU the library runs on holds until the process ends. A
+ * shape and plan whose wn_decode_workspace_bytes exceeds it is rejected with
+ * WN_E_WORKSPACE before any launch. Calls on one GPU share that array, so calls
+ * that overlap on one GPU (different streams, or threads) race; calls ordered on
+ * one stream do not. Nothing is allocated or freed. */
+#define WN_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int wn_decode_attention_noalloc(
+    const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+    const float* pi_k, const float* pi_v,
+    const float* codebook_k, const float* codebook_v,
+    const uint8_t* k_pages, int64_t k_stride_p, int64_t k_stride_h,
+    const uint8_t* v_pages, int64_t v_stride_p, int64_t v_stride_h,
+    const uint16_t* k_norms, int64_t kn_stride_p, int64_t kn_stride_h,
+    const uint16_t* v_norms, int64_t vn_stride_p, int64_t vn_stride_h,
+    const int32_t* page_table, int64_t table_stride_b,
+    const int32_t* seq_lens,
+    void* out, int out_dtype,
     int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
     float scale, int pages_per_split, int num_splits,
     void* stream, void* ev_begin, void* ev_end);

@@ -712,6 +712,74 @@ extern "C" int wn_decode_attention(
   return check_launch("wn_decode_attention");
 }
 
+// ------------------------------------------------- allocation-free decode entry
+
+// Scratch of wn_decode_attention_noalloc: a file-scope device array, so a caller
+// that cannot allocate device memory (code under graph capture, a serving loop
+// that forbids it) still gets the rotated query, chunk prefix, partial ranges and
+// partials somewhere. Each GPU the library runs on holds its own copy until the
+// process ends. On the host the array's name is only a stand-in for its symbol:
+// its device address comes from hipGetSymbolAddress, once per device, and only
+// that address is ever handed to a kernel.
+static constexpr int64_t kNoAllocScratchBytes = WN_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on its first use there).
+int current_scratch(void** addr) {
+  using namespace wn;
+  int dev = -1;
+  WN_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices, WN_E_LAUNCH,
+             "decode (no-alloc): no current device (or device %d beyond %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    WN_REQUIRE(e == hipSuccess && p, WN_E_LAUNCH, "decode (no-alloc): hipGetSymbolAddress on device %d: %s", dev,
+               hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return WN_OK;
+}
+}  // namespace
+
+extern "C" int wn_decode_attention_noalloc(
+    const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+    const float* pi_k, const float* pi_v, const float* codebook_k, const float* codebook_v,
+    const uint8_t* k_pages, int64_t k_stride_p, int64_t k_stride_h,
+    const uint8_t* v_pages, int64_t v_stride_p, int64_t v_stride_h,
+    const uint16_t* k_norms, int64_t kn_stride_p, int64_t kn_stride_h,
+    const uint16_t* v_norms, int64_t vn_stride_p, int64_t vn_stride_h,
+    const int32_t* page_table, int64_t table_stride_b, const int32_t* seq_lens,
+    void* out, int out_dtype,
+    int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
+    float scale, int pages_per_split, int num_splits,
+    void* stream, void* ev_begin, void* ev_end) {
+  using namespace wn;
+  clear_error();
+  const int64_t need = wn_decode_workspace_bytes(B, Hq, Hkv, D, pages_per_split, num_splits);
+  WN_REQUIRE(need <= kNoAllocScratchBytes, WN_E_WORKSPACE,
+             "decode (no-alloc): B=%d Hq=%d Hkv=%d D=%d with %d splits x %d pages needs %lld bytes of scratch, "
+             "more than the %lld-byte static scratch; call wn_decode_attention with a workspace",
+             B, Hq, Hkv, D, num_splits, pages_per_split, (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int rc = current_scratch(&ws);
+  if (rc != WN_OK) return rc;
+  // every byte of the scratch a call reads is written earlier in the same call
+  // (rotate: q_rot, prefix, unit_meta reset; scan: partial rows and ranges), so
+  // nothing is cleared between calls
+  return wn_decode_attention(q, q_dtype, q_stride_b, q_stride_h, pi_k, pi_v, codebook_k, codebook_v, k_pages,
+                             k_stride_p, k_stride_h, v_pages, v_stride_p, v_stride_h, k_norms, kn_stride_p,
+                             kn_stride_h, v_norms, vn_stride_p, vn_stride_h, page_table, table_stride_b, seq_lens, out,
+                             out_dtype, ws, kNoAllocScratchBytes, B, Hq, Hkv, D, S, bw_k, bw_v, max_pages, scale,
+                             pages_per_split, num_splits, stream, ev_begin, ev_end);
+}
+
 // ---------------------------------------------------------------- dense pages
 
 extern "C" int wn_dense_decode_plan(int B, int Hq, int Hkv, int D, int S, int page_dtype, int max_pages,

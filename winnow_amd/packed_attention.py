@@ -283,7 +283,6 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
     check_kernel_contract(q, kv, check_ranges=check_ranges)
     B, Hq, _, D = q.shape
     Hkv = kv.num_kv_heads
-    max_pages = kv.page_table.shape[1]
     pps, ns = plan if plan is not None else plan_for(q, kv, num_splits)
     out_dtype = out_dtype or q.dtype
     if out_dtype not in _lib.DTYPE_CODE:
@@ -295,23 +294,56 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
     elif workspace.numel() * workspace.element_size() < need or workspace.device != q.device:
         raise UnsupportedLayout(f"workspace needs {need} bytes on {q.device}")
     ev0, ev1 = timing_events or (None, None)
-    qv = q[:, :, 0]
     with torch.cuda.device(q.device):
-        _lib.call(
-            "wn_decode_attention",
-            _lib.ptr(qv), _lib.DTYPE_CODE[q.dtype], qv.stride(0), qv.stride(1),
+        _lib.call("wn_decode_attention", *_operands(q, kv), _lib.ptr(out), _lib.DTYPE_CODE[out_dtype],
+                  _lib.ptr(workspace), workspace.numel() * workspace.element_size(),
+                  *_sizes(q, kv), float(scale), pps, ns, _lib.stream_of(q.device), ev0, ev1)
+    return out
+
+
+def _operands(q: torch.Tensor, kv: PackedKV) -> tuple:
+    """The C-ABI arguments of a decode from q through seq_lens."""
+    qv = q[:, :, 0]
+    return (_lib.ptr(qv), _lib.DTYPE_CODE[q.dtype], qv.stride(0), qv.stride(1),
             _lib.ptr(kv.k_quant.Pi), _lib.ptr(kv.v_quant.Pi),
             _lib.ptr(kv.k_quant.centroids), _lib.ptr(kv.v_quant.centroids),
             _lib.ptr(kv.k_pages), kv.k_pages.stride(0), kv.k_pages.stride(1),
             _lib.ptr(kv.v_pages), kv.v_pages.stride(0), kv.v_pages.stride(1),
             _lib.ptr(kv.k_norms), kv.k_norms.stride(0), kv.k_norms.stride(1),
             _lib.ptr(kv.v_norms), kv.v_norms.stride(0), kv.v_norms.stride(1),
-            _lib.ptr(kv.page_table), kv.page_table.stride(0), _lib.ptr(kv.seq_lens),
-            _lib.ptr(out), _lib.DTYPE_CODE[out_dtype],
-            _lib.ptr(workspace), workspace.numel() * workspace.element_size(),
-            B, Hq, Hkv, D, kv.page_size, kv.k_quant.bit_width, kv.v_quant.bit_width, max_pages,
-            float(scale), pps, ns,
-            _lib.stream_of(q.device), ev0, ev1)
+            _lib.ptr(kv.page_table), kv.page_table.stride(0), _lib.ptr(kv.seq_lens))
+
+
+def _sizes(q: torch.Tensor, kv: PackedKV) -> tuple:
+    B, Hq, _, D = q.shape
+    return (B, Hq, kv.num_kv_heads, D, kv.page_size, kv.k_quant.bit_width, kv.v_quant.bit_width,
+            kv.page_table.shape[1])
+
+
+def packed_decode_attention_noalloc(q: torch.Tensor, kv: PackedKV, scale: float, out: torch.Tensor, *,
+                                    num_splits: int | None = None, plan: tuple[int, int] | None = None,
+                                    check_ranges: bool = True, timing_events=None) -> torch.Tensor:
+    """``packed_decode_attention`` into a caller-owned ``out`` (B, Hq, 1, D), contiguous,
+    fp32/fp16/bf16, with no device allocation at all: the scratch is the library's
+    static per-GPU array (``wn_decode_attention_noalloc``, 32 MiB). For callers that
+    cannot allocate (graph capture, allocation-free serving loops). A shape and plan
+    needing more scratch than that raises ``UnsupportedLayout`` before any launch.
+    Calls that overlap on one GPU (other streams or threads) share the array and race.
+    """
+    check_kernel_contract(q, kv, check_ranges=check_ranges)
+    B, Hq, _, D = q.shape
+    if out.shape != (B, Hq, 1, D) or out.dtype not in _lib.DTYPE_CODE or not out.is_contiguous() \
+            or out.device != q.device:
+        raise UnsupportedLayout(f"out must be a contiguous ({B}, {Hq}, 1, {D}) fp32/fp16/bf16 tensor on {q.device}")
+    pps, ns = plan if plan is not None else plan_for(q, kv, num_splits)
+    need = workspace_bytes(B, Hq, kv.num_kv_heads, D, pps, ns)
+    if need > _lib.NOALLOC_SCRATCH_BYTES:
+        raise UnsupportedLayout(f"this shape and plan need {need} bytes of scratch, more than the "
+                                f"{_lib.NOALLOC_SCRATCH_BYTES}-byte static scratch")
+    ev0, ev1 = timing_events or (None, None)
+    with torch.cuda.device(q.device):
+        _lib.call("wn_decode_attention_noalloc", *_operands(q, kv), _lib.ptr(out), _lib.DTYPE_CODE[out.dtype],
+                  *_sizes(q, kv), float(scale), pps, ns, _lib.stream_of(q.device), ev0, ev1)
     return out
 
 
