@@ -1,7 +1,8 @@
 #!/usr/bin/env python
 """Headline benchmark: packed decode attention on one MI355X (BASELINE config 2 by default).
 
-    python bench.py [--steps K] [--warmup W] [--config 2|3|4|5] [--cpu-baseline on|off]
+    python bench.py [--steps K] [--warmup W] [--config 2|3|4|5] [--configs 3,4,5|none]
+                    [--cpu-baseline on|off]
 
 A step is one decode-attention call (rotate q, split-K page scan, merge + output
 rotation) over the whole batch, one new query token per sequence, with the
@@ -20,6 +21,8 @@ scaled by what the same counters read for a 1 GiB device copy.
 ``cpu_baseline`` times the CPU restatement of the reference's CPU decode path
 (``tiled_compressed_attention``) on a bounded sample of page-table columns of
 the same workload and scales it to the full step.
+``configs`` repeats the decode measurement (scan time, its fraction of 8 TB/s,
+tokens/s, sampled parity against the oracle) for the other BASELINE configs.
 """
 from __future__ import annotations
 
@@ -39,93 +42,18 @@ sys.path.insert(0, str(ROOT))
 METRIC = "decode-attn tokens/s + HBM GB/s (% peak), 4-bit packed KV, 32k ctx, 1 GPU"
 HBM_PEAK_GBPS = 8000.0
 
-# BASELINE.json configs 2-5 (config 1 is the CPU plumbing/parity case).
-CONFIGS = {
-    2: dict(B=16, Hq=32, Hkv=8, D=128, L=32768, S=16, bwk=4, bwv=4, seed=1, table="contiguous",
-            data="outliers"),
-    3: dict(B=16, Hq=32, Hkv=8, D=128, L=32768, S=16, bwk=6, bwv=6, seed=2, table="contiguous",
-            data="outliers"),
-    4: dict(B=64, Hq=32, Hkv=8, D=128, L=None, S=16, bwk=4, bwv=4, seed=3, table="shuffled",
-            data="normal"),
-    5: dict(B=4, Hq=64, Hkv=8, D=128, L=131072, S=16, bwk=4, bwv=6, seed=4, table="contiguous",
-            data="lognormal_heads"),
-}
+sys.path.insert(0, str(ROOT / "tests"))
+import workloads  # noqa: E402  (shared with the full-size GPU parity tests)
+
+CONFIGS = workloads.CONFIGS
+DATA_NOTE = ("synthetic, seeded: lengths, page order, outlier channels, head scales and q from "
+             "torch.Generator().manual_seed(config seed); K/V drawn on the GPU from a generator seeded "
+             "with the same seed (a CPU draw of the 1e9-4.4e9 normals takes minutes), cast to bf16 and "
+             "packed by the product append kernel; q ~N(0,1) bf16")
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
-
-
-def build_workload(cfg: int, dev, copies: int):
-    """Pool pages for config ``cfg`` filled by the product append kernel, plus the query.
-
-    Seeded CPU generator: sequence lengths, page order, outlier channels, per-head
-    scales and q. K/V values are drawn on the device from a generator seeded with
-    the same seed (a billion CPU normals would take ~50 s) and cast to bf16.
-    """
-    import torch
-    from winnow_amd import packed_attention as pa
-    from winnow_amd import packed_backend as pb
-    from winnow_amd.packing import packed_bytes
-    from winnow_amd.quantizer import get_quantizer
-
-    c = CONFIGS[cfg]
-    B, Hq, Hkv, D, S = c["B"], c["Hq"], c["Hkv"], c["D"], c["S"]
-    g = torch.Generator().manual_seed(c["seed"])
-    gd = torch.Generator(device=dev).manual_seed(c["seed"])
-    if c["L"] is None:
-        lens = torch.randint(512, 65537, (B,), generator=g).tolist()
-    else:
-        lens = [c["L"]] * B
-    need = [(L + S - 1) // S for L in lens]
-    P = sum(need)
-    order = torch.randperm(P, generator=g) if c["table"] == "shuffled" else torch.arange(P)
-    table = torch.full((B, max(need)), -1, dtype=torch.int32)
-    off = 0
-    for b in range(B):
-        table[b, :need[b]] = order[off:off + need[b]].to(torch.int32)
-        off += need[b]
-    # 1% of channels x10: max(1, round(0.01 * D)) = 1 channel per (kv head) for K and for V
-    n_out = max(1, round(0.01 * D))
-    k_ch = [torch.randperm(D, generator=g)[:n_out] for _ in range(Hkv)]
-    v_ch = [torch.randperm(D, generator=g)[:n_out] for _ in range(Hkv)]
-    head_std = torch.exp(torch.randn(B, Hkv, 2, generator=g) * 0.5)       # LogNormal(0, 0.5)
-    q = (torch.randn(B, Hq, 1, D, generator=g)).to(dev, torch.bfloat16)
-
-    kq = get_quantizer(c["bwk"], D, dev, 42)
-    vq = get_quantizer(c["bwv"], D, dev, 42)
-    nbk, nbv = packed_bytes(D, c["bwk"]), packed_bytes(D, c["bwv"])
-    kp = torch.zeros(P, Hkv, S, nbk, dtype=torch.uint8, device=dev)
-    vp = torch.zeros(P, Hkv, S, nbv, dtype=torch.uint8, device=dev)
-    kn = torch.zeros(P, Hkv, S, dtype=torch.float16, device=dev)
-    vn = torch.zeros(P, Hkv, S, dtype=torch.float16, device=dev)
-    dtable = table.to(dev)
-    sample = None
-    for b in range(B):
-        L = lens[b]
-        k = torch.randn(1, Hkv, L, D, generator=gd, device=dev)
-        v = torch.randn(1, Hkv, L, D, generator=gd, device=dev)
-        if c["data"] == "outliers":
-            for h in range(Hkv):
-                k[:, h, :, k_ch[h].to(dev)] *= 10
-                v[:, h, :, v_ch[h].to(dev)] *= 10
-        elif c["data"] == "lognormal_heads":
-            k *= head_std[b, :, 0].to(dev)[None, :, None, None]
-            v *= head_std[b, :, 1].to(dev)[None, :, None, None]
-        k, v = k.bfloat16(), v.bfloat16()
-        if b == 0:
-            sample = (k[:, :, :256].cpu(), v[:, :, :256].cpu())
-        pb.append_kv(k, v, kq, vq, kp, vp, kn, vn, dtable[b:b + 1],
-                     torch.zeros(1, dtype=torch.int32, device=dev))
-        del k, v
-    seq = torch.tensor(lens, dtype=torch.int32)
-    kvs = []
-    for i in range(copies):
-        t = (kp, kn, vp, vn) if i == 0 else tuple(x.clone() for x in (kp, kn, vp, vn))
-        kvs.append(pa.PackedKV(t[0], t[1], t[2], t[3], dtable, seq.to(dev), pa.Quantizer.from_tq(kq),
-                               pa.Quantizer.from_tq(vq), D, seq_lens_host=seq, page_table_host=table))
-    torch.cuda.synchronize()
-    return c, lens, q, kvs, (kq, vq), sample
 
 
 def scan_kernel_name(c) -> str:
@@ -138,8 +66,7 @@ def scan_kernel_name(c) -> str:
     return "decode_split_kernel"
 
 
-def kv_bytes(lens, Hkv, nbk, nbv):
-    return sum(lens) * Hkv * ((nbk + 2) + (nbv + 2))
+kv_bytes = workloads.kv_bytes
 
 
 def copy_peak(dev, nbytes: int = 1 << 30, reps: int = 10):
@@ -192,6 +119,7 @@ def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
             cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "run", "--",
                    sys.executable, str(ROOT / "bench.py"), "--config", str(cfg), "--steps", "3", "--warmup", "1",
                    "--settle", "0", "--parity", "off", "--cpu-baseline", "off", "--traffic", "off", "--append", "off",
+                   "--configs", "none",
                    "--dequant", "off", "--dense", "off",
                    "--copy-peak", "on"]
             try:
@@ -334,9 +262,10 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
     vn = torch.zeros(P, Hkv, S, dtype=torch.float16, device=dev)
     kd, vd, td, sd = k.to(dev), v.to(dev), tab.to(dev), start.to(dev)
 
-    def call():
-        pb.append_kv(kd, vd, kq, vq, kp, vp, kn, vn, td, sd)
+    def call(check=False):
+        pb.append_kv(kd, vd, kq, vq, kp, vp, kn, vn, td, sd, check_ranges=check)
 
+    call(check=True)                             # full validation once, outside the timed region
     for _ in range(20):
         call()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -454,39 +383,118 @@ def dequant_bench(dev, bws=(4, 6), reps: int = 50, check_rows: int = 2048, cpu_r
     return res
 
 
-def parity(c, lens, q, kv, quants, sample):
-    """Same-run checks: two sequences' attention vs the CPU oracle on the same pages, and
-    the first 256 tokens of sequence 0 re-quantized by the oracle vs the pool bytes."""
+def parity(w, kv=None, seqs=None):
+    """Same-run checks on the same pages: the first, middle and last sequences' attention
+    against the CPU oracle (2e-3 max-abs / 1e-3 relative of the fp32 output) and the
+    float64 oracle (relative L2), and sequence 0's first 256 tokens re-quantized by the
+    oracle against the pool bytes (adjudicated flips)."""
     import torch
-    sys.path.insert(0, str(ROOT / "tests"))
-    from adjudicate import adjudicate_codes
     from cases import to_host
     from oracle import attention as oa
-    from oracle import packing as opk
-    from oracle.quantizer import get_quantizer as oq
     from winnow_amd import packed_attention as pa
 
-    D, S = c["D"], c["S"]
-    scale = oa.default_scale(D)
-    seqs = [0, len(lens) - 1]
-    got = pa.packed_decode_attention(q, kv, scale, out_dtype=torch.float32).cpu()[seqs]
+    kv = kv or w.kvs[0]
+    B = len(w.lens)
+    seqs = seqs or sorted({0, B // 2, B - 1})
+    scale = oa.default_scale(w.c["D"])
+    got = pa.packed_decode_attention(w.q, kv, scale, out_dtype=torch.float32).cpu()[seqs]
     sub = to_host(kv, seqs)
-    ref = oa.tiled_compressed_attention(q.float().cpu()[seqs], sub, scale)
-    err = (got - ref).abs().max().item()
-    ok = bool(torch.allclose(got, ref, atol=2e-3, rtol=1e-3))
-    f64 = oa.reconstruct_attention_f64(q.float().cpu()[seqs], sub, scale)
-    rel = ((got.double() - f64).norm() / f64.norm()).item()
-    flips = 0
-    for side, (src, quant, pages) in enumerate(((sample[0], oq(c["bwk"], D, 42), kv.k_pages),
-                                                (sample[1], oq(c["bwv"], D, 42), kv.v_pages))):
-        codes, _ = quant.quantize(src)                                   # (1, Hkv, 256, D)
-        ids = kv.page_table_host[0, :256 // S].long()
-        stored = pages[ids.to(pages.device)].cpu()                       # (16, Hkv, S, NB)
-        stored = torch.from_numpy(opk.unpack(stored.numpy(), quant.bit_width, D))
-        stored = stored.permute(1, 0, 2, 3).reshape(1, stored.shape[1], 256, D)
-        flips += adjudicate_codes(src, stored, codes, quant)
-    return {"attn_max_abs_err": err, "attn_within_2e-3_1e-3": ok, "rel_l2_vs_f64": rel,
-            "codes_checked": 2 * 256 * c["Hkv"] * D, "adjudicated_code_flips": flips}
+    qs = w.q.float().cpu()[seqs]
+    ref = oa.tiled_compressed_attention(qs, sub, scale)
+    f64 = oa.reconstruct_attention_f64(qs, sub, scale)
+    flips = workloads.requantize_flips(w, kv)
+    return {"sequences": seqs, "attn_max_abs_err": (got - ref).abs().max().item(),
+            "attn_within_2e-3_1e-3": bool(torch.allclose(got, ref, atol=2e-3, rtol=1e-3)),
+            "rel_l2_vs_f64": ((got.double() - f64).norm() / f64.norm()).item(),
+            "codes_checked": 2 * w.sample[0].shape[2] * w.c["Hkv"] * w.c["D"], "adjudicated_code_flips": flips}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (``lscpu``'s "Model name", read from /proc/cpuinfo)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def measure_decode(w, steps: int, warmup: int, settle: float, splits=None):
+    """Time ``steps`` decode steps of workload ``w`` (pools rotated between steps): the
+    step time from events around the calls, the page-scan kernel from HIP events the C
+    ABI records on its stream around every launch."""
+    import torch
+    from winnow_amd import packed_attention as pa
+
+    q, kvs = w.q, w.kvs
+    B, Hq, Hkv, D = len(w.lens), w.c["Hq"], w.c["Hkv"], w.c["D"]
+    scale = 1.0 / math.sqrt(D)
+    pps, ns = pa.plan_for(q, kvs[0], splits)
+    ws = torch.empty(pa.workspace_bytes(B, Hq, Hkv, D, pps, ns), dtype=torch.uint8, device=q.device)
+    for kv in kvs:
+        pa.check_kernel_contract(q, kv)          # full validation once, outside the timed region
+
+    def step(i, evs=None):
+        return pa.packed_decode_attention(q, kvs[i % len(kvs)], scale, workspace=ws, check_ranges=False,
+                                          timing_events=evs, plan=(pps, ns))
+
+    # Bring the GPU to its sustained clocks before the warm-up steps: a few ms of work
+    # otherwise times a part-clocked GPU, which a decode server running continuously
+    # never sees.
+    t_settle = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t_settle < settle:
+        for _ in range(20):
+            step(i)
+            i += 1
+        torch.cuda.synchronize()
+    for i in range(warmup):
+        step(i)
+    ev_pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for _ in range(steps)]
+    for e0, e1 in ev_pairs:                       # materialise the underlying hipEvents
+        e0.record()
+        e1.record()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        e0, e1 = ev_pairs[i]
+        step(i, (ctypes.c_void_p(e0.cuda_event), ctypes.c_void_p(e1.cuda_event)))
+    end.record()
+    torch.cuda.synchronize()
+    kern = [e0.elapsed_time(e1) for e0, e1 in ev_pairs]
+    return {"ms_per_step": start.elapsed_time(end) / steps, "kernel_ms": statistics.fmean(kern),
+            "kernel_ms_median": statistics.median(kern), "splits": ns, "pages_per_split": pps}
+
+
+def config_line(cfg: int, dev, steps: int, warmup: int, settle: float, copies: int, check: bool):
+    """Decode throughput, roofline fraction of the scan and same-run parity at config ``cfg``."""
+    import torch
+    from winnow_amd.packing import packed_bytes
+
+    t0 = time.time()
+    w = workloads.build(cfg, dev, copies=copies)
+    c = w.c
+    log(f"config {cfg} built in {time.time() - t0:.1f} s: B={len(w.lens)} sum(L)={sum(w.lens)}")
+    m = measure_decode(w, steps, warmup, settle)
+    nbytes = kv_bytes(w.lens, c["Hkv"], packed_bytes(c["D"], c["bwk"]), packed_bytes(c["D"], c["bwv"]))
+    gbps = nbytes / (m["kernel_ms"] * 1e-3) / 1e9
+    line = {"workload": f"BASELINE config {cfg}", "batch": len(w.lens), "q_heads": c["Hq"], "kv_heads": c["Hkv"],
+            "seq_len": c["L"] or "U[512,65536]", "sum_seq_len": sum(w.lens), "bits_k": c["bwk"], "bits_v": c["bwv"],
+            "table": c["table"], "data": workloads.DATA[c["data"]],
+            "tokens_per_s": len(w.lens) / (m["ms_per_step"] * 1e-3), "us_per_step": m["ms_per_step"] * 1e3,
+            "scan_kernel": scan_kernel_name(c), "scan_us": m["kernel_ms"] * 1e3, "algorithmic_bytes": nbytes,
+            "scan_GBps": gbps, "frac": gbps / HBM_PEAK_GBPS, "splits": m["splits"],
+            "pages_per_split": m["pages_per_split"], "steps": steps}
+    if check:
+        line["parity"] = parity(w)
+    log(f"config {cfg}: {line}")
+    del w
+    torch.cuda.empty_cache()
+    return line
 
 
 def cpu_baseline(c, lens, q, kv, budget_s: float):
@@ -526,7 +534,7 @@ def cpu_baseline(c, lens, q, kv, budget_s: float):
             break
         cols = int(min(width, max(2 * cols, cols * budget_s / max(dt, 1e-3))))
     t_step = dt / cols * width
-    return {"value": B / t_step, "unit": "tokens/s", "cores": cores, "kind": "port",
+    return {"value": B / t_step, "unit": "tokens/s", "cores": cores, "cpu_model": cpu_model(), "kind": "port",
             "sample": f"tiled_compressed_attention (torch CPU fp32) over {cols} of {width} page-table "
                       f"columns of the same batch ({dt:.1f} s), scaled x{width / cols:.1f} to the full step",
             "ms_per_step": t_step * 1e3}
@@ -538,6 +546,10 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--configs", default="3,4,5",
+                    help="other BASELINE configs to measure in the same run (comma list, or 'none'): "
+                         "scan time, roofline fraction, tokens/s and sampled parity per config")
+    ap.add_argument("--config-steps", type=int, default=30, help="timed steps per extra config")
     ap.add_argument("--copies", type=int, default=2)
     ap.add_argument("--splits", type=int, default=None)
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
@@ -566,7 +578,6 @@ def main(argv=None):
         return 2
 
     import torch
-    from winnow_amd import packed_attention as pa
     from winnow_amd.packing import packed_bytes
 
     dev = torch.device("cuda:0")
@@ -578,53 +589,16 @@ def main(argv=None):
                           "copy_peak": cp}))
         return 0
     t0 = time.time()
-    c, lens, q, kvs, quants, sample = build_workload(args.config, dev, args.copies)
+    w = workloads.build(args.config, dev, copies=args.copies)
+    c, lens, q = w.c, w.lens, w.q
     log(f"workload config {args.config} built in {time.time() - t0:.1f} s: B={len(lens)} sum(L)={sum(lens)}")
     D, Hkv, Hq = c["D"], c["Hkv"], c["Hq"]
-    nbk, nbv = packed_bytes(D, c["bwk"]), packed_bytes(D, c["bwv"])
-    bytes_step = kv_bytes(lens, Hkv, nbk, nbv)
-    scale = 1.0 / math.sqrt(D)
+    bytes_step = kv_bytes(lens, Hkv, packed_bytes(D, c["bwk"]), packed_bytes(D, c["bwv"]))
     B = len(lens)
-    max_pages = kvs[0].page_table.shape[1]
-    pps, ns = pa.plan_for(q, kvs[0], args.splits)
-    ws = torch.empty(pa.workspace_bytes(B, Hq, Hkv, D, pps, ns), dtype=torch.uint8, device=dev)
-    for kv in kvs:
-        pa.check_kernel_contract(q, kv)          # full validation once, outside the timed region
-
-    def step(i, evs=None):
-        return pa.packed_decode_attention(q, kvs[i % len(kvs)], scale, num_splits=args.splits,
-                                          workspace=ws, check_ranges=False, timing_events=evs)
-
-    # Bring the GPU to its sustained clocks before the W warm-up steps: a few ms of
-    # work (30 steps) otherwise times a part-clocked GPU, which a decode server
-    # running continuously never sees.
-    t_settle = time.perf_counter()
-    i = 0
-    while time.perf_counter() - t_settle < args.settle:
-        for _ in range(20):
-            step(i)
-            i += 1
-        torch.cuda.synchronize()
-    for i in range(args.warmup):
-        step(i)
-    ev_pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                for _ in range(args.steps)]
-    for e0, e1 in ev_pairs:                       # materialise the underlying hipEvents
-        e0.record()
-        e1.record()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(args.steps):
-        e0, e1 = ev_pairs[i]
-        step(i, (ctypes.c_void_p(e0.cuda_event), ctypes.c_void_p(e1.cuda_event)))
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
-    kern = [e0.elapsed_time(e1) for e0, e1 in ev_pairs]
-    kern_ms = statistics.fmean(kern)
+    m = measure_decode(w, args.steps, args.warmup, args.settle, args.splits)
+    ms, kern_ms, ns, pps = m["ms_per_step"], m["kernel_ms"], m["splits"], m["pages_per_split"]
     log(f"step {ms * 1e3:.1f} us; page-scan kernel mean {kern_ms * 1e3:.1f} us "
-        f"(median {statistics.median(kern) * 1e3:.1f}); plan {ns} splits x {pps} pages")
+        f"(median {m['kernel_ms_median'] * 1e3:.1f}); plan {ns} splits x {pps} pages")
     achieved = bytes_step / (kern_ms * 1e-3) / 1e9
     cp = copy_peak(dev) if args.copy_peak == "on" else None
     if cp:
@@ -636,19 +610,27 @@ def main(argv=None):
         dense["packed_speedup_per_step"] = dense["us_per_step"] / (ms * 1e3)
         dense["packed_speedup_scan"] = dense["scan_kernel_us"] / (kern_ms * 1e3)
         log(f"dense: {dense}")
-    app = append_bench(c, lens, kvs[0].page_table_host, quants, dev) if args.append == "on" else None
-    deq = {**dequant_bench(dev), **dequant_bench(dev, fast=True)} if args.dequant == "on" else None
+    app = append_bench(c, lens, w.table, w.quants, dev) if args.append == "on" else None
     if app:
         log(f"append: {app}")
+    deq = {**dequant_bench(dev), **dequant_bench(dev, fast=True)} if args.dequant == "on" else None
+    par = parity(w) if args.parity == "on" else None
+    if par:
+        log(f"parity: {par}")
+    cpu = cpu_baseline(c, lens, q, w.kvs[0], args.cpu_budget) if args.cpu_baseline == "on" else None
+    if cpu:
+        log(f"cpu baseline: {cpu}")
+    del w
+    torch.cuda.empty_cache()
     traffic = hbm_traffic(args.config, scan_kernel_name(c)) if args.traffic == "on" else None
     if traffic:
         log(f"traffic: {traffic}")
-    par = parity(c, lens, q, kvs[0], quants, sample) if args.parity == "on" else None
-    if par:
-        log(f"parity: {par}")
-    cpu = cpu_baseline(c, lens, q, kvs[0], args.cpu_budget) if args.cpu_baseline == "on" else None
-    if cpu:
-        log(f"cpu baseline: {cpu}")
+    others = {}
+    extra = [] if args.configs in ("", "none") else [int(x) for x in args.configs.split(",")]
+    for cfg in extra:
+        if cfg != args.config:
+            others[str(cfg)] = config_line(cfg, dev, args.config_steps, min(args.warmup, 10), args.settle,
+                                           args.copies, args.parity == "on")
 
     result = {
         "metric": METRIC,
@@ -662,12 +644,11 @@ def main(argv=None):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic: bf16 K/V ~N(0,1) (config-specific outliers/scales), seeded; packed by the "
-                "product append kernel; q ~N(0,1) bf16",
+        "data": DATA_NOTE + "; " + workloads.DATA[c["data"]],
         "config": {"workload": f"BASELINE config {args.config}", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
                    "head_dim": D, "seq_len": c["L"] or "U[512,65536]", "sum_seq_len": sum(lens),
                    "page_size": c["S"], "bits_k": c["bwk"], "bits_v": c["bwv"], "table": c["table"],
-                   "splits": ns, "pages_per_split": pps, "pool_copies": len(kvs)},
+                   "splits": ns, "pages_per_split": pps, "pool_copies": args.copies},
         "step_GBps": bytes_step / (ms * 1e-3) / 1e9,
         "kv_tokens_per_s": sum(lens) / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -682,6 +663,7 @@ def main(argv=None):
                      "copy_peak_GBps": cp["GBps"] if cp else None,
                      "frac_of_copy_peak": achieved / cp["GBps"] if cp else None},
         "cpu_baseline": cpu,
+        "configs": others,
         "dense_baseline": dense,
         "append": app,
         "dequant": deq,
