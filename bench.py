@@ -62,7 +62,9 @@ def scan_kernel_name(c) -> str:
     n_rep = c["Hq"] // c["Hkv"]
     fits = n_rep <= 8 or (n_rep <= 16 and n_rep % 2 == 0)   # even n_rep > 8: two virtual heads per kv head
     if c["D"] == 128 and fits and c["S"] >= 16 and scan != "valu":
-        return "decode_rows_kernel"
+        pair = (c["bwk"], c["bwv"])
+        fp16_split = (pair[0] == pair[1] and pair[0] in (2, 3, 4, 5, 6)) or pair in ((4, 6), (6, 4))
+        return "decode_rows16_kernel" if fp16_split and scan != "rows32" else "decode_rows_kernel"
     return "decode_split_kernel"
 
 

@@ -36,6 +36,8 @@
 // computes.
 // Algebra: turboquant_kv/packed_attention.py:260-334 (the schedule of the
 // reference kernel packed_attention_triton.py:51-134).
+#include <cstdlib>
+#include <cstring>
 #include <utility>
 
 #include "wn_decode.h"
@@ -282,11 +284,13 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, i
   constexpr int NBV = 16 * BWV, VW = RowBuf<BWK, BWV>::VW;
   const int smask = (1 << a.log2S) - 1;
   const int p = lane & 15;
-  const int lane_off = (lane >> 4) * NBV + BWV * p;
+  const uint32_t lane_off = uint32_t((lane >> 4) * NBV + BWV * p);
   static_for<0, 4>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     const int pid_j = __builtin_amdgcn_readlane(pid_lane, 16 * j);
-    const uint8_t* vj = a.v_pages + int64_t(pid_j) * a.vsp + (kvh >> a.kvshift) * a.vsh + ((c0 + 16 * j) & smask) * NBV + lane_off;
+    const uint8_t* blk = a.v_pages + int64_t(pid_j) * a.vsp + (kvh >> a.kvshift) * a.vsh +
+                         int64_t((c0 + 16 * j) & smask) * NBV;
+    const uint8_t* vj = blk + lane_off;
     static_for<0, 4>([&](auto qc) {
       constexpr int qq = decltype(qc)::value;
       uint32_t t[VW];
@@ -600,34 +604,20 @@ __device__ __forceinline__ int xcd_major(int p, int n) {
   return x * q + min(x, r) + s;
 }
 
-// Work-group of WPB independent waves sharing the codebook tables; wave w =
-// blockIdx.x * WPB + wave-in-group.
+// The work list of wave w, one scan(b, kvh, t_lo, t_hi, prow) call per (sequence,
+// kv head, token range) it owns.
 // Fixed splits: wave w is unit (split, kv head, sequence) of the flattened
 // num_splits x Hkv x B space and scans pages [split * pages_per_split, ...) of its
 // sequence.
 // Balanced (a.balanced): the W = num_splits waves share the flattened space of
 // 64-token chunks ordered (sequence, kv head, chunk); wave w takes chunks
 // [C w / W', C (w+1) / W') with C the total and W' = min(W, C), and writes one
-// partial per (sequence, kv head) it touches, at row w + b*Hkv + kvh.
-template <int BWK, int BWV, int NG, int WPB>
-__global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
-  using Lay = RowsLds<BWK, BWV, NG, WPB>;
-  __shared__ __align__(16) char lds[Lay::total];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_table<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
-  stage_table<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
-  __syncthreads();  // the only block-wide barrier: waves run independently from here
-  // Work-groups are dealt to the eight XCDs round robin (group p on XCD p % 8); the
-  // logical group index gives each XCD a contiguous stretch of the flattened work,
-  // so the kv heads of a sequence run on one XCD and share the 128-byte lines that
-  // hold their norms in its L2.
-  const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
-  float* ptile = reinterpret_cast<float*>(lds + Lay::tiles + wig * Lay::tile_bytes);
-
-  // The work list: one (sequence, kv head, token range) for a fixed split, or the
-  // units overlapping this wave's share of the flattened chunk space. One call site
-  // for the scan keeps a single copy of its code.
+// partial per (sequence, kv head) it touches, at row w + b*Hkv + kvh. The wave that
+// scans a unit's first chunk records where the unit's partials start and how many
+// there are (unit_meta), so the merge reads exactly that range.
+template <class Scan>
+__device__ __forceinline__ void for_each_range(const DecodeArgs& a, int64_t w, int lane, Scan&& scan) {
+  // One call site of the scan keeps a single copy of its code.
   int b, kvh, t_lo, t_hi;
   int64_t prow;
   int64_t s = 0, e = 0;  // balanced: flattened chunks [s, e) still to do
@@ -665,9 +655,6 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
     kvh = t_lo = t_hi = 0;
     prow = 0;
   }
-  Tab<BWK> cbk = make_tab<BWK>(lds, Lay::k_off, lane);
-  Tab<BWV> cbv = make_tab<BWV>(lds, Lay::v_off, lane);
-
   while (true) {
     int nb = 0, c_hi = 0;
     if (a.balanced) {
@@ -684,8 +671,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
       t_hi = min(64 * c_hi, a.seq_lens[b]);
       prow = w + int64_t(b) * a.Hkv + kvh;
       if (c_lo == 0 && lane == 0) {
-        // the group's first wave: its partials are rows prow .. prow + n - 1, one per
-        // wave up to the last wave starting before the group's end U1
+        // the unit's first wave: its partials are rows prow .. prow + n - 1, one per
+        // wave up to the last wave starting before the unit's end U1
         const int64_t C = int64_t(a.Hkv) * pre[a.B];
         const int64_t Wp = min(int64_t(a.num_splits), C);
         const int64_t U1 = base + int64_t(kvh + 1) * nb;
@@ -694,10 +681,517 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
       }
       s += c_hi - c_lo;
     }
-    scan_range<BWK, BWV, NG>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+    scan(b, kvh, t_lo, t_hi, prow);
     if (!a.balanced || s >= e) break;
     if (kvh + 1 == a.Hkv && c_hi == nb) ++b;
   }
+}
+
+// Work-group of WPB independent waves sharing the codebook tables; wave w =
+// blockIdx.x * WPB + wave-in-group walks the work list of for_each_range.
+template <int BWK, int BWV, int NG, int WPB>
+__global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
+  using Lay = RowsLds<BWK, BWV, NG, WPB>;
+  __shared__ __align__(16) char lds[Lay::total];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
+  stage_table<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
+  stage_table<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
+  __syncthreads();  // the only block-wide barrier: waves run independently from here
+  // Work-groups are dealt to the eight XCDs round robin (group p on XCD p % 8); the
+  // logical group index gives each XCD a contiguous stretch of the flattened work,
+  // so the kv heads of a sequence run on one XCD and share the 128-byte lines that
+  // hold their norms in its L2.
+  const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
+  float* ptile = reinterpret_cast<float*>(lds + Lay::tiles + wig * Lay::tile_bytes);
+  Tab<BWK> cbk = make_tab<BWK>(lds, Lay::k_off, lane);
+  Tab<BWV> cbv = make_tab<BWV>(lds, Lay::v_off, lane);
+  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow) {
+    scan_range<BWK, BWV, NG>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+  });
+}
+
+// ------------------------------------------------------------------ 16-bit matrix-core scan
+//
+// The page scan on v_mfma_f32_16x16x32_f16 (16 times the MAC rate of the fp32 4x4x1
+// MFMA on gfx950), for 2, 3, 4, 5 and 6-bit codes. Every fp32 factor x is carried as
+// an fp16 pair x = H + L (H = fp16(x), L = fp16(x - H)) after an exact power-of-two
+// scaling that keeps both in fp16's normal range; products of fp16 values are exact
+// in the fp32 accumulators and each factor keeps 22 bits, so scores and values keep
+// fp32 accuracy.
+//
+// A codebook table entry holds (H, L) of 2^8 c for each of its two codes,
+// [H0, L0, H1, L1]; two entries loaded side by side are an 8-slot MFMA operand, and
+// the other operand carries its factor twice per code ([f0, f0, f1, f1, ...]), so
+// the k-slots pair each code's H and L with the same factor. Lane l = 16g + c.
+//
+//   scores   tile r (tokens 16r .. 16r+15 of the chunk) x 16 columns x 32 k-slots
+//            per MFMA. Row c of
+//            lane 16g+c is token 16r + 4(c%4) + c/4; its k-slots in K-step s are dims
+//            32g + 4s .. +3, so a lane reads the 16-byte quarter g of one token row and
+//            one load instruction reads a whole 16-token page block. Column c is head
+//            c % NH of the group and the H (c < NH) or L (c >= NH) part of q' = q 2^e
+//            (e per (sequence, kv head), |q'| < 2^15); with four heads the columns
+//            8..15 are zero. 8 K-steps x 4 tiles = 32 MFMAs per chunk. Output lane
+//            16g+c register i holds token 16r + 4i + g of column c.
+//   softmax  the two column halves are added (row rotate by NH), the scores pass
+//            through a per-wave LDS tile to lane = token, and the online softmax runs as
+//            in the fp32 scan. p n_V 2^-gs goes back to the same tile as H | L << 16
+//            words.
+//   values   M-tile mt: row c of lane 16g+c is dim 8c + mt, so a lane needs codes
+//            8c..8c+7 of each token: the V loads of the fp32 scan, unchanged. K-step ks:
+//            k-slots of group g are tokens 16ks + 4j + g, j = 0..3; the codes of dim
+//            8c + mt of tokens (j = 0, 1) and (2, 3) are merged into pair indices (4-bit:
+//            a bit-field insert per four dims), whose entries form the A operand. B =
+//            H or L of p n_V 2^-gs of the column's head for those tokens. 8 x 4 = 32 MFMAs
+//            per chunk; output lane 16g+c register i holds dim 32g + 8i + mt, column c.
+//   scales   scores are multiplied by 2^-(e+8) before the softmax; pv' = p n_V 2^-gs
+//            with gs the smallest shift that keeps 256 max(n_V) 2^-gs < 2^15 (raised,
+//            with an exact rescale of the accumulators, when a chunk needs it); the
+//            partials are multiplied by 2^(gs-8) when written.
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr float kCbScale = 256.0f;  // codebook values scaled by 2^8 before the split
+constexpr int kTileStride = 80;     // words per head in the per-wave score / p n_V tile
+
+// Maximum of a non-negative value over the wave, in a scalar register, with DPP moves
+// only (no LDS permutes): row reductions, then the row broadcasts into lane 63.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_max(float x) {
+  return fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROWS,
+                                                                          0xf, false)));
+}
+__device__ __forceinline__ float wave_max_nonneg(float x) {
+  x = dpp_max<0xb1, 0xf>(x);   // quad_perm [1,0,3,2]
+  x = dpp_max<0x4e, 0xf>(x);   // quad_perm [2,3,0,1]
+  x = dpp_max<0x141, 0xf>(x);  // row_half_mirror
+  x = dpp_max<0x140, 0xf>(x);  // row_mirror
+  x = dpp_max<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+  x = dpp_max<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
+// H | L << 16 of x with H = fp16(x) and L = fp16(x - H), both rounded toward zero.
+__device__ __forceinline__ uint32_t split_word(float x) {
+  typedef __fp16 h2 __attribute__((ext_vector_type(2)));
+  const h2 hi = __builtin_amdgcn_cvt_pkrtz(x, 0.f);
+  const float r = x - (float)hi[0];
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, r));
+}
+
+// Table entry of two codebook values: [H(2^8 lo), L(2^8 lo), H(2^8 hi), L(2^8 hi)].
+__device__ __forceinline__ uint2 split_pair(float lo, float hi) {
+  return make_uint2(split_word(lo * kCbScale), split_word(hi * kCbScale));
+}
+
+// The pair tables of stage_table with 16-bit split entries (4-bit: replicated and
+// byte-indexed; 2, 3, 5, 6 bits: 2^(2 BW) entries).
+template <int BW>
+__device__ __forceinline__ void stage_table16(const float* cb, char* dst, int tid, int nthr) {
+  static_assert(BW == 4 || pair_coded<BW>(), "16-bit tables are pair tables");
+  uint2* t = reinterpret_cast<uint2*>(dst);
+  if constexpr (BW == 4) {
+    for (int i = tid; i < 256 * 32; i += nthr) {
+      const int b = i >> 5;
+      t[i] = split_pair(cb[b & 15], cb[b >> 4]);
+    }
+  } else {
+    for (int i = tid; i < (1 << (2 * BW)); i += nthr) t[i] = split_pair(cb[i & ((1 << BW) - 1)], cb[i >> BW]);
+  }
+}
+
+// Table reads in flight ahead of their MFMA in the 16-bit scan: eight steps where
+// the widths leave the registers for them, else four.
+template <int BWK, int BWV>
+constexpr int mx_lookahead() { return BWK <= 4 && BWV <= 4 ? 8 : 4; }
+
+// Two table entries side by side as an 8-slot operand.
+__device__ __forceinline__ h8 as_h8(uint2 a, uint2 b) { return __builtin_bit_cast(h8, u32x4{a.x, a.y, b.x, b.y}); }
+
+// [x, x, y, y, z, z, w, w] of the halves picked by sel from four H | L words
+// (sel 0x01000100: H; 0x03020302: L; 0x0c0c0c0c: zeros).
+__device__ __forceinline__ h8 dup4(uint32_t x, uint32_t y, uint32_t z, uint32_t w, uint32_t sel) {
+  return __builtin_bit_cast(h8, u32x4{__builtin_amdgcn_perm(x, x, sel), __builtin_amdgcn_perm(y, y, sel),
+                                      __builtin_amdgcn_perm(z, z, sel), __builtin_amdgcn_perm(w, w, sel)});
+}
+
+// Table entry of the 4-bit pair held in byte K of x (SDWA address move, as lookup8).
+template <int K>
+__device__ __forceinline__ uint2 entry4(Tab<4>& tab, uint32_t x) {
+  tab.r[K] = put_byte1<K>(tab.r[K], x);
+  return *reinterpret_cast<const uint2*>(tab.lds + tab.r[K]);
+}
+
+// Table entry of pair N (codes 2N, 2N+1) of a packed piece held as words.
+template <int BW, int N>
+__device__ __forceinline__ uint2 piece_pair(const uint32_t* w, Tab<BW>& tab) {
+  if constexpr (BW == 4) {
+    return entry4<N & 3>(tab, w[N >> 2]);
+  } else {
+    constexpr int bit = 2 * BW * N, wi = bit >> 5, sh = bit & 31;
+    uint32_t x = w[wi] >> sh;
+    if constexpr (sh + 2 * BW > 32) x |= w[wi + 1] << (32 - sh);
+    return reinterpret_cast<const uint2*>(tab.t)[x & ((1u << (2 * BW)) - 1u)];
+  }
+}
+
+// The 16-bit scan keeps its rows in RowBuf words too. As a K buffer: for each tile
+// t, the 4 BWK bytes of quarter g of token 16t + 4(c%4) + c/4 (words [t*BWK, t*BWK +
+// BWK)), then the fp16 K and V norms of token c0 + lane (words KW, KW+1). As a V
+// buffer: the layout of the fp32 scan.
+
+// Token (within its 16-token tile) whose scores row c of a score MFMA holds.
+__device__ __forceinline__ int tile_token(int c) { return 4 * (c & 3) + (c >> 2); }
+
+// K side of chunk [c0, c0+64) for the 16-bit scan: quarter g of the rows of the
+// tile tokens (one whole 16-token page block per load instruction) and both norms of
+// token c0 + lane, whose page is pid_lane.
+template <int BWK, int BWV>
+__device__ __forceinline__ void load_k16(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane,
+                                         RowBuf<BWK, BWV>& r) {
+  constexpr int NBK = 16 * BWK, QB = 4 * BWK, QW = BWK, KW = RowBuf<BWK, BWV>::KW;
+  const int smask = (1 << a.log2S) - 1;
+  // the tile's 16 tokens share a page (c0 + 16t is a multiple of 16 and S >= 16): a
+  // wave-uniform block base plus this lane's fixed 32-bit offset in it
+  const uint32_t lane_off = uint32_t(tile_token(lane & 15) * NBK + QB * (lane >> 4));
+  static_for<0, 4>([&](auto rc) {
+    constexpr int t = decltype(rc)::value;
+    const int pid_t = __builtin_amdgcn_readlane(pid_lane, 16 * t);
+    const uint8_t* blk = a.k_pages + int64_t(pid_t) * a.ksp + (kvh >> a.kvshift) * a.ksh +
+                         int64_t((c0 + 16 * t) & smask) * NBK;
+    const uint8_t* q = blk + lane_off;
+    if constexpr (QB == 16) {
+      const uint4 x = *reinterpret_cast<const uint4*>(q);
+      r.w[t * QW] = x.x;
+      r.w[t * QW + 1] = x.y;
+      r.w[t * QW + 2] = x.z;
+      r.w[t * QW + 3] = x.w;
+    } else if constexpr (QB % 8 == 0) {
+#pragma unroll
+      for (int i = 0; i < QB / 8; ++i) {
+        const uint2 x = reinterpret_cast<const uint2*>(q)[i];
+        r.w[t * QW + 2 * i] = x.x;
+        r.w[t * QW + 2 * i + 1] = x.y;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < QB / 4; ++i) r.w[t * QW + i] = reinterpret_cast<const uint32_t*>(q)[i];
+    }
+  });
+  const int slot = (c0 + lane) & smask;
+  r.w[KW] = a.k_norms[int64_t(pid_lane) * a.knp + (kvh >> a.kvshift) * a.knh + slot];
+  r.w[KW + 1] = a.v_norms[int64_t(pid_lane) * a.vnp + (kvh >> a.kvshift) * a.vnh + slot];
+}
+
+template <int NG>
+struct MxState {
+  f32x4 acc[8];       // acc[mt] register i: dim 32g + 8i + mt of column c, scaled by 2^(8-gs)
+  float m[4 * NG];    // reference maxima (wave-uniform), log2 units
+  float l[4 * NG];    // sum of 2^(s - m) over this lane's tokens
+  int gs;             // value scale shift (wave-uniform)
+};
+
+// Value of lane (c + NH) % 16's x added to x: the two halves of a column pair.
+template <int NH>
+__device__ __forceinline__ float add_half(float x) {
+  // row_ror:(16 - NH): lane c of a row receives lane (c + NH) % 16
+  return x + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x120 + (16 - NH), 0xf,
+                                                                 0xf, true));
+}
+
+// Scores of the chunk into the tile (head h of token 16r + 4i + g at word
+// h * kTileStride + 16r + 4g + i), before the 2^-(e+8) scale.
+template <int BWK, int BWV, int NG>
+__device__ __forceinline__ void score_phase_mx(const RowBuf<BWK, BWV>& K, Tab<BWK>& cbk, const h8 (&qb)[8], int lane,
+                                               uint32_t* pt) {
+  constexpr int NH = 4 * NG, QW = BWK, LA = mx_lookahead<BWK, BWV>();
+  f32x4 d[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) d[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // step k = 4s + r: K-step s (codes 8s..8s+3 of the quarter: pairs 2s, 2s+1) of tile r
+  uint2 e[LA + 1][2];
+  auto look = [&](auto kc, uint2 (&o)[2]) {
+    constexpr int k = decltype(kc)::value, s = k >> 2, r = k & 3;
+    o[0] = piece_pair<BWK, 2 * s>(K.w + r * QW, cbk);
+    o[1] = piece_pair<BWK, 2 * s + 1>(K.w + r * QW, cbk);
+  };
+  static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
+  __builtin_amdgcn_sched_barrier(0);
+  static_for<0, 32>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    if constexpr (k + LA < 32) {
+      look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    d[k & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(e[k % (LA + 1)][0], e[k % (LA + 1)][1]), qb[k >> 2],
+                                                      d[k & 3], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d[r][i] = add_half<NH>(d[r][i]);
+  wave_lds_sync();  // the previous chunk's reads of the tile are done
+  if (c < NH) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<float4*>(pt + c * kTileStride + 16 * r + 4 * g) = make_float4(d[r][0], d[r][1], d[r][2], d[r][3]);
+  }
+  wave_lds_sync();
+}
+
+// Online softmax of one chunk (lane = token) from the score tile; p n_V 2^-gs goes
+// back to the same words as H | L << 16.
+template <int NG>
+__device__ __forceinline__ void softmax_phase_mx(float sc, uint32_t nk_h, uint32_t nv_h, bool valid, int lane,
+                                                 uint32_t* pt, MxState<NG>& st) {
+  constexpr int H = 4 * NG;
+  const int off = 16 * (lane >> 4) + 4 * (lane & 3) + ((lane >> 2) & 3);  // word of token lane
+  const float nk = half_lo(nk_h) * sc;
+  const float nv = valid ? half_lo(nv_h) : 0.f;
+  float sv[H];
+#pragma unroll
+  for (int i = 0; i < H; ++i) sv[i] = valid ? __builtin_bit_cast(float, pt[i * kTileStride + off]) * nk : -INFINITY;
+  // value scale: 2^kRescale * max(n_V) * 2^-gs < 2^15
+  int ge;
+  frexpf(wave_max_nonneg(nv), &ge);
+  const int gs_need = max(0, ge - 7);
+  if (gs_need > st.gs) {  // wave-uniform, rare
+    const float f = ldexpf(1.f, st.gs - gs_need);
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) st.acc[mm] *= f;
+    st.gs = gs_need;
+  }
+  bool move = st.m[0] == -INFINITY;
+#pragma unroll
+  for (int i = 0; i < H; ++i) move = move || __any(sv[i] > st.m[i] + kRescale);
+  if (move) {  // wave-uniform
+    const int hc = (lane & 15) % H;  // head of this lane's accumulator column
+    float alpha_c = 1.f;
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const float m_new = uniform(fmaxf(st.m[i], wave_max(sv[i])));
+      const float alpha = __builtin_amdgcn_exp2f(st.m[i] - m_new);  // 0 on the first chunk
+      st.m[i] = m_new;
+      st.l[i] *= alpha;
+      alpha_c = hc == i ? alpha : alpha_c;
+    }
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) st.acc[mm] *= alpha_c;
+  }
+  const float nvs = ldexpf(nv, -st.gs);
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const float p = __builtin_amdgcn_exp2f(sv[i] - st.m[i]);  // 0 for masked tokens
+    st.l[i] += p;
+    pt[i * kTileStride + off] = split_word(p * nvs);
+  }
+  wave_lds_sync();
+}
+
+// Values of a chunk: 4 K-steps (16 tokens each) x 8 M-tiles (one dim of each lane's
+// eight), one MFMA each; lookups run LA steps ahead.
+template <int BWK, int BWV, int NG>
+__device__ __forceinline__ void value_phase_mx(const RowBuf<BWK, BWV>& V, Tab<BWV>& cbv, const uint32_t* pt, int lane,
+                                               f32x4 (&acc)[8]) {
+  constexpr int NH = 4 * NG, VW = VWords<BWV>::N, LA = mx_lookahead<BWK, BWV>();
+  const int c = lane & 15, g = lane >> 4;
+  const uint32_t sel = c < NH ? 0x01000100u : c < 2 * NH ? 0x03020302u : 0x0c0c0c0cu;
+  const uint32_t* prow = pt + (c % NH) * kTileStride + 4 * g;
+  // step k = 8ks + mt
+  auto look = [&](auto kc, uint2 (&o)[2]) {
+    constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7;
+    if constexpr (BWV == 4) {
+      // 4-bit: byte mt/2 of the merged bytes of token pairs (0,1), (2,3) of K-step ks
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const uint32_t wa = V.w[(4 * ks + 2 * p) * VW], wb = V.w[(4 * ks + 2 * p + 1) * VW];
+        const uint32_t x = (mt & 1) ? (((wa >> 4) & 0x0F0F0F0Fu) | (wb & 0xF0F0F0F0u))
+                                    : ((wa & 0x0F0F0F0Fu) | ((wb << 4) & 0xF0F0F0F0u));
+        o[p] = entry4<(mt >> 1)>(cbv, x);
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const uint32_t* wa = V.w + (4 * ks + 2 * p) * VW;
+        const uint32_t* wb = V.w + (4 * ks + 2 * p + 1) * VW;
+        constexpr int bit = BWV * mt, wi = bit >> 5, sh = bit & 31;
+        uint32_t xa = wa[wi] >> sh, xb = wb[wi] >> sh;
+        if constexpr (sh + BWV > 32) {
+          xa |= wa[wi + 1] << (32 - sh);
+          xb |= wb[wi + 1] << (32 - sh);
+        }
+        constexpr uint32_t mask = (1u << BWV) - 1u;
+        o[p] = reinterpret_cast<const uint2*>(cbv.t)[(xa & mask) | ((xb & mask) << BWV)];
+      }
+    }
+  };
+  uint2 e[LA + 1][2];
+  static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
+  h8 bq;
+  __builtin_amdgcn_sched_barrier(0);
+  static_for<0, 32>([&](auto kc) {
+    constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7;
+    if constexpr (mt == 0) {
+      const uint4 w = *reinterpret_cast<const uint4*>(prow + 16 * ks);
+      bq = dup4(w.x, w.y, w.z, w.w, sel);
+    }
+    if constexpr (k + LA < 32) {
+      look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(e[k % (LA + 1)][0], e[k % (LA + 1)][1]), bq, acc[mt], 0,
+                                                     0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
+// Adds the column halves, undoes the value scale and writes the (acc, m, l) partial of
+// each query head h < n_rep to row prow * n_rep + h: lane 16g + h writes dims
+// 32g .. 32g+31.
+template <int NG>
+__device__ __forceinline__ void write_partial_mx(const DecodeArgs& a, MxState<NG>& st, int64_t prow, int lane) {
+  constexpr int D = 128, H = 4 * NG;
+  const float f = ldexpf(1.f, st.gs - 8);
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.acc[mm][i] = add_half<H>(st.acc[mm][i]) * f;
+#pragma unroll
+  for (int i = 0; i < H; ++i) st.l[i] = wave_sum(st.l[i]);
+  const int64_t row0 = prow * a.n_rep;
+  const int c = lane & 15, g = lane >> 4;
+  if (c < H && c < a.n_rep) {
+    float* dst = a.part_acc + (row0 + c) * D + 32 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<float4*>(dst + 8 * i) =
+          make_float4(st.acc[0][i], st.acc[1][i], st.acc[2][i], st.acc[3][i]);
+      *reinterpret_cast<float4*>(dst + 8 * i + 4) =
+          make_float4(st.acc[4][i], st.acc[5][i], st.acc[6][i], st.acc[7][i]);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      if (i < a.n_rep) {
+        a.part_ml[2 * (row0 + i)] = st.m[i];
+        a.part_ml[2 * (row0 + i) + 1] = st.l[i];
+      }
+    }
+  }
+}
+
+// scan_range on the 16x16x32 fp16 MFMA.
+template <int BWK, int BWV, int NG>
+__device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh, int t_lo, int t_hi, int64_t prow,
+                                             int lane, Tab<BWK>& cbk, Tab<BWV>& cbv, uint32_t* ptile) {
+  constexpr int D = 128, NH = 4 * NG;
+  const int page_hi = (t_hi + (1 << a.log2S) - 1) >> a.log2S;
+  const int n = (t_hi - t_lo + 63) >> 6;
+  const int c = lane & 15, g = lane >> 4;
+
+  // B operands of the scores: column c, K-step s, k-slots of group g = dims
+  // 32g + 4s + (0..3), each twice; H (c < NH) or L (c >= NH) of q' = q 2^e, zero
+  // for columns past 2 NH
+  float qv[32];
+  float amax = 0.f;
+  {
+    const float4* qp = reinterpret_cast<const float4*>(
+        a.q_rot + ((int64_t(b) * a.Hkv + kvh) * NH + (c % NH)) * D + 32 * g);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const float4 x = qp[s];
+      qv[4 * s] = x.x;
+      qv[4 * s + 1] = x.y;
+      qv[4 * s + 2] = x.z;
+      qv[4 * s + 3] = x.w;
+    }
+#pragma unroll
+    for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(qv[k]));
+  }
+  int qe;
+  frexpf(uniform(wave_max(amax)), &qe);
+  const int e = 15 - qe;  // |q| < 2^qe, so |q 2^e| < 2^15
+  const float sc = ldexpf(1.f, -(e + 8));
+  const uint32_t qsel = c < NH ? 0x01000100u : c < 2 * NH ? 0x03020302u : 0x0c0c0c0cu;
+  h8 qb[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    qb[s] = dup4(split_word(ldexpf(qv[4 * s], e)), split_word(ldexpf(qv[4 * s + 1], e)),
+                 split_word(ldexpf(qv[4 * s + 2], e)), split_word(ldexpf(qv[4 * s + 3], e)), qsel);
+
+  const int32_t* trow = a.table + b * a.tsb;
+  auto pid_of = [&](int ch) {
+    const int col = min((t_lo + 64 * ch + lane) >> a.log2S, page_hi - 1);
+    return trow[col];
+  };
+  MxState<NG> st;
+#pragma unroll
+  for (int mm = 0; mm < 8; ++mm) st.acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NH; ++i) {
+    st.m[i] = -INFINITY;
+    st.l[i] = 0.f;
+  }
+  st.gs = 0;
+  using Buf = RowBuf<BWK, BWV>;
+  int pid_next;
+  auto step = [&](int ch, Buf& X, Buf& Y, Buf& Z) {
+    const int c0 = t_lo + 64 * ch;
+    const int pid_after = pid_of(ch + 2);
+    const bool more = ch + 1 < n;
+    if (more) load_k16(a, kvh, lane, c0 + 64, pid_next, Z);
+    score_phase_mx<BWK, BWV, NG>(X, cbk, qb, lane, ptile);
+    softmax_phase_mx<NG>(sc, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
+    if (more) load_v(a, kvh, lane, c0 + 64, pid_next, X);
+    value_phase_mx<BWK, BWV, NG>(Y, cbv, ptile, lane, st.acc);
+    pid_next = pid_after;
+  };
+
+  Buf b0, b1, b2;
+  load_k16(a, kvh, lane, t_lo, pid_of(0), b0);
+  load_v(a, kvh, lane, t_lo, pid_of(0), b1);
+  pid_next = pid_of(1);
+  wait_vmem_all();
+  for (int ch = 0; ch < n; ch += 3) {
+    step(ch, b0, b1, b2);
+    if (ch + 1 >= n) break;
+    step(ch + 1, b2, b0, b1);
+    if (ch + 2 >= n) break;
+    step(ch + 2, b1, b2, b0);
+  }
+  write_partial_mx<NG>(a, st, prow, lane);
+}
+
+template <int BWK, int BWV, int NG, int WPB>
+struct Rows16Lds {
+  static constexpr int k_off = RowsLds<BWK, BWV, NG, WPB>::k_off;
+  static constexpr int v_off = RowsLds<BWK, BWV, NG, WPB>::v_off;
+  static constexpr int tiles = RowsLds<BWK, BWV, NG, WPB>::tiles;
+  static constexpr int tile_bytes = 4 * NG * kTileStride * 4;
+  static constexpr int total = tiles + WPB * tile_bytes;
+  static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
+};
+
+template <int BWK, int BWV, int NG, int WPB>
+__global__ __launch_bounds__(64 * WPB) void decode_rows16_kernel(DecodeArgs a) {
+  using Lay = Rows16Lds<BWK, BWV, NG, WPB>;
+  __shared__ __align__(16) char lds[Lay::total];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
+  stage_table16<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
+  stage_table16<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
+  __syncthreads();  // the only block-wide barrier: waves run independently from here
+  const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
+  uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);
+  Tab<BWK> cbk = make_tab<BWK>(lds, Lay::k_off, lane);
+  Tab<BWV> cbv = make_tab<BWV>(lds, Lay::v_off, lane);
+  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow) {
+    scan_range16<BWK, BWV, NG>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+  });
 }
 
 // Waves per work-group: three per SIMD where the scan fits in 168 VGPRs, else two.
@@ -738,12 +1232,60 @@ SplitKernel rows_for(int bw_k, int bw_v) {
   return SplitKernel{};
 }
 
+template <int BWK, int BWV, int NG>
+SplitKernel rows16_kernel() {
+  constexpr int wpb = 8;  // two waves per SIMD: the 16-bit scan needs up to 256 VGPRs
+  SplitKernel k;
+  k.fn = decode_rows16_kernel<BWK, BWV, NG, wpb>;
+  k.block = 64 * wpb;
+  k.wpb = wpb;
+  k.nrep = 4 * NG;
+  k.log2_units = true;
+  k.rows = true;
+  return k;
+}
+
+// The 16-bit scan's width pairs: pair-table widths (2, 3, 4, 5, 6 bits) alike for K
+// and V, and 4/6, 6/4.
+template <int NG>
+SplitKernel rows16_for(int bw_k, int bw_v) {
+  if (bw_k == bw_v) {
+    switch (bw_k) {
+      case 2: return rows16_kernel<2, 2, NG>();
+      case 3: return rows16_kernel<3, 3, NG>();
+      case 4: return rows16_kernel<4, 4, NG>();
+      case 5: return rows16_kernel<5, 5, NG>();
+      case 6: return rows16_kernel<6, 6, NG>();
+    }
+  } else if (bw_k == 4 && bw_v == 6) {
+    return rows16_kernel<4, 6, NG>();
+  } else if (bw_k == 6 && bw_v == 4) {
+    return rows16_kernel<6, 4, NG>();
+  }
+  return SplitKernel{};
+}
+
+// WN_DECODE_SCAN=rows32 keeps the fp32-product row scan for every width (the two
+// compute the same result to fp32 rounding; the knob exists to compare them on one
+// machine). Read once.
+bool rows16_allowed() {
+  static const bool allowed = [] {
+    const char* e = getenv("WN_DECODE_SCAN");
+    return !(e && !strcmp(e, "rows32"));
+  }();
+  return allowed;
+}
+
 }  // namespace
 
 SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep) {
-  if (n_rep <= 4) return rows_for<1>(bw_k, bw_v);
-  if (n_rep <= 8) return rows_for<2>(bw_k, bw_v);
-  return SplitKernel{};
+  const int ng = n_rep <= 4 ? 1 : n_rep <= 8 ? 2 : 0;
+  if (ng == 0) return SplitKernel{};
+  if (rows16_allowed()) {
+    const SplitKernel k = ng == 1 ? rows16_for<1>(bw_k, bw_v) : rows16_for<2>(bw_k, bw_v);
+    if (k.fn) return k;
+  }
+  return ng == 1 ? rows_for<1>(bw_k, bw_v) : rows_for<2>(bw_k, bw_v);
 }
 
 }  // namespace wn
