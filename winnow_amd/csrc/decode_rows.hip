@@ -216,9 +216,32 @@ struct RowBuf {
 // another instruction: those loads are nontemporal (streamed past the caches),
 // which measured 1.3 % faster on the 4/4-bit scan. The 6-bit pieces of a row come
 // from two instructions, and 3/5-bit rows from bytes, so they keep cached loads.
+//
+// RAW (5 and 6 bits only): the 8 bytes from p rounded down to 4 bytes, one dwordx2
+// load, left unshifted; raw_shift gives the bit offset of the codes in them and
+// unshift_raw moves them down (done where the words are used, so no wait for the load
+// is needed right after it). The window ends at most at the end of the lane's
+// 16-token page block (p + BWV <= block end and 8 bytes from the rounded-down start
+// reach at most 3 bytes past p + 5).
 template <int BWV>
+__device__ __forceinline__ uint32_t raw_shift(int lane) { return 8u * uint32_t((BWV * (lane & 15)) & 3); }
+__device__ __forceinline__ void unshift_raw(uint32_t& w0, uint32_t& w1, uint32_t sh) {
+  w0 = __builtin_amdgcn_alignbit(w1, w0, sh);
+  w1 >>= sh;
+}
+
+template <int BWV, bool RAW = false>
 __device__ __forceinline__ void load_vcodes(const uint8_t* p, bool odd_lane, uint32_t (&out)[VWords<BWV>::N]) {
-  if constexpr (BWV == 4) {
+  if constexpr (RAW) {
+    static_assert(BWV == 5 || BWV == 6, "raw windows are for 5 and 6-bit rows");
+    // offset arithmetic on p itself keeps it a global pointer (a flat load would also
+    // count against the LDS counter)
+    const uint8_t* q = p - (reinterpret_cast<uintptr_t>(p) & 3);
+    uint2 x;
+    __builtin_memcpy(&x, __builtin_assume_aligned(q, 4), 8);
+    out[0] = x.x;
+    out[1] = x.y;
+  } else if constexpr (BWV == 4) {
     out[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
   } else if constexpr (BWV == 8) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -278,13 +301,15 @@ __device__ __forceinline__ void load_k(const DecodeArgs& a, int kvh, int lane, i
 // 8p..8p+7 of token c0+4q+G (G = lane/16, p = lane%16). c0 is a multiple of 16 and
 // pages hold >= 16 tokens, so the four quads of 16-token block j share the page of
 // lane 16j (pid_lane is the page of token c0+lane).
-template <int BWK, int BWV>
+template <int BWK, int BWV, bool RAW = false>
 __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane,
-                                       RowBuf<BWK, BWV>& r) {
+                                       RowBuf<BWK, BWV>& r, bool live = true) {
   constexpr int NBV = 16 * BWV, VW = RowBuf<BWK, BWV>::VW;
   const int smask = (1 << a.log2S) - 1;
   const int p = lane & 15;
-  const uint32_t lane_off = uint32_t((lane >> 4) * NBV + BWV * p);
+  // live == false (a chunk past the range, loaded only so that every path of the
+  // scan loop issues the same loads): every lane reads the first bytes of the block
+  const uint32_t lane_off = live ? uint32_t((lane >> 4) * NBV + BWV * p) : 0u;
   static_for<0, 4>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     const int pid_j = __builtin_amdgcn_readlane(pid_lane, 16 * j);
@@ -294,7 +319,7 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, i
     static_for<0, 4>([&](auto qc) {
       constexpr int qq = decltype(qc)::value;
       uint32_t t[VW];
-      load_vcodes<BWV>(vj + 4 * qq * NBV, p & 1, t);
+      load_vcodes<BWV, RAW>(vj + 4 * qq * NBV, p & 1, t);
 #pragma unroll
       for (int x = 0; x < VW; ++x) r.w[(4 * j + qq) * VW + x] = t[x];
     });
@@ -753,23 +778,37 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr float kCbScale = 256.0f;  // codebook values scaled by 2^8 before the split
+template <int BWV>
+constexpr bool kRawV = BWV == 5 || BWV == 6;  // V rows loaded as raw windows (load_vcodes)
 constexpr int kTileStride = 80;     // words per head in the per-wave score / p n_V tile
 
-// Maximum of a non-negative value over the wave, in a scalar register, with DPP moves
-// only (no LDS permutes): row reductions, then the row broadcasts into lane 63.
+// Maximum over the wave, in a scalar register, with DPP moves only (no LDS permutes):
+// row reductions, then the row broadcasts into lane 63. The reduction runs on
+// unsigned keys (0 is the identity, so lanes a row mask leaves out keep 0 and each
+// move folds into its max as one DPP instruction).
 template <int CTRL, int ROWS>
-__device__ __forceinline__ float dpp_max(float x) {
-  return fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROWS,
-                                                                          0xf, false)));
+__device__ __forceinline__ uint32_t dpp_umax(uint32_t x) {
+  return max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), CTRL, ROWS, 0xf, false)));
 }
+__device__ __forceinline__ uint32_t wave_umax(uint32_t x) {
+  x = dpp_umax<0xb1, 0xf>(x);   // quad_perm [1,0,3,2]
+  x = dpp_umax<0x4e, 0xf>(x);   // quad_perm [2,3,0,1]
+  x = dpp_umax<0x141, 0xf>(x);  // row_half_mirror
+  x = dpp_umax<0x140, 0xf>(x);  // row_mirror
+  x = dpp_umax<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+  x = dpp_umax<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+  return uint32_t(__builtin_amdgcn_readlane(int(x), 63));
+}
+// Non-negative floats order as their bit patterns.
 __device__ __forceinline__ float wave_max_nonneg(float x) {
-  x = dpp_max<0xb1, 0xf>(x);   // quad_perm [1,0,3,2]
-  x = dpp_max<0x4e, 0xf>(x);   // quad_perm [2,3,0,1]
-  x = dpp_max<0x141, 0xf>(x);  // row_half_mirror
-  x = dpp_max<0x140, 0xf>(x);  // row_mirror
-  x = dpp_max<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
-  x = dpp_max<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+  return __builtin_bit_cast(float, wave_umax(__builtin_bit_cast(uint32_t, x)));
+}
+// Any float but NaN: the key flips every bit of a negative value and the sign bit of
+// a non-negative one, which orders keys as the floats.
+__device__ __forceinline__ float wave_max_dpp(float x) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, x);
+  const uint32_t k = wave_umax(b ^ (uint32_t(int32_t(b) >> 31) | 0x80000000u));
+  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
 }
 
 // H | L << 16 of x with H = fp16(x) and L = fp16(x - H), both rounded toward zero.
@@ -802,9 +841,10 @@ __device__ __forceinline__ void stage_table16(const float* cb, char* dst, int ti
 }
 
 // Table reads in flight ahead of their MFMA in the 16-bit scan: eight steps where
-// the widths leave the registers for them, else four.
+// the widths leave the registers for them (2 and 4 bits, whose pieces are whole
+// bytes), else four.
 template <int BWK, int BWV>
-constexpr int mx_lookahead() { return BWK <= 4 && BWV <= 4 ? 8 : 4; }
+constexpr int mx_lookahead() { return (BWK == 2 || BWK == 4) && (BWV == 2 || BWV == 4) ? 8 : 4; }
 
 // Two table entries side by side as an 8-slot operand.
 __device__ __forceinline__ h8 as_h8(uint2 a, uint2 b) { return __builtin_bit_cast(h8, u32x4{a.x, a.y, b.x, b.y}); }
@@ -849,12 +889,13 @@ __device__ __forceinline__ int tile_token(int c) { return 4 * (c & 3) + (c >> 2)
 // token c0 + lane, whose page is pid_lane.
 template <int BWK, int BWV>
 __device__ __forceinline__ void load_k16(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane,
-                                         RowBuf<BWK, BWV>& r) {
+                                         RowBuf<BWK, BWV>& r, bool live = true) {
   constexpr int NBK = 16 * BWK, QB = 4 * BWK, QW = BWK, KW = RowBuf<BWK, BWV>::KW;
   const int smask = (1 << a.log2S) - 1;
   // the tile's 16 tokens share a page (c0 + 16t is a multiple of 16 and S >= 16): a
-  // wave-uniform block base plus this lane's fixed 32-bit offset in it
-  const uint32_t lane_off = uint32_t(tile_token(lane & 15) * NBK + QB * (lane >> 4));
+  // wave-uniform block base plus this lane's fixed 32-bit offset in it (0 when the
+  // chunk is past the range, as in load_v)
+  const uint32_t lane_off = live ? uint32_t(tile_token(lane & 15) * NBK + QB * (lane >> 4)) : 0u;
   static_for<0, 4>([&](auto rc) {
     constexpr int t = decltype(rc)::value;
     const int pid_t = __builtin_amdgcn_readlane(pid_lane, 16 * t);
@@ -972,7 +1013,7 @@ __device__ __forceinline__ void softmax_phase_mx(float sc, uint32_t nk_h, uint32
     float alpha_c = 1.f;
 #pragma unroll
     for (int i = 0; i < H; ++i) {
-      const float m_new = uniform(fmaxf(st.m[i], wave_max(sv[i])));
+      const float m_new = fmaxf(st.m[i], wave_max_dpp(sv[i]));
       const float alpha = __builtin_amdgcn_exp2f(st.m[i] - m_new);  // 0 on the first chunk
       st.m[i] = m_new;
       st.l[i] *= alpha;
@@ -994,10 +1035,15 @@ __device__ __forceinline__ void softmax_phase_mx(float sc, uint32_t nk_h, uint32
 // Values of a chunk: 4 K-steps (16 tokens each) x 8 M-tiles (one dim of each lane's
 // eight), one MFMA each; lookups run LA steps ahead.
 template <int BWK, int BWV, int NG>
-__device__ __forceinline__ void value_phase_mx(const RowBuf<BWK, BWV>& V, Tab<BWV>& cbv, const uint32_t* pt, int lane,
+__device__ __forceinline__ void value_phase_mx(RowBuf<BWK, BWV>& V, Tab<BWV>& cbv, const uint32_t* pt, int lane,
                                                f32x4 (&acc)[8]) {
   constexpr int NH = 4 * NG, VW = VWords<BWV>::N, LA = mx_lookahead<BWK, BWV>();
   const int c = lane & 15, g = lane >> 4;
+  if constexpr (kRawV<BWV>) {
+    const uint32_t sh = raw_shift<BWV>(lane);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) unshift_raw(V.w[2 * i], V.w[2 * i + 1], sh);
+  }
   const uint32_t sel = c < NH ? 0x01000100u : c < 2 * NH ? 0x03020302u : 0x0c0c0c0cu;
   const uint32_t* prow = pt + (c % NH) * kTileStride + 4 * g;
   // step k = 8ks + mt
@@ -1028,6 +1074,10 @@ __device__ __forceinline__ void value_phase_mx(const RowBuf<BWK, BWV>& V, Tab<BW
       }
     }
   };
+  // the p n_V words of K-step ks + 1 are read one K-step ahead: LDS returns a wave's
+  // reads in order, so a read issued just before its use would also wait for every
+  // lookup issued ahead of it
+  uint4 wq = *reinterpret_cast<const uint4*>(prow);
   uint2 e[LA + 1][2];
   static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
   h8 bq;
@@ -1035,8 +1085,8 @@ __device__ __forceinline__ void value_phase_mx(const RowBuf<BWK, BWV>& V, Tab<BW
   static_for<0, 32>([&](auto kc) {
     constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7;
     if constexpr (mt == 0) {
-      const uint4 w = *reinterpret_cast<const uint4*>(prow + 16 * ks);
-      bq = dup4(w.x, w.y, w.z, w.w, sel);
+      bq = dup4(wq.x, wq.y, wq.z, wq.w, sel);
+      if constexpr (ks + 1 < 4) wq = *reinterpret_cast<const uint4*>(prow + 16 * (ks + 1));
     }
     if constexpr (k + LA < 32) {
       look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
@@ -1139,30 +1189,38 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
   st.gs = 0;
   using Buf = RowBuf<BWK, BWV>;
   int pid_next;
+  // The next chunk's loads are issued on every step, the last one included (its
+  // addresses clamped into the range's last page, all lanes on one line): with loads
+  // on only some paths, the compiler's wait counts for a chunk's rows would have to
+  // cover the paths that skipped them, and each step would wait for every load in
+  // flight, the next chunk's V rows included, before it could start.
   auto step = [&](int ch, Buf& X, Buf& Y, Buf& Z) {
     const int c0 = t_lo + 64 * ch;
     const int pid_after = pid_of(ch + 2);
     const bool more = ch + 1 < n;
-    if (more) load_k16(a, kvh, lane, c0 + 64, pid_next, Z);
+    load_k16(a, kvh, lane, c0 + 64, pid_next, Z, more);
     score_phase_mx<BWK, BWV, NG>(X, cbk, qb, lane, ptile);
     softmax_phase_mx<NG>(sc, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
-    if (more) load_v(a, kvh, lane, c0 + 64, pid_next, X);
+    load_v<BWK, BWV, kRawV<BWV>>(a, kvh, lane, c0 + 64, pid_next, X, more);
     value_phase_mx<BWK, BWV, NG>(Y, cbv, ptile, lane, st.acc);
     pid_next = pid_after;
   };
 
   Buf b0, b1, b2;
   load_k16(a, kvh, lane, t_lo, pid_of(0), b0);
-  load_v(a, kvh, lane, t_lo, pid_of(0), b1);
+  load_v<BWK, BWV, kRawV<BWV>>(a, kvh, lane, t_lo, pid_of(0), b1);
   pid_next = pid_of(1);
   wait_vmem_all();
-  for (int ch = 0; ch < n; ch += 3) {
+  // whole turns of the three buffers in a loop without early exits (a loop header
+  // reached from an exit path gets its wait counts from that path), then the rest
+  int ch = 0;
+  for (; ch + 3 <= n; ch += 3) {
     step(ch, b0, b1, b2);
-    if (ch + 1 >= n) break;
     step(ch + 1, b2, b0, b1);
-    if (ch + 2 >= n) break;
     step(ch + 2, b1, b2, b0);
   }
+  if (ch < n) step(ch, b0, b1, b2);
+  if (ch + 1 < n) step(ch + 1, b2, b0, b1);
   write_partial_mx<NG>(a, st, prow, lane);
 }
 
