@@ -312,9 +312,9 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, i
   const uint32_t lane_off = live ? uint32_t((lane >> 4) * NBV + BWV * p) : 0u;
   static_for<0, 4>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
-    const int pid_j = __builtin_amdgcn_readlane(pid_lane, 16 * j);
-    const uint8_t* blk = a.v_pages + int64_t(pid_j) * a.vsp + (kvh >> a.kvshift) * a.vsh +
-                         int64_t((c0 + 16 * j) & smask) * NBV;
+    const uint32_t pid_j = __builtin_amdgcn_readlane(pid_lane, 16 * j);  // a live page id, >= 0
+    const uint8_t* blk = a.v_pages + uint64_t(pid_j) * uint64_t(a.vsp) + (kvh >> a.kvshift) * a.vsh +
+                         uint32_t((c0 + 16 * j) & smask) * uint32_t(NBV);
     const uint8_t* vj = blk + lane_off;
     static_for<0, 4>([&](auto qc) {
       constexpr int qq = decltype(qc)::value;
@@ -778,6 +778,11 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr float kCbScale = 256.0f;  // codebook values scaled by 2^8 before the split
+// One head group: the score tile keeps both column halves (q' H and L parts) and the
+// softmax adds them as it reads (four adds per lane) instead of a row rotate and add
+// on the sixteen output registers; two groups keep the rotate, for LDS room.
+template <int NG>
+constexpr bool kTileHalves = NG == 1;
 template <int BWV>
 constexpr bool kRawV = BWV == 5 || BWV == 6;  // V rows loaded as raw windows (load_vcodes)
 constexpr int kTileStride = 80;     // words per head in the per-wave score / p n_V tile
@@ -898,9 +903,9 @@ __device__ __forceinline__ void load_k16(const DecodeArgs& a, int kvh, int lane,
   const uint32_t lane_off = live ? uint32_t(tile_token(lane & 15) * NBK + QB * (lane >> 4)) : 0u;
   static_for<0, 4>([&](auto rc) {
     constexpr int t = decltype(rc)::value;
-    const int pid_t = __builtin_amdgcn_readlane(pid_lane, 16 * t);
-    const uint8_t* blk = a.k_pages + int64_t(pid_t) * a.ksp + (kvh >> a.kvshift) * a.ksh +
-                         int64_t((c0 + 16 * t) & smask) * NBK;
+    const uint32_t pid_t = __builtin_amdgcn_readlane(pid_lane, 16 * t);  // a live page id, >= 0
+    const uint8_t* blk = a.k_pages + uint64_t(pid_t) * uint64_t(a.ksp) + (kvh >> a.kvshift) * a.ksh +
+                         uint32_t((c0 + 16 * t) & smask) * uint32_t(NBK);
     const uint8_t* q = blk + lane_off;
     if constexpr (QB == 16) {
       const uint4 x = *reinterpret_cast<const uint4*>(q);
@@ -942,7 +947,8 @@ __device__ __forceinline__ float add_half(float x) {
 }
 
 // Scores of the chunk into the tile (head h of token 16r + 4i + g at word
-// h * kTileStride + 16r + 4g + i), before the 2^-(e+8) scale.
+// h * kTileStride + 16r + 4g + i; with kTileHalves the part of q' L at word
+// (h + NH) * kTileStride + ...), before the 2^-(e+8) scale.
 template <int BWK, int BWV, int NG>
 __device__ __forceinline__ void score_phase_mx(const RowBuf<BWK, BWV>& K, Tab<BWK>& cbk, const h8 (&qb)[8], int lane,
                                                uint32_t* pt) {
@@ -970,12 +976,14 @@ __device__ __forceinline__ void score_phase_mx(const RowBuf<BWK, BWV>& K, Tab<BW
     __builtin_amdgcn_sched_barrier(0);
   });
   const int c = lane & 15, g = lane >> 4;
+  if constexpr (!kTileHalves<NG>) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d[r][i] = add_half<NH>(d[r][i]);
+      for (int i = 0; i < 4; ++i) d[r][i] = add_half<NH>(d[r][i]);
+  }
   wave_lds_sync();  // the previous chunk's reads of the tile are done
-  if (c < NH) {
+  if (c < (kTileHalves<NG> ? 2 * NH : NH)) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       *reinterpret_cast<float4*>(pt + c * kTileStride + 16 * r + 4 * g) = make_float4(d[r][0], d[r][1], d[r][2], d[r][3]);
@@ -994,7 +1002,15 @@ __device__ __forceinline__ void softmax_phase_mx(float sc, uint32_t nk_h, uint32
   const float nv = valid ? half_lo(nv_h) : 0.f;
   float sv[H];
 #pragma unroll
-  for (int i = 0; i < H; ++i) sv[i] = valid ? __builtin_bit_cast(float, pt[i * kTileStride + off]) * nk : -INFINITY;
+  for (int i = 0; i < H; ++i) {
+    if constexpr (kTileHalves<NG>) {
+      const float x = __builtin_bit_cast(float, pt[i * kTileStride + off]) +
+                      __builtin_bit_cast(float, pt[(i + H) * kTileStride + off]);
+      sv[i] = valid ? x * nk : -INFINITY;
+    } else {
+      sv[i] = valid ? __builtin_bit_cast(float, pt[i * kTileStride + off]) * nk : -INFINITY;
+    }
+  }
   // value scale: 2^kRescale * max(n_V) * 2^-gs < 2^15
   int ge;
   frexpf(wave_max_nonneg(nv), &ge);
@@ -1229,7 +1245,7 @@ struct Rows16Lds {
   static constexpr int k_off = RowsLds<BWK, BWV, NG, WPB>::k_off;
   static constexpr int v_off = RowsLds<BWK, BWV, NG, WPB>::v_off;
   static constexpr int tiles = RowsLds<BWK, BWV, NG, WPB>::tiles;
-  static constexpr int tile_bytes = 4 * NG * kTileStride * 4;
+  static constexpr int tile_bytes = (kTileHalves<NG> ? 2 : 1) * 4 * NG * kTileStride * 4;
   static constexpr int total = tiles + WPB * tile_bytes;
   static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
 };
