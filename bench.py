@@ -232,8 +232,10 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
     The new tokens go to one fresh page per sequence, addressed through the
     sequence's page-table column L_b / S as in the cache; they land in a small
     separate pool so the decode pool is left as it is. Timed with hipEvents over
-    ``reps`` back-to-back calls; checked against the CPU restatement (codes under
-    the adjudication protocol) and timed beside it.
+    events the library records around the kernel on each of ``reps`` calls (and, as
+    ``us_per_call_from_python``, over ``reps`` back-to-back calls of the Python wrapper,
+    whose host overhead is longer than the kernel); checked against the CPU
+    restatement (codes under the adjudication protocol) and timed beside it.
     """
     import torch
     sys.path.insert(0, str(ROOT / "tests"))
@@ -264,12 +266,24 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
     vn = torch.zeros(P, Hkv, S, dtype=torch.float16, device=dev)
     kd, vd, td, sd = k.to(dev), v.to(dev), tab.to(dev), start.to(dev)
 
-    def call(check=False):
-        pb.append_kv(kd, vd, kq, vq, kp, vp, kn, vn, td, sd, check_ranges=check)
+    def call(check=False, evs=None):
+        pb.append_kv(kd, vd, kq, vq, kp, vp, kn, vn, td, sd, check_ranges=check, timing_events=evs)
 
     call(check=True)                             # full validation once, outside the timed region
     for _ in range(20):
         call()
+    # kernel time: events the library records on the stream right around the kernel
+    # (the Python wrapper's host overhead per call is longer than the kernel)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in evs:                           # torch's "recorded" flag; the library records them again
+        e0.record()
+        e1.record()
+    torch.cuda.synchronize()
+    for e0, e1 in evs:
+        call(evs=(ctypes.c_void_p(e0.cuda_event), ctypes.c_void_p(e1.cuda_event)))
+    torch.cuda.synchronize()
+    us = statistics.fmean(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3
+    # the same calls back to back from Python, host overhead included
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
@@ -277,7 +291,7 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
         call()
     e1.record()
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) / reps * 1e3
+    host_us = e0.elapsed_time(e1) / reps * 1e3
 
     # CPU restatement on the same inputs, timed, then the byte check
     ref = [torch.zeros(P, Hkv, S, nb, dtype=torch.uint8) for nb in (nbk, nbv)]
@@ -296,7 +310,8 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
         sel = lambda t: t[pids, :, pos % S].permute(0, 2, 1, 3)      # noqa: E731
         flips += adjudicate_codes(src, sel(gc), sel(wc), tq)
     vectors = 2 * B * Hkv * n_new
-    return {"us_per_call": us, "vectors_per_call": vectors, "vectors_per_s": vectors / (us * 1e-6),
+    return {"us_per_call": us, "timing": "kernel, hipEvents recorded by wn_append_kv around its launch",
+            "us_per_call_from_python": host_us, "vectors_per_call": vectors, "vectors_per_s": vectors / (us * 1e-6),
             "new_tokens_per_seq": n_new, "bytes_read": 2 * B * Hkv * n_new * D * 2,
             "bytes_written": B * Hkv * n_new * (nbk + 2 + nbv + 2),
             "cpu_us_per_call": cpu_us, "cpu_kind": "port", "adjudicated_code_flips": flips,

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define WN_ABI_VERSION 5
+#define WN_ABI_VERSION 6
 
 /* element types of floating-point tensors crossing the ABI */
 enum { WN_F32 = 0, WN_F16 = 1, WN_BF16 = 2 };
@@ -151,7 +151,10 @@ int wn_decode_attention_noalloc(
  *   the packed row goes to pages, fp16(n) to norms. max_pages is the width of
  *   page_table. Callers must keep every position inside the table row and every
  *   page id it names inside [0, num_pages) (the Python layer raises otherwise);
- *   as a last guard the device skips, without writing, any vector that does not. */
+ *   as a last guard the device skips, without writing, any vector that does not.
+ *   Pi_K / Pi_V 16-byte aligned; pages 8-byte aligned with strides in multiples of
+ *   8 bytes. ev_begin / ev_end (hipEvent_t or NULL) are recorded on `stream`
+ *   around the kernel (its time without the caller's host overhead). */
 int wn_append_kv(
     const void* k, int64_t ks_b, int64_t ks_h, int64_t ks_n,
     const void* v, int64_t vs_b, int64_t vs_h, int64_t vs_n, int x_dtype,
@@ -163,7 +166,8 @@ int wn_append_kv(
     uint8_t* v_pages, int64_t v_stride_p, int64_t v_stride_h,
     uint16_t* k_norms, int64_t kn_stride_p, int64_t kn_stride_h,
     uint16_t* v_norms, int64_t vn_stride_p, int64_t vn_stride_h,
-    int B, int Hkv, int n, int D, int S, int num_pages, int max_pages, void* stream);
+    int B, int Hkv, int n, int D, int S, int num_pages, int max_pages,
+    void* stream, void* ev_begin, void* ev_end);
 
 /* TurboQuantMSE.quantize on `rows` contiguous-D vectors at x + r*row_stride
  * (elements): codes (rows, D) uint8 and fp32 norms (rows,). */

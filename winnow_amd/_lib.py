@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libwinnow_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 WN_F32, WN_F16, WN_BF16 = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 32 << 20          # WN_NOALLOC_SCRATCH_BYTES
@@ -65,7 +65,8 @@ SIGNATURES = {
         _c_p, _c_i64, _c_i64,
         _c_p, _c_i64, _c_i64,
         _c_p, _c_i64, _c_i64,
-        _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
+        _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,
+        _c_p, _c_p, _c_p]),                         # stream, ev_begin, ev_end
     "wn_quantize": (_c_i, [_c_p, _c_i, _c_i64, _c_i64, _c_p, _c_p, _c_i, _c_i, _c_p, _c_p, _c_p]),
     "wn_pack": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_p, _c_p]),
     "wn_unpack": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_p, _c_p]),

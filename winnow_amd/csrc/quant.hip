@@ -14,8 +14,7 @@ namespace wn {
 namespace {
 
 constexpr int kQBlock = 256;                // 4 waves
-constexpr int kVW = 4;                      // vectors a wave quantizes together
-constexpr int kVecPerBlock = 4 * kVW;       // 16 per work-group
+constexpr int kVecPerBlock = 16;            // vectors per work-group (the rows of one f64 MFMA tile)
 
 struct QuantSide {
   const void* x;
@@ -60,115 +59,186 @@ __device__ __forceinline__ uint8_t packed_byte(const uint8_t* codes, int k, int 
   return uint8_t(v & 0xffu);
 }
 
-// Each wave quantizes kVW vectors together (lane j forms output dims j, j+64 of all
-// of them: 2*kVW independent float64 accumulation chains), so the 128-term dot
-// products overlap instead of running one after another; sixteen vectors per
-// work-group keep even a 4096-vector append spread over the whole GPU. Pi is
-// staged in LDS in 16-byte rows of stride D+4 floats: the 16 lanes a 16-byte LDS
-// read serves hit distinct banks.
+// The bw bytes of eight bw-bit codes packed LSB-first, stored at p (p is aligned to
+// the largest power of two dividing bw).
+__device__ __forceinline__ void store_packed8(uint8_t* p, uint64_t v, int bw) {
+  if (bw == 8) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(uint32_t(v), uint32_t(v >> 32));
+  } else if (bw == 4) {
+    *reinterpret_cast<uint32_t*>(p) = uint32_t(v);
+  } else if (bw == 2) {
+    *reinterpret_cast<uint16_t*>(p) = uint16_t(v);
+  } else if (bw == 6) {
+    reinterpret_cast<uint16_t*>(p)[0] = uint16_t(v);
+    reinterpret_cast<uint16_t*>(p)[1] = uint16_t(v >> 16);
+    reinterpret_cast<uint16_t*>(p)[2] = uint16_t(v >> 32);
+  } else {
+    for (int k = 0; k < bw; ++k) p[k] = uint8_t(v >> (8 * k));
+  }
+}
+
+// A work-group quantizes sixteen vectors (sixteen per work-group keep even a
+// 4096-vector append spread over the whole GPU), in phases that each run over all
+// sixteen at once, so a small append costs a few round trips, not one per vector:
+//   loads     sixteen threads per vector for x (D/16 consecutive elements each),
+//             then the rows of Pi this wave's rotation needs (B operands, from L2 with
+//             16-byte loads: Pi is not staged in LDS); in scatter mode threads 0-15
+//             look up the start position, later the page, of vector tid.
+//   norms     float64 sum of squares over each vector's sixteen threads, n =
+//             max(fp32(sqrt), 1e-10), x / n rounded once to fp32 into the LDS rows xs.
+//   rotation  y = (x / n) Pi^T on the float64 matrix cores (v_mfma_f64_16x16x4f64:
+//             products of fp32 values are exact in float64 and the sums stay in
+//             float64), rows = the sixteen vectors, columns = output dims: wave w
+//             forms output dims [D/4 w, D/4 (w+1)), D/64 tiles of sixteen. K-step
+//             s, slot k (= lane / 16) is input dim (D/4) k + s, so a lane's A
+//             operands are D/4 consecutive floats of one xs row and its B operands
+//             D/4 consecutive floats of one row of Pi. Output lane l, register i of a
+//             tile is vector l/16 + 4i, column l%16.
+//   codes     each y is rounded once to fp32 and bucketized into the LDS codes cs.
+//   stores    D/8 threads per vector each pack eight codes (bw bytes) and store
+//             them; thread 0 of the vector stores its norm.
 template <int D>
 __global__ __launch_bounds__(kQBlock) void quantize_kernel(QuantArgs a) {
-  constexpr int LD = D + 4;
-  constexpr int KPL = D / 64;  // output dims per lane
-  __shared__ __align__(16) float pis[D * LD];
+  constexpr int EPT = D / 16;  // x elements per thread in the norm phase
+  constexpr int KS = D / 4;    // K-steps of the rotation (4 input dims each)
+  constexpr int TPW = D / 64;  // output tiles of sixteen dims per wave
+  constexpr int TPV = D / 8;   // threads per vector in the store phase
+  typedef double f64x4 __attribute__((ext_vector_type(4)));
   __shared__ float bnd[255];
-  __shared__ __align__(16) double xs[4][kVW][D];
-  __shared__ uint8_t cs[4][kVW][D];
+  __shared__ __align__(16) float xs[kVecPerBlock][D];
+  __shared__ uint8_t cs[kVecPerBlock][D];
+  __shared__ float nrms[kVecPerBlock];
+  __shared__ int64_t rowoff[kVecPerBlock];  // byte offset of the vector's packed row (-1: skipped)
+  __shared__ int64_t nrmoff[kVecPerBlock];  // element offset of its norm
 
   const QuantSide& sd = a.side[blockIdx.y];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int nb = (1 << sd.bw) - 1;
   const int64_t v0 = int64_t(blockIdx.x) * kVecPerBlock;
-  if (v0 >= a.total) return;
-  for (int i = tid; i < D * D / 4; i += kQBlock) {
-    const float4 pv = reinterpret_cast<const float4*>(sd.pi)[i];
-    *reinterpret_cast<float4*>(pis + (4 * i / D) * LD + (4 * i) % D) = pv;
-  }
+  if (v0 >= a.total) return;  // block-uniform
+  // destination of vector v0 + tid (threads 0-15): its start position is loaded
+  // first, its page-table entry after the norms (the two loads depend), and both are
+  // used only by the stores
+  const bool dst_thread = tid < kVecPerBlock && v0 + tid < a.total;
+  int dst_pos = 0;
+  if (dst_thread && a.scatter)
+    dst_pos = a.start_pos[int((v0 + tid) / (int64_t(a.n) * a.H))] + int((v0 + tid) % a.n);
   for (int i = tid; i < nb; i += kQBlock) bnd[i] = sd.bnd[i];
-  __syncthreads();
 
-  const int64_t vw = v0 + int64_t(w) * kVW;  // this wave's first vector
-  float nrm[kVW];
-#pragma unroll
-  for (int t = 0; t < kVW; ++t) {
-    const int64_t v = vw + t;
-    nrm[t] = 1e-10f;
-    if (v < a.total) {  // wave-uniform
+  float4 pb[TPW][KS / 4];  // B operands: rows of Pi (from L2, not staged in LDS)
+  // norms: vector tid / 16, elements EPT * (tid % 16) ..
+  {
+    const int vl = tid >> 4, part = tid & 15;
+    const int64_t v = v0 + vl;
+    float xv[EPT];
+    if (v < a.total) {
       const int i = int(v % a.n);
       const int h = int((v / a.n) % a.H);
       const int b = int(v / (int64_t(a.n) * a.H));
-      const int64_t xo = b * sd.sb + h * sd.sh + i * sd.sn;
-      float xv[KPL];
-      double ss = 0.0;
+      const int64_t xo = b * sd.sb + h * sd.sh + i * sd.sn + EPT * part;
 #pragma unroll
-      for (int k = 0; k < KPL; ++k) {
-        xv[k] = load_elem(sd.x, xo + lane + 64 * k, a.x_dtype);
-        ss = fma(double(xv[k]), double(xv[k]), ss);
-      }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-      nrm[t] = fmaxf(float(sqrt(ss)), 1e-10f);
-#pragma unroll
-      for (int k = 0; k < KPL; ++k) xs[w][t][lane + 64 * k] = double(float(double(xv[k]) / double(nrm[t])));
+      for (int k = 0; k < EPT; ++k) xv[k] = load_elem(sd.x, xo + k, a.x_dtype);
     } else {
 #pragma unroll
-      for (int k = 0; k < KPL; ++k) xs[w][t][lane + 64 * k] = 0.0;
+      for (int k = 0; k < EPT; ++k) xv[k] = 0.f;
     }
-  }
-  wave_lds_sync();
-  // y[t][k] = sum_d (x_t / n_t)[d] * Pi[lane + 64k][d], exact products, float64 sums
-  double y[kVW][KPL];
+    // the B operands of this wave (rows of Pi) are issued after x: loads return in
+    // order, so the norms wait only for x and Pi arrives during them
 #pragma unroll
-  for (int t = 0; t < kVW; ++t)
+    for (int j = 0; j < TPW; ++j) {
+      const float4* row = reinterpret_cast<const float4*>(sd.pi + int64_t(w * KS + 16 * j + (lane & 15)) * D +
+                                                          KS * (lane >> 4));
 #pragma unroll
-    for (int k = 0; k < KPL; ++k) y[t][k] = 0.0;
-#pragma unroll 2
-  for (int d = 0; d < D; d += 4) {
-    float4 pr[KPL];
-#pragma unroll
-    for (int k = 0; k < KPL; ++k) pr[k] = *reinterpret_cast<const float4*>(pis + (lane + 64 * k) * LD + d);
-#pragma unroll
-    for (int t = 0; t < kVW; ++t) {
-      const double2 xa = *reinterpret_cast<const double2*>(&xs[w][t][d]);
-      const double2 xb = *reinterpret_cast<const double2*>(&xs[w][t][d + 2]);
-#pragma unroll
-      for (int k = 0; k < KPL; ++k) {
-        y[t][k] = fma(xa.x, double(pr[k].x), y[t][k]);
-        y[t][k] = fma(xa.y, double(pr[k].y), y[t][k]);
-        y[t][k] = fma(xb.x, double(pr[k].z), y[t][k]);
-        y[t][k] = fma(xb.y, double(pr[k].w), y[t][k]);
-      }
+      for (int q = 0; q < KS / 4; ++q) pb[j][q] = row[q];
     }
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) ss = fma(double(xv[k]), double(xv[k]), ss);
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+    const float n = fmaxf(float(sqrt(ss)), 1e-10f);
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) xs[vl][EPT * part + k] = float(double(xv[k]) / double(n));
+    if (part == 0) nrms[vl] = n;
   }
-#pragma unroll
-  for (int t = 0; t < kVW; ++t)
-#pragma unroll
-    for (int k = 0; k < KPL; ++k) cs[w][t][lane + 64 * k] = uint8_t(bucketize(bnd, sd.bw, float(y[t][k])));
-  wave_lds_sync();
+  int dst_pid = -1;
+  if (dst_thread && a.scatter) {
+    const int b = int((v0 + tid) / (int64_t(a.n) * a.H)), col = dst_pos >> a.log2S;
+    if (dst_pos >= 0 && col < a.max_pages) dst_pid = a.table[b * a.tsb + col];
+  }
+  __syncthreads();  // xs, bnd, nrms
 
-  const int S = 1 << a.log2S;
-  const int NB = D * sd.bw / 8;
+  // A operands: row lane%16 of xs, input dims KS (lane/16) .. + KS - 1
+  float4 xa[KS / 4];
+  {
+    const float4* xr = reinterpret_cast<const float4*>(&xs[lane & 15][KS * (lane >> 4)]);
 #pragma unroll
-  for (int t = 0; t < kVW; ++t) {
-    const int64_t v = vw + t;
-    if (v >= a.total) break;  // wave-uniform
-    const int i = int(v % a.n);
-    const int h = int((v / a.n) % a.H);
-    const int b = int(v / (int64_t(a.n) * a.H));
-    if (a.scatter) {
-      const int pos = a.start_pos[b] + i;
-      const int col = pos >> a.log2S;
-      const int pid = (pos >= 0 && col < a.max_pages) ? a.table[b * a.tsb + col] : -1;
-      if (pid >= 0 && pid < a.num_pages) {
-        const int slot = pos & (S - 1);
-        uint8_t* row = sd.pages + pid * sd.psp + h * sd.psh + int64_t(slot) * NB;
-        for (int k = lane; k < NB; k += 64) row[k] = packed_byte(cs[w][t], k, sd.bw, D);
-        if (lane == 0) sd.norms[pid * sd.nsp + h * sd.nsh + slot] = f32_to_f16(nrm[t]);
+    for (int q = 0; q < KS / 4; ++q) xa[q] = xr[q];
+  }
+  // two accumulators per tile (even and odd K-step pairs), summed at the end: four
+  // independent MFMA chains per wave at D = 128
+  f64x4 acc[TPW][2];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) acc[j][0] = acc[j][1] = f64x4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int q = 0; q < KS / 4; ++q) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const double xe = double(e == 0 ? xa[q].x : e == 1 ? xa[q].y : e == 2 ? xa[q].z : xa[q].w);
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        const float pe = e == 0 ? pb[j][q].x : e == 1 ? pb[j][q].y : e == 2 ? pb[j][q].z : pb[j][q].w;
+        acc[j][e >> 1] = __builtin_amdgcn_mfma_f64_16x16x4f64(xe, double(pe), acc[j][e >> 1], 0, 0, 0);
       }
-    } else {
+    }
+  }
 #pragma unroll
-      for (int k = 0; k < KPL; ++k) sd.codes_out[v * D + lane + 64 * k] = cs[w][t][lane + 64 * k];
-      if (lane == 0) sd.norms_out[v] = nrm[t];
+  for (int j = 0; j < TPW; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      cs[(lane >> 4) + 4 * i][w * KS + 16 * j + (lane & 15)] =
+          uint8_t(bucketize(bnd, sd.bw, float(acc[j][0][i] + acc[j][1][i])));
+  if (tid < kVecPerBlock) {
+    // byte offset of the vector's packed row and element offset of its norm; -1: the
+    // vector is past the end, or (scatter) its position lies outside the page table
+    // or its page outside the pool (skipped without writing)
+    const int64_t v = v0 + tid;
+    int64_t ro = -1, no = 0;
+    if (dst_thread) {
+      const int h = int((v / a.n) % a.H);
+      if (!a.scatter) {
+        ro = v * D;
+        no = v;
+      } else if (dst_pid >= 0 && dst_pid < a.num_pages) {
+        const int64_t slot = dst_pos & ((1 << a.log2S) - 1);
+        ro = dst_pid * sd.psp + h * sd.psh + slot * (D * sd.bw / 8);
+        no = dst_pid * sd.nsp + h * sd.nsh + slot;
+      }
+    }
+    rowoff[tid] = ro;
+    nrmoff[tid] = no;
+  }
+  __syncthreads();  // codes of all sixteen vectors, their destinations
+
+  // stores: vector tid / TPV, codes 8 (tid % TPV) .. + 7
+  if (tid < kVecPerBlock * TPV) {
+    const int vl = tid / TPV, part = tid % TPV;
+    const int64_t ro = rowoff[vl];
+    if (ro >= 0) {
+      const uint8_t* c = &cs[vl][8 * part];
+      if (a.scatter) {
+        uint64_t pk = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) pk |= uint64_t(c[k]) << (sd.bw * k);
+        store_packed8(sd.pages + ro + int64_t(part) * sd.bw, pk, sd.bw);
+        if (part == 0) sd.norms[nrmoff[vl]] = f32_to_f16(nrms[vl]);
+      } else {
+        uint64_t cw = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) cw |= uint64_t(c[k]) << (8 * k);
+        *reinterpret_cast<uint2*>(sd.codes_out + ro + 8 * part) = make_uint2(uint32_t(cw), uint32_t(cw >> 32));
+        if (part == 0) sd.norms_out[nrmoff[vl]] = nrms[vl];
+      }
     }
   }
 }
@@ -215,13 +285,16 @@ __global__ __launch_bounds__(D) void dequantize_kernel(const uint8_t* codes, con
 
 using namespace wn;
 
-static int launch_quantize(QuantArgs& a, int sides, int D, hipStream_t st, const char* what) {
+static int launch_quantize(QuantArgs& a, int sides, int D, hipStream_t st, const char* what,
+                           void* ev_begin = nullptr, void* ev_end = nullptr) {
   if (a.total == 0) return WN_OK;
   dim3 grid(unsigned((a.total + kVecPerBlock - 1) / kVecPerBlock), sides);
+  if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
   if (D == 128)
     hipLaunchKernelGGL(quantize_kernel<128>, grid, dim3(kQBlock), 0, st, a);
   else
     hipLaunchKernelGGL(quantize_kernel<64>, grid, dim3(kQBlock), 0, st, a);
+  if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
   return check_launch(what);
 }
 
@@ -235,7 +308,8 @@ extern "C" int wn_append_kv(
     uint8_t* v_pages, int64_t v_stride_p, int64_t v_stride_h,
     uint16_t* k_norms, int64_t kn_stride_p, int64_t kn_stride_h,
     uint16_t* v_norms, int64_t vn_stride_p, int64_t vn_stride_h,
-    int B, int Hkv, int n, int D, int S, int num_pages, int max_pages, void* stream) {
+    int B, int Hkv, int n, int D, int S, int num_pages, int max_pages,
+    void* stream, void* ev_begin, void* ev_end) {
   clear_error();
   WN_REQUIRE(B >= 0 && Hkv > 0 && n >= 0 && num_pages >= 0 && max_pages >= 0, WN_E_INVALID,
              "append: bad sizes B=%d Hkv=%d n=%d", B, Hkv, n);
@@ -248,6 +322,11 @@ extern "C" int wn_append_kv(
   WN_REQUIRE(k && pi_k && boundaries_k && page_table && start_pos && k_pages && k_norms, WN_E_INVALID,
              "append: null operand");
   WN_REQUIRE(!v || (pi_v && boundaries_v && v_pages && v_norms), WN_E_INVALID, "append: null V operand");
+  WN_REQUIRE(aligned(pi_k, 16) && (!v || aligned(pi_v, 16)), WN_E_INVALID,
+             "append: rotations need 16-byte aligned rows (read with 16-byte loads)");
+  WN_REQUIRE(aligned(k_pages, 8) && k_stride_p % 8 == 0 && k_stride_h % 8 == 0 &&
+                 (!v || (aligned(v_pages, 8) && v_stride_p % 8 == 0 && v_stride_h % 8 == 0)),
+             WN_E_INVALID, "append: pages need 8-byte aligned base and strides");
   QuantArgs a{};
   a.side[0] = QuantSide{k, ks_b, ks_h, ks_n, pi_k, boundaries_k, bw_k, k_pages, k_stride_p, k_stride_h,
                         k_norms, kn_stride_p, kn_stride_h, nullptr, nullptr};
@@ -265,7 +344,7 @@ extern "C" int wn_append_kv(
   a.max_pages = max_pages;
   a.x_dtype = x_dtype;
   a.scatter = 1;
-  return launch_quantize(a, v ? 2 : 1, D, static_cast<hipStream_t>(stream), "wn_append_kv");
+  return launch_quantize(a, v ? 2 : 1, D, static_cast<hipStream_t>(stream), "wn_append_kv", ev_begin, ev_end);
 }
 
 extern "C" int wn_quantize(const void* x, int x_dtype, int64_t rows, int64_t row_stride, const float* pi,
@@ -278,6 +357,8 @@ extern "C" int wn_quantize(const void* x, int x_dtype, int64_t rows, int64_t row
   WN_REQUIRE(x_dtype >= WN_F32 && x_dtype <= WN_BF16, WN_E_INVALID, "quantize: dtype code %d", x_dtype);
   if (rows == 0) return WN_OK;
   WN_REQUIRE(x && pi && boundaries && codes && norms, WN_E_INVALID, "quantize: null operand");
+  WN_REQUIRE(aligned(pi, 16), WN_E_INVALID, "quantize: the rotation needs 16-byte aligned rows");
+  WN_REQUIRE(aligned(codes, 8), WN_E_INVALID, "quantize: codes need an 8-byte aligned base");
   QuantArgs a{};
   a.side[0] = QuantSide{x, row_stride, 0, 0, pi, boundaries, bw, nullptr, 0, 0, nullptr, 0, 0, codes, norms};
   a.total = rows;

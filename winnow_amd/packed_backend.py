@@ -126,7 +126,7 @@ def append_kv(k: torch.Tensor, v: torch.Tensor | None, k_tq, v_tq,
               page_table: torch.Tensor, start_pos: torch.Tensor, *,
               page_table_host: torch.Tensor | None = None,
               start_pos_host: torch.Tensor | None = None,
-              check_ranges: bool = True) -> None:
+              check_ranges: bool = True, timing_events=None) -> None:
     """Quantize, pack and scatter (B, Hkv, n, D) K (and V, unless ``v`` is None) into one
     layer's pages in one launch; token i of sequence b lands at position
     ``start_pos[b] + i``: page ``page_table[b, pos // S]``, slot ``pos % S``
@@ -136,6 +136,8 @@ def append_kv(k: torch.Tensor, v: torch.Tensor | None, k_tq, v_tq,
     wrong shape, and (``check_ranges``) for a position beyond the table row or a page
     id outside the pool. The range check reads ``page_table_host`` /
     ``start_pos_host`` when given, else copies the two small tensors to the host.
+    ``timing_events`` is an optional pair of raw ``hipEvent_t`` handles recorded
+    around the kernel.
     """
     operands = [k, k_pages, k_norms, page_table, start_pos] + ([v, v_pages, v_norms] if v is not None else [])
     if any(t is None for t in operands):
@@ -192,7 +194,7 @@ def append_kv(k: torch.Tensor, v: torch.Tensor | None, k_tq, v_tq,
             _lib.ptr(vp), *((vp.stride(0), vp.stride(1)) if has_v else (0, 0)),
             _lib.ptr(k_norms), k_norms.stride(0), k_norms.stride(1),
             _lib.ptr(vn), *((vn.stride(0), vn.stride(1)) if has_v else (0, 0)),
-            B, Hkv, n, D, S, P, page_table.shape[1], _lib.stream_of(k.device))
+            B, Hkv, n, D, S, P, page_table.shape[1], _lib.stream_of(k.device), *(timing_events or (None, None)))
 
 
 def _append_dense_rows(src: torch.Tensor, pages: torch.Tensor, meta: PageTable) -> None:
