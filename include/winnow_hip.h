@@ -68,12 +68,14 @@ const char* wn_last_error(void);
  * reference's num_splits, packed_attention_triton.py:211-216): *pages_per_split
  * = cdiv(max_pages, splits), one partial per (sequence, kv head, split).
  * requested_splits == 0 lets the library choose. Where the row-per-lane
- * matrix-core scan applies (head_dim 128, <= 8 query heads per kv head or an
- * even number up to 16, page
- * size >= 16) the plan is balanced: *pages_per_split = 0 and *num_splits = the
- * number of resident waves on the current device, which then share the
- * flattened (sequence, kv head, 64-token chunk) space equally, ragged batches
- * included. Otherwise fixed splits sized to fill the GPU. */
+ * matrix-core scan applies (head_dim 128, page size >= 16, widths 2-6 bits alike
+ * for K and V, 4/6, 6/4 or 8/8, 4/8, and n_rep that 2^s virtual kv heads per kv
+ * head bring to <= 8 query heads each) the plan is balanced: *pages_per_split = 0
+ * and *num_splits = the number of resident waves on the current device, which then
+ * share the flattened (sequence, kv head, 64-token chunk) space equally, ragged
+ * batches included. Otherwise (any other pair of widths in {2,3,4,5,6,8}, head_dim
+ * 64, any other n_rep, run as groups of <= 16 query heads) fixed splits sized to
+ * fill the GPU. */
 int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
                    int requested_splits, int* pages_per_split, int* num_splits);
 

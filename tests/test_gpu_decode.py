@@ -69,6 +69,49 @@ def test_widths_and_groups(bwk, bwv, Hq, Hkv):
         _check(got, ref, lens)
 
 
+WIDTHS = (2, 3, 4, 5, 6, 8)
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_every_width_pair(D):
+    """Every pair of supported widths for K and V (packing.py SUPPORTED), at both head
+    dims: the reference kernel takes any pair per call (packed_attention_triton.py:247).
+    The pairs without a tuned kernel run on the vector-ALU scan; each is checked
+    against the oracle with one, two and the library's splits."""
+    pa = _pa()
+    lens = (0, 5, 40, 333)
+    scale = oa.default_scale(D)
+    for bwk in WIDTHS:
+        for bwv in WIDTHS:
+            print(f"widths {bwk}/{bwv} D={D}", flush=True)
+            q, kv = build(500 + 10 * bwk + bwv, len(lens), 8, 2, D, lens, 16, bwk, bw_v=bwv)
+            ref = oa.tiled_compressed_attention(q, kv, scale)
+            kvd = to_device(kv, DEV)
+            for splits in (None, 1, 2):
+                got = pa.packed_decode_attention(q.to(DEV), kvd, scale, num_splits=splits, out_dtype=torch.float32)
+                _check(got, ref, lens)
+
+
+@pytest.mark.parametrize("bwk,bwv,Hq,Hkv,D", [(4, 4, 34, 2, 128), (4, 4, 40, 2, 128), (4, 4, 48, 2, 128),
+                                               (4, 6, 64, 2, 128), (4, 4, 128, 2, 128), (6, 6, 96, 1, 128),
+                                               (2, 4, 48, 2, 128), (4, 4, 64, 2, 64), (8, 8, 68, 2, 64)])
+def test_more_than_sixteen_query_heads(bwk, bwv, Hq, Hkv, D):
+    """n_rep > 16 (the reference pads its head block to next_pow2(n_rep),
+    packed_attention_triton.py:209): the row scan runs 2^s virtual kv heads of <= 8
+    query heads (n_rep 20, 24, 32, 48, 64, 96 at head_dim 128), the vector-ALU scan groups
+    of <= 16 (n_rep 17 and 34: a prime group count; head_dim 64; a pair without a
+    row scan)."""
+    print(f"n_rep {Hq // Hkv} widths {bwk}/{bwv} D={D}", flush=True)
+    lens = (0, 17, 260)
+    q, kv = build(700 + Hq + D, len(lens), Hq, Hkv, D, lens, 16, bwk, bw_v=bwv)
+    scale = oa.default_scale(D)
+    ref = oa.tiled_compressed_attention(q, kv, scale)
+    kvd = to_device(kv, DEV)
+    for splits in (None, 3):
+        got = _pa().packed_decode_attention(q.to(DEV), kvd, scale, num_splits=splits, out_dtype=torch.float32)
+        _check(got, ref, lens)
+
+
 def test_config1_plumbing():
     """B1, 8/8 heads, D128, L1024, fp32 ~N(0,1) seed 0, 4-bit, S16."""
     g = torch.Generator().manual_seed(0)

@@ -5,9 +5,9 @@
 //                        one block also writes the per-sequence chunk prefix the
 //                        balanced scan partitions by
 //   2. page scan         the row-per-lane matrix-core scan (decode_rows.hip) where
-//                        it applies (head_dim 128, <= 8 query heads per kv head
-//                        or an even number up to 16),
-//                        else decode_split_kernel below: one work-group per
+//                        it applies (head_dim 128, a width pair it compiles, and
+//                        n_rep that 2^s virtual heads per kv head bring to <= 8),
+//                        else decode_split_kernel (wn_split.h): one work-group per
 //                        (split, kv head, sequence), score phase (lane = token),
 //                        online softmax, value phase (16 lanes per token row),
 //                        cross-wave max-stable merge into one (acc, m, l) partial
@@ -21,61 +21,10 @@
 #include <mutex>
 #include <utility>
 
-#include "wn_decode.h"
+#include "wn_split.h"
 
 namespace wn {
 namespace {
-
-constexpr int kBlock = 256;  // 4 waves
-
-// The bytes holding codes [8*g, 8*g+8) of a row: exactly BW bytes at byte
-// offset g*BW, loaded with the widest accesses their alignment allows.
-template <int BW>
-__device__ __forceinline__ void load_group(const uint8_t* p, uint32_t (&v)[2]) {
-  if constexpr (BW == 8) {
-    uint2 x = *reinterpret_cast<const uint2*>(p);
-    v[0] = x.x;
-    v[1] = x.y;
-  } else if constexpr (BW == 4) {
-    v[0] = *reinterpret_cast<const uint32_t*>(p);
-    v[1] = 0;
-  } else if constexpr (BW == 2) {
-    v[0] = *reinterpret_cast<const uint16_t*>(p);
-    v[1] = 0;
-  } else if constexpr (BW == 6) {
-    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
-    v[0] = uint32_t(h[0]) | (uint32_t(h[1]) << 16);
-    v[1] = h[2];
-  } else if constexpr (BW == 3) {
-    v[0] = uint32_t(p[0]) | (uint32_t(p[1]) << 8) | (uint32_t(p[2]) << 16);
-    v[1] = 0;
-  } else {  // 5
-    v[0] = uint32_t(p[0]) | (uint32_t(p[1]) << 8) | (uint32_t(p[2]) << 16) | (uint32_t(p[3]) << 24);
-    v[1] = p[4];
-  }
-}
-
-// A whole packed row (NB bytes, NB a multiple of 8) into registers.
-template <int NB>
-__device__ __forceinline__ void load_row(const uint8_t* p, uint32_t (&w)[NB / 4]) {
-  if constexpr (NB % 16 == 0) {
-#pragma unroll
-    for (int i = 0; i < NB / 16; ++i) {
-      uint4 x = reinterpret_cast<const uint4*>(p)[i];
-      w[4 * i] = x.x;
-      w[4 * i + 1] = x.y;
-      w[4 * i + 2] = x.z;
-      w[4 * i + 3] = x.w;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < NB / 8; ++i) {
-      uint2 x = reinterpret_cast<const uint2*>(p)[i];
-      w[2 * i] = x.x;
-      w[2 * i + 1] = x.y;
-    }
-  }
-}
 
 struct RotArgs {
   const void* q;
@@ -159,172 +108,6 @@ __global__ __launch_bounds__(256) void rotate_q_kernel(RotArgs a) {
 #pragma unroll 8
     for (int d = 0; d < D; ++d) acc = fmaf(qs[h][d], prow[d], acc);
     out[h * D + j] = acc * a.scale;
-  }
-}
-
-template <int D, int BWK, int BWV, int NREP>
-__global__ __launch_bounds__(kBlock) void decode_split_kernel(DecodeArgs a) {
-  constexpr int NBK = D * BWK / 8;
-  constexpr int NBV = D * BWV / 8;
-  constexpr int G = D / 8;     // lanes per token row in the value phase (8 dims each)
-  constexpr int TPS = 64 / G;  // token rows per value step
-  constexpr int LK = 1 << BWK, LV = 1 << BWV;
-
-  __shared__ float cbk[LK];
-  __shared__ float cbv[LV];
-  __shared__ float pw[4][64][NREP];  // p * n_V per token of the wave's chunk
-  __shared__ int pidl[4][64];        // page id per token of the chunk
-  __shared__ float red_m[4][NREP], red_l[4][NREP];
-  __shared__ float red_acc[4][NREP][D];
-
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int S = 1 << a.log2S;
-  const int L = a.seq_lens[b];
-  const int n_pages = (L + S - 1) >> a.log2S;
-  const int page_lo = split * a.pages_per_split;
-  if (page_lo >= n_pages) return;  // block-uniform: this split is past the sequence
-  const int page_hi = min(page_lo + a.pages_per_split, n_pages);
-  const int t_lo = page_lo << a.log2S;
-  const int t_hi = min(page_hi << a.log2S, L);
-
-  if (split == 0 && tid == 0)
-    a.unit_meta[b * a.Hkv + kvh] =
-        make_int2((b * a.Hkv + kvh) * a.num_splits, (n_pages + a.pages_per_split - 1) / a.pages_per_split);
-  for (int i = tid; i < LK; i += kBlock) cbk[i] = a.cb_k[i];
-  for (int i = tid; i < LV; i += kBlock) cbv[i] = a.cb_v[i];
-  __syncthreads();
-
-  const float* __restrict__ qp = a.q_rot + (int64_t(b) * a.Hkv + kvh) * NREP * D;
-  const int32_t* __restrict__ trow = a.table + b * a.tsb;
-  const uint8_t* kbase = a.k_pages + kvh * a.ksh;
-  const uint8_t* vbase = a.v_pages + kvh * a.vsh;
-  const uint16_t* knb = a.k_norms + kvh * a.knh;
-  const uint16_t* vnb = a.v_norms + kvh * a.vnh;
-
-  float m[NREP], l[NREP], acc[NREP][8];
-#pragma unroll
-  for (int h = 0; h < NREP; ++h) {
-    m[h] = -INFINITY;
-    l[h] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
-  }
-  const int tsub = lane / G, dg = lane % G;
-
-  for (int c0 = t_lo + w * 64; c0 < t_hi; c0 += 4 * 64) {
-    // ---- score phase: lane = token
-    const int t = c0 + lane;
-    const bool valid = t < t_hi;
-    int pid = 0;
-    float nv = 0.f;
-    float s[NREP];
-    if (valid) {
-      pid = trow[t >> a.log2S];
-      const int slot = t & (S - 1);
-      uint32_t kw[NBK / 4];
-      load_row<NBK>(kbase + pid * a.ksp + slot * NBK, kw);
-      const float nk = f16_to_f32(knb[pid * a.knp + slot]);
-      nv = f16_to_f32(vnb[pid * a.vnp + slot]);
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) s[h] = 0.f;
-#pragma unroll
-      for (int d = 0; d < D; ++d) {
-        const float c = cbk[code_at<BWK>(kw, d)];
-#pragma unroll
-        for (int h = 0; h < NREP; ++h) s[h] = fmaf(qp[h * D + d], c, s[h]);
-      }
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) s[h] *= nk;
-    } else {
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) s[h] = -INFINITY;
-    }
-
-    wave_lds_sync();  // the previous chunk's value phase has read pw / pidl
-    float alpha[NREP];
-#pragma unroll
-    for (int h = 0; h < NREP; ++h) {
-      const float mn = fmaxf(m[h], wave_max(s[h]));  // finite: lane 0 of a chunk is valid
-      alpha[h] = expf(m[h] - mn);                     // 0 on the first chunk (m = -inf)
-      const float p = valid ? expf(s[h] - mn) : 0.f;
-      l[h] = l[h] * alpha[h] + wave_sum(p);
-      m[h] = mn;
-      pw[w][lane][h] = p * nv;
-    }
-    pidl[w][lane] = pid;
-    wave_lds_sync();
-
-    // ---- value phase: G lanes per token row, 8 dims per lane
-#pragma unroll
-    for (int h = 0; h < NREP; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] *= alpha[h];
-#pragma unroll 2
-    for (int j = 0; j < 64 / TPS; ++j) {
-      const int tl = j * TPS + tsub;
-      const int tt = c0 + tl;
-      if (tt < t_hi) {
-        const int pv = pidl[w][tl];
-        uint32_t vb[2];
-        load_group<BWV>(vbase + pv * a.vsp + (tt & (S - 1)) * NBV + dg * BWV, vb);
-        float wv[NREP];
-#pragma unroll
-        for (int h = 0; h < NREP; ++h) wv[h] = pw[w][tl][h];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float c = cbv[code_at<BWV>(vb, i)];
-#pragma unroll
-          for (int h = 0; h < NREP; ++h) acc[h][i] = fmaf(wv[h], c, acc[h][i]);
-        }
-      }
-    }
-  }
-
-  // Token subgroups of a wave share m: plain sums.
-#pragma unroll
-  for (int o = G; o < 64; o <<= 1)
-#pragma unroll
-    for (int h = 0; h < NREP; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] += __shfl_xor(acc[h][i], o, 64);
-  if (lane < G) {
-#pragma unroll
-    for (int h = 0; h < NREP; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) red_acc[w][h][dg * 8 + i] = acc[h][i];
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < NREP; ++h) {
-      red_m[w][h] = m[h];
-      red_l[w][h] = l[h];
-    }
-  }
-  __syncthreads();
-
-  // Max-stable merge of the four waves; a wave that saw no chunk has m = -inf.
-  const int64_t row0 = ((int64_t(b) * a.Hkv + kvh) * a.num_splits + split) * a.n_rep;
-  for (int e = tid; e < a.n_rep * D; e += kBlock) {
-    const int h = e / D, d = e % D;
-    float M = red_m[0][h];
-#pragma unroll
-    for (int ww = 1; ww < 4; ++ww) M = fmaxf(M, red_m[ww][h]);
-    float af = 0.f, lf = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      const float mw = red_m[ww][h];
-      if (mw != -INFINITY) {
-        const float sc = expf(mw - M);
-        af = fmaf(sc, red_acc[ww][h][d], af);
-        lf = fmaf(sc, red_l[ww][h], lf);
-      }
-    }
-    a.part_acc[(row0 + h) * D + d] = af;
-    if (d == 0) {
-      a.part_ml[2 * (row0 + h)] = M;
-      a.part_ml[2 * (row0 + h) + 1] = lf;
-    }
   }
 }
 
@@ -421,18 +204,6 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
 
 using RotFn = void (*)(RotArgs);
 
-template <int D, int BWK, int BWV>
-SplitFn pick_nrep(int nrep) {
-  switch (nrep) {
-    case 1: return decode_split_kernel<D, BWK, BWV, 1>;
-    case 2: return decode_split_kernel<D, BWK, BWV, 2>;
-    case 4: return decode_split_kernel<D, BWK, BWV, 4>;
-    case 8: return decode_split_kernel<D, BWK, BWV, 8>;
-    case 16: return decode_split_kernel<D, BWK, BWV, 16>;
-  }
-  return nullptr;
-}
-
 template <int D>
 SplitFn pick_split(int bwk, int bwv, int nrep) {
   if (bwk == bwv) {
@@ -451,7 +222,7 @@ SplitFn pick_split(int bwk, int bwv, int nrep) {
     if (bwk == 6 && bwv == 4) return pick_nrep<D, 6, 4>(nrep);
     if (bwk == 4 && bwv == 8) return pick_nrep<D, 4, 8>(nrep);
   }
-  return nullptr;
+  return pick_split_any(D, bwk, bwv, nrep);  // every other pair (decode_split_any*.hip)
 }
 
 template <int D>
@@ -484,25 +255,47 @@ int pad_nrep(int n_rep) {
   return p;
 }
 
-// The scan wn_decode_attention runs for this shape. An even n_rep of 10..16 runs on
-// the row scan as twice the kv heads with n_rep / 2 query heads each (kvshift 1):
-// q_rot rows, partial rows and output heads are laid out alike in both views, and
-// only the scan's page and norm addresses map a virtual head back to its kv head.
+// Virtual heads. A kv head with more query heads than a scan holds runs as kvdiv
+// virtual kv heads of n_rep / kvdiv query heads each: q_rot rows, partial rows and
+// output heads are laid out alike in both views (virtual head v of kv head k is
+// v = k kvdiv + j and holds query heads v (n_rep / kvdiv) + h), and only the scan's
+// page and norm addresses map a virtual head back to its kv head.
+// Row scan: kvdiv = 2^s, the smallest with n_rep / 2^s <= 8 whole, or -1.
+int row_shift(int n_rep) {
+  for (int s = 0; (1 << s) <= n_rep; ++s)
+    if (n_rep % (1 << s) == 0 && (n_rep >> s) <= 8) return s;
+  return -1;
+}
+// Vector-ALU scan: the smallest divisor kvdiv of n_rep with n_rep / kvdiv <= 16.
+int valu_groups(int n_rep) {
+  for (int g = 1; g < n_rep; ++g)
+    if (n_rep % g == 0 && n_rep / g <= 16) return g;
+  return n_rep > 0 ? n_rep : 1;
+}
+
+// The scan wn_decode_attention runs for this shape: the row-per-lane matrix-core
+// scan where it applies (head_dim 128, page size >= 16, a compiled width pair, any
+// n_rep that 2^s virtual heads bring to <= 8), else the vector-ALU scan (any
+// supported width pair, n_rep split into groups of <= 16).
 SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v) {
   SplitKernel sk;
   const int n_rep = Hq / Hkv;
-  const int shift = (n_rep > 8 && n_rep <= 16 && n_rep % 2 == 0) ? 1 : 0;
-  if (D == 128 && (n_rep >> shift) <= 8 && S >= 16 && rows_allowed()) {
+  const int shift = row_shift(n_rep);
+  if (D == 128 && shift >= 0 && S >= 16 && rows_allowed()) {
     sk = pick_split_rows(bw_k, bw_v, n_rep >> shift);
-    // the virtual-head view exists only on the row scan; the VALU scan below reads
-    // physical kv heads
-    if (sk.fn) sk.kvshift = shift;
+    if (sk.fn) {
+      sk.kvshift = shift;
+      sk.kvdiv = 1 << shift;
+    }
   }
   if (!sk.fn) {
-    const int nrp = pad_nrep(n_rep);
+    const int g = valu_groups(n_rep);
+    const int nrp = pad_nrep(n_rep / g);
+    sk = SplitKernel{};
     sk.fn = D == 128 ? pick_split<128>(bw_k, bw_v, nrp) : pick_split<64>(bw_k, bw_v, nrp);
     sk.block = kBlock;
     sk.nrep = nrp;
+    sk.kvdiv = g;
   }
   return sk;
 }
@@ -533,18 +326,32 @@ struct WsLayout {
   int64_t qrot, prefix, meta, acc, ml, total;
 };
 
-// Scratch: q_rot (B, Hkv, max(NREP, 4), D) fp32, chunk prefix (B+1) int32, and
+// Virtual heads per kv head either scan may use, and the q_rot rows per kv head it
+// needs (NREP rows per virtual head, at least 4 on the matrix-core scan).
+int max_virtual_heads(int n_rep) {
+  const int s = row_shift(n_rep);
+  return max(s >= 0 ? 1 << s : 1, valu_groups(n_rep));
+}
+int qrot_rows(int n_rep) {
+  int rows = max(pad_nrep(n_rep), 4);
+  const int s = row_shift(n_rep);
+  if (s >= 0) rows = max(rows, (1 << s) * max(pad_nrep(n_rep >> s), 4));
+  const int g = valu_groups(n_rep);
+  return max(rows, g * pad_nrep(n_rep / g));
+}
+
+// Scratch: q_rot (B, Hkv, qrot_rows, D) fp32, chunk prefix (B+1) int32, and
 // the partials, (rows * n_rep) x D for acc and x 2 for (m, l).
 WsLayout ws_layout(int B, int Hq, int Hkv, int D, int pages_per_split, int num_splits) {
   WsLayout l;
   const int n_rep = Hq / Hkv;
-  const int nrp = max(pad_nrep(n_rep), 4);  // the matrix-core scan reads 4 rows per kv head
+  const int nrp = qrot_rows(n_rep);
   const int64_t rows = pages_per_split > 0 ? int64_t(B) * Hkv * num_splits : int64_t(num_splits) + int64_t(B) * Hkv;
   l.qrot = 0;
   l.prefix = align256(int64_t(B) * Hkv * nrp * D * 4);
   l.meta = l.prefix + align256(int64_t(B + 1) * 4);
-  // unit_meta: one per kv head, or per virtual head when n_rep > 8 (choose_scan)
-  l.acc = l.meta + align256(int64_t(B) * Hkv * (n_rep > 8 ? 2 : 1) * 8);
+  // unit_meta: one per (virtual) kv head of either scan (choose_scan)
+  l.acc = l.meta + align256(int64_t(B) * Hkv * max_virtual_heads(n_rep) * 8);
   l.ml = l.acc + align256(rows * n_rep * D * 4);
   l.total = l.ml + align256(rows * n_rep * 2 * 4);
   return l;
@@ -616,7 +423,6 @@ extern "C" int wn_decode_attention(
   WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, WN_E_INVALID,
              "decode: need B>=0, Hq%%Hkv==0 (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
   const int n_rep = Hq / Hkv;
-  WN_REQUIRE(n_rep <= 16, WN_E_UNSUPPORTED, "decode: n_rep=%d > 16 not compiled", n_rep);
   WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "decode: head_dim %d not compiled (64, 128)", D);
   WN_REQUIRE(valid_bw(bw_k) && valid_bw(bw_v), WN_E_INVALID, "decode: bit widths %d/%d", bw_k, bw_v);
   WN_REQUIRE(is_pow2(S), WN_E_INVALID, "decode: page size %d is not a power of two", S);
@@ -660,7 +466,7 @@ extern "C" int wn_decode_attention(
   const float q_scale = sk.log2_units ? float(double(scale) * 1.4426950408889634) : scale;
   int2* meta = reinterpret_cast<int2*>(ws + lay.meta);
   // from here on the kv heads are the scan's (virtual) ones
-  const int Hkv_s = Hkv << sk.kvshift, n_rep_s = n_rep >> sk.kvshift;
+  const int Hkv_s = Hkv * sk.kvdiv, n_rep_s = n_rep / sk.kvdiv;
   RotArgs ra{q, q_stride_b, q_stride_h, pi_k, reinterpret_cast<float*>(ws + lay.qrot), seq_lens, prefix, meta,
              q_scale, B, Hkv_s, n_rep_s, q_dtype};
   hipLaunchKernelGGL(rot, dim3(Hkv_s, B, 4), dim3(256), 0, st, ra);
@@ -697,6 +503,7 @@ extern "C" int wn_decode_attention(
   da.balanced = balanced ? 1 : 0;
   da.qrows = max(sk.nrep, 1);
   da.kvshift = sk.kvshift;
+  da.kvdiv = sk.kvdiv;
   // the row scan numbers its waves across work-groups of sk.wpb waves
   const int64_t waves = balanced ? int64_t(num_splits) : int64_t(num_splits) * Hkv_s * B;
   const dim3 grid = sk.rows ? dim3(unsigned((waves + sk.wpb - 1) / sk.wpb)) : dim3(num_splits, Hkv_s, B);
@@ -856,6 +663,7 @@ extern "C" int wn_dense_decode_attention(
   hipLaunchKernelGGL(rot, dim3(Hkv, B, 4), dim3(256), 0, st, ra);
 
   DecodeArgs da{};
+  da.kvdiv = 1;
   da.q_rot = ra.q_rot;
   da.k_pages = static_cast<const uint8_t*>(k_pages);
   da.v_pages = static_cast<const uint8_t*>(v_pages);

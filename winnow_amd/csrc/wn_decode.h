@@ -25,7 +25,8 @@ struct DecodeArgs {
   int B, Hkv, n_rep, log2S, pages_per_split, num_splits;
   int balanced;  // 1: persistent waves share the flattened chunk space (pages_per_split unused)
   int qrows;     // rows of q_rot per kv head
-  int kvshift;   // the pages of (virtual) kv head h are those of kv head h >> kvshift
+  int kvshift;   // the pages of (virtual) kv head h are those of kv head h >> kvshift (row scans)
+  int kvdiv;     // the same for the vector-ALU scan: kv head h / kvdiv
 };
 
 using SplitFn = void (*)(DecodeArgs);
@@ -37,7 +38,8 @@ struct SplitKernel {
   int nrep = 0;   // query-head rows per kv head the kernel reads from q_rot
   bool log2_units = false;  // scores/maxima in log2 units (q_rot scaled by log2 e)
   bool rows = false;        // the row-per-lane matrix-core scan (balanced plans allowed)
-  int kvshift = 0;          // 1: each kv head runs as two virtual heads of n_rep / 2 query heads
+  int kvshift = 0;          // row scan: each kv head runs as 2^kvshift virtual heads of n_rep >> kvshift
+  int kvdiv = 1;            // virtual heads per kv head (1 << kvshift on the row scan)
 };
 
 // Row-per-lane matrix-core page scan for head_dim 128, power-of-two page sizes
@@ -51,5 +53,11 @@ SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep);
 // per kv head, page size >= 16) on the row scan's work plan, or an empty SplitKernel
 // for another page dtype or head_dim.
 SplitKernel pick_dense_scan(int page_dtype, int D);
+
+// The vector-ALU scan for the width pairs decode.hip does not instantiate (any pair
+// of supported widths), nrep query rows per kv head (1, 2, 4, 8 or 16), or nullptr.
+SplitFn pick_split_any(int D, int bw_k, int bw_v, int nrep);
+SplitFn pick_split_any_d128(int bw_k, int bw_v, int nrep);
+SplitFn pick_split_any_d64(int bw_k, int bw_v, int nrep);
 
 }  // namespace wn

@@ -34,7 +34,7 @@ from winnow_amd import _lib
 from winnow_amd.packing import packed_bytes
 
 SUPPORTED_HEAD_DIMS = (64, 128)
-MAX_N_REP = 16
+MAX_N_REP = 16   # the dense decode's query heads per kv head (the packed decode takes any)
 
 
 class UnsupportedLayout(ValueError):
@@ -207,8 +207,6 @@ def check_kernel_contract(q: torch.Tensor, kv: PackedKV, *, check_ranges: bool =
         raise UnsupportedLayout("page_size and head_dim must be powers of two >= 16")
     if kv.head_dim not in SUPPORTED_HEAD_DIMS:
         raise UnsupportedLayout(f"head_dim {kv.head_dim} is not compiled {SUPPORTED_HEAD_DIMS}")
-    if q.shape[1] // kv.num_kv_heads > MAX_N_REP:
-        raise UnsupportedLayout(f"more than {MAX_N_REP} query heads per kv head")
     if q.dtype not in _lib.DTYPE_CODE or q.stride(-1) != 1:
         raise UnsupportedLayout("q must be fp32/fp16/bf16 with a contiguous head_dim")
     for pages in (kv.k_pages, kv.v_pages):
