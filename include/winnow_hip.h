@@ -217,20 +217,23 @@ int wn_dequantize_history(const uint8_t* pages, int64_t page_stride, int64_t hea
                           void* out, int out_dtype, int fast, void* stream);
 
 /* Plan of wn_dense_decode_attention (as wn_decode_plan: requested_splits > 0 gives
- * the reference's cdiv split of max_pages; 0 a balanced plan of persistent waves,
- * pages_per_split = 0). page_dtype WN_BF16 or WN_F16. */
+ * the reference's cdiv split of max_pages; 0 lets the library choose: a balanced
+ * plan of persistent waves, pages_per_split = 0, for WN_BF16 and WN_F16 pages, fixed
+ * splits for WN_F32 pages). */
 int wn_dense_decode_plan(int B, int Hq, int Hkv, int D, int S, int page_dtype, int max_pages,
                          int requested_splits, int* pages_per_split, int* num_splits);
 
 /* Decode attention over unquantized paged K/V (replaces dense_decode_attention,
  * turboquant_kv/packed_attention_triton.py:190-201): pages (P, Hkv, S, D) of
- * page_dtype (bf16 or fp16), the (S, D) rows of one (page, head) contiguous,
+ * page_dtype (bf16, fp16 or fp32), the (S, D) rows of one (page, head) contiguous,
  * strides in bytes; page_table, seq_lens, q, out, the scratch (sized by
  * wn_decode_workspace_bytes with this plan) and the events as for
- * wn_decode_attention. head_dim 64 or 128, n_rep <= 16, S a power of two >= 16, pages
- * and their strides 16-byte aligned. Scores and the value sum carry fp32
- * accuracy (q and the probabilities as 16-bit hi + lo pairs against exact
- * 16-bit K and V). */
+ * wn_decode_attention. head_dim 64 or 128, any n_rep (over 16: virtual kv heads of
+ * <= 16 query heads), S a power of two >= 16, pages and their strides 16-byte
+ * aligned. bf16 / fp16 pages run on the matrix cores with fp32 accuracy (q and the
+ * probabilities as 16-bit hi + lo pairs against exact 16-bit K and V); fp32 pages
+ * on a vector-ALU scan that needs fixed splits (pages_per_split > 0, which
+ * wn_dense_decode_plan returns for them). */
 int wn_dense_decode_attention(
     const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
     const void* k_pages, int64_t k_stride_p, int64_t k_stride_h,

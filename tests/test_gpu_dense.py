@@ -6,8 +6,9 @@ SDPA over contiguous K/V) on the same bf16 / fp16 page values, at the tolerance 
 the packed decode: fp32 output within 2e-3 abs / 1e-3 rel. The case matrix: the
 reference's own test case (test_packed_attention_triton.py:153-173: B 3, Hq 28, Hkv
 4, lengths 33 / 0 / 70, shuffled tables, splits 1, 2, 3), every n_rep class up to
-16, page sizes 16 / 32 / 64, ragged lengths including 0, 1, 15, 16, 17, head_dim 64
-and 128, fp16 pages, bf16 output, long contexts, and the rejections.
+16 and n_rep 17-96 as virtual kv heads, page sizes 16 / 32 / 64, ragged lengths
+including 0, 1, 15, 16, 17, head_dim 64 and 128, fp16 and fp32 pages, bf16 output,
+long contexts, and the rejections.
 """
 from __future__ import annotations
 
@@ -119,12 +120,44 @@ def test_dense_large_scores_stay_finite():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (28, 4), (32, 8), (16, 1)])
+def test_dense_fp32_pages(D, Hq, Hkv):
+    """fp32 pages (the reference's dense_decode_attention takes them,
+    packed_attention_triton.py:190-201) on the vector-ALU scan, fixed splits: the
+    library's plan, one and three splits, ragged lengths including 0."""
+    lens = (0, 1, 17, 333, 1024)
+    kp, vp, table, sl = _pages(80 + Hq + D, lens, Hkv, 16, dtype=torch.float32, D=D)
+    q = torch.randn(len(lens), Hq, 1, D, generator=torch.Generator().manual_seed(81))
+    ref = oa.dense_paged_attention_f64(q, kp, vp, table, sl, D ** -0.5)
+    for splits in (None, 1, 3):
+        print(f"fp32 pages D={D} Hq={Hq} Hkv={Hkv} splits={splits}", flush=True)
+        got = _run(q, kp, vp, table, sl, D ** -0.5, num_splits=splits, out_dtype=torch.float32).cpu()
+        assert torch.allclose(got.double(), ref, atol=ATOL, rtol=RTOL), (got.double() - ref).abs().max()
+        assert bool((got[0] == 0).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("Hq,Hkv", [(34, 2), (40, 2), (64, 2), (96, 1)])
+def test_dense_more_than_sixteen_query_heads(dtype, Hq, Hkv):
+    """n_rep 17, 20, 32 and 96 run as virtual kv heads of <= 16 query heads each
+    (the reference pads its head block to next_pow2(n_rep), packed_attention_triton.py:209)."""
+    lens = (0, 33, 300)
+    kp, vp, table, sl = _pages(90 + Hq, lens, Hkv, 16, dtype=dtype)
+    q = torch.randn(len(lens), Hq, 1, 128, generator=torch.Generator().manual_seed(91))
+    ref = oa.dense_paged_attention_f64(q, kp, vp, table, sl, 0.088)
+    for splits in (None, 2):
+        print(f"dense n_rep={Hq // Hkv} {dtype} splits={splits}", flush=True)
+        got = _run(q, kp, vp, table, sl, 0.088, num_splits=splits, out_dtype=torch.float32).cpu()
+        assert torch.allclose(got.double(), ref, atol=ATOL, rtol=RTOL), (got.double() - ref).abs().max()
+
+
+@pytest.mark.gpu
 def test_dense_rejections():
     from winnow_amd import packed_attention as pa
     kp, vp, table, sl = _pages(61, (20,), 2, 16)
     q = torch.randn(1, 4, 1, 128)
-    with pytest.raises(pa.UnsupportedLayout):        # fp32 pages are not compiled
-        _run(q, kp.float(), vp.float(), table, sl, 0.1)
     with pytest.raises(pa.UnsupportedLayout):        # more than one query token
         _run(torch.randn(1, 4, 2, 128), kp, vp, table, sl, 0.1)
     kp8, vp8, table8, sl8 = _pages(62, (20,), 2, 8)

@@ -365,6 +365,20 @@ WsLayout ws_layout(int B, int Hq, int Hkv, int D, int pages_per_split, int num_s
 // per-split partials stay a few percent of the page bytes.
 static constexpr int64_t kTargetGroups = 4096;
 
+// Fixed splits for the vector-ALU scans: about kTargetGroups work-groups over the
+// (sequence, virtual kv head) units, each split >= 16 pages.
+static void fixed_plan(int B, int units_per_seq, int mp, int* pages_per_split, int* num_splits) {
+  const int64_t units = int64_t(B > 0 ? B : 1) * units_per_seq;
+  int64_t want = (kTargetGroups + units - 1) / units;
+  if (want < 1) want = 1;
+  if (want > mp) want = mp;
+  int64_t pps = (mp + want - 1) / want;
+  if (pps < 16) pps = 16;  // >= 256 tokens at S=16: all four waves of a group busy
+  if (pps > mp) pps = mp;
+  *pages_per_split = int(pps);
+  *num_splits = int((mp + pps - 1) / pps);
+}
+
 extern "C" int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
                               int requested_splits, int* pages_per_split, int* num_splits) {
   using namespace wn;
@@ -389,15 +403,7 @@ extern "C" int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, in
     *num_splits = w;
     return WN_OK;
   }
-  const int64_t units = int64_t(B > 0 ? B : 1) * Hkv;
-  int64_t want = (kTargetGroups + units - 1) / units;
-  if (want < 1) want = 1;
-  if (want > mp) want = mp;
-  int64_t pps = (mp + want - 1) / want;
-  if (pps < 16) pps = 16;  // >= 256 tokens at S=16: all four waves of a group busy
-  if (pps > mp) pps = mp;
-  *pages_per_split = int(pps);
-  *num_splits = int((mp + pps - 1) / pps);
+  fixed_plan(B, Hkv * sk.kvdiv, mp, pages_per_split, num_splits);
   return WN_OK;
 }
 
@@ -604,8 +610,13 @@ extern "C" int wn_dense_decode_plan(int B, int Hq, int Hkv, int D, int S, int pa
     *pages_per_split = (mp + ns - 1) / ns;
     return WN_OK;
   }
+  if (page_dtype == WN_F32) {  // the fp32 scan runs on fixed splits
+    WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "wn_dense_decode_plan: head_dim %d (64, 128)", D);
+    fixed_plan(B, Hkv * valu_groups(Hq / Hkv), mp, pages_per_split, num_splits);
+    return WN_OK;
+  }
   const SplitKernel sk = pick_dense_scan(page_dtype, D);
-  WN_REQUIRE(sk.fn, WN_E_UNSUPPORTED, "wn_dense_decode_plan: page dtype %d (bf16 or fp16), head_dim %d (64, 128)",
+  WN_REQUIRE(sk.fn, WN_E_UNSUPPORTED, "wn_dense_decode_plan: page dtype %d (fp32, bf16 or fp16), head_dim %d (64, 128)",
              page_dtype, D);
   const int w = resident_waves(sk);
   WN_REQUIRE(w > 0, WN_E_LAUNCH, "wn_dense_decode_plan: cannot query the device occupancy");
@@ -627,14 +638,17 @@ extern "C" int wn_dense_decode_attention(
   WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, WN_E_INVALID,
              "dense decode: need B>=0, Hq%%Hkv==0 (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
   const int n_rep = Hq / Hkv;
-  WN_REQUIRE(n_rep <= 16, WN_E_UNSUPPORTED, "dense decode: n_rep=%d > 16 not compiled", n_rep);
   WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "dense decode: head_dim %d not compiled (64, 128)", D);
   WN_REQUIRE(is_pow2(S) && S >= 16, WN_E_UNSUPPORTED, "dense decode: page size %d (a power of two >= 16)", S);
   WN_REQUIRE(q_dtype >= WN_F32 && q_dtype <= WN_BF16 && out_dtype >= WN_F32 && out_dtype <= WN_BF16,
              WN_E_INVALID, "dense decode: dtype codes %d/%d", q_dtype, out_dtype);
-  const SplitKernel sk = pick_dense_scan(page_dtype, D);
-  WN_REQUIRE(sk.fn, WN_E_UNSUPPORTED, "dense decode: page dtype %d (bf16 or fp16)", page_dtype);
+  // more than 16 query heads per kv head: virtual kv heads of n_rep / g each
+  const int g = valu_groups(n_rep), Hkv_s = Hkv * g, n_rep_s = n_rep / g;
+  const SplitKernel sk = page_dtype == WN_F32 ? pick_dense_f32_scan(D, pad_nrep(n_rep_s)) : pick_dense_scan(page_dtype, D);
+  WN_REQUIRE(sk.fn, WN_E_UNSUPPORTED, "dense decode: page dtype %d (fp32, bf16 or fp16)", page_dtype);
   const bool balanced = pages_per_split == 0;
+  WN_REQUIRE(!balanced || sk.rows, WN_E_INVALID,
+             "dense decode: fp32 pages need fixed splits (pages_per_split > 0); ask wn_dense_decode_plan");
   WN_REQUIRE(num_splits > 0 && pages_per_split >= 0 &&
                  (balanced || int64_t(pages_per_split) * num_splits >= int64_t(max_pages)),
              WN_E_INVALID, "dense decode: plan %d x %d does not cover %d pages", num_splits, pages_per_split,
@@ -644,9 +658,10 @@ extern "C" int wn_dense_decode_attention(
   WN_REQUIRE(aligned(k_pages, 16) && aligned(v_pages, 16) && k_stride_p % 16 == 0 && k_stride_h % 16 == 0 &&
                  v_stride_p % 16 == 0 && v_stride_h % 16 == 0,
              WN_E_INVALID, "dense decode: pages need 16-byte aligned bases and strides");
-  WN_REQUIRE(k_stride_h >= int64_t(S) * D * 2 && v_stride_h >= int64_t(S) * D * 2, WN_E_INVALID,
+  const int64_t esz = page_dtype == WN_F32 ? 4 : 2;
+  WN_REQUIRE(k_stride_h >= int64_t(S) * D * esz && v_stride_h >= int64_t(S) * D * esz, WN_E_INVALID,
              "dense decode: head stride smaller than one (S, D) page block");
-  RotFn rot = D == 128 ? pick_rot<128>(pad_nrep(n_rep)) : pick_rot<64>(pad_nrep(n_rep));
+  RotFn rot = D == 128 ? pick_rot<128>(pad_nrep(n_rep_s)) : pick_rot<64>(pad_nrep(n_rep_s));
   WN_REQUIRE(rot, WN_E_UNSUPPORTED, "dense decode: n_rep=%d", n_rep);
 
   const WsLayout lay = ws_layout(B, Hq, Hkv, D, pages_per_split, num_splits);
@@ -659,11 +674,11 @@ extern "C" int wn_dense_decode_attention(
   int2* meta = reinterpret_cast<int2*>(ws + lay.meta);
   // scores in log2 units: q_rot = scale * log2(e) * q, no rotation
   RotArgs ra{q, q_stride_b, q_stride_h, nullptr, reinterpret_cast<float*>(ws + lay.qrot), seq_lens, prefix, meta,
-             float(double(scale) * 1.4426950408889634), B, Hkv, n_rep, q_dtype};
-  hipLaunchKernelGGL(rot, dim3(Hkv, B, 4), dim3(256), 0, st, ra);
+             float(double(scale) * 1.4426950408889634), B, Hkv_s, n_rep_s, q_dtype};
+  hipLaunchKernelGGL(rot, dim3(Hkv_s, B, 4), dim3(256), 0, st, ra);
 
   DecodeArgs da{};
-  da.kvdiv = 1;
+  da.kvdiv = g;
   da.q_rot = ra.q_rot;
   da.k_pages = static_cast<const uint8_t*>(k_pages);
   da.v_pages = static_cast<const uint8_t*>(v_pages);
@@ -679,22 +694,25 @@ extern "C" int wn_dense_decode_attention(
   da.chunk_prefix = prefix;
   da.unit_meta = meta;
   da.B = B;
-  da.Hkv = Hkv;
-  da.n_rep = n_rep;
+  da.Hkv = Hkv_s;
+  da.n_rep = n_rep_s;
   da.log2S = ilog2(S);
   da.pages_per_split = pages_per_split;
   da.num_splits = num_splits;
   da.balanced = balanced ? 1 : 0;
-  da.qrows = pad_nrep(n_rep);
-  const int64_t waves = balanced ? int64_t(num_splits) : int64_t(num_splits) * Hkv * B;
+  da.qrows = pad_nrep(n_rep_s);
+  const int64_t waves = balanced ? int64_t(num_splits) : int64_t(num_splits) * Hkv_s * B;
+  // the MFMA scan numbers its waves across work-groups of sk.wpb waves; the fp32 scan
+  // runs one work-group per (split, virtual kv head, sequence)
+  const dim3 grid = sk.rows ? dim3(unsigned((waves + sk.wpb - 1) / sk.wpb)) : dim3(num_splits, Hkv_s, B);
   if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
-  hipLaunchKernelGGL(sk.fn, dim3(unsigned((waves + sk.wpb - 1) / sk.wpb)), dim3(sk.block), 0, st, da);
+  hipLaunchKernelGGL(sk.fn, grid, dim3(sk.block), 0, st, da);
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
-  MergeArgs ma{da.part_acc, da.part_ml, nullptr, meta, out, out_dtype, Hq, Hkv, n_rep, 1};
+  MergeArgs ma{da.part_acc, da.part_ml, nullptr, meta, out, out_dtype, Hq, Hkv_s, n_rep_s, 1};
   if (D == 128)
-    hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep, Hkv, B), dim3(128), 0, st, ma);
+    hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep_s, Hkv_s, B), dim3(128), 0, st, ma);
   else
-    hipLaunchKernelGGL(merge_kernel<64>, dim3(n_rep, Hkv, B), dim3(64), 0, st, ma);
+    hipLaunchKernelGGL(merge_kernel<64>, dim3(n_rep_s, Hkv_s, B), dim3(64), 0, st, ma);
   return check_launch("wn_dense_decode_attention");
 }

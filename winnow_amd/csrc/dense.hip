@@ -120,8 +120,8 @@ __device__ __forceinline__ void dense_range(const DecodeArgs& a, int b, int kvh,
   }
   const int smask = (1 << a.log2S) - 1;
   const int32_t* trow = a.table + b * a.tsb;
-  const uint8_t* kb = a.k_pages + kvh * a.ksh + LB * g;
-  const uint8_t* vb = a.v_pages + kvh * a.vsh + LB * g;
+  const uint8_t* kb = a.k_pages + (kvh / a.kvdiv) * a.ksh + LB * g;  // virtual kv head -> its kv head
+  const uint8_t* vb = a.v_pages + (kvh / a.kvdiv) * a.vsh + LB * g;
   const int nsub = (t_hi - t_lo + 15) >> 4;
   // page of tile u (clamped to the last tile, which is then read again)
   auto pid_of = [&](int u) { return trow[(t_lo + 16 * min(u, nsub - 1)) >> a.log2S]; };
@@ -323,7 +323,178 @@ __global__ __launch_bounds__(64 * kDenseWpb) void dense_scan_kernel(DecodeArgs a
   }
 }
 
+// fp32 pages (a vector-ALU scan: K and V are not exact in a 16-bit MFMA type). One
+// work-group of four waves per (split, kv head, sequence) on fixed splits, as the
+// packed pages' vector-ALU scan: score phase lane = token (its K row read as 16-byte
+// pieces, NREP heads), online softmax per head in log2 units, value phase D/8 lanes
+// per token row (8 dims each), then the max-stable merge of the four waves into one
+// (acc, m, l) partial. Virtual kv head h reads the pages of kv head h / kvdiv.
+constexpr int kF32Block = 256;
+
+template <int D, int NREP>
+__global__ __launch_bounds__(kF32Block) void dense_f32_kernel(DecodeArgs a) {
+  constexpr int G = D / 8;     // lanes per token row in the value phase
+  constexpr int TPS = 64 / G;  // token rows per value step
+  __shared__ float pw[4][64][NREP];
+  __shared__ int pidl[4][64];
+  __shared__ float red_m[4][NREP], red_l[4][NREP];
+  __shared__ float red_acc[4][NREP][D];
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int S = 1 << a.log2S;
+  const int L = a.seq_lens[b];
+  const int n_pages = (L + S - 1) >> a.log2S;
+  const int page_lo = split * a.pages_per_split;
+  if (page_lo >= n_pages) return;  // block-uniform: this split is past the sequence
+  const int page_hi = min(page_lo + a.pages_per_split, n_pages);
+  const int t_lo = page_lo << a.log2S;
+  const int t_hi = min(page_hi << a.log2S, L);
+  if (split == 0 && tid == 0)
+    a.unit_meta[b * a.Hkv + kvh] =
+        make_int2((b * a.Hkv + kvh) * a.num_splits, (n_pages + a.pages_per_split - 1) / a.pages_per_split);
+  const int kvp = kvh / a.kvdiv;
+  const float* __restrict__ qp = a.q_rot + (int64_t(b) * a.Hkv + kvh) * a.qrows * D;
+  const int32_t* __restrict__ trow = a.table + b * a.tsb;
+  const uint8_t* kbase = a.k_pages + kvp * a.ksh;
+  const uint8_t* vbase = a.v_pages + kvp * a.vsh;
+
+  float m[NREP], l[NREP], acc[NREP][8];
+#pragma unroll
+  for (int h = 0; h < NREP; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
+  }
+  const int tsub = lane / G, dg = lane % G;
+  for (int c0 = t_lo + w * 64; c0 < t_hi; c0 += 4 * 64) {
+    const int t = c0 + lane;
+    const bool valid = t < t_hi;
+    int pid = 0;
+    float s[NREP];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) s[h] = 0.f;
+    if (valid) {
+      pid = trow[t >> a.log2S];
+      const float4* kr = reinterpret_cast<const float4*>(kbase + pid * a.ksp + int64_t(t & (S - 1)) * D * 4);
+#pragma unroll 4
+      for (int d4 = 0; d4 < D / 4; ++d4) {
+        const float4 k = kr[d4];
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) {
+          const float4 qv = reinterpret_cast<const float4*>(qp + h * D)[d4];
+          s[h] = fmaf(qv.x, k.x, fmaf(qv.y, k.y, fmaf(qv.z, k.z, fmaf(qv.w, k.w, s[h]))));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) s[h] = -INFINITY;
+    }
+    wave_lds_sync();  // the previous chunk's value phase has read pw / pidl
+    float alpha[NREP];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+      const float mn = fmaxf(m[h], wave_max(s[h]));  // finite: lane 0 of a chunk is valid
+      alpha[h] = __builtin_amdgcn_exp2f(m[h] - mn);   // 0 on the first chunk (m = -inf)
+      const float pr = valid ? __builtin_amdgcn_exp2f(s[h] - mn) : 0.f;
+      l[h] = l[h] * alpha[h] + wave_sum(pr);
+      m[h] = mn;
+      pw[w][lane][h] = pr;
+    }
+    pidl[w][lane] = pid;
+    wave_lds_sync();
+#pragma unroll
+    for (int h = 0; h < NREP; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[h][i] *= alpha[h];
+#pragma unroll 2
+    for (int j = 0; j < 64 / TPS; ++j) {
+      const int tl = j * TPS + tsub;
+      const int tt = c0 + tl;
+      if (tt < t_hi) {
+        const float4* vr = reinterpret_cast<const float4*>(vbase + pidl[w][tl] * a.vsp +
+                                                           int64_t(tt & (S - 1)) * D * 4 + dg * 32);
+        const float4 v0 = vr[0], v1 = vr[1];
+        const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) {
+          const float wv = pw[w][tl][h];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(wv, vv[i], acc[h][i]);
+        }
+      }
+    }
+  }
+  // token subgroups of a wave share m: plain sums
+#pragma unroll
+  for (int o = G; o < 64; o <<= 1)
+#pragma unroll
+    for (int h = 0; h < NREP; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[h][i] += __shfl_xor(acc[h][i], o, 64);
+  if (lane < G) {
+#pragma unroll
+    for (int h = 0; h < NREP; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) red_acc[w][h][dg * 8 + i] = acc[h][i];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+      red_m[w][h] = m[h];
+      red_l[w][h] = l[h];
+    }
+  }
+  __syncthreads();
+  // max-stable merge of the four waves; a wave that saw no chunk has m = -inf
+  const int64_t row0 = ((int64_t(b) * a.Hkv + kvh) * a.num_splits + split) * a.n_rep;
+  for (int e = tid; e < a.n_rep * D; e += kF32Block) {
+    const int h = e / D, d = e % D;
+    float M = red_m[0][h];
+#pragma unroll
+    for (int ww = 1; ww < 4; ++ww) M = fmaxf(M, red_m[ww][h]);
+    float af = 0.f, lf = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float mw = red_m[ww][h];
+      if (mw != -INFINITY) {
+        const float sc = __builtin_amdgcn_exp2f(mw - M);
+        af = fmaf(sc, red_acc[ww][h][d], af);
+        lf = fmaf(sc, red_l[ww][h], lf);
+      }
+    }
+    a.part_acc[(row0 + h) * D + d] = af;
+    if (d == 0) {
+      a.part_ml[2 * (row0 + h)] = M;
+      a.part_ml[2 * (row0 + h) + 1] = lf;
+    }
+  }
+}
+
+template <int D>
+SplitFn pick_f32_nrep(int nrep) {
+  switch (nrep) {
+    case 1: return dense_f32_kernel<D, 1>;
+    case 2: return dense_f32_kernel<D, 2>;
+    case 4: return dense_f32_kernel<D, 4>;
+    case 8: return dense_f32_kernel<D, 8>;
+    case 16: return dense_f32_kernel<D, 16>;
+  }
+  return nullptr;
+}
+
 }  // namespace
+
+SplitKernel pick_dense_f32_scan(int D, int nrep) {
+  SplitKernel k;
+  k.fn = D == 128 ? pick_f32_nrep<128>(nrep) : D == 64 ? pick_f32_nrep<64>(nrep) : nullptr;
+  if (!k.fn) return SplitKernel{};
+  k.block = kF32Block;
+  k.nrep = nrep;
+  k.log2_units = true;
+  return k;
+}
 
 SplitKernel pick_dense_scan(int page_dtype, int D) {
   SplitKernel k;

@@ -54,6 +54,10 @@ SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep);
 // for another page dtype or head_dim.
 SplitKernel pick_dense_scan(int page_dtype, int D);
 
+// The dense scan for fp32 pages (a vector-ALU scan on fixed splits), nrep query rows
+// per (virtual) kv head (1, 2, 4, 8 or 16), head_dim 64 or 128.
+SplitKernel pick_dense_f32_scan(int D, int nrep);
+
 // The vector-ALU scan for the width pairs decode.hip does not instantiate (any pair
 // of supported widths), nrep query rows per kv head (1, 2, 4, 8 or 16), or nullptr.
 SplitFn pick_split_any(int D, int bw_k, int bw_v, int nrep);
