@@ -107,10 +107,12 @@ def test_dequant_and_dense_entry_points_reject_before_any_launch(lib):
                   None, 0, 0, None)
     dense = ("wn_dense_decode_attention", None, _lib.WN_BF16 if hasattr(_lib, "WN_BF16") else 2, 0, 0,
              None, 0, 0, None, 0, 0)
-    with pytest.raises(_lib.WinnowHipError, match="n_rep"):             # 17 query heads per kv head
-        _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 1, 17, 1, 128, 16, 1, 1.0, 0, 1, None, None, None)
-    with pytest.raises(_lib.WinnowHipError, match="page dtype"):        # fp32 pages
+    with pytest.raises(_lib.WinnowHipError, match="head_dim"):          # head_dim 96 is not compiled
+        _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 1, 4, 1, 96, 16, 1, 1.0, 0, 1, None, None, None)
+    with pytest.raises(_lib.WinnowHipError, match="fixed splits"):      # fp32 pages on a balanced plan
         _lib.call(*dense, 0, None, 0, None, None, 0, None, 0, 1, 4, 1, 128, 16, 1, 1.0, 0, 1, None, None, None)
+    with pytest.raises(_lib.WinnowHipError, match="page dtype"):        # no such dtype code
+        _lib.call(*dense, 7, None, 0, None, None, 0, None, 0, 1, 4, 1, 128, 16, 1, 1.0, 0, 1, None, None, None)
     with pytest.raises(_lib.WinnowHipError, match="page size"):
         _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 1, 4, 1, 128, 8, 1, 1.0, 0, 1, None, None, None)
     # no sequences: a successful no-op
