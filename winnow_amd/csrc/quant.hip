@@ -39,12 +39,20 @@ struct QuantArgs {
   int H, n, log2S, num_pages, max_pages, x_dtype, scatter;
 };
 
-__device__ __forceinline__ uint32_t bucketize(const float* bnd, int bw, float y) {
-  // #{b < y} over the 2^bw - 1 ascending boundaries (torch.bucketize, right=False).
-  uint32_t pos = 0;
-  for (int step = 1 << (bw - 1); step > 0; step >>= 1)
-    if (bnd[pos + step - 1] < y) pos += step;
-  return pos;
+// pos[k] = #{b < y[k]} over the 2^bw - 1 ascending boundaries (torch.bucketize,
+// right=False), for N values at once: the N binary searches advance in lockstep, so
+// each level issues N independent LDS reads instead of one dependent read per value.
+template <int N>
+__device__ __forceinline__ void bucketize_n(const float* bnd, int bw, const float (&y)[N], uint32_t (&pos)[N]) {
+#pragma unroll
+  for (int k = 0; k < N; ++k) pos[k] = 0;
+  for (int step = 1 << (bw - 1); step > 0; step >>= 1) {
+    float b[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) b[k] = bnd[pos[k] + step - 1];
+#pragma unroll
+    for (int k = 0; k < N; ++k) pos[k] += b[k] < y[k] ? step : 0;
+  }
 }
 
 // Byte k of the LSB-first packing of `codes` (D codes of bw bits).
@@ -94,7 +102,8 @@ __device__ __forceinline__ void store_packed8(uint8_t* p, uint64_t v, int bw) {
 //             operands are D/4 consecutive floats of one xs row and its B operands
 //             D/4 consecutive floats of one row of Pi. Output lane l, register i of a
 //             tile is vector l/16 + 4i, column l%16.
-//   codes     each y is rounded once to fp32 and bucketized into the LDS codes cs.
+//   codes     each y is rounded once to fp32 and bucketized into the LDS codes cs
+//             (a lane's D/16 searches in lockstep).
 //   stores    D/8 threads per vector each pack eight codes (bw bytes) and store
 //             them; thread 0 of the vector stores its norm.
 template <int D>
@@ -192,12 +201,19 @@ __global__ __launch_bounds__(kQBlock) void quantize_kernel(QuantArgs a) {
       }
     }
   }
+  {
+    float y[TPW * 4];
+    uint32_t code[TPW * 4];
 #pragma unroll
-  for (int j = 0; j < TPW; ++j)
+    for (int j = 0; j < TPW; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      cs[(lane >> 4) + 4 * i][w * KS + 16 * j + (lane & 15)] =
-          uint8_t(bucketize(bnd, sd.bw, float(acc[j][0][i] + acc[j][1][i])));
+      for (int i = 0; i < 4; ++i) y[4 * j + i] = float(acc[j][0][i] + acc[j][1][i]);
+    bucketize_n(bnd, sd.bw, y, code);
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cs[(lane >> 4) + 4 * i][w * KS + 16 * j + (lane & 15)] = uint8_t(code[4 * j + i]);
+  }
   if (tid < kVecPerBlock) {
     // byte offset of the vector's packed row and element offset of its norm; -1: the
     // vector is past the end, or (scatter) its position lies outside the page table
