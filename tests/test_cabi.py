@@ -90,6 +90,24 @@ def test_argument_errors_are_reported_not_fatal(lib):
     assert lib.wn_last_error() == b""
 
 
+def test_head_dims_compiled_and_refused(lib):
+    """Powers of two 16 .. 256 pass the head_dim check (the next check, a null operand,
+    reports); 8, 96 and 512 are refused with the compiled list; bf16 dense pages at a
+    head_dim without the matrix-core scan need fixed splits."""
+    from winnow_amd import _lib
+    for D in (16, 32, 64, 128, 256):
+        with pytest.raises(_lib.WinnowHipError, match="null operand"):
+            _lib.call("wn_quantize", None, 0, 1, D, None, None, 4, D, None, None, None)
+    for D in (8, 96, 512):
+        with pytest.raises(_lib.WinnowHipError, match="16, 32, 64, 128, 256"):
+            _lib.call("wn_quantize", None, 0, 1, D, None, None, 4, D, None, None, None)
+    dense = ("wn_dense_decode_attention", None, 2, 0, 0, None, 0, 0, None, 0, 0)
+    with pytest.raises(_lib.WinnowHipError, match="fixed splits"):
+        _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 1, 4, 1, 256, 16, 1, 1.0, 0, 1, None, None, None)
+    with pytest.raises(_lib.WinnowHipError, match="16, 32, 64, 128, 256"):
+        _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 1, 4, 1, 512, 16, 1, 1.0, 0, 1, None, None, None)
+
+
 def test_dequant_and_dense_entry_points_reject_before_any_launch(lib):
     """Argument errors of the newer entry points come back as codes with a message,
     before anything touches a device (no GPU here)."""

@@ -38,8 +38,18 @@ def _run(cmd):
     return proc
 
 
+# Sources that take longest to compile (many kernel instantiations) start first.
+_SLOW_FIRST = ("decode_split_any256", "decode_rows", "decode_split_any128", "decode_split_any64",
+               "decode_split_any16", "decode_split_any32", "decode")
+
+
 def sources():
-    return sorted(CSRC.glob("*.hip"))
+    def rank(p):
+        for i, prefix in enumerate(_SLOW_FIRST):
+            if p.stem.startswith(prefix):
+                return i
+        return len(_SLOW_FIRST)
+    return sorted(CSRC.glob("*.hip"), key=lambda p: (rank(p), p.name))
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> Path:

@@ -64,12 +64,15 @@ __device__ void chunk_prefix_block(const int32_t* seq_lens, int B, int32_t* pref
   if (tid == 0) prefix[B] = carry;
 }
 
+// Output-dim blocks of the rotation: quarters up to head_dim 128, 32 dims above.
+constexpr int rot_blocks(int D) { return D <= 128 ? 4 : D / 32; }
+
 // q_rot[b, kvh, h, j] = scale * sum_d q[b, kvh*n_rep + h, d] Pi_K[j, d] for output dims
-// j in quarter blockIdx.z of [0, D) (zero rows for h >= n_rep). The quarter's 32 rows
+// j in block blockIdx.z of rot_blocks(D) (zero rows for h >= n_rep). The block's rows
 // of Pi_K are staged in LDS with a padded stride (thread j reads row j: banks j + d).
 template <int D, int NREP>
 __global__ __launch_bounds__(256) void rotate_q_kernel(RotArgs a) {
-  constexpr int LDP = D + 1, JQ = D / 4;
+  constexpr int LDP = D + 1, JQ = D / rot_blocks(D);
   __shared__ float pis[JQ * LDP];
   __shared__ float qs[NREP][D];
   const int kvh = blockIdx.x, b = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
@@ -127,9 +130,10 @@ constexpr int kMergeBatch = 32;  // partial rows whose loads are in flight toget
 // w_s = exp(m_s - max m) (2^(m_s - max m) for log2-unit partials), zero when no
 // key was seen (packed_attention_triton.py:137-159 plus :261).
 //
-// One work-group of D threads per (query head h, kv head, sequence). Thread d
-// first issues the loads of column d of Pi_V, so that they travel together with
-// the partials' (one round trip for both). The partials are taken 64 at a time:
+// One work-group of max(D, 64) threads per (query head h, kv head, sequence); thread
+// d < D owns output dim d. Up to head_dim 128 thread d first issues the loads of
+// column d of Pi_V, so that they travel together with the partials' (one round trip
+// for both); at 256 the column is read during the product instead. The partials are taken 64 at a time:
 // lane k of each wave loads (m, l) of partial k, the wave reduces the maximum,
 // and lane k forms the weight of partial k with one exponential; thread d then
 // sums its dim of the acc rows against those weights (read from the lanes that
@@ -140,12 +144,17 @@ constexpr int kMergeBatch = 32;  // partial rows whose loads are in flight toget
 // holding tokens; balanced: rows w + b*Hkv + kvh of the waves w that touched the
 // group); a group without keys has n = 0 and an output row of zeros.
 template <int D>
-__global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
+constexpr int merge_threads() { return D < 64 ? 64 : D; }
+
+template <int D>
+__global__ __launch_bounds__(merge_threads<D>()) void merge_kernel(MergeArgs a) {
+  constexpr bool kPreload = D <= 128;  // Pi_V column in registers
   __shared__ float av[D];
-  const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
-  const int lane = d & 63;
-  float pc[D];  // column d of Pi_V (none: no output rotation, dense pages)
-  if (a.pi_v) {
+  const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int d = min(tid, D - 1);  // threads past D (D < 64) only help the wave reductions
+  float pc[kPreload ? D : 1];     // column d of Pi_V (none: no output rotation, dense pages)
+  if (kPreload && a.pi_v) {
 #pragma unroll
     for (int k = 0; k < D; ++k) pc[k] = a.pi_v[k * D + d];
   }
@@ -189,17 +198,36 @@ __global__ __launch_bounds__(D) void merge_kernel(MergeArgs a) {
       }
     }
   }
-  av[d] = (n > 0 && den > 0.f) ? num / fmaxf(den, 1e-30f) : 0.f;
+  if (tid < D) av[d] = (n > 0 && den > 0.f) ? num / fmaxf(den, 1e-30f) : 0.f;
   __syncthreads();
+  if (tid >= D) return;
   // out_j = sum_k a_k Pi_V[k, j]; (a / l) Pi_V == (a Pi_V) / l up to rounding
   float o = 0.f;
   if (a.pi_v) {
+    if constexpr (kPreload) {
 #pragma unroll
-    for (int k = 0; k < D; ++k) o = fmaf(av[k], pc[k], o);
+      for (int k = 0; k < D; ++k) o = fmaf(av[k], pc[k], o);
+    } else {
+#pragma unroll 16
+      for (int k = 0; k < D; ++k) o = fmaf(av[k], a.pi_v[k * D + d], o);
+    }
   } else {
     o = av[d];
   }
   store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + d, a.out_dtype, o);
+}
+
+using MergeFn = void (*)(MergeArgs);
+
+// The merge for head_dim D and its work-group size.
+void launch_merge(int D, dim3 grid, hipStream_t st, const MergeArgs& ma) {
+  switch (D) {
+    case 16: hipLaunchKernelGGL(merge_kernel<16>, grid, dim3(merge_threads<16>()), 0, st, ma); break;
+    case 32: hipLaunchKernelGGL(merge_kernel<32>, grid, dim3(merge_threads<32>()), 0, st, ma); break;
+    case 64: hipLaunchKernelGGL(merge_kernel<64>, grid, dim3(merge_threads<64>()), 0, st, ma); break;
+    case 128: hipLaunchKernelGGL(merge_kernel<128>, grid, dim3(merge_threads<128>()), 0, st, ma); break;
+    case 256: hipLaunchKernelGGL(merge_kernel<256>, grid, dim3(merge_threads<256>()), 0, st, ma); break;
+  }
 }
 
 using RotFn = void (*)(RotArgs);
@@ -236,6 +264,19 @@ RotFn pick_rot(int nrep) {
   }
   return nullptr;
 }
+
+RotFn pick_rot_d(int D, int nrep) {
+  switch (D) {
+    case 16: return pick_rot<16>(nrep);
+    case 32: return pick_rot<32>(nrep);
+    case 64: return pick_rot<64>(nrep);
+    case 128: return pick_rot<128>(nrep);
+    case 256: return pick_rot<256>(nrep);
+  }
+  return nullptr;
+}
+
+int rot_blocks_d(int D) { return D <= 128 ? 4 : D / 32; }
 
 // Page-scan kernel preference, read once from WN_DECODE_SCAN: "rows" (default)
 // uses the row-per-lane matrix-core scan where it applies, "valu" always the
@@ -292,7 +333,9 @@ SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v) {
     const int g = valu_groups(n_rep);
     const int nrp = pad_nrep(n_rep / g);
     sk = SplitKernel{};
-    sk.fn = D == 128 ? pick_split<128>(bw_k, bw_v, nrp) : pick_split<64>(bw_k, bw_v, nrp);
+    sk.fn = D == 128 ? pick_split<128>(bw_k, bw_v, nrp)
+            : D == 64 ? pick_split<64>(bw_k, bw_v, nrp)
+                      : pick_split_any(D, bw_k, bw_v, nrp);  // 16, 32, 256: every pair there
     sk.block = kBlock;
     sk.nrep = nrp;
     sk.kvdiv = g;
@@ -429,7 +472,7 @@ extern "C" int wn_decode_attention(
   WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, WN_E_INVALID,
              "decode: need B>=0, Hq%%Hkv==0 (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
   const int n_rep = Hq / Hkv;
-  WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "decode: head_dim %d not compiled (64, 128)", D);
+  WN_REQUIRE(valid_head_dim(D), WN_E_UNSUPPORTED, "decode: head_dim %d not compiled (16, 32, 64, 128, 256)", D);
   WN_REQUIRE(valid_bw(bw_k) && valid_bw(bw_v), WN_E_INVALID, "decode: bit widths %d/%d", bw_k, bw_v);
   WN_REQUIRE(is_pow2(S), WN_E_INVALID, "decode: page size %d is not a power of two", S);
   WN_REQUIRE(q_dtype >= WN_F32 && q_dtype <= WN_BF16 && out_dtype >= WN_F32 && out_dtype <= WN_BF16,
@@ -454,7 +497,7 @@ extern "C" int wn_decode_attention(
   WN_REQUIRE(aligned(pi_k, 16) && aligned(pi_v, 4), WN_E_INVALID, "decode: rotation alignment");
 
   const SplitKernel sk = choose_scan(Hq, Hkv, D, S, bw_k, bw_v);
-  RotFn rot = D == 128 ? pick_rot<128>(max(sk.nrep, 1)) : pick_rot<64>(max(sk.nrep, 1));
+  RotFn rot = pick_rot_d(D, max(sk.nrep, 1));
   WN_REQUIRE(sk.fn && rot, WN_E_UNSUPPORTED, "decode: (D=%d, bw_k=%d, bw_v=%d) not compiled", D, bw_k,
              bw_v);
   WN_REQUIRE(!balanced || sk.rows, WN_E_INVALID,
@@ -475,7 +518,7 @@ extern "C" int wn_decode_attention(
   const int Hkv_s = Hkv * sk.kvdiv, n_rep_s = n_rep / sk.kvdiv;
   RotArgs ra{q, q_stride_b, q_stride_h, pi_k, reinterpret_cast<float*>(ws + lay.qrot), seq_lens, prefix, meta,
              q_scale, B, Hkv_s, n_rep_s, q_dtype};
-  hipLaunchKernelGGL(rot, dim3(Hkv_s, B, 4), dim3(256), 0, st, ra);
+  hipLaunchKernelGGL(rot, dim3(Hkv_s, B, rot_blocks_d(D)), dim3(256), 0, st, ra);
 
   DecodeArgs da;
   da.q_rot = ra.q_rot;
@@ -518,10 +561,7 @@ extern "C" int wn_decode_attention(
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
   MergeArgs ma{da.part_acc, da.part_ml, pi_v, meta, out, out_dtype, Hq, Hkv_s, n_rep_s, sk.log2_units ? 1 : 0};
-  if (D == 128)
-    hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep_s, Hkv_s, B), dim3(128), 0, st, ma);
-  else
-    hipLaunchKernelGGL(merge_kernel<64>, dim3(n_rep_s, Hkv_s, B), dim3(64), 0, st, ma);
+  launch_merge(D, dim3(n_rep_s, Hkv_s, B), st, ma);
   return check_launch("wn_decode_attention");
 }
 
@@ -610,8 +650,10 @@ extern "C" int wn_dense_decode_plan(int B, int Hq, int Hkv, int D, int S, int pa
     *pages_per_split = (mp + ns - 1) / ns;
     return WN_OK;
   }
-  if (page_dtype == WN_F32) {  // the fp32 scan runs on fixed splits
-    WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "wn_dense_decode_plan: head_dim %d (64, 128)", D);
+  WN_REQUIRE(valid_head_dim(D), WN_E_UNSUPPORTED, "wn_dense_decode_plan: head_dim %d (16, 32, 64, 128, 256)", D);
+  if (page_dtype == WN_F32 || (D != 64 && D != 128)) {  // the vector-ALU scan runs on fixed splits
+    WN_REQUIRE(page_dtype >= WN_F32 && page_dtype <= WN_BF16, WN_E_UNSUPPORTED,
+               "wn_dense_decode_plan: page dtype %d (fp32, bf16 or fp16)", page_dtype);
     fixed_plan(B, Hkv * valu_groups(Hq / Hkv), mp, pages_per_split, num_splits);
     return WN_OK;
   }
@@ -638,17 +680,22 @@ extern "C" int wn_dense_decode_attention(
   WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, WN_E_INVALID,
              "dense decode: need B>=0, Hq%%Hkv==0 (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
   const int n_rep = Hq / Hkv;
-  WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "dense decode: head_dim %d not compiled (64, 128)", D);
+  WN_REQUIRE(valid_head_dim(D), WN_E_UNSUPPORTED, "dense decode: head_dim %d not compiled (16, 32, 64, 128, 256)",
+             D);
   WN_REQUIRE(is_pow2(S) && S >= 16, WN_E_UNSUPPORTED, "dense decode: page size %d (a power of two >= 16)", S);
   WN_REQUIRE(q_dtype >= WN_F32 && q_dtype <= WN_BF16 && out_dtype >= WN_F32 && out_dtype <= WN_BF16,
              WN_E_INVALID, "dense decode: dtype codes %d/%d", q_dtype, out_dtype);
   // more than 16 query heads per kv head: virtual kv heads of n_rep / g each
   const int g = valu_groups(n_rep), Hkv_s = Hkv * g, n_rep_s = n_rep / g;
-  const SplitKernel sk = page_dtype == WN_F32 ? pick_dense_f32_scan(D, pad_nrep(n_rep_s)) : pick_dense_scan(page_dtype, D);
+  // the MFMA scan for bf16/fp16 pages at head_dim 64 and 128, the vector-ALU scan otherwise
+  const bool valu = page_dtype == WN_F32 || (D != 64 && D != 128);
+  const SplitKernel sk =
+      valu ? pick_dense_valu_scan(page_dtype, D, pad_nrep(n_rep_s)) : pick_dense_scan(page_dtype, D);
   WN_REQUIRE(sk.fn, WN_E_UNSUPPORTED, "dense decode: page dtype %d (fp32, bf16 or fp16)", page_dtype);
   const bool balanced = pages_per_split == 0;
   WN_REQUIRE(!balanced || sk.rows, WN_E_INVALID,
-             "dense decode: fp32 pages need fixed splits (pages_per_split > 0); ask wn_dense_decode_plan");
+             "dense decode: fp32 pages and head_dim %d need fixed splits (pages_per_split > 0); ask "
+             "wn_dense_decode_plan", D);
   WN_REQUIRE(num_splits > 0 && pages_per_split >= 0 &&
                  (balanced || int64_t(pages_per_split) * num_splits >= int64_t(max_pages)),
              WN_E_INVALID, "dense decode: plan %d x %d does not cover %d pages", num_splits, pages_per_split,
@@ -661,7 +708,7 @@ extern "C" int wn_dense_decode_attention(
   const int64_t esz = page_dtype == WN_F32 ? 4 : 2;
   WN_REQUIRE(k_stride_h >= int64_t(S) * D * esz && v_stride_h >= int64_t(S) * D * esz, WN_E_INVALID,
              "dense decode: head stride smaller than one (S, D) page block");
-  RotFn rot = D == 128 ? pick_rot<128>(pad_nrep(n_rep_s)) : pick_rot<64>(pad_nrep(n_rep_s));
+  RotFn rot = pick_rot_d(D, pad_nrep(n_rep_s));
   WN_REQUIRE(rot, WN_E_UNSUPPORTED, "dense decode: n_rep=%d", n_rep);
 
   const WsLayout lay = ws_layout(B, Hq, Hkv, D, pages_per_split, num_splits);
@@ -675,7 +722,7 @@ extern "C" int wn_dense_decode_attention(
   // scores in log2 units: q_rot = scale * log2(e) * q, no rotation
   RotArgs ra{q, q_stride_b, q_stride_h, nullptr, reinterpret_cast<float*>(ws + lay.qrot), seq_lens, prefix, meta,
              float(double(scale) * 1.4426950408889634), B, Hkv_s, n_rep_s, q_dtype};
-  hipLaunchKernelGGL(rot, dim3(Hkv_s, B, 4), dim3(256), 0, st, ra);
+  hipLaunchKernelGGL(rot, dim3(Hkv_s, B, rot_blocks_d(D)), dim3(256), 0, st, ra);
 
   DecodeArgs da{};
   da.kvdiv = g;
@@ -710,9 +757,6 @@ extern "C" int wn_dense_decode_attention(
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
   MergeArgs ma{da.part_acc, da.part_ml, nullptr, meta, out, out_dtype, Hq, Hkv_s, n_rep_s, 1};
-  if (D == 128)
-    hipLaunchKernelGGL(merge_kernel<128>, dim3(n_rep_s, Hkv_s, B), dim3(128), 0, st, ma);
-  else
-    hipLaunchKernelGGL(merge_kernel<64>, dim3(n_rep_s, Hkv_s, B), dim3(64), 0, st, ma);
+  launch_merge(D, dim3(n_rep_s, Hkv_s, B), st, ma);
   return check_launch("wn_dense_decode_attention");
 }

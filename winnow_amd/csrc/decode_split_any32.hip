@@ -1,0 +1,11 @@
+// The vector-ALU page scan (wn_split.h) at head_dim 32 for every pair of supported
+// widths (2, 3, 4, 5, 6, 8 bits for K and for V): this head_dim has no tuned
+// kernel, and the reference kernel takes any power-of-two head_dim >= 16
+// (packed_attention_triton.py:160-172) and any pair per call (:247).
+#include "wn_split_any.h"
+
+namespace wn {
+
+SplitFn pick_split_any_d32(int bw_k, int bw_v, int nrep) { return any_for<32>(bw_k, bw_v, nrep); }
+
+}  // namespace wn

@@ -2,7 +2,7 @@
 // widths (2, 3, 4, 5, 6, 8 bits for K and for V) that decode.hip does not
 // instantiate. These pairs have no tuned kernel; the reference kernel takes any
 // pair per call (packed_attention_triton.py:247). One source file per head_dim so
-// that the two compile beside each other.
+// that they compile beside each other.
 #include "wn_split_any.h"
 
 namespace wn {

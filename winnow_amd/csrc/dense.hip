@@ -323,16 +323,31 @@ __global__ __launch_bounds__(64 * kDenseWpb) void dense_scan_kernel(DecodeArgs a
   }
 }
 
-// fp32 pages (a vector-ALU scan: K and V are not exact in a 16-bit MFMA type). One
-// work-group of four waves per (split, kv head, sequence) on fixed splits, as the
-// packed pages' vector-ALU scan: score phase lane = token (its K row read as 16-byte
-// pieces, NREP heads), online softmax per head in log2 units, value phase D/8 lanes
-// per token row (8 dims each), then the max-stable merge of the four waves into one
-// (acc, m, l) partial. Virtual kv head h reads the pages of kv head h / kvdiv.
+// The vector-ALU dense scan: fp32 pages (K and V are not exact in a 16-bit MFMA
+// type) at every head_dim, and bf16/fp16 pages at the head dims the MFMA scan does
+// not take (16, 32, 256). One work-group of four waves per (split, kv head,
+// sequence) on fixed splits, as the packed pages' vector-ALU scan: score phase lane =
+// token (its K row read 4 elements at a time, NREP heads), online softmax per head in
+// log2 units, value phase D/8 lanes per token row (8 dims each), then the max-stable
+// merge of the four waves into one (acc, m, l) partial. Virtual kv head h reads the
+// pages of kv head h / kvdiv.
 constexpr int kF32Block = 256;
 
-template <int D, int NREP>
-__global__ __launch_bounds__(kF32Block) void dense_f32_kernel(DecodeArgs a) {
+// Elements 4 i .. 4 i + 3 of a page row of dtype DT (WN_F32, WN_F16, WN_BF16).
+template <int DT>
+__device__ __forceinline__ float4 row4(const uint8_t* row, int i) {
+  if constexpr (DT == WN_F32) {
+    return reinterpret_cast<const float4*>(row)[i];
+  } else {
+    const uint2 x = reinterpret_cast<const uint2*>(row)[i];
+    auto cv = [](uint32_t h) { return DT == WN_BF16 ? bf16_to_f32(uint16_t(h)) : f16_to_f32(uint16_t(h)); };
+    return make_float4(cv(x.x & 0xffffu), cv(x.x >> 16), cv(x.y & 0xffffu), cv(x.y >> 16));
+  }
+}
+
+template <int D, int NREP, int DT>
+__global__ __launch_bounds__(kF32Block) void dense_valu_kernel(DecodeArgs a) {
+  constexpr int ESZ = DT == WN_F32 ? 4 : 2;  // bytes per element
   constexpr int G = D / 8;     // lanes per token row in the value phase
   constexpr int TPS = 64 / G;  // token rows per value step
   __shared__ float pw[4][64][NREP];
@@ -377,10 +392,10 @@ __global__ __launch_bounds__(kF32Block) void dense_f32_kernel(DecodeArgs a) {
     for (int h = 0; h < NREP; ++h) s[h] = 0.f;
     if (valid) {
       pid = trow[t >> a.log2S];
-      const float4* kr = reinterpret_cast<const float4*>(kbase + pid * a.ksp + int64_t(t & (S - 1)) * D * 4);
+      const uint8_t* kr = kbase + pid * a.ksp + int64_t(t & (S - 1)) * D * ESZ;
 #pragma unroll 4
       for (int d4 = 0; d4 < D / 4; ++d4) {
-        const float4 k = kr[d4];
+        const float4 k = row4<DT>(kr, d4);
 #pragma unroll
         for (int h = 0; h < NREP; ++h) {
           const float4 qv = reinterpret_cast<const float4*>(qp + h * D)[d4];
@@ -413,9 +428,8 @@ __global__ __launch_bounds__(kF32Block) void dense_f32_kernel(DecodeArgs a) {
       const int tl = j * TPS + tsub;
       const int tt = c0 + tl;
       if (tt < t_hi) {
-        const float4* vr = reinterpret_cast<const float4*>(vbase + pidl[w][tl] * a.vsp +
-                                                           int64_t(tt & (S - 1)) * D * 4 + dg * 32);
-        const float4 v0 = vr[0], v1 = vr[1];
+        const uint8_t* vr = vbase + pidl[w][tl] * a.vsp + int64_t(tt & (S - 1)) * D * ESZ + dg * 8 * ESZ;
+        const float4 v0 = row4<DT>(vr, 0), v1 = row4<DT>(vr, 1);
         const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
         for (int h = 0; h < NREP; ++h) {
@@ -472,23 +486,40 @@ __global__ __launch_bounds__(kF32Block) void dense_f32_kernel(DecodeArgs a) {
   }
 }
 
-template <int D>
-SplitFn pick_f32_nrep(int nrep) {
+template <int D, int DT>
+SplitFn pick_valu_nrep(int nrep) {
   switch (nrep) {
-    case 1: return dense_f32_kernel<D, 1>;
-    case 2: return dense_f32_kernel<D, 2>;
-    case 4: return dense_f32_kernel<D, 4>;
-    case 8: return dense_f32_kernel<D, 8>;
-    case 16: return dense_f32_kernel<D, 16>;
+    case 1: return dense_valu_kernel<D, 1, DT>;
+    case 2: return dense_valu_kernel<D, 2, DT>;
+    case 4: return dense_valu_kernel<D, 4, DT>;
+    case 8: return dense_valu_kernel<D, 8, DT>;
+    case 16: return dense_valu_kernel<D, 16, DT>;
+  }
+  return nullptr;
+}
+
+// fp32 pages at every head_dim; bf16/fp16 only where the MFMA scan does not run
+template <int D>
+SplitFn pick_valu_dtype(int page_dtype, int nrep) {
+  if (page_dtype == WN_F32) return pick_valu_nrep<D, WN_F32>(nrep);
+  if constexpr (D != 64 && D != 128) {
+    if (page_dtype == WN_BF16) return pick_valu_nrep<D, WN_BF16>(nrep);
+    if (page_dtype == WN_F16) return pick_valu_nrep<D, WN_F16>(nrep);
   }
   return nullptr;
 }
 
 }  // namespace
 
-SplitKernel pick_dense_f32_scan(int D, int nrep) {
+SplitKernel pick_dense_valu_scan(int page_dtype, int D, int nrep) {
   SplitKernel k;
-  k.fn = D == 128 ? pick_f32_nrep<128>(nrep) : D == 64 ? pick_f32_nrep<64>(nrep) : nullptr;
+  switch (D) {
+    case 16: k.fn = pick_valu_dtype<16>(page_dtype, nrep); break;
+    case 32: k.fn = pick_valu_dtype<32>(page_dtype, nrep); break;
+    case 64: k.fn = pick_valu_dtype<64>(page_dtype, nrep); break;
+    case 128: k.fn = pick_valu_dtype<128>(page_dtype, nrep); break;
+    case 256: k.fn = pick_valu_dtype<256>(page_dtype, nrep); break;
+  }
   if (!k.fn) return SplitKernel{};
   k.block = kF32Block;
   k.nrep = nrep;

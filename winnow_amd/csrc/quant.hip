@@ -3,7 +3,9 @@
 //
 // quantize (turboquant_kv/cache.py:108-115):
 //   n = max(||x||_2, 1e-10);  y = (x / n) Pi^T;  code = #{boundaries < y}
-// Each wave handles four vectors at once. The squared norm and the rotation are
+// A work-group quantizes sixteen vectors (quantize_kernel on the float64 matrix
+// cores at head_dim 64 and 128, quantize_any_kernel on the vector ALU at 16, 32 and
+// 256). The squared norm and the rotation are
 // accumulated in float64 from exact fp32 inputs and rounded once to fp32, and
 // x / n is the correctly rounded fp32 quotient, so every code is the bucket of
 // the correctly rounded fp32 y; an fp32 GEMM elsewhere can differ from it only
@@ -259,6 +261,127 @@ __global__ __launch_bounds__(kQBlock) void quantize_kernel(QuantArgs a) {
   }
 }
 
+// The same computation for the head dims without the matrix-core kernel (16, 32,
+// 256), on the vector ALU: a work-group quantizes sixteen vectors; norms as above
+// (float64 sums of squares, x / n rounded once to fp32 into LDS), then thread j
+// forms output dims j, j + 256, ... of every vector as float64 dot products with the
+// rows of Pi (each product exact, the sum in float64, rounded once to fp32),
+// bucketizes them into the LDS codes, and the store phase packs and scatters as
+// quantize_kernel does.
+template <int D>
+__global__ __launch_bounds__(kQBlock) void quantize_any_kernel(QuantArgs a) {
+  constexpr int TPV = D / 8;  // store threads per vector (eight codes each)
+  __shared__ float bnd[255];
+  __shared__ float xs[kVecPerBlock][D];
+  __shared__ uint8_t cs[kVecPerBlock][D];
+  __shared__ float nrms[kVecPerBlock];
+  __shared__ double ssq[kVecPerBlock][16];
+  __shared__ int64_t rowoff[kVecPerBlock];
+  __shared__ int64_t nrmoff[kVecPerBlock];
+
+  const QuantSide& sd = a.side[blockIdx.y];
+  const int tid = threadIdx.x;
+  const int nb = (1 << sd.bw) - 1;
+  const int64_t v0 = int64_t(blockIdx.x) * kVecPerBlock;
+  if (v0 >= a.total) return;  // block-uniform
+  for (int i = tid; i < nb; i += kQBlock) bnd[i] = sd.bnd[i];
+  // x into LDS as fp32 (zeros past the end)
+  for (int e = tid; e < kVecPerBlock * D; e += kQBlock) {
+    const int vl = e / D, dd = e % D;
+    const int64_t v = v0 + vl;
+    float x = 0.f;
+    if (v < a.total) {
+      const int i = int(v % a.n);
+      const int h = int((v / a.n) % a.H);
+      const int b = int(v / (int64_t(a.n) * a.H));
+      x = load_elem(sd.x, b * sd.sb + h * sd.sh + i * sd.sn + dd, a.x_dtype);
+    }
+    xs[vl][dd] = x;
+  }
+  __syncthreads();
+  // squared norms: sixteen threads per vector, D/16 elements each, float64
+  {
+    const int vl = tid >> 4, part = tid & 15;
+    double ss = 0.0;
+    for (int k = part; k < D; k += 16) ss = fma(double(xs[vl][k]), double(xs[vl][k]), ss);
+    ssq[vl][part] = ss;
+  }
+  __syncthreads();
+  if (tid < kVecPerBlock) {
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ss += ssq[tid][k];
+    nrms[tid] = fmaxf(float(sqrt(ss)), 1e-10f);
+  }
+  __syncthreads();
+  for (int e = tid; e < kVecPerBlock * D; e += kQBlock) {
+    const int vl = e / D, dd = e % D;
+    xs[vl][dd] = float(double(xs[vl][dd]) / double(nrms[vl]));
+  }
+  __syncthreads();
+  // rotation and codes: thread j, output dims j, j + kQBlock, ...
+  for (int j = tid; j < D; j += kQBlock) {
+    const float* prow = sd.pi + int64_t(j) * D;
+    double y[kVecPerBlock];
+#pragma unroll
+    for (int v = 0; v < kVecPerBlock; ++v) y[v] = 0.0;
+    for (int dd = 0; dd < D; ++dd) {
+      const double pe = double(prow[dd]);
+#pragma unroll
+      for (int v = 0; v < kVecPerBlock; ++v) y[v] = fma(double(xs[v][dd]), pe, y[v]);
+    }
+    float yf[kVecPerBlock];
+    uint32_t code[kVecPerBlock];
+#pragma unroll
+    for (int v = 0; v < kVecPerBlock; ++v) yf[v] = float(y[v]);
+    bucketize_n(bnd, sd.bw, yf, code);
+#pragma unroll
+    for (int v = 0; v < kVecPerBlock; ++v) cs[v][j] = uint8_t(code[v]);
+  }
+  if (tid < kVecPerBlock) {
+    const int64_t v = v0 + tid;
+    int64_t ro = -1, no = 0;
+    if (v < a.total) {
+      const int h = int((v / a.n) % a.H);
+      if (!a.scatter) {
+        ro = v * D;
+        no = v;
+      } else {
+        const int b = int(v / (int64_t(a.n) * a.H));
+        const int pos = a.start_pos[b] + int(v % a.n), col = pos >> a.log2S;
+        const int pid = (pos >= 0 && col < a.max_pages) ? a.table[b * a.tsb + col] : -1;
+        if (pid >= 0 && pid < a.num_pages) {
+          const int64_t slot = pos & ((1 << a.log2S) - 1);
+          ro = pid * sd.psp + h * sd.psh + slot * (D * sd.bw / 8);
+          no = pid * sd.nsp + h * sd.nsh + slot;
+        }
+      }
+    }
+    rowoff[tid] = ro;
+    nrmoff[tid] = no;
+  }
+  __syncthreads();
+  for (int e = tid; e < kVecPerBlock * TPV; e += kQBlock) {
+    const int vl = e / TPV, part = e % TPV;
+    const int64_t ro = rowoff[vl];
+    if (ro < 0) continue;
+    const uint8_t* c = &cs[vl][8 * part];
+    if (a.scatter) {
+      uint64_t pk = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) pk |= uint64_t(c[k]) << (sd.bw * k);
+      store_packed8(sd.pages + ro + int64_t(part) * sd.bw, pk, sd.bw);
+      if (part == 0) sd.norms[nrmoff[vl]] = f32_to_f16(nrms[vl]);
+    } else {
+      uint64_t cw = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) cw |= uint64_t(c[k]) << (8 * k);
+      *reinterpret_cast<uint2*>(sd.codes_out + ro + 8 * part) = make_uint2(uint32_t(cw), uint32_t(cw >> 32));
+      if (part == 0) sd.norms_out[nrmoff[vl]] = nrms[vl];
+    }
+  }
+}
+
 __global__ void pack_kernel(const uint8_t* codes, int64_t rows, int D, int bw, uint8_t* out) {
   const int NB = D * bw / 8;
   const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -306,10 +429,13 @@ static int launch_quantize(QuantArgs& a, int sides, int D, hipStream_t st, const
   if (a.total == 0) return WN_OK;
   dim3 grid(unsigned((a.total + kVecPerBlock - 1) / kVecPerBlock), sides);
   if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
-  if (D == 128)
-    hipLaunchKernelGGL(quantize_kernel<128>, grid, dim3(kQBlock), 0, st, a);
-  else
-    hipLaunchKernelGGL(quantize_kernel<64>, grid, dim3(kQBlock), 0, st, a);
+  switch (D) {
+    case 16: hipLaunchKernelGGL(quantize_any_kernel<16>, grid, dim3(kQBlock), 0, st, a); break;
+    case 32: hipLaunchKernelGGL(quantize_any_kernel<32>, grid, dim3(kQBlock), 0, st, a); break;
+    case 64: hipLaunchKernelGGL(quantize_kernel<64>, grid, dim3(kQBlock), 0, st, a); break;
+    case 128: hipLaunchKernelGGL(quantize_kernel<128>, grid, dim3(kQBlock), 0, st, a); break;
+    case 256: hipLaunchKernelGGL(quantize_any_kernel<256>, grid, dim3(kQBlock), 0, st, a); break;
+  }
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
   return check_launch(what);
 }
@@ -329,7 +455,7 @@ extern "C" int wn_append_kv(
   clear_error();
   WN_REQUIRE(B >= 0 && Hkv > 0 && n >= 0 && num_pages >= 0 && max_pages >= 0, WN_E_INVALID,
              "append: bad sizes B=%d Hkv=%d n=%d", B, Hkv, n);
-  WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "append: head_dim %d not compiled (64, 128)", D);
+  WN_REQUIRE(valid_head_dim(D), WN_E_UNSUPPORTED, "append: head_dim %d not compiled (16, 32, 64, 128, 256)", D);
   WN_REQUIRE(is_pow2(S), WN_E_INVALID, "append: page size %d is not a power of two", S);
   WN_REQUIRE(x_dtype >= WN_F32 && x_dtype <= WN_BF16, WN_E_INVALID, "append: dtype code %d", x_dtype);
   WN_REQUIRE(valid_bw(bw_k) && (!v || valid_bw(bw_v)), WN_E_INVALID, "append: bit widths %d/%d", bw_k,
@@ -368,7 +494,7 @@ extern "C" int wn_quantize(const void* x, int x_dtype, int64_t rows, int64_t row
                            void* stream) {
   clear_error();
   WN_REQUIRE(rows >= 0, WN_E_INVALID, "quantize: rows %lld", (long long)rows);
-  WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "quantize: head_dim %d not compiled (64, 128)", D);
+  WN_REQUIRE(valid_head_dim(D), WN_E_UNSUPPORTED, "quantize: head_dim %d not compiled (16, 32, 64, 128, 256)", D);
   WN_REQUIRE(valid_bw(bw), WN_E_INVALID, "quantize: bit width %d", bw);
   WN_REQUIRE(x_dtype >= WN_F32 && x_dtype <= WN_BF16, WN_E_INVALID, "quantize: dtype code %d", x_dtype);
   if (rows == 0) return WN_OK;
@@ -413,17 +539,20 @@ extern "C" int wn_dequantize(const uint8_t* codes, const uint16_t* norms, int64_
                              const float* centroids, int bw, int D, void* out, int out_dtype, void* stream) {
   clear_error();
   WN_REQUIRE(rows >= 0 && valid_bw(bw), WN_E_INVALID, "dequantize: rows=%lld bw=%d", (long long)rows, bw);
-  WN_REQUIRE(D == 64 || D == 128, WN_E_UNSUPPORTED, "dequantize: head_dim %d not compiled (64, 128)", D);
+  WN_REQUIRE(valid_head_dim(D), WN_E_UNSUPPORTED, "dequantize: head_dim %d not compiled (16, 32, 64, 128, 256)",
+             D);
   WN_REQUIRE(out_dtype >= WN_F32 && out_dtype <= WN_BF16, WN_E_INVALID, "dequantize: dtype %d", out_dtype);
   if (rows == 0) return WN_OK;
   WN_REQUIRE(rows < (int64_t(1) << 31), WN_E_INVALID, "dequantize: too many rows");
   WN_REQUIRE(codes && norms && pi && centroids && out, WN_E_INVALID, "dequantize: null operand");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 128)
-    hipLaunchKernelGGL(dequantize_kernel<128>, dim3(unsigned(rows)), dim3(128), 0, st, codes, norms, pi,
-                       centroids, bw, out, out_dtype);
-  else
-    hipLaunchKernelGGL(dequantize_kernel<64>, dim3(unsigned(rows)), dim3(64), 0, st, codes, norms, pi,
-                       centroids, bw, out, out_dtype);
+  const dim3 grid(static_cast<unsigned>(rows));
+  switch (D) {
+    case 16: hipLaunchKernelGGL(dequantize_kernel<16>, grid, dim3(16), 0, st, codes, norms, pi, centroids, bw, out, out_dtype); break;
+    case 32: hipLaunchKernelGGL(dequantize_kernel<32>, grid, dim3(32), 0, st, codes, norms, pi, centroids, bw, out, out_dtype); break;
+    case 64: hipLaunchKernelGGL(dequantize_kernel<64>, grid, dim3(64), 0, st, codes, norms, pi, centroids, bw, out, out_dtype); break;
+    case 128: hipLaunchKernelGGL(dequantize_kernel<128>, grid, dim3(128), 0, st, codes, norms, pi, centroids, bw, out, out_dtype); break;
+    case 256: hipLaunchKernelGGL(dequantize_kernel<256>, grid, dim3(256), 0, st, codes, norms, pi, centroids, bw, out, out_dtype); break;
+  }
   return check_launch("wn_dequantize");
 }

@@ -32,6 +32,9 @@ inline int ilog2(int64_t x) {
   return r;
 }
 inline bool valid_bw(int bw) { return bw == 2 || bw == 3 || bw == 4 || bw == 5 || bw == 6 || bw == 8; }
+// Head dims the library compiles: the powers of two 16 .. 256 (the reference kernel
+// takes any power of two >= 16, packed_attention_triton.py:160-172).
+inline bool valid_head_dim(int D) { return D == 16 || D == 32 || D == 64 || D == 128 || D == 256; }
 inline bool aligned(const void* p, int a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // ------------------------------------------------------------- device helpers

@@ -54,14 +54,19 @@ SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep);
 // for another page dtype or head_dim.
 SplitKernel pick_dense_scan(int page_dtype, int D);
 
-// The dense scan for fp32 pages (a vector-ALU scan on fixed splits), nrep query rows
-// per (virtual) kv head (1, 2, 4, 8 or 16), head_dim 64 or 128.
-SplitKernel pick_dense_f32_scan(int D, int nrep);
+// The vector-ALU dense scan on fixed splits, for fp32 pages at every head_dim and
+// for bf16/fp16 pages at the head dims the MFMA scan does not take (16, 32, 256),
+// nrep query rows per (virtual) kv head (1, 2, 4, 8 or 16).
+SplitKernel pick_dense_valu_scan(int page_dtype, int D, int nrep);
 
-// The vector-ALU scan for the width pairs decode.hip does not instantiate (any pair
-// of supported widths), nrep query rows per kv head (1, 2, 4, 8 or 16), or nullptr.
+// The vector-ALU scan for what decode.hip does not instantiate: at head_dim 64 and
+// 128 the width pairs without a tuned kernel, at 16, 32 and 256 every pair of
+// supported widths; nrep query rows per kv head (1, 2, 4, 8 or 16), or nullptr.
 SplitFn pick_split_any(int D, int bw_k, int bw_v, int nrep);
+SplitFn pick_split_any_d256(int bw_k, int bw_v, int nrep);
 SplitFn pick_split_any_d128(int bw_k, int bw_v, int nrep);
 SplitFn pick_split_any_d64(int bw_k, int bw_v, int nrep);
+SplitFn pick_split_any_d32(int bw_k, int bw_v, int nrep);
+SplitFn pick_split_any_d16(int bw_k, int bw_v, int nrep);
 
 }  // namespace wn

@@ -38,9 +38,11 @@ __device__ __forceinline__ void load_group(const uint8_t* p, uint32_t (&v)[2]) {
   }
 }
 
-// A whole packed row (NB bytes, NB a multiple of 8) into registers.
+// A whole packed row (NB bytes, NB even) into registers, with the widest accesses
+// its alignment allows (rows start at multiples of NB from an 8-byte aligned base).
 template <int NB>
-__device__ __forceinline__ void load_row(const uint8_t* p, uint32_t (&w)[NB / 4]) {
+__device__ __forceinline__ void load_row(const uint8_t* p, uint32_t (&w)[(NB + 3) / 4]) {
+  static_assert(NB % 2 == 0, "packed rows of head_dim >= 16 are whole 16-bit pieces");
   if constexpr (NB % 16 == 0) {
 #pragma unroll
     for (int i = 0; i < NB / 16; ++i) {
@@ -50,13 +52,21 @@ __device__ __forceinline__ void load_row(const uint8_t* p, uint32_t (&w)[NB / 4]
       w[4 * i + 2] = x.z;
       w[4 * i + 3] = x.w;
     }
-  } else {
+  } else if constexpr (NB % 8 == 0) {
 #pragma unroll
     for (int i = 0; i < NB / 8; ++i) {
       uint2 x = reinterpret_cast<const uint2*>(p)[i];
       w[2 * i] = x.x;
       w[2 * i + 1] = x.y;
     }
+  } else if constexpr (NB % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < NB / 4; ++i) w[i] = reinterpret_cast<const uint32_t*>(p)[i];
+  } else {  // 6 or 10 bytes (head_dim 16 at 3 or 5 bits): 16-bit pieces
+#pragma unroll
+    for (int i = 0; i < (NB + 3) / 4; ++i) w[i] = 0;
+#pragma unroll
+    for (int i = 0; i < NB / 2; ++i) w[i >> 1] |= uint32_t(reinterpret_cast<const uint16_t*>(p)[i]) << (16 * (i & 1));
   }
 }
 
@@ -121,7 +131,7 @@ __global__ __launch_bounds__(kBlock) void decode_split_kernel(DecodeArgs a) {
     if (valid) {
       pid = trow[t >> a.log2S];
       const int slot = t & (S - 1);
-      uint32_t kw[NBK / 4];
+      uint32_t kw[(NBK + 3) / 4];
       load_row<NBK>(kbase + pid * a.ksp + slot * NBK, kw);
       const float nk = f16_to_f32(knb[pid * a.knp + slot]);
       nv = f16_to_f32(vnb[pid * a.vnp + slot]);

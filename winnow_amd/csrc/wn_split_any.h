@@ -1,5 +1,5 @@
-// Instantiation helpers of the vector-ALU scan for the width pairs decode.hip does
-// not instantiate (decode_split_any128.hip, decode_split_any64.hip).
+// Instantiation helpers of the vector-ALU scan for what decode.hip does not
+// instantiate (decode_split_any{16,32,64,128,256}.hip).
 #pragma once
 
 #include "wn_split.h"
@@ -7,10 +7,11 @@
 namespace wn {
 namespace {
 
-// The pairs decode.hip's pick_split instantiates itself.
+// The pairs decode.hip's pick_split instantiates itself (head_dim 64 and 128 only).
 template <int D, int BWK, int BWV>
 constexpr bool tuned_pair() {
-  return BWK == BWV || (D == 128 && ((BWK == 4 && BWV == 6) || (BWK == 6 && BWV == 4) || (BWK == 4 && BWV == 8)));
+  return ((D == 64 || D == 128) && BWK == BWV) ||
+         (D == 128 && ((BWK == 4 && BWV == 6) || (BWK == 6 && BWV == 4) || (BWK == 4 && BWV == 8)));
 }
 
 template <int D, int BWK, int BWV>
@@ -31,6 +32,26 @@ SplitFn any_for_k(int bwv, int nrep) {
     case 5: return any_pair<D, BWK, 5>(nrep);
     case 6: return any_pair<D, BWK, 6>(nrep);
     case 8: return any_pair<D, BWK, 8>(nrep);
+  }
+  return nullptr;
+}
+
+// K widths 2-4 and 5-8 separately, so that a large head_dim compiles in two files.
+template <int D>
+SplitFn any_for_lo(int bwk, int bwv, int nrep) {
+  switch (bwk) {
+    case 2: return any_for_k<D, 2>(bwv, nrep);
+    case 3: return any_for_k<D, 3>(bwv, nrep);
+    case 4: return any_for_k<D, 4>(bwv, nrep);
+  }
+  return nullptr;
+}
+template <int D>
+SplitFn any_for_hi(int bwk, int bwv, int nrep) {
+  switch (bwk) {
+    case 5: return any_for_k<D, 5>(bwv, nrep);
+    case 6: return any_for_k<D, 6>(bwv, nrep);
+    case 8: return any_for_k<D, 8>(bwv, nrep);
   }
   return nullptr;
 }

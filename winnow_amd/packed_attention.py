@@ -33,7 +33,7 @@ import torch
 from winnow_amd import _lib
 from winnow_amd.packing import packed_bytes
 
-SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 
 
 class UnsupportedLayout(ValueError):
@@ -348,11 +348,11 @@ DENSE_PAGE_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
 def dense_supported(q: torch.Tensor, kv: DenseKV) -> bool:
-    """Whether ``dense_decode_attention`` compiles this shape (head_dim 64 or 128, page
+    """Whether ``dense_decode_attention`` compiles this shape (head_dim 16 .. 256, page
     size >= 16 and a power of two, bf16/fp16/fp32 pages with contiguous rows, one query
     token)."""
     D = q.shape[-1]
-    return (q.dim() == 4 and q.shape[2] == 1 and D in (64, 128) and kv.head_dim == D
+    return (q.dim() == 4 and q.shape[2] == 1 and D in SUPPORTED_HEAD_DIMS and kv.head_dim == D
             and kv.k_pages.dtype in DENSE_PAGE_DTYPES and kv.v_pages.dtype == kv.k_pages.dtype
             and kv.page_size >= 16 and _pow2(kv.page_size) and kv.k_pages.stride(-1) == 1
             and kv.k_pages.stride(-2) == D and kv.v_pages.stride() == kv.k_pages.stride()
@@ -381,11 +381,12 @@ def dense_decode_attention(q: torch.Tensor, kv: DenseKV, scale: float, *,
     """Unquantized paged decode on the packed decode's schedule, the matched baseline
     (packed_attention_triton.py:190-201): q (B, Hq, 1, D) -> (B, Hq, 1, D) in q.dtype.
 
-    Pages (P, Hkv, S, D) bf16, fp16 (matrix-core scan) or fp32 (vector-ALU scan on
-    fixed splits). Errors before any launch, as the reference's (``UnsupportedLayout``):
-    a query of more than one token or off the GPU, a page size or head dim that is not
-    a power of two, non-unit element stride, K and V strides that differ; and what this
-    build does not compile (head_dim other than 64 or 128, page size below 16). A length
+    Pages (P, Hkv, S, D) bf16 or fp16 (matrix-core scan at head_dim 64 and 128) or
+    fp32 and the other head dims (vector-ALU scan on fixed splits). Errors before any
+    launch, as the reference's (``UnsupportedLayout``): a query of more than one token
+    or off the GPU, a page size or head dim that is not a power of two, non-unit element
+    stride, K and V strides that differ; and what this build does not compile (head_dim
+    above 256, page size below 16). A length
     beyond the table or a live page id outside the pool is rejected too (a host copy
     of the metadata; ``check_ranges=False`` skips it for callers that own the
     metadata). The schedule keywords and ``plan`` behave as in ``packed_decode_attention``.
@@ -400,8 +401,8 @@ def dense_decode_attention(q: torch.Tensor, kv: DenseKV, scale: float, *,
         raise UnsupportedLayout("dense kernel: unsupported page layout")
     B, Hq, _, D = q.shape
     Hkv = kv.num_kv_heads
-    if D not in (64, 128) or kv.head_dim != D or kv.k_pages.shape[-1] != D:
-        raise UnsupportedLayout(f"dense kernel: head_dim {D} (64 and 128 compiled)")
+    if D not in SUPPORTED_HEAD_DIMS or kv.head_dim != D or kv.k_pages.shape[-1] != D:
+        raise UnsupportedLayout(f"dense kernel: head_dim {D} (compiled: {SUPPORTED_HEAD_DIMS})")
     if Hq % Hkv:
         raise UnsupportedLayout(f"dense kernel: {Hq} query heads over {Hkv} kv heads")
     if kv.page_size < 16:

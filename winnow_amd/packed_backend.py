@@ -294,7 +294,7 @@ def select_decode_backend(query: torch.Tensor, kv, requested: str) -> str:
         if pa.dense_supported(query, kv):
             return "hip_dense"
         if requested == "hip_dense":
-            raise ValueError("hip_dense does not compile this shape (head_dim 64/128, fp32/bf16/fp16 pages, S >= 16)")
+            raise ValueError("hip_dense does not compile this shape (head_dim 16-256, fp32/bf16/fp16 pages, S >= 16)")
         return "dense_sdpa"
     if requested in ("auto", "triton_packed", "hip_packed"):
         if not _lib.is_hip(query):
