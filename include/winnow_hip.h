@@ -74,8 +74,8 @@ const char* wn_last_error(void);
  * and *num_splits = the number of resident waves on the current device, which then
  * share the flattened (sequence, kv head, 64-token chunk) space equally, ragged
  * batches included. Otherwise (any other pair of widths in {2,3,4,5,6,8}, head_dim
- * 64, any other n_rep, run as groups of <= 16 query heads) fixed splits sized to
- * fill the GPU. */
+ * 16, 32, 64 or 256, any other n_rep, run as groups of <= 16 query heads) fixed
+ * splits sized to fill the GPU. Head dims: the powers of two 16 .. 256. */
 int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
                    int requested_splits, int* pages_per_split, int* num_splits);
 
@@ -155,8 +155,9 @@ int wn_decode_attention_noalloc(
  *   page id it names inside [0, num_pages) (the Python layer raises otherwise);
  *   as a last guard the device skips, without writing, any vector that does not.
  *   Pi_K / Pi_V 16-byte aligned; pages 8-byte aligned with strides in multiples of
- *   8 bytes. ev_begin / ev_end (hipEvent_t or NULL) are recorded on `stream`
- *   around the kernel (its time without the caller's host overhead). */
+ *   8 bytes. D a power of two 16 .. 256. ev_begin / ev_end (hipEvent_t or NULL)
+ *   are recorded on `stream` around the kernel (its time without the caller's
+ *   host overhead). */
 int wn_append_kv(
     const void* k, int64_t ks_b, int64_t ks_h, int64_t ks_n,
     const void* v, int64_t vs_b, int64_t vs_h, int64_t vs_n, int x_dtype,
@@ -172,7 +173,8 @@ int wn_append_kv(
     void* stream, void* ev_begin, void* ev_end);
 
 /* TurboQuantMSE.quantize on `rows` contiguous-D vectors at x + r*row_stride
- * (elements): codes (rows, D) uint8 and fp32 norms (rows,). */
+ * (elements): codes (rows, D) uint8 and fp32 norms (rows,). D 16 .. 256 (powers of
+ * two), as for wn_dequantize. */
 int wn_quantize(const void* x, int x_dtype, int64_t rows, int64_t row_stride,
                 const float* pi, const float* boundaries, int bw, int D,
                 uint8_t* codes, float* norms, void* stream);
@@ -228,11 +230,12 @@ int wn_dense_decode_plan(int B, int Hq, int Hkv, int D, int S, int page_dtype, i
  * page_dtype (bf16, fp16 or fp32), the (S, D) rows of one (page, head) contiguous,
  * strides in bytes; page_table, seq_lens, q, out, the scratch (sized by
  * wn_decode_workspace_bytes with this plan) and the events as for
- * wn_decode_attention. head_dim 64 or 128, any n_rep (over 16: virtual kv heads of
- * <= 16 query heads), S a power of two >= 16, pages and their strides 16-byte
- * aligned. bf16 / fp16 pages run on the matrix cores with fp32 accuracy (q and the
- * probabilities as 16-bit hi + lo pairs against exact 16-bit K and V); fp32 pages
- * on a vector-ALU scan that needs fixed splits (pages_per_split > 0, which
+ * wn_decode_attention. head_dim a power of two 16 .. 256, any n_rep (over 16:
+ * virtual kv heads of <= 16 query heads), S a power of two >= 16, pages and their
+ * strides 16-byte aligned. bf16 / fp16 pages at head_dim 64 and 128 run on the
+ * matrix cores with fp32 accuracy (q and the probabilities as 16-bit hi + lo pairs
+ * against exact 16-bit K and V); fp32 pages, and the other head dims, on a
+ * vector-ALU scan that needs fixed splits (pages_per_split > 0, which
  * wn_dense_decode_plan returns for them). */
 int wn_dense_decode_attention(
     const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
