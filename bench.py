@@ -23,6 +23,12 @@ scaled by what the same counters read for a 1 GiB device copy.
 the same workload and scales it to the full step.
 ``configs`` repeats the decode measurement (scan time, its fraction of 8 TB/s,
 tokens/s, sampled parity against the oracle) for the other BASELINE configs.
+``lds_floor`` is the scan's other ceiling: its codebook lookups are 8-byte LDS
+reads at data-dependent addresses, head_dim wave-level reads per 64-token chunk of
+a kv head, and the LDS of a CU serves them at a rate the probe
+``wn_probe_lds_lookup_rate`` measures in the same run (eight waves per CU, as the
+scan runs); ``floor_us`` is the time those reads alone need, ``scan_over_floor``
+the scan's time against it.
 """
 from __future__ import annotations
 
@@ -487,7 +493,29 @@ def measure_decode(w, steps: int, warmup: int, settle: float, splits=None):
             "kernel_ms_median": statistics.median(kern), "splits": ns, "pages_per_split": pps}
 
 
-def config_line(cfg: int, dev, steps: int, warmup: int, settle: float, copies: int, check: bool):
+def lds_lookup_rate(waves_per_cu: int = 8, iters: int = 8192):
+    """Table lookups (8-byte LDS reads at data-dependent addresses, wave instructions)
+    one CU's LDS serves per microsecond with ``waves_per_cu`` waves on every CU
+    (wn_probe_lds_lookup_rate): the rate the packed row scans' lookups run against."""
+    import ctypes
+    from winnow_amd import _lib
+    r = ctypes.c_double(0.0)
+    _lib.call("wn_probe_lds_lookup_rate", waves_per_cu, iters, ctypes.byref(r))
+    return r.value
+
+
+def lds_floor(lens, c, rate, cus):
+    """The row scan's LDS floor: it looks codebook entries up in LDS, one 8-byte read
+    per two codes, so each 64-token chunk of a kv head costs head_dim wave-level
+    lookups (D/2 for K, D/2 for V) whatever its widths and head groups; at ``rate``
+    lookups per microsecond per CU the chunks need at least this long."""
+    chunks = sum((L + 63) // 64 for L in lens) * c["Hkv"]
+    return {"lookups_per_chunk": c["D"], "chunks": chunks, "rate_per_cu_per_us": rate, "cus": cus,
+            "floor_us": chunks * c["D"] / (cus * rate)}
+
+
+def config_line(cfg: int, dev, steps: int, warmup: int, settle: float, copies: int, check: bool,
+                lds_rate: float | None = None):
     """Decode throughput, roofline fraction of the scan and same-run parity at config ``cfg``."""
     import torch
     from winnow_amd.packing import packed_bytes
@@ -506,6 +534,10 @@ def config_line(cfg: int, dev, steps: int, warmup: int, settle: float, copies: i
             "scan_kernel": scan_kernel_name(c), "scan_us": m["kernel_ms"] * 1e3, "algorithmic_bytes": nbytes,
             "scan_GBps": gbps, "frac": gbps / HBM_PEAK_GBPS, "splits": m["splits"],
             "pages_per_split": m["pages_per_split"], "steps": steps}
+    if lds_rate:
+        fl = lds_floor(w.lens, c, lds_rate, torch.cuda.get_device_properties(dev).multi_processor_count)
+        line["lds_floor_us"] = fl["floor_us"]
+        line["scan_over_lds_floor"] = line["scan_us"] / fl["floor_us"]
     if check:
         line["parity"] = parity(w)
     log(f"config {cfg}: {line}")
@@ -584,6 +616,9 @@ def main(argv=None):
                     help="time the quantize+pack append of 16 new tokens per sequence (BASELINE config 3)")
     ap.add_argument("--traffic", choices=["on", "off"], default="on",
                     help="measure HBM bytes per scan launch with two rocprofv3 --pmc child runs")
+    ap.add_argument("--lds-floor", choices=["on", "off"], default="on",
+                    help="measure the LDS lookup rate (wn_probe_lds_lookup_rate, 8 waves per CU as the "
+                         "row scans run) and report each scan's LDS floor beside its HBM roofline")
     ap.add_argument("--settle", type=float, default=0.5,
                     help="seconds of untimed steps before the warm-up, to reach sustained clocks")
     args = ap.parse_args(argv)
@@ -642,12 +677,18 @@ def main(argv=None):
     traffic = hbm_traffic(args.config, scan_kernel_name(c)) if args.traffic == "on" else None
     if traffic:
         log(f"traffic: {traffic}")
+    rate = lds_lookup_rate() if args.lds_floor == "on" else None
+    ldsf = None
+    if rate:
+        ldsf = lds_floor(lens, c, rate, torch.cuda.get_device_properties(dev).multi_processor_count)
+        ldsf["scan_over_floor"] = kern_ms * 1e3 / ldsf["floor_us"]
+        log(f"lds floor: {ldsf}")
     others = {}
     extra = [] if args.configs in ("", "none") else [int(x) for x in args.configs.split(",")]
     for cfg in extra:
         if cfg != args.config:
             others[str(cfg)] = config_line(cfg, dev, args.config_steps, min(args.warmup, 10), args.settle,
-                                           args.copies, args.parity == "on")
+                                           args.copies, args.parity == "on", rate)
 
     result = {
         "metric": METRIC,
@@ -679,6 +720,7 @@ def main(argv=None):
                      "algorithmic_bytes": bytes_step,
                      "copy_peak_GBps": cp["GBps"] if cp else None,
                      "frac_of_copy_peak": achieved / cp["GBps"] if cp else None},
+        "lds_floor": ldsf,
         "cpu_baseline": cpu,
         "configs": others,
         "dense_baseline": dense,

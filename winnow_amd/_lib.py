@@ -89,6 +89,7 @@ SIGNATURES = {
         _c_p, _c_i, _c_i, _c_i,                     # table row, L, Hkv, S
         _c_p, _c_p, _c_i, _c_i,                     # centroids, Pi, bw, D
         _c_p, _c_i, _c_i, _c_p]),                   # out, out dtype, fast, stream
+    "wn_probe_lds_lookup_rate": (_c_i, [_c_i, _c_i, ctypes.POINTER(ctypes.c_double)]),
 }
 
 

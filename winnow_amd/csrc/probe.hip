@@ -1,0 +1,71 @@
+// Measurement only (no counterpart in the reference): the LDS lookup rate that
+// bounds the packed row scans. Their table lookups are 8-byte LDS reads at
+// data-dependent addresses, one per two codes (K and V: D per lane per 64-token
+// chunk); the probe issues the same kind of read, at random byte-indexed offsets
+// of a 16-replica pair table (entry (b, r) at 128 b + 8 r, r = lane % 16), eight in
+// flight per wave, from `waves` waves on every CU, and times them with HIP events.
+#include "wn_common.h"
+
+namespace wn {
+namespace {
+
+__global__ __launch_bounds__(1024) void lds_lookup_probe(int iters, uint32_t* sink) {
+  __shared__ __align__(16) uint8_t tab[32768];
+  for (int i = threadIdx.x; i < 32768 / 4; i += blockDim.x) reinterpret_cast<uint32_t*>(tab)[i] = i * 2654435761u;
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  uint32_t x = (threadIdx.x * 0x9e3779b9u) ^ (blockIdx.x * 0x85ebca6bu), acc = 0;
+  for (int it = 0; it < iters; ++it) {
+    uint32_t a[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      x = x * 1664525u + 1013904223u;
+      a[k] = (((x >> 16) & 0xffu) << 7) | (8u * (lane & 15));
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint2 v = *reinterpret_cast<const uint2*>(tab + a[k]);
+      acc += v.x ^ v.y;
+    }
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;  // keeps the reads; practically never stored
+}
+
+}  // namespace
+}  // namespace wn
+
+extern "C" int wn_probe_lds_lookup_rate(int waves_per_cu, int iters, double* lookups_per_us_per_cu) {
+  using namespace wn;
+  clear_error();
+  WN_REQUIRE(waves_per_cu >= 1 && waves_per_cu <= 16 && iters > 0 && lookups_per_us_per_cu, WN_E_INVALID,
+             "probe: waves_per_cu %d (1-16), iters %d", waves_per_cu, iters);
+  int dev = 0, cus = 0;
+  WN_REQUIRE(hipGetDevice(&dev) == hipSuccess &&
+                 hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0,
+             WN_E_LAUNCH, "probe: no device");
+  uint32_t* sink = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  WN_REQUIRE(hipMalloc(&sink, 64) == hipSuccess, WN_E_LAUNCH, "probe: hipMalloc");
+  int rc = WN_OK;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    set_error("probe: hipEventCreate");
+    rc = WN_E_LAUNCH;
+  } else {
+    const dim3 grid(cus), block(64 * waves_per_cu);
+    hipLaunchKernelGGL(lds_lookup_probe, grid, block, 0, nullptr, 64, sink);  // warm-up
+    hipEventRecord(e0, nullptr);
+    hipLaunchKernelGGL(lds_lookup_probe, grid, block, 0, nullptr, iters, sink);
+    hipEventRecord(e1, nullptr);
+    float ms = 0.f;
+    if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess || ms <= 0.f) {
+      set_error("probe: %s", hipGetErrorString(hipGetLastError()));
+      rc = WN_E_LAUNCH;
+    } else {
+      *lookups_per_us_per_cu = double(waves_per_cu) * iters * 8 / (double(ms) * 1e3);
+    }
+  }
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  hipFree(sink);
+  return rc;
+}
