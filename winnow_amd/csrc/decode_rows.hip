@@ -868,16 +868,75 @@ __device__ __forceinline__ uint2 entry4(Tab<4>& tab, uint32_t x) {
   return *reinterpret_cast<const uint2*>(tab.lds + tab.r[K]);
 }
 
+// Byte offset (8 x index) of the pair-table entry whose 2 BW-bit index starts at bit
+// BIT of the little-endian words w: the index is cut out already multiplied by 8
+// (a shift or alignbit, then one mask), two instructions per lookup.
+template <int BW, int BIT>
+__device__ __forceinline__ uint32_t pair_offset(const uint32_t* w) {
+  constexpr uint32_t m8 = ((1u << (2 * BW)) - 1u) << 3;
+  constexpr int s = BIT - 3;  // the index's bit 0 lands on bit 3
+  if constexpr (s < 0) {
+    return (w[0] << (-s)) & m8;
+  } else {
+    constexpr int wi = s >> 5, sh = s & 31;
+    if constexpr (sh + 2 * BW + 3 <= 32) return (w[wi] >> sh) & m8;
+    else return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & m8;
+  }
+}
+
+template <int BW>
+__device__ __forceinline__ uint2 pair_entry(const Tab<BW>& tab, uint32_t off) {
+  return *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(tab.t) + off);
+}
+
 // Table entry of pair N (codes 2N, 2N+1) of a packed piece held as words.
 template <int BW, int N>
 __device__ __forceinline__ uint2 piece_pair(const uint32_t* w, Tab<BW>& tab) {
-  if constexpr (BW == 4) {
-    return entry4<N & 3>(tab, w[N >> 2]);
-  } else {
-    constexpr int bit = 2 * BW * N, wi = bit >> 5, sh = bit & 31;
-    uint32_t x = w[wi] >> sh;
-    if constexpr (sh + 2 * BW > 32) x |= w[wi + 1] << (32 - sh);
-    return reinterpret_cast<const uint2*>(tab.t)[x & ((1u << (2 * BW)) - 1u)];
+  if constexpr (BW == 4) return entry4<N & 3>(tab, w[N >> 2]);
+  else return pair_entry<BW>(tab, pair_offset<BW, 2 * BW * N>(w));
+}
+
+// Pair indices of the value phase combine one dim of two tokens A and B (A's code
+// low). Before the phase, each token pair's words are rewritten in place (A's slot,
+// B's slot) = (Ce, Co): Ce holds A's even-numbered codes with B's codes shifted up
+// one field into the gaps, Co the same for the odd ones, so the index of dim m is the
+// 2 BW bits of Ce (m even) or Co (m odd) from bit BW m, and each lookup costs two
+// instructions (pair_offset). RAW windows are unshifted on the way.
+template <int BW>
+constexpr uint64_t field_mask(int parity) {
+  uint64_t m = 0;
+  for (int k = parity; k < 8; k += 2) m |= ((uint64_t(1) << BW) - 1) << (BW * k);
+  return m;
+}
+
+template <int BWK, int BWV>
+__device__ __forceinline__ void merge_value_pairs(RowBuf<BWK, BWV>& V, int lane) {
+  constexpr int VW = VWords<BWV>::N;
+  constexpr uint64_t E = field_mask<BWV>(0), O = field_mask<BWV>(1);
+  [[maybe_unused]] uint32_t sh = 0;
+  if constexpr (kRawV<BWV>) sh = raw_shift<BWV>(lane);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    uint32_t* a = V.w + (2 * q) * VW;
+    uint32_t* b = V.w + (2 * q + 1) * VW;
+    if constexpr (VW == 1) {
+      const uint32_t bs = b[0] << BWV;
+      const uint32_t ce = (a[0] & uint32_t(E)) | (bs & ~uint32_t(E));
+      b[0] = (a[0] & uint32_t(O)) | (bs & ~uint32_t(O));
+      a[0] = ce;
+    } else {
+      if constexpr (kRawV<BWV>) {
+        unshift_raw(a[0], a[1], sh);
+        unshift_raw(b[0], b[1], sh);
+      }
+      const uint32_t bs0 = b[0] << BWV, bs1 = __builtin_amdgcn_alignbit(b[1], b[0], 32 - BWV);
+      const uint32_t e0 = (a[0] & uint32_t(E)) | (bs0 & ~uint32_t(E));
+      const uint32_t e1 = (a[1] & uint32_t(E >> 32)) | (bs1 & ~uint32_t(E >> 32));
+      b[0] = (a[0] & uint32_t(O)) | (bs0 & ~uint32_t(O));
+      b[1] = (a[1] & uint32_t(O >> 32)) | (bs1 & ~uint32_t(O >> 32));
+      a[0] = e0;
+      a[1] = e1;
+    }
   }
 }
 
@@ -1055,11 +1114,7 @@ __device__ __forceinline__ void value_phase_mx(RowBuf<BWK, BWV>& V, Tab<BWV>& cb
                                                f32x4 (&acc)[8]) {
   constexpr int NH = 4 * NG, VW = VWords<BWV>::N, LA = mx_lookahead<BWK, BWV>();
   const int c = lane & 15, g = lane >> 4;
-  if constexpr (kRawV<BWV>) {
-    const uint32_t sh = raw_shift<BWV>(lane);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) unshift_raw(V.w[2 * i], V.w[2 * i + 1], sh);
-  }
+  if constexpr (BWV != 4) merge_value_pairs<BWK, BWV>(V, lane);
   const uint32_t sel = c < NH ? 0x01000100u : c < 2 * NH ? 0x03020302u : 0x0c0c0c0cu;
   const uint32_t* prow = pt + (c % NH) * kTileStride + 4 * g;
   // step k = 8ks + mt
@@ -1075,19 +1130,11 @@ __device__ __forceinline__ void value_phase_mx(RowBuf<BWK, BWV>& V, Tab<BWV>& cb
         o[p] = entry4<(mt >> 1)>(cbv, x);
       }
     } else {
+      // token pair (4 ks + 2p, 4 ks + 2p + 1), merged by merge_value_pairs: Ce in the
+      // first token's slot (even dims), Co in the second's (odd dims)
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const uint32_t* wa = V.w + (4 * ks + 2 * p) * VW;
-        const uint32_t* wb = V.w + (4 * ks + 2 * p + 1) * VW;
-        constexpr int bit = BWV * mt, wi = bit >> 5, sh = bit & 31;
-        uint32_t xa = wa[wi] >> sh, xb = wb[wi] >> sh;
-        if constexpr (sh + BWV > 32) {
-          xa |= wa[wi + 1] << (32 - sh);
-          xb |= wb[wi + 1] << (32 - sh);
-        }
-        constexpr uint32_t mask = (1u << BWV) - 1u;
-        o[p] = reinterpret_cast<const uint2*>(cbv.t)[(xa & mask) | ((xb & mask) << BWV)];
-      }
+      for (int p = 0; p < 2; ++p)
+        o[p] = pair_entry<BWV>(cbv, pair_offset<BWV, BWV * mt>(V.w + (4 * ks + 2 * p + (mt & 1)) * VW));
     }
   };
   // the p n_V words of K-step ks + 1 are read one K-step ahead: LDS returns a wave's
