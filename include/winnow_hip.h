@@ -173,8 +173,9 @@ int wn_append_kv(
     void* stream, void* ev_begin, void* ev_end);
 
 /* TurboQuantMSE.quantize on `rows` contiguous-D vectors at x + r*row_stride
- * (elements): codes (rows, D) uint8 and fp32 norms (rows,). D 16 .. 256 (powers of
- * two), as for wn_dequantize. */
+ * (elements): codes (rows, D) uint8 and fp32 norms (rows,). Any D from 1 to 256, as
+ * for wn_dequantize (the legacy cache's regular / outlier channel splits have
+ * arbitrary widths); the powers of two 16 .. 256 run the tuned kernels. */
 int wn_quantize(const void* x, int x_dtype, int64_t rows, int64_t row_stride,
                 const float* pi, const float* boundaries, int bw, int D,
                 uint8_t* codes, float* norms, void* stream);
@@ -184,7 +185,8 @@ int wn_pack(const uint8_t* codes, int64_t rows, int D, int bw, uint8_t* packed, 
 int wn_unpack(const uint8_t* packed, int64_t rows, int D, int bw, uint8_t* codes, void* stream);
 
 /* TurboQuantMSE.dequantize_into: out = (centroids[codes] Pi) * norm for
- * (rows, D) uint8 codes and fp16 norms; out (rows, D) contiguous of out_dtype. */
+ * (rows, D) uint8 codes and fp16 norms; out (rows, D) contiguous of out_dtype.
+ * Any D from 1 to 256. */
 int wn_dequantize(const uint8_t* codes, const uint16_t* norms, int64_t rows,
                   const float* pi, const float* centroids, int bw, int D,
                   void* out, int out_dtype, void* stream);

@@ -84,28 +84,30 @@ def test_argument_errors_are_reported_not_fatal(lib):
         _lib.call("wn_pack", None, 1, 128, 7, None, None)
     assert b"bit width" in lib.wn_last_error()
     with pytest.raises(_lib.WinnowHipError, match="head_dim"):
-        _lib.call("wn_quantize", None, 0, 1, 128, None, None, 4, 96, None, None, None)
+        _lib.call("wn_quantize", None, 0, 1, 128, None, None, 4, 300, None, None, None)
     # empty work is a successful no-op and clears the error
     _lib.call("wn_pack", None, 0, 128, 4, None, None)
     assert lib.wn_last_error() == b""
 
 
 def test_head_dims_compiled_and_refused(lib):
-    """Powers of two 16 .. 256 pass the head_dim check (the next check, a null operand,
-    reports); 8, 96 and 512 are refused with the compiled list; bf16 dense pages at a
-    head_dim without the matrix-core scan need fixed splits."""
+    """The decode entry points take the powers of two 16 .. 256 and refuse 8, 96 and
+    512 with the compiled list; bf16 dense pages at a head_dim without the matrix-core
+    scan need fixed splits. wn_quantize / wn_dequantize take any head_dim up to 256 (the
+    legacy cache's regular and outlier channel splits), so 8 and 96 pass their head_dim
+    check (the next check, a null operand, reports) and 512 is refused."""
     from winnow_amd import _lib
-    for D in (16, 32, 64, 128, 256):
+    for D in (8, 16, 96, 128, 256):
         with pytest.raises(_lib.WinnowHipError, match="null operand"):
             _lib.call("wn_quantize", None, 0, 1, D, None, None, 4, D, None, None, None)
-    for D in (8, 96, 512):
-        with pytest.raises(_lib.WinnowHipError, match="16, 32, 64, 128, 256"):
-            _lib.call("wn_quantize", None, 0, 1, D, None, None, 4, D, None, None, None)
+    with pytest.raises(_lib.WinnowHipError, match="head_dim 512"):
+        _lib.call("wn_quantize", None, 0, 1, 512, None, None, 4, 512, None, None, None)
     dense = ("wn_dense_decode_attention", None, 2, 0, 0, None, 0, 0, None, 0, 0)
     with pytest.raises(_lib.WinnowHipError, match="fixed splits"):
         _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 1, 4, 1, 256, 16, 1, 1.0, 0, 1, None, None, None)
-    with pytest.raises(_lib.WinnowHipError, match="16, 32, 64, 128, 256"):
-        _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 1, 4, 1, 512, 16, 1, 1.0, 0, 1, None, None, None)
+    for D in (8, 96, 512):
+        with pytest.raises(_lib.WinnowHipError, match="16, 32, 64, 128, 256"):
+            _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 1, 4, 1, D, 16, 1, 1.0, 0, 1, None, None, None)
 
 
 def test_dequant_and_dense_entry_points_reject_before_any_launch(lib):

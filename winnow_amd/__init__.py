@@ -8,6 +8,10 @@ C ABI in ``include/winnow_hip.h`` (``libwinnow_hip.so``):
              ``packed_backend.PagedPackedCache.update`` (fused quantize+pack+scatter)
 * layout:    ``page_pool.PagePool`` (paged packed pool, fenced reclamation)
 * attention: ``packed_attention.packed_decode_attention``
+
+Around them: ``cache.TQPackedCache`` (the contiguous packed cache, imported on its
+own: it pulls in transformers), ``packed_backend`` (the HF attention backend),
+``engine`` (continuous batching) and ``kernel.tq_dequant`` (fused dequantization).
 """
 from winnow_amd.packed_attention import (  # noqa: F401
     DenseKV, PackedKV, Quantizer, UnsupportedLayout, check_contract, default_scale,

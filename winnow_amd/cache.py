@@ -1,0 +1,291 @@
+"""The contiguous packed KV cache: a drop-in for ``TQPackedLayer`` / ``TQPackedCache``
+(``turboquant_kv/cache.py:154-419``), the reference's first packed cache and the
+quantized reference its model tests compare the paged path with
+(``test_packed_model.py:44-61``).
+
+Each layer keeps, per K and V, packed codes ``(B, H, max_cache_len, NB)`` uint8 and
+fp16 norms ``(B, H, max_cache_len)``, optionally split into regular channels and a
+few high-RMS outlier channels quantized at a higher width (``num_outlier_channels``,
+``outlier_bits``; the channels are the top RMS channels of the first keys stored).
+``update`` appends the new tokens and hands attention the whole history
+dequantized, as ``DynamicLayer.update`` does with plain tensors.
+
+On MI355X:
+
+* the append is one ``wn_append_kv`` launch for K and V together (quantize, pack
+  and write into the contiguous rows: the buffer is addressed as B pages of one
+  power-of-two page each, page b = sequence b) when there are no outlier channels
+  and the rows allow it; otherwise ``wn_quantize`` + ``wn_pack`` per channel group
+  (any group width up to 256);
+* the history comes back through ``wn_tq_dequant`` (the fused kernel, read in place
+  from the ``max_cache_len`` buffer) at head_dim 128 without outlier channels, else
+  through ``wn_unpack`` + ``wn_dequantize`` in chunks of ``chunk`` positions.
+
+``kernel_backend`` keeps the reference's names: ``"triton_fp32"`` and
+``"native_cuda_fp32"`` select the fused kernel at fp32 accuracy, ``"triton_tf32"``
+the fused kernel's fast mode (one fp16 product per term), ``"torch_fp32"`` the
+chunked standalone kernels, and ``"auto"`` the fused kernel where it applies (fast
+when ``allow_tf32``) and the chunked path elsewhere. The reference's dispatcher
+(``dispatch.py``) is not used: ``native_kernel`` and ``dispatcher`` are accepted
+and ignored, and ``last_dispatch_decision`` records the path taken.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from transformers.cache_utils import DynamicCache, DynamicLayer
+
+from winnow_amd import _lib
+from winnow_amd.kernel import tq_dequant
+from winnow_amd.packing import pack, packed_bytes, unpack
+from winnow_amd.quantizer import get_quantizer
+
+KERNEL_BACKENDS = ("auto", "torch_fp32", "triton_fp32", "triton_tf32", "native_cuda_fp32")
+_FUSED_HEAD_DIM = 128   # wn_tq_dequant's head_dim
+_APPEND_HEAD_DIMS = (16, 32, 64, 128, 256)
+
+
+@dataclass
+class DequantChoice:
+    """The history path one ``update`` took (the reference keeps its dispatcher's decision)."""
+    backend: str          # "fused" or "chunked"
+    fast: bool            # the fused kernel's fast mode
+    reason: str
+
+
+@dataclass
+class _Group:
+    """Packed codes and fp16 norms of one channel group of one side (K or V)."""
+    codes: torch.Tensor   # (B, H, max, NB) uint8
+    norms: torch.Tensor   # (B, H, max) fp16
+
+    def nbytes(self) -> int:
+        return self.codes.numel() + 2 * self.norms.numel()
+
+
+class TQPackedLayer(DynamicLayer):
+    """Per-layer packed KV storage; shapes (batch, kv_heads, seq, head_dim)."""
+
+    def __init__(self, head_dim: int, bit_width: int, device, max_cache_len: int,
+                 num_outlier_channels: int = 0, outlier_bits: int = 0, chunk: int = 1024,
+                 use_kernel: bool = True, allow_tf32: bool = True, kernel_backend: str = "auto",
+                 native_kernel=None, dispatcher=None):
+        super().__init__()
+        del native_kernel, dispatcher  # planner objects of the reference, not used here
+        backend = kernel_backend if use_kernel else "torch_fp32"
+        if backend not in KERNEL_BACKENDS:
+            raise ValueError(f"unknown kernel_backend={kernel_backend!r}")
+        self.use_kernel, self.allow_tf32, self.kernel_backend = use_kernel, allow_tf32, backend
+        self.last_dispatch_decision: DequantChoice | None = None
+        self._hd, self._bw, self._max, self._chunk = head_dim, bit_width, max_cache_len, chunk
+        split = num_outlier_channels > 0 and outlier_bits > bit_width
+        self._out_dim = num_outlier_channels if split else 0
+        self._reg_dim = head_dim - self._out_dim
+        self._out_bw = outlier_bits
+        # K and V share each group's quantizer (seed 42 regular, 43 outlier), as the reference's
+        self._tq = get_quantizer(bit_width, self._reg_dim, device)
+        self._tq_out = get_quantizer(outlier_bits, self._out_dim, device, seed=43) if split else None
+        self._nb_reg = packed_bytes(self._reg_dim, bit_width)
+        self._nb_out = packed_bytes(self._out_dim, outlier_bits) if split else 0
+        self._len = 0
+        self._mask = None          # (head_dim,) bool: the outlier channels
+        self._k = self._v = None   # lists of _Group: regular, then outlier
+        self.is_initialized = False
+
+    # ---------------------------------------------------------------- storage
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        B, H, _, D = key_states.shape
+        if D != self._hd:
+            raise ValueError(f"TQPackedLayer: head_dim {D} != {self._hd}")
+        self.dtype, self.device = key_states.dtype, key_states.device
+        dev = key_states.device
+
+        def group(nb):
+            return _Group(torch.empty(B, H, self._max, nb, dtype=torch.uint8, device=dev),
+                          torch.empty(B, H, self._max, dtype=torch.float16, device=dev))
+        widths = [self._nb_reg] + ([self._nb_out] if self._out_dim else [])
+        self._k = [group(nb) for nb in widths]
+        self._v = [group(nb) for nb in widths]
+        if self._out_dim:
+            rms = key_states.float().pow(2).mean(dim=(0, 1, 2)).sqrt()
+            self._mask = torch.zeros(D, dtype=torch.bool, device=dev)
+            self._mask[rms.topk(min(self._out_dim, D)).indices] = True
+        self._shape = (B, H, D)
+        self.is_initialized = True
+
+    def _fused_append_ok(self, x: torch.Tensor) -> bool:
+        """One wn_append_kv launch writes both sides: no outlier split, a compiled
+        head_dim, rows whose byte strides keep the kernel's 8-byte alignment."""
+        g = self._k[0]
+        return (not self._out_dim and self._hd in _APPEND_HEAD_DIMS and x.dtype in _lib.DTYPE_CODE
+                and (self._max * self._nb_reg) % 8 == 0 and g.codes.data_ptr() % 8 == 0
+                and self._v[0].codes.data_ptr() % 8 == 0)
+
+    @torch.no_grad()
+    def _append_fused(self, k: torch.Tensor, v: torch.Tensor, pos: int) -> None:
+        B, H, n, D = k.shape
+        k = k if k.stride(-1) == 1 else k.contiguous()
+        v = v if (v.stride(-1) == 1 and v.dtype == k.dtype) else v.to(k.dtype).contiguous()
+        S = 1 << max(self._max - 1, 1).bit_length()   # one power-of-two page holds a whole row
+        dev = k.device
+        table = torch.arange(B, dtype=torch.int32, device=dev).view(B, 1)
+        start = torch.full((B,), pos, dtype=torch.int32, device=dev)
+        kg, vg, q = self._k[0], self._v[0], self._tq
+        with torch.cuda.device(dev):
+            _lib.call("wn_append_kv",
+                      _lib.ptr(k), *k.stride()[:3], _lib.ptr(v), *v.stride()[:3], _lib.DTYPE_CODE[k.dtype],
+                      _lib.ptr(q.Pi), _lib.ptr(q.boundaries), self._bw, _lib.ptr(q.Pi), _lib.ptr(q.boundaries), self._bw,
+                      _lib.ptr(table), 1, _lib.ptr(start),
+                      _lib.ptr(kg.codes), kg.codes.stride(0), kg.codes.stride(1),
+                      _lib.ptr(vg.codes), vg.codes.stride(0), vg.codes.stride(1),
+                      _lib.ptr(kg.norms), kg.norms.stride(0), kg.norms.stride(1),
+                      _lib.ptr(vg.norms), vg.norms.stride(0), vg.norms.stride(1),
+                      B, H, n, D, S, B, 1, _lib.stream_of(dev), None, None)
+
+    @torch.no_grad()
+    def _append_groups(self, x: torch.Tensor, groups, pos: int) -> None:
+        """wn_quantize + wn_pack per channel group, written into [pos, pos + n)."""
+        n = x.shape[-2]
+        if self._out_dim:
+            xf = x.float()
+            parts = [(xf[..., ~self._mask], self._tq, self._bw), (xf[..., self._mask], self._tq_out, self._out_bw)]
+        else:
+            parts = [(x, self._tq, self._bw)]
+        for (xp, q, bw), g in zip(parts, groups):
+            idx, nrm = q.quantize(xp)
+            g.codes[:, :, pos:pos + n] = pack(idx, bw)
+            g.norms[:, :, pos:pos + n] = nrm.to(torch.float16)
+
+    # ---------------------------------------------------------------- history
+    def _choose(self) -> DequantChoice:
+        fused_ok = not self._out_dim and self._hd == _FUSED_HEAD_DIM
+        b = self.kernel_backend
+        if b == "torch_fp32":
+            return DequantChoice("chunked", False, "kernel_backend torch_fp32")
+        if b == "auto":
+            if fused_ok:
+                return DequantChoice("fused", self.allow_tf32, "auto: fused kernel (head_dim 128, no outliers)")
+            return DequantChoice("chunked", False, "auto: the fused kernel needs head_dim 128 without outlier channels")
+        if not fused_ok:
+            raise RuntimeError(f"requested {b}, but the fused dequant serves head_dim 128 without outlier channels")
+        return DequantChoice("fused", b == "triton_tf32", f"kernel_backend {b}")
+
+    @torch.no_grad()
+    def _history(self, groups, length: int) -> torch.Tensor:
+        B, H, D = self._shape
+        out = torch.empty(B, H, length, D, dtype=self.dtype, device=self.device)
+        choice = self._choose()
+        self.last_dispatch_decision = choice
+        if length == 0:
+            return out
+        if choice.backend == "fused":
+            g = groups[0]
+            tq_dequant(g.codes[:, :, :length], g.norms[:, :, :length], self._tq.centroids, self._tq.Pi,
+                       self._bw, D, out=out, allow_tf32=choice.fast)
+            return out
+        quants = [(self._tq, self._bw, self._reg_dim)] + \
+            ([(self._tq_out, self._out_bw, self._out_dim)] if self._out_dim else [])
+        for s in range(0, length, self._chunk):
+            e = min(s + self._chunk, length)
+            pieces = []
+            for g, (q, bw, dim) in zip(groups, quants):
+                part = torch.empty(B, H, e - s, dim, dtype=self.dtype, device=self.device)
+                q.dequantize_into(unpack(g.codes[:, :, s:e].contiguous(), bw, dim), g.norms[:, :, s:e], part)
+                pieces.append(part)
+            if self._out_dim:
+                sl = out[:, :, s:e]
+                sl[..., ~self._mask] = pieces[0]
+                sl[..., self._mask] = pieces[1]
+            else:
+                out[:, :, s:e] = pieces[0]
+        return out
+
+    # ---------------------------------------------------------------- cache protocol
+    def update(self, key_states, value_states, *args, **kwargs):
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        n = key_states.shape[-2]
+        if self._len + n > self._max:
+            raise RuntimeError(f"TQPackedLayer overflow: {self._len}+{n} > max_cache_len={self._max}. "
+                               f"Raise max_cache_len.")
+        if self._fused_append_ok(key_states):
+            self._append_fused(key_states, value_states, self._len)
+        else:
+            self._append_groups(key_states, self._k, self._len)
+            self._append_groups(value_states, self._v, self._len)
+        self._len += n
+        return self._history(self._k, self._len), self._history(self._v, self._len)
+
+    def get_seq_length(self, *a, **k) -> int:
+        return self._len
+
+    def get_mask_sizes(self, query_length: int, *a, **k):
+        # asked before the layer stores the query's tokens (transformers' mask preparation)
+        return self._len + query_length, 0
+
+    def get_max_length(self, *a, **k) -> int:
+        return self._max
+
+    def get_max_cache_shape(self, *a, **k) -> int:
+        return self.get_max_length()
+
+    def reset(self) -> None:
+        self._len = 0
+
+    # ---------------------------------------------------------------- accounting
+    def persistent_bytes(self) -> int:
+        """Bytes this layer holds between steps (what limits concurrency)."""
+        if not self.is_initialized:
+            return 0
+        return sum(g.nbytes() for g in self._k + self._v)
+
+    def persistent_bytes_used(self) -> int:
+        """The same, counting only the positions written so far."""
+        if not self.is_initialized or self._max == 0:
+            return 0
+        return int(self.persistent_bytes() * self._len / self._max)
+
+    def transient_bytes(self) -> int:
+        """Bytes of the dequantized K and V handed to attention each step."""
+        if not self.is_initialized:
+            return 0
+        B, H, D = self._shape
+        return 2 * B * H * self._len * D * torch.empty((), dtype=self.dtype).element_size()
+
+
+class TQPackedCache(DynamicCache):
+    """``past_key_values`` of ``TQPackedLayer``s, one per decoder layer (cache.py:356-419)."""
+
+    def __init__(self, config, bit_width: int, max_cache_len: int, device="cuda",
+                 num_outlier_channels: int = 0, outlier_bits: int = 0, chunk: int = 1024,
+                 use_kernel: bool = True, allow_tf32: bool = True, kernel_backend: str = "auto",
+                 native_kernel=None, dispatcher=None):
+        head_dim = getattr(config, "head_dim", None) or config.hidden_size // config.num_attention_heads
+        super().__init__()
+        self.layers = [TQPackedLayer(head_dim, bit_width, device, max_cache_len, num_outlier_channels,
+                                     outlier_bits, chunk, use_kernel, allow_tf32, kernel_backend,
+                                     native_kernel, dispatcher)
+                       for _ in range(config.num_hidden_layers)]
+        self.layer_class_to_replicate = None   # the layers are fixed, not grown on demand
+        self.bit_width, self.head_dim = bit_width, head_dim
+
+    def persistent_bytes(self) -> int:
+        return sum(l.persistent_bytes() for l in self.layers)
+
+    def persistent_bytes_used(self) -> int:
+        return sum(l.persistent_bytes_used() for l in self.layers)
+
+    def transient_bytes(self) -> int:
+        return max((l.transient_bytes() for l in self.layers), default=0)
+
+    def effective_bits(self) -> float:
+        """Stored bits per KV element, norms included."""
+        l = self.layers[0]
+        if not l.is_initialized:
+            return float("nan")
+        bits = 8 * (l._nb_reg + l._nb_out) + 16 * (2 if l._out_dim else 1)
+        return bits / self.head_dim
+
+    def get_seq_length(self, layer_idx: int = 0, *a, **k) -> int:
+        return self.layers[layer_idx].get_seq_length()

@@ -382,6 +382,70 @@ __global__ __launch_bounds__(kQBlock) void quantize_any_kernel(QuantArgs a) {
   }
 }
 
+// wn_quantize at any other head_dim up to 256 (the legacy cache splits a head into
+// regular and outlier channels, cache.py:185-196, so its quantizers see arbitrary
+// widths): quantize_any_kernel with a run-time D and flat output only, each code
+// stored as its byte, each norm as fp32.
+constexpr int kRtMaxD = 256;
+
+__global__ __launch_bounds__(kQBlock) void quantize_rt_kernel(QuantArgs a, int D) {
+  __shared__ float bnd[255];
+  __shared__ float xs[kVecPerBlock][kRtMaxD];
+  __shared__ float nrms[kVecPerBlock];
+  __shared__ double ssq[kVecPerBlock][16];
+  const QuantSide& sd = a.side[0];
+  const int tid = threadIdx.x;
+  const int nb = (1 << sd.bw) - 1;
+  const int64_t v0 = int64_t(blockIdx.x) * kVecPerBlock;
+  if (v0 >= a.total) return;  // block-uniform
+  for (int i = tid; i < nb; i += kQBlock) bnd[i] = sd.bnd[i];
+  for (int e = tid; e < kVecPerBlock * D; e += kQBlock) {
+    const int vl = e / D, dd = e % D;
+    const int64_t v = v0 + vl;
+    xs[vl][dd] = v < a.total ? load_elem(sd.x, v * sd.sb + dd, a.x_dtype) : 0.f;
+  }
+  __syncthreads();
+  {
+    const int vl = tid >> 4, part = tid & 15;
+    double ss = 0.0;
+    for (int k = part; k < D; k += 16) ss = fma(double(xs[vl][k]), double(xs[vl][k]), ss);
+    ssq[vl][part] = ss;
+  }
+  __syncthreads();
+  if (tid < kVecPerBlock) {
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ss += ssq[tid][k];
+    nrms[tid] = fmaxf(float(sqrt(ss)), 1e-10f);
+    if (v0 + tid < a.total) sd.norms_out[v0 + tid] = nrms[tid];
+  }
+  __syncthreads();
+  for (int e = tid; e < kVecPerBlock * D; e += kQBlock) {
+    const int vl = e / D, dd = e % D;
+    xs[vl][dd] = float(double(xs[vl][dd]) / double(nrms[vl]));
+  }
+  __syncthreads();
+  for (int j = tid; j < D; j += kQBlock) {
+    const float* prow = sd.pi + int64_t(j) * D;
+    double y[kVecPerBlock];
+#pragma unroll
+    for (int v = 0; v < kVecPerBlock; ++v) y[v] = 0.0;
+    for (int dd = 0; dd < D; ++dd) {
+      const double pe = double(prow[dd]);
+#pragma unroll
+      for (int v = 0; v < kVecPerBlock; ++v) y[v] = fma(double(xs[v][dd]), pe, y[v]);
+    }
+    float yf[kVecPerBlock];
+    uint32_t code[kVecPerBlock];
+#pragma unroll
+    for (int v = 0; v < kVecPerBlock; ++v) yf[v] = float(y[v]);
+    bucketize_n(bnd, sd.bw, yf, code);
+#pragma unroll
+    for (int v = 0; v < kVecPerBlock; ++v)
+      if (v0 + v < a.total) sd.codes_out[(v0 + v) * D + j] = uint8_t(code[v]);
+  }
+}
+
 __global__ void pack_kernel(const uint8_t* codes, int64_t rows, int D, int bw, uint8_t* out) {
   const int NB = D * bw / 8;
   const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -401,6 +465,20 @@ __global__ void unpack_kernel(const uint8_t* packed, int64_t rows, int D, int bw
   uint32_t v = uint32_t(p[byte]) >> sh;
   if (sh + bw > 8) v |= uint32_t(p[byte + 1]) << (8 - sh);
   out[e] = uint8_t(v & ((1u << bw) - 1u));
+}
+
+// out[r, j] = (sum_d c[code[r, d]] Pi[d, j]) * n[r] at a run-time head_dim <= 256.
+__global__ __launch_bounds__(kRtMaxD) void dequantize_rt_kernel(const uint8_t* codes, const uint16_t* norms,
+                                                                const float* pi, const float* cb, int bw, int D,
+                                                                void* out, int out_dtype) {
+  __shared__ float y[kRtMaxD];
+  const int64_t r = blockIdx.x;
+  const int j = threadIdx.x;
+  y[j] = cb[codes[r * D + j] & ((1u << bw) - 1u)];
+  __syncthreads();
+  float o = 0.f;
+  for (int d = 0; d < D; ++d) o = fmaf(y[d], pi[d * D + j], o);
+  store_elem(out, r * D + j, out_dtype, o * f16_to_f32(norms[r]));
 }
 
 // out[r, j] = (sum_d c[code[r, d]] Pi[d, j]) * n[r]  (cache.py:125-131)
@@ -494,7 +572,7 @@ extern "C" int wn_quantize(const void* x, int x_dtype, int64_t rows, int64_t row
                            void* stream) {
   clear_error();
   WN_REQUIRE(rows >= 0, WN_E_INVALID, "quantize: rows %lld", (long long)rows);
-  WN_REQUIRE(valid_head_dim(D), WN_E_UNSUPPORTED, "quantize: head_dim %d not compiled (16, 32, 64, 128, 256)", D);
+  WN_REQUIRE(D >= 1 && D <= kRtMaxD, WN_E_UNSUPPORTED, "quantize: head_dim %d (1 .. %d)", D, kRtMaxD);
   WN_REQUIRE(valid_bw(bw), WN_E_INVALID, "quantize: bit width %d", bw);
   WN_REQUIRE(x_dtype >= WN_F32 && x_dtype <= WN_BF16, WN_E_INVALID, "quantize: dtype code %d", x_dtype);
   if (rows == 0) return WN_OK;
@@ -508,6 +586,11 @@ extern "C" int wn_quantize(const void* x, int x_dtype, int64_t rows, int64_t row
   a.n = 1;
   a.x_dtype = x_dtype;
   a.scatter = 0;
+  if (!valid_head_dim(D)) {  // run-time head_dim: codes as bytes, any width
+    hipLaunchKernelGGL(quantize_rt_kernel, dim3(unsigned((rows + kVecPerBlock - 1) / kVecPerBlock)), dim3(kQBlock), 0,
+                       static_cast<hipStream_t>(stream), a, D);
+    return check_launch("wn_quantize");
+  }
   return launch_quantize(a, 1, D, static_cast<hipStream_t>(stream), "wn_quantize");
 }
 
@@ -539,8 +622,7 @@ extern "C" int wn_dequantize(const uint8_t* codes, const uint16_t* norms, int64_
                              const float* centroids, int bw, int D, void* out, int out_dtype, void* stream) {
   clear_error();
   WN_REQUIRE(rows >= 0 && valid_bw(bw), WN_E_INVALID, "dequantize: rows=%lld bw=%d", (long long)rows, bw);
-  WN_REQUIRE(valid_head_dim(D), WN_E_UNSUPPORTED, "dequantize: head_dim %d not compiled (16, 32, 64, 128, 256)",
-             D);
+  WN_REQUIRE(D >= 1 && D <= kRtMaxD, WN_E_UNSUPPORTED, "dequantize: head_dim %d (1 .. %d)", D, kRtMaxD);
   WN_REQUIRE(out_dtype >= WN_F32 && out_dtype <= WN_BF16, WN_E_INVALID, "dequantize: dtype %d", out_dtype);
   if (rows == 0) return WN_OK;
   WN_REQUIRE(rows < (int64_t(1) << 31), WN_E_INVALID, "dequantize: too many rows");
@@ -553,6 +635,8 @@ extern "C" int wn_dequantize(const uint8_t* codes, const uint16_t* norms, int64_
     case 64: hipLaunchKernelGGL(dequantize_kernel<64>, grid, dim3(64), 0, st, codes, norms, pi, centroids, bw, out, out_dtype); break;
     case 128: hipLaunchKernelGGL(dequantize_kernel<128>, grid, dim3(128), 0, st, codes, norms, pi, centroids, bw, out, out_dtype); break;
     case 256: hipLaunchKernelGGL(dequantize_kernel<256>, grid, dim3(256), 0, st, codes, norms, pi, centroids, bw, out, out_dtype); break;
+    default:
+      hipLaunchKernelGGL(dequantize_rt_kernel, grid, dim3(D), 0, st, codes, norms, pi, centroids, bw, D, out, out_dtype);
   }
   return check_launch("wn_dequantize");
 }
