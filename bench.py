@@ -23,12 +23,13 @@ scaled by what the same counters read for a 1 GiB device copy.
 the same workload and scales it to the full step.
 ``configs`` repeats the decode measurement (scan time, its fraction of 8 TB/s,
 tokens/s, sampled parity against the oracle) for the other BASELINE configs.
-``lds_floor`` is the scan's other ceiling: its codebook lookups are 8-byte LDS
+``lds_floor`` is the scan's LDS ceiling: its codebook lookups are 8-byte LDS
 reads at data-dependent addresses, head_dim wave-level reads per 64-token chunk of
 a kv head, and the LDS of a CU serves them at a rate the probe
 ``wn_probe_lds_lookup_rate`` measures in the same run (eight waves per CU, as the
 scan runs); ``floor_us`` is the time those reads alone need, ``scan_over_floor``
-the scan's time against it.
+the scan's time against it. It is a floor of one resource only: the scan also
+issues vector-ALU and matrix-core instructions around every lookup.
 """
 from __future__ import annotations
 

@@ -1,31 +1,36 @@
 // Measurement only (no counterpart in the reference): the LDS lookup rate that
-// bounds the packed row scans. Their table lookups are 8-byte LDS reads at
+// bounds the packed row scans' table reads. Their lookups are 8-byte LDS reads at
 // data-dependent addresses, one per two codes (K and V: D per lane per 64-token
-// chunk); the probe issues the same kind of read, at random byte-indexed offsets
-// of a 16-replica pair table (entry (b, r) at 128 b + 8 r, r = lane % 16), eight in
-// flight per wave, from `waves` waves on every CU, and times them with HIP events.
+// chunk), into a pair table replicated once per lane of a half-wave (entry (b, r) at
+// byte 256 b + 8 r, r = lane % 32). The probe issues the same reads: each lane holds
+// eight random entry addresses of such a table (opaque to the compiler on every
+// iteration, so the reads are not hoisted, and costing no address arithmetic), eight
+// reads in flight per wave, one three-input add per read, from `waves` waves on
+// every CU, timed with HIP events.
 #include "wn_common.h"
 
 namespace wn {
 namespace {
 
 __global__ __launch_bounds__(1024) void lds_lookup_probe(int iters, uint32_t* sink) {
-  __shared__ __align__(16) uint8_t tab[32768];
-  for (int i = threadIdx.x; i < 32768 / 4; i += blockDim.x) reinterpret_cast<uint32_t*>(tab)[i] = i * 2654435761u;
+  __shared__ __align__(16) uint8_t tab[65536];
+  for (int i = threadIdx.x; i < 65536 / 4; i += blockDim.x) reinterpret_cast<uint32_t*>(tab)[i] = i * 2654435761u;
   __syncthreads();
   const int lane = threadIdx.x & 63;
   uint32_t x = (threadIdx.x * 0x9e3779b9u) ^ (blockIdx.x * 0x85ebca6bu), acc = 0;
-  for (int it = 0; it < iters; ++it) {
-    uint32_t a[8];
+  uint32_t a[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      x = x * 1664525u + 1013904223u;
-      a[k] = (((x >> 16) & 0xffu) << 7) | (8u * (lane & 15));
-    }
+  for (int k = 0; k < 8; ++k) {
+    x = x * 1664525u + 1013904223u;
+    a[k] = (((x >> 16) & 0xffu) << 8) | (8u * (lane & 31));  // entry (random byte, lane % 32)
+  }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) asm volatile("" : "+v"(a[k]));
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const uint2 v = *reinterpret_cast<const uint2*>(tab + a[k]);
-      acc += v.x ^ v.y;
+      acc = acc + v.x + v.y;
     }
   }
   if (acc == 0x9e3779b9u) sink[0] = acc;  // keeps the reads; practically never stored
