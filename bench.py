@@ -28,8 +28,8 @@ reads at data-dependent addresses, head_dim wave-level reads per 64-token chunk 
 a kv head, and the LDS of a CU serves them at a rate the probe
 ``wn_probe_lds_lookup_rate`` measures in the same run (eight waves per CU, as the
 scan runs); ``floor_us`` is the time those reads alone need, ``scan_over_floor``
-the scan's time against it. It is a floor of one resource only: the scan also
-issues vector-ALU and matrix-core instructions around every lookup.
+the scan's time against it. The scan's other LDS traffic (its score tile and p
+words) comes on top.
 """
 from __future__ import annotations
 

@@ -254,9 +254,9 @@ int wn_dense_decode_attention(
 /* Measurement only; no counterpart in the reference. The rate at which one CU's
  * LDS serves the packed row scans' table lookups (8-byte reads at random addresses
  * of a pair table replicated once per lane of a half-wave, as the 4-bit scans read
- * theirs; the addresses sit in registers, so the probe spends no instructions
- * forming them; eight reads in flight per wave) with waves_per_cu waves on every
- * CU (1-16): *lookups_per_us_per_cu, timed with HIP events over `iters` x 8
+ * theirs, every address moved to another row by one instruction before its read as
+ * the scans form theirs; eight reads in flight per wave) with waves_per_cu waves on
+ * every CU (1-16): *lookups_per_us_per_cu, timed with HIP events over `iters` x 8
  * lookups per lane on the null stream. bench.py turns it into the scans' LDS floor. */
 int wn_probe_lds_lookup_rate(int waves_per_cu, int iters, double* lookups_per_us_per_cu);
 

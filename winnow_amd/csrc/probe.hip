@@ -2,11 +2,12 @@
 // bounds the packed row scans' table reads. Their lookups are 8-byte LDS reads at
 // data-dependent addresses, one per two codes (K and V: D per lane per 64-token
 // chunk), into a pair table replicated once per lane of a half-wave (entry (b, r) at
-// byte 256 b + 8 r, r = lane % 32). The probe issues the same reads: each lane holds
-// eight random entry addresses of such a table (opaque to the compiler on every
-// iteration, so the reads are not hoisted, and costing no address arithmetic), eight
-// reads in flight per wave, one three-input add per read, from `waves` waves on
-// every CU, timed with HIP events.
+// byte 256 b + 8 r, r = lane % 32), each address written by one vector instruction
+// (an SDWA byte move) just before its read. The probe issues the same reads: each
+// lane holds eight random entry addresses of such a table and moves every one to
+// another row with one XOR before each read (reads that repeat their addresses run
+// faster, so none does), eight reads in flight per wave, one three-input add per
+// read, from `waves` waves on every CU, timed with HIP events.
 #include "wn_common.h"
 
 namespace wn {
@@ -26,7 +27,10 @@ __global__ __launch_bounds__(1024) void lds_lookup_probe(int iters, uint32_t* si
   }
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) asm volatile("" : "+v"(a[k]));
+    for (int k = 0; k < 8; ++k) {
+      a[k] ^= uint32_t(it & 1) << (8 + k);  // another row of the table every iteration
+      asm volatile("" : "+v"(a[k]));
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const uint2 v = *reinterpret_cast<const uint2*>(tab + a[k]);
