@@ -217,8 +217,9 @@ struct RowBuf {
 // which measured 1.3 % faster on the 4/4-bit scan. The 6-bit pieces of a row come
 // from two instructions, and 3/5-bit rows from bytes, so they keep cached loads.
 //
-// RAW (5 and 6 bits only): the 8 bytes from p rounded down to 4 bytes, one dwordx2
-// load, left unshifted; raw_shift gives the bit offset of the codes in them and
+// RAW (5 and 6 bits only): the 8 bytes from p, which the caller has rounded down to 4
+// bytes, one dwordx2 load, left unshifted; raw_shift gives the bit offset of the codes
+// in them and
 // unshift_raw moves them down (done where the words are used, so no wait for the load
 // is needed right after it). The window ends at most at the end of the lane's
 // 16-token page block (p + BWV <= block end and 8 bytes from the rounded-down start
@@ -234,11 +235,9 @@ template <int BWV, bool RAW = false>
 __device__ __forceinline__ void load_vcodes(const uint8_t* p, bool odd_lane, uint32_t (&out)[VWords<BWV>::N]) {
   if constexpr (RAW) {
     static_assert(BWV == 5 || BWV == 6, "raw windows are for 5 and 6-bit rows");
-    // offset arithmetic on p itself keeps it a global pointer (a flat load would also
-    // count against the LDS counter)
-    const uint8_t* q = p - (reinterpret_cast<uintptr_t>(p) & 3);
+    // p is already rounded down to 4 bytes (load_v rounds the lane's offset)
     uint2 x;
-    __builtin_memcpy(&x, __builtin_assume_aligned(q, 4), 8);
+    __builtin_memcpy(&x, __builtin_assume_aligned(p, 4), 8);
     out[0] = x.x;
     out[1] = x.y;
   } else if constexpr (BWV == 4) {
@@ -309,7 +308,8 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, i
   const int p = lane & 15;
   // live == false (a chunk past the range, loaded only so that every path of the
   // scan loop issues the same loads): every lane reads the first bytes of the block
-  const uint32_t lane_off = live ? uint32_t((lane >> 4) * NBV + BWV * p) : 0u;
+  // (RAW: rounded down to 4 bytes; page blocks are 8-byte aligned, so the windows are)
+  const uint32_t lane_off = live ? uint32_t((lane >> 4) * NBV + BWV * p) & (RAW ? ~3u : ~0u) : 0u;
   static_for<0, 4>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     const uint32_t pid_j = __builtin_amdgcn_readlane(pid_lane, 16 * j);  // a live page id, >= 0
@@ -597,18 +597,22 @@ __device__ __forceinline__ void scan_range(const DecodeArgs& a, int b, int kvh, 
   write_partial(a, st, prow, lane);
 }
 
-// LDS of a work-group of WPB waves: the codebook tables (a replicated pair table
-// first, at a 64 KB slot, so that its address registers need no base add), then
-// one p tile per wave.
+// LDS of a work-group of WPB waves: the codebook tables (a replicated 4-bit pair table
+// at a 64 KB slot, so that its address registers need no base add), then one p tile
+// per wave.
 template <int BWK, int BWV, int NG, int WPB>
 struct RowsLds {
-  static constexpr int k_off = (BWK == 4 || BWV != 4) ? 0 : kPairTableBytes;
-  static constexpr int v_off = BWV == 4 ? (BWK == 4 ? kPairTableBytes : 0) : (BWK == 4 ? kPairTableBytes
-                                                                                      : table_bytes<BWK>());
+  // A 4-bit table takes a 64 KB slot of its own: its address registers carry the slot.
+  // Beside a pair-coded table (2, 3, 5, 6 bits) it takes slot 1 and the pair table
+  // offset 0, where its entry offsets (below 64 KB) need no base added: the read's
+  // 16-bit offset field cannot hold a base of 64 KB, which would cost an add per lookup.
+  static constexpr bool k4 = BWK == 4, v4 = BWV == 4;
+  static constexpr int k_off = k4 ? (pair_coded<BWV>() ? kPairTableBytes : 0) : (v4 && !pair_coded<BWK>() ? kPairTableBytes : 0);
+  static constexpr int v_off = v4 ? (k4 || pair_coded<BWK>() ? kPairTableBytes : 0)
+                                  : (k4 ? (pair_coded<BWV>() ? 0 : kPairTableBytes) : table_bytes<BWK>());
   static constexpr int k_slot = k_off >> 16, v_slot = v_off >> 16;
-  static constexpr int tiles = (BWK == 4 && BWV != 4) ? v_off + table_bytes<BWV>()
-                               : (BWV == 4 && BWK != 4) ? k_off + table_bytes<BWK>()
-                                                        : v_off + table_bytes<BWV>();
+  static constexpr int tiles = k_off + table_bytes<BWK>() > v_off + table_bytes<BWV>() ? k_off + table_bytes<BWK>()
+                                                                                       : v_off + table_bytes<BWV>();
   static constexpr int tile_bytes = NG * 16 * kPStride * 4;
   static constexpr int total = tiles + WPB * tile_bytes;
   static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
@@ -912,6 +916,13 @@ constexpr uint64_t field_mask(int parity) {
   return m;
 }
 
+// (a & m) | (b & ~m) in one instruction whatever the compiler knows of a's and b's bits.
+__device__ __forceinline__ uint32_t bitsel(uint32_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(a), "v"(b));
+  return r;
+}
+
 template <int BWK, int BWV>
 __device__ __forceinline__ void merge_value_pairs(RowBuf<BWK, BWV>& V, int lane) {
   constexpr int VW = VWords<BWV>::N;
@@ -924,8 +935,8 @@ __device__ __forceinline__ void merge_value_pairs(RowBuf<BWK, BWV>& V, int lane)
     uint32_t* b = V.w + (2 * q + 1) * VW;
     if constexpr (VW == 1) {
       const uint32_t bs = b[0] << BWV;
-      const uint32_t ce = (a[0] & uint32_t(E)) | (bs & ~uint32_t(E));
-      b[0] = (a[0] & uint32_t(O)) | (bs & ~uint32_t(O));
+      const uint32_t ce = bitsel(uint32_t(E), a[0], bs);
+      b[0] = bitsel(uint32_t(O), a[0], bs);
       a[0] = ce;
     } else {
       if constexpr (kRawV<BWV>) {
@@ -933,10 +944,10 @@ __device__ __forceinline__ void merge_value_pairs(RowBuf<BWK, BWV>& V, int lane)
         unshift_raw(b[0], b[1], sh);
       }
       const uint32_t bs0 = b[0] << BWV, bs1 = __builtin_amdgcn_alignbit(b[1], b[0], 32 - BWV);
-      const uint32_t e0 = (a[0] & uint32_t(E)) | (bs0 & ~uint32_t(E));
-      const uint32_t e1 = (a[1] & uint32_t(E >> 32)) | (bs1 & ~uint32_t(E >> 32));
-      b[0] = (a[0] & uint32_t(O)) | (bs0 & ~uint32_t(O));
-      b[1] = (a[1] & uint32_t(O >> 32)) | (bs1 & ~uint32_t(O >> 32));
+      const uint32_t e0 = bitsel(uint32_t(E), a[0], bs0);
+      const uint32_t e1 = bitsel(uint32_t(E >> 32), a[1], bs1);
+      b[0] = bitsel(uint32_t(O), a[0], bs0);
+      b[1] = bitsel(uint32_t(O >> 32), a[1], bs1);
       a[0] = e0;
       a[1] = e1;
     }
