@@ -495,6 +495,12 @@ extern "C" int wn_decode_attention(
   WN_REQUIRE(k_stride_h >= int64_t(S) * nbk && v_stride_h >= int64_t(S) * nbv, WN_E_INVALID,
              "decode: head stride smaller than one (S, NB) page block");
   WN_REQUIRE(aligned(pi_k, 16) && aligned(pi_v, 4), WN_E_INVALID, "decode: rotation alignment");
+  // the row scans form a norm's offset as a 32 x 32 -> 64-bit product of the page id
+  // and the page stride plus a 32-bit in-page offset
+  const int64_t lim = int64_t(1) << 31;
+  WN_REQUIRE(kn_stride_p >= 0 && kn_stride_p < lim && vn_stride_p >= 0 && vn_stride_p < lim && kn_stride_h >= 0 &&
+                 vn_stride_h >= 0 && int64_t(Hkv) * kn_stride_h + S <= lim && int64_t(Hkv) * vn_stride_h + S <= lim,
+             WN_E_INVALID, "decode: norm strides of 2^31 elements or more");
 
   const SplitKernel sk = choose_scan(Hq, Hkv, D, S, bw_k, bw_v);
   RotFn rot = pick_rot_d(D, max(sk.nrep, 1));

@@ -302,7 +302,7 @@ __device__ __forceinline__ void load_k(const DecodeArgs& a, int kvh, int lane, i
 // lane 16j (pid_lane is the page of token c0+lane).
 template <int BWK, int BWV, bool RAW = false>
 __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane,
-                                       RowBuf<BWK, BWV>& r, bool live = true) {
+                                       RowBuf<BWK, BWV>& r, bool live = true, const uint32_t* pg = nullptr) {
   constexpr int NBV = 16 * BWV, VW = RowBuf<BWK, BWV>::VW;
   const int smask = (1 << a.log2S) - 1;
   const int p = lane & 15;
@@ -312,7 +312,8 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, i
   const uint32_t lane_off = live ? uint32_t((lane >> 4) * NBV + BWV * p) & (RAW ? ~3u : ~0u) : 0u;
   static_for<0, 4>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
-    const uint32_t pid_j = __builtin_amdgcn_readlane(pid_lane, 16 * j);  // a live page id, >= 0
+    // a live page id, >= 0 (pg: the block page ids the caller has read already)
+    const uint32_t pid_j = pg ? pg[j] : __builtin_amdgcn_readlane(pid_lane, 16 * j);
     const uint8_t* blk = a.v_pages + uint64_t(pid_j) * uint64_t(a.vsp) + (kvh >> a.kvshift) * a.vsh +
                          uint32_t((c0 + 16 * j) & smask) * uint32_t(NBV);
     const uint8_t* vj = blk + lane_off;
@@ -967,7 +968,7 @@ __device__ __forceinline__ int tile_token(int c) { return 4 * (c & 3) + (c >> 2)
 // token c0 + lane, whose page is pid_lane.
 template <int BWK, int BWV>
 __device__ __forceinline__ void load_k16(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane,
-                                         RowBuf<BWK, BWV>& r, bool live = true) {
+                                         RowBuf<BWK, BWV>& r, bool live = true, const uint32_t* pg = nullptr) {
   constexpr int NBK = 16 * BWK, QB = 4 * BWK, QW = BWK, KW = RowBuf<BWK, BWV>::KW;
   const int smask = (1 << a.log2S) - 1;
   // the tile's 16 tokens share a page (c0 + 16t is a multiple of 16 and S >= 16): a
@@ -976,7 +977,7 @@ __device__ __forceinline__ void load_k16(const DecodeArgs& a, int kvh, int lane,
   const uint32_t lane_off = live ? uint32_t(tile_token(lane & 15) * NBK + QB * (lane >> 4)) : 0u;
   static_for<0, 4>([&](auto rc) {
     constexpr int t = decltype(rc)::value;
-    const uint32_t pid_t = __builtin_amdgcn_readlane(pid_lane, 16 * t);  // a live page id, >= 0
+    const uint32_t pid_t = pg ? pg[t] : __builtin_amdgcn_readlane(pid_lane, 16 * t);  // a live page id, >= 0
     const uint8_t* blk = a.k_pages + uint64_t(pid_t) * uint64_t(a.ksp) + (kvh >> a.kvshift) * a.ksh +
                          uint32_t((c0 + 16 * t) & smask) * uint32_t(NBK);
     const uint8_t* q = blk + lane_off;
@@ -998,9 +999,12 @@ __device__ __forceinline__ void load_k16(const DecodeArgs& a, int kvh, int lane,
       for (int i = 0; i < QB / 4; ++i) r.w[t * QW + i] = reinterpret_cast<const uint32_t*>(q)[i];
     }
   });
-  const int slot = (c0 + lane) & smask;
-  r.w[KW] = a.k_norms[int64_t(pid_lane) * a.knp + (kvh >> a.kvshift) * a.knh + slot];
-  r.w[KW + 1] = a.v_norms[int64_t(pid_lane) * a.vnp + (kvh >> a.kvshift) * a.vnh + slot];
+  // page ids are >= 0 and the norm strides below 2^31 (checked on the host): one
+  // 32 x 32 -> 64-bit multiply-add per offset
+  const uint32_t slot = uint32_t((c0 + lane) & smask);
+  const uint32_t pid = uint32_t(pid_lane), kvr = uint32_t(kvh >> a.kvshift);
+  r.w[KW] = a.k_norms[uint64_t(pid) * uint32_t(a.knp) + (kvr * uint32_t(a.knh) + slot)];
+  r.w[KW + 1] = a.v_norms[uint64_t(pid) * uint32_t(a.vnp) + (kvr * uint32_t(a.vnh) + slot)];
 }
 
 template <int NG>
@@ -1084,11 +1088,12 @@ __device__ __forceinline__ void softmax_phase_mx(float sc, uint32_t nk_h, uint32
       sv[i] = valid ? __builtin_bit_cast(float, pt[i * kTileStride + off]) * nk : -INFINITY;
     }
   }
-  // value scale: 2^kRescale * max(n_V) * 2^-gs < 2^15
-  int ge;
-  frexpf(wave_max_nonneg(nv), &ge);
-  const int gs_need = max(0, ge - 7);
-  if (gs_need > st.gs) {  // wave-uniform, rare
+  // value scale: 2^kRescale * max(n_V) * 2^-gs < 2^15, i.e. every n_V < 2^(7 + gs); the
+  // scale only grows, so the wave's maximum is taken only when a norm reaches the limit
+  if (__any(nv >= ldexpf(1.f, 7 + st.gs))) {  // wave-uniform, rare
+    int ge;
+    frexpf(wave_max_nonneg(nv), &ge);
+    const int gs_need = max(0, ge - 7);
     const float f = ldexpf(1.f, st.gs - gs_need);
 #pragma unroll
     for (int mm = 0; mm < 8; ++mm) st.acc[mm] *= f;
@@ -1275,10 +1280,14 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
     const int c0 = t_lo + 64 * ch;
     const int pid_after = pid_of(ch + 2);
     const bool more = ch + 1 < n;
-    load_k16(a, kvh, lane, c0 + 64, pid_next, Z, more);
+    // page ids of the next chunk's four 16-token blocks, for its K and its V rows
+    uint32_t pg[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pg[j] = __builtin_amdgcn_readlane(pid_next, 16 * j);
+    load_k16(a, kvh, lane, c0 + 64, pid_next, Z, more, pg);
     score_phase_mx<BWK, BWV, NG>(X, cbk, qb, lane, ptile);
     softmax_phase_mx<NG>(sc, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
-    load_v<BWK, BWV, kRawV<BWV>>(a, kvh, lane, c0 + 64, pid_next, X, more);
+    load_v<BWK, BWV, kRawV<BWV>>(a, kvh, lane, c0 + 64, pid_next, X, more, pg);
     value_phase_mx<BWK, BWV, NG>(Y, cbv, ptile, lane, st.acc);
     pid_next = pid_after;
   };
