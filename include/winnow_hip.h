@@ -98,7 +98,9 @@ int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int pages_per_s
  *   Preconditions the device reads unchecked (the Python layer checks them on
  *   host copies before the call): 0 <= seq_lens[b] <= max_pages * S, and every
  *   page id a sequence reads, page_table[b, j] for j < cdiv(seq_lens[b], S), lies
- *   in [0, P) of the pages the strides address.
+ *   in [0, P) of the pages the strides address. Norm strides (elements) are >= 0
+ *   with kn_stride_p, vn_stride_p < 2^31 and Hkv * head stride + S <= 2^31
+ *   (WN_E_INVALID otherwise): the scans form norm offsets in 32-bit pieces.
  *   ev_begin / ev_end (hipEvent_t or NULL) are recorded on `stream` around
  *   the split-K page-scan kernel only, for in-situ timing of that kernel. */
 int wn_decode_attention(

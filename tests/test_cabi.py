@@ -138,3 +138,24 @@ def test_dequant_and_dense_entry_points_reject_before_any_launch(lib):
     # no sequences: a successful no-op
     _lib.call(*dense, 2, None, 0, None, None, 0, None, 0, 0, 4, 1, 128, 16, 1, 1.0, 0, 1, None, None, None)
     assert lib.wn_last_error() == b""
+
+
+def test_decode_rejects_norm_strides_past_32_bits(lib):
+    """Norm strides of 2^31 elements or more come back as an error before any launch
+    (fake, aligned, never dereferenced device pointers; no GPU here)."""
+    from winnow_amd import _lib
+    P = 1 << 20
+    B, Hq, Hkv, D, S, NB, max_pages = 1, 8, 8, 128, 16, 64, 4
+
+    def call(kn_p, kn_h):
+        _lib.call("wn_decode_attention", P, _lib.WN_F32, Hq * D, D, P, P, P, P,
+                  P, Hkv * S * NB, S * NB, P, Hkv * S * NB, S * NB,
+                  P, kn_p, kn_h, P, Hkv * S, S,
+                  P, max_pages, P, P, _lib.WN_F32, P, 1 << 30,
+                  B, Hq, Hkv, D, S, 4, 4, max_pages, 1.0, 0, 4, None, None, None)
+
+    with pytest.raises(_lib.WinnowHipError, match="norm strides"):
+        call(1 << 31, S)
+    with pytest.raises(_lib.WinnowHipError, match="norm strides"):
+        call(Hkv * S, 1 << 28)
+

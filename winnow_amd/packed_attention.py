@@ -217,6 +217,11 @@ def check_kernel_contract(q: torch.Tensor, kv: PackedKV, *, check_ranges: bool =
     for norms in (kv.k_norms, kv.v_norms):
         if norms.stride(-1) != 1:
             raise UnsupportedLayout("norms need a contiguous slot axis")
+        # the scans form norm offsets in 32-bit pieces (page id x page stride, head x
+        # head stride + slot)
+        if not (0 <= norms.stride(0) < 2 ** 31 and 0 <= norms.stride(1)
+                and norms.shape[1] * norms.stride(1) + kv.page_size <= 2 ** 31):
+            raise UnsupportedLayout("norm strides of 2^31 elements or more")
     for quant in (kv.k_quant, kv.v_quant):
         if not quant.Pi.is_contiguous() or not quant.centroids.is_contiguous():
             raise UnsupportedLayout("rotations and codebooks must be contiguous")
