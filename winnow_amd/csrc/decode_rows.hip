@@ -219,9 +219,8 @@ struct RowBuf {
 //
 // RAW (5 and 6 bits only): the 8 bytes from p, which the caller has rounded down to 4
 // bytes, one dwordx2 load, left unshifted; raw_shift gives the bit offset of the codes
-// in them and
-// unshift_raw moves them down (done where the words are used, so no wait for the load
-// is needed right after it). The window ends at most at the end of the lane's
+// in them and unshift_raw moves them down (done where the words are used, so no wait
+// for the load is needed right after it). The window ends at most at the end of the lane's
 // 16-token page block (p + BWV <= block end and 8 bytes from the rounded-down start
 // reach at most 3 bytes past p + 5).
 template <int BWV>
@@ -608,7 +607,8 @@ struct RowsLds {
   // offset 0, where its entry offsets (below 64 KB) need no base added: the read's
   // 16-bit offset field cannot hold a base of 64 KB, which would cost an add per lookup.
   static constexpr bool k4 = BWK == 4, v4 = BWV == 4;
-  static constexpr int k_off = k4 ? (pair_coded<BWV>() ? kPairTableBytes : 0) : (v4 && !pair_coded<BWK>() ? kPairTableBytes : 0);
+  static constexpr int k_off = k4 ? (pair_coded<BWV>() ? kPairTableBytes : 0)
+                                  : (v4 && !pair_coded<BWK>() ? kPairTableBytes : 0);
   static constexpr int v_off = v4 ? (k4 || pair_coded<BWK>() ? kPairTableBytes : 0)
                                   : (k4 ? (pair_coded<BWV>() ? 0 : kPairTableBytes) : table_bytes<BWK>());
   static constexpr int k_slot = k_off >> 16, v_slot = v_off >> 16;
