@@ -14,7 +14,8 @@
 // class of tf32's 10-bit mantissa.
 //
 // A persistent work-group of four waves stages Pi^T as bf16 hi and lo planes in LDS
-// once; each wave then takes passes of 32 rows (two 16-row tiles) and computes the
+// once; each wave then takes passes of 64 rows (four 16-row tiles; the fast mode 32,
+// two tiles) and computes the
 // transposed product out^T = Pi^T y^T, so that a lane ends with four consecutive
 // output dims of one row:
 // The reduction order over the 128 input dims is permuted so that lane group
@@ -250,6 +251,10 @@ __device__ __forceinline__ int pit_row(int d) {
 template <int BW, bool FAST, int OUT, bool PAGED>
 __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void tq_dequant_kernel(DqArgs a) {
   constexpr int D = kDqD, NB = D * BW / 8, PLANES = FAST ? 1 : 2;
+  // 16-row tiles per pass: each Pi^T operand read from LDS feeds RT MFMAs; four in the
+  // accurate mode (half the LDS reads per row), two in the fast mode, whose registers
+  // keep it at four waves per SIMD
+  constexpr int RT = FAST ? 2 : 3, kRows = 16 * RT;
   __shared__ __align__(16) uint16_t pit[PLANES][D * kPiRow];  // Pi^T: bf16 hi and lo, or fp16
   __shared__ DqTab<BW> tab;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -275,7 +280,7 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
   __syncthreads();
 
   const int g = lane >> 4, c16 = lane & 15;
-  const int64_t passes = (a.N + 31) / 32, stride = int64_t(gridDim.x) * kDqWaves;
+  const int64_t passes = (a.N + kRows - 1) / kRows, stride = int64_t(gridDim.x) * kDqWaves;
   // Loads and stores share one in-order counter (vmcnt), so a wait for a load also
   // waits for every store issued before it. The pipeline is laid out so that no wait
   // covers the stores of the pass just finished:
@@ -287,24 +292,24 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
   //  - no store is conditional: rows past N read row N - 1 (every load is in
   //    bounds) and store to row N - 1, the same bits that row's own lane writes
   //    (equal inputs, equal MFMA column), so no path skips the stores.
-  auto page_ids = [&](int64_t pass, int32_t (&pg)[2]) {
+  auto page_ids = [&](int64_t pass, int32_t (&pg)[RT]) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) pg[rt] = PAGED ? row_page(a, pass * 32 + 16 * rt + c16) : 0;
+    for (int rt = 0; rt < RT; ++rt) pg[rt] = PAGED ? row_page(a, pass * kRows + 16 * rt + c16) : 0;
   };
   // codes 32g .. 32g+31 of row r0 + 16 rt + c16 and that row's norm
-  auto load_pass = [&](int64_t pass, const int32_t (&pg)[2], uint32_t (&cw)[2][BW], uint32_t (&nh)[2]) {
+  auto load_pass = [&](int64_t pass, const int32_t (&pg)[RT], uint32_t (&cw)[RT][BW], uint32_t (&nh)[RT]) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const uint8_t* p;
       const uint16_t* n;
-      row_src<NB, PAGED>(a, pass * 32 + 16 * rt + c16, pg[rt], p, n);
+      row_src<NB, PAGED>(a, pass * kRows + 16 * rt + c16, pg[rt], p, n);
       load_codes32<BW>(p, g, cw[rt]);
       nh[rt] = *n;
     }
   };
-  auto compute_pass = [&](const uint32_t (&cw)[2][BW], f32x4 (&acc)[2][8]) {
+  auto compute_pass = [&](const uint32_t (&cw)[RT][BW], f32x4 (&acc)[RT][8]) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int t = 0; t < 8; ++t) acc[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -312,9 +317,9 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
       // keeps the scheduler from hoisting the LDS reads of later k-steps (register
       // pressure past two waves per SIMD)
       __builtin_amdgcn_sched_barrier(0);
-      s16x8 yh[2], yl[2];
+      s16x8 yh[RT], yl[RT];
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         uint32_t cs[2];
         step_codes<BW>(cw[rt], s, cs);
         codes_to_a<BW, FAST>(cs, tab, yh[rt], yl[rt]);
@@ -334,33 +339,33 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
           for (int u = 0; u < kDqTU; ++u)
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
+            for (int rt = 0; rt < RT; ++rt)
               acc[rt][t0 + u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                   __builtin_bit_cast(f16x8, ph[u]), __builtin_bit_cast(f16x8, yh[rt]), acc[rt][t0 + u], 0, 0, 0);
         } else {
 #pragma unroll
           for (int u = 0; u < kDqTU; ++u)
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
+            for (int rt = 0; rt < RT; ++rt)
               acc[rt][t0 + u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[u], yh[rt], acc[rt][t0 + u], 0, 0, 0);
 #pragma unroll
           for (int u = 0; u < kDqTU; ++u)
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
+            for (int rt = 0; rt < RT; ++rt)
               acc[rt][t0 + u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl[u], yh[rt], acc[rt][t0 + u], 0, 0, 0);
 #pragma unroll
           for (int u = 0; u < kDqTU; ++u)
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
+            for (int rt = 0; rt < RT; ++rt)
               acc[rt][t0 + u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[u], yl[rt], acc[rt][t0 + u], 0, 0, 0);
         }
       }
     }
   };
-  auto store_pass = [&](int64_t pass, const uint32_t (&nh)[2], const f32x4 (&acc)[2][8]) {
+  auto store_pass = [&](int64_t pass, const uint32_t (&nh)[RT], const f32x4 (&acc)[RT][8]) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      int64_t row = pass * 32 + 16 * rt + c16;
+    for (int rt = 0; rt < RT; ++rt) {
+      int64_t row = pass * kRows + 16 * rt + c16;
       row = row < a.N ? row : a.N - 1;
       const float nv = f16_to_f32(uint16_t(nh[rt]));
 #pragma unroll
@@ -369,20 +374,20 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     }
   };
   // One pass: page ids two passes ahead, codes of the next pass, then this pass.
-  auto half = [&](int64_t pass, const uint32_t (&cur)[2][BW], const uint32_t (&ncur)[2], uint32_t (&nxt)[2][BW],
-                  uint32_t (&nnxt)[2], const int32_t (&pg_nxt)[2], int32_t (&pg_after)[2]) {
+  auto half = [&](int64_t pass, const uint32_t (&cur)[RT][BW], const uint32_t (&ncur)[RT], uint32_t (&nxt)[RT][BW],
+                  uint32_t (&nnxt)[RT], const int32_t (&pg_nxt)[RT], int32_t (&pg_after)[RT]) {
     page_ids(pass + 2 * stride, pg_after);
     load_pass(pass + stride, pg_nxt, nxt, nnxt);
-    f32x4 acc[2][8];
+    f32x4 acc[RT][8];
     compute_pass(cur, acc);
     store_pass(pass, ncur, acc);
   };
 
   int64_t pass = int64_t(blockIdx.x) * kDqWaves + wave;
   if (pass >= passes) return;
-  uint32_t b0[2][BW], b1[2][BW];
-  uint32_t n0[2], n1[2];  // fp16 bits, one register each (a packed pair would wait for both loads)
-  int32_t pa[2], pb[2];
+  uint32_t b0[RT][BW], b1[RT][BW];
+  uint32_t n0[RT], n1[RT];  // fp16 bits, one register each (a packed pair would wait for both loads)
+  int32_t pa[RT], pb[RT];
   page_ids(pass, pa);
   load_pass(pass, pa, b0, n0);
   page_ids(pass + stride, pb);
@@ -446,7 +451,8 @@ int launch_dq(DqArgs& a, int bw, int fast, int out_dtype, hipStream_t st, const 
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDqWaves * 64, 0) != hipSuccess || per_cu < 1)
     per_cu = 1;
-  const int64_t want = (a.N + 32 * kDqWaves - 1) / (32 * kDqWaves);
+  const int64_t rows = fast ? 32 : 48;  // rows per pass (16 * RT of the kernel)
+  const int64_t want = (a.N + rows * kDqWaves - 1) / (rows * kDqWaves);
   const int64_t grid = want < int64_t(per_cu) * cus ? want : int64_t(per_cu) * cus;
   hipLaunchKernelGGL(fn, dim3(unsigned(grid)), dim3(kDqWaves * 64), 0, st, a);
   return check_launch(what);
