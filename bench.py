@@ -241,7 +241,9 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
     separate pool so the decode pool is left as it is. Timed with hipEvents over
     events the library records around the kernel on each of ``reps`` calls (and, as
     ``us_per_call_from_python``, over ``reps`` back-to-back calls of the Python wrapper,
-    whose host overhead is longer than the kernel); checked against the CPU
+    whose host overhead is longer than the kernel; as ``us_per_call_graph``, over replays
+    of a HIP graph of back-to-back calls, the GPU time per call of a serving loop that
+    captures its appends); checked against the CPU
     restatement (codes under the adjudication protocol) and timed beside it.
     """
     import torch
@@ -299,6 +301,26 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
     e1.record()
     torch.cuda.synchronize()
     host_us = e0.elapsed_time(e1) / reps * 1e3
+    # back to back on the GPU with neither events nor Python between the calls: 32 calls
+    # captured in one HIP graph (no memsets or allocations inside), replayed; the byte
+    # check below reads the pages the replays wrote last
+    graph_calls, graph_reps = 32, 20
+    graph_us = None
+    try:
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(graph_calls):
+                call()
+        gr.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(graph_reps):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        graph_us = e0.elapsed_time(e1) / (graph_reps * graph_calls) * 1e3
+    except RuntimeError as exc:                  # capture refused: report the other two timings
+        print(f"append graph timing skipped: {exc}", file=sys.stderr, flush=True)
 
     # CPU restatement on the same inputs, timed, then the byte check
     ref = [torch.zeros(P, Hkv, S, nb, dtype=torch.uint8) for nb in (nbk, nbv)]
@@ -318,7 +340,9 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
         flips += adjudicate_codes(src, sel(gc), sel(wc), tq)
     vectors = 2 * B * Hkv * n_new
     return {"us_per_call": us, "timing": "kernel, hipEvents recorded by wn_append_kv around its launch",
-            "us_per_call_from_python": host_us, "vectors_per_call": vectors, "vectors_per_s": vectors / (us * 1e-6),
+            "us_per_call_from_python": host_us, "us_per_call_graph": graph_us,
+            "graph": f"{graph_calls} calls per HIP graph, {graph_reps} replays between one event pair",
+            "vectors_per_call": vectors, "vectors_per_s": vectors / (us * 1e-6),
             "new_tokens_per_seq": n_new, "bytes_read": 2 * B * Hkv * n_new * D * 2,
             "bytes_written": B * Hkv * n_new * (nbk + 2 + nbv + 2),
             "cpu_us_per_call": cpu_us, "cpu_kind": "port", "adjudicated_code_flips": flips,

@@ -100,7 +100,9 @@ int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int pages_per_s
  *   page id a sequence reads, page_table[b, j] for j < cdiv(seq_lens[b], S), lies
  *   in [0, P) of the pages the strides address. Norm strides (elements) are >= 0
  *   with kn_stride_p, vn_stride_p < 2^31 and Hkv * head stride + S <= 2^31
- *   (WN_E_INVALID otherwise): the scans form norm offsets in 32-bit pieces.
+ *   (WN_E_INVALID otherwise): the scans form norm offsets in 32-bit pieces. Page
+ *   strides (bytes) are >= 0 and below 2^32 (WN_E_INVALID otherwise): the scans form
+ *   a page block's address from page id x page stride in 32 x 32 -> 64 bits.
  *   ev_begin / ev_end (hipEvent_t or NULL) are recorded on `stream` around
  *   the split-K page-scan kernel only, for in-situ timing of that kernel. */
 int wn_decode_attention(

@@ -159,3 +159,24 @@ def test_decode_rejects_norm_strides_past_32_bits(lib):
     with pytest.raises(_lib.WinnowHipError, match="norm strides"):
         call(Hkv * S, 1 << 28)
 
+
+
+def test_decode_rejects_page_strides_past_32_bits(lib):
+    """Page strides of 2^32 bytes or more come back as an error before any launch: the
+    row scans form a page block's address from page id x page stride in 32 x 32 bits
+    (fake, aligned, never dereferenced device pointers; no GPU here)."""
+    from winnow_amd import _lib
+    P = 1 << 20
+    B, Hq, Hkv, D, S, NB, max_pages = 1, 8, 8, 128, 16, 64, 4
+
+    def call(k_p, v_p):
+        _lib.call("wn_decode_attention", P, _lib.WN_F32, Hq * D, D, P, P, P, P,
+                  P, k_p, S * NB, P, v_p, S * NB,
+                  P, Hkv * S, S, P, Hkv * S, S,
+                  P, max_pages, P, P, _lib.WN_F32, P, 1 << 30,
+                  B, Hq, Hkv, D, S, 4, 4, max_pages, 1.0, 0, 4, None, None, None)
+
+    with pytest.raises(_lib.WinnowHipError, match="page strides"):
+        call(1 << 32, Hkv * S * NB)
+    with pytest.raises(_lib.WinnowHipError, match="page strides"):
+        call(Hkv * S * NB, 1 << 32)

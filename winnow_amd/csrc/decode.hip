@@ -501,6 +501,9 @@ extern "C" int wn_decode_attention(
   WN_REQUIRE(kn_stride_p >= 0 && kn_stride_p < lim && vn_stride_p >= 0 && vn_stride_p < lim && kn_stride_h >= 0 &&
                  vn_stride_h >= 0 && int64_t(Hkv) * kn_stride_h + S <= lim && int64_t(Hkv) * vn_stride_h + S <= lim,
              WN_E_INVALID, "decode: norm strides of 2^31 elements or more");
+  // the row scans form a page block's address as page id x page stride (32 x 32 -> 64 bits)
+  WN_REQUIRE(k_stride_p >= 0 && k_stride_p < 2 * lim && v_stride_p >= 0 && v_stride_p < 2 * lim, WN_E_INVALID,
+             "decode: page strides of 2^32 bytes or more");
 
   const SplitKernel sk = choose_scan(Hq, Hkv, D, S, bw_k, bw_v);
   RotFn rot = pick_rot_d(D, max(sk.nrep, 1));

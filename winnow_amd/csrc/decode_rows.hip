@@ -295,13 +295,21 @@ __device__ __forceinline__ void load_k(const DecodeArgs& a, int kvh, int lane, i
   r.w[KW + 1] = a.v_norms[int64_t(pid_lane) * a.vnp + (kvh >> a.kvshift) * a.vnh + slot];
 }
 
+// A page-block address formed on the device (block_bases) as a pointer into global memory: the address space is
+// stated, so loads through it stay global loads (a plain pointer rebuilt from an integer
+// would make them flat loads, which also count against the LDS wait counter).
+typedef __attribute__((address_space(1))) const uint8_t global_u8;
+__device__ __forceinline__ const uint8_t* global_ptr(uint64_t x) {
+  return (const uint8_t*)(global_u8*)(x);
+}
+
 // V side of chunk [c0, c0+64): for every token quad q the BWV bytes of codes
 // 8p..8p+7 of token c0+4q+G (G = lane/16, p = lane%16). c0 is a multiple of 16 and
 // pages hold >= 16 tokens, so the four quads of 16-token block j share the page of
 // lane 16j (pid_lane is the page of token c0+lane).
 template <int BWK, int BWV, bool RAW = false>
 __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane,
-                                       RowBuf<BWK, BWV>& r, bool live = true, const uint32_t* pg = nullptr) {
+                                       RowBuf<BWK, BWV>& r, bool live = true, const uint64_t* ba = nullptr) {
   constexpr int NBV = 16 * BWV, VW = RowBuf<BWK, BWV>::VW;
   const int smask = (1 << a.log2S) - 1;
   const int p = lane & 15;
@@ -311,10 +319,14 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, int kvh, int lane, i
   const uint32_t lane_off = live ? uint32_t((lane >> 4) * NBV + BWV * p) & (RAW ? ~3u : ~0u) : 0u;
   static_for<0, 4>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
-    // a live page id, >= 0 (pg: the block page ids the caller has read already)
-    const uint32_t pid_j = pg ? pg[j] : __builtin_amdgcn_readlane(pid_lane, 16 * j);
-    const uint8_t* blk = a.v_pages + uint64_t(pid_j) * uint64_t(a.vsp) + (kvh >> a.kvshift) * a.vsh +
-                         uint32_t((c0 + 16 * j) & smask) * uint32_t(NBV);
+    const uint8_t* blk;
+    if (ba) {  // the block's address, formed by block_bases
+      blk = global_ptr(ba[j]);
+    } else {
+      const uint32_t pid_j = __builtin_amdgcn_readlane(pid_lane, 16 * j);  // a live page id, >= 0
+      blk = a.v_pages + uint64_t(pid_j) * uint64_t(a.vsp) + (kvh >> a.kvshift) * a.vsh +
+            uint32_t((c0 + 16 * j) & smask) * uint32_t(NBV);
+    }
     const uint8_t* vj = blk + lane_off;
     static_for<0, 4>([&](auto qc) {
       constexpr int qq = decltype(qc)::value;
@@ -963,12 +975,30 @@ __device__ __forceinline__ void merge_value_pairs(RowBuf<BWK, BWV>& V, int lane)
 // Token (within its 16-token tile) whose scores row c of a score MFMA holds.
 __device__ __forceinline__ int tile_token(int c) { return 4 * (c & 3) + (c >> 2); }
 
+// Byte addresses of the four 16-token page blocks of the chunk that starts at token c0
+// (a multiple of 16): each lane forms the address of its own token's block with two
+// 64-bit multiply-adds (page id x page stride, slot x row bytes; base = the pages plus
+// the kv head's offset) and the blocks' addresses are read from lanes 0, 16, 32 and 48.
+// Page strides are below 2^32 bytes (checked on the host).
+template <int NB>
+__device__ __forceinline__ void block_bases(uint64_t base, uint32_t sp, int pid, int c0, int lane, int smask,
+                                            uint64_t (&out)[4]) {
+  const uint32_t slot = uint32_t((c0 + lane) & smask) & ~15u;
+  const uint64_t x = base + uint64_t(uint32_t(pid)) * sp + uint64_t(slot * uint32_t(NB));
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t lo = __builtin_amdgcn_readlane(uint32_t(x), 16 * t);
+    const uint32_t hi = __builtin_amdgcn_readlane(uint32_t(x >> 32), 16 * t);
+    out[t] = uint64_t(hi) << 32 | lo;
+  }
+}
+
 // K side of chunk [c0, c0+64) for the 16-bit scan: quarter g of the rows of the
 // tile tokens (one whole 16-token page block per load instruction) and both norms of
 // token c0 + lane, whose page is pid_lane.
 template <int BWK, int BWV>
 __device__ __forceinline__ void load_k16(const DecodeArgs& a, int kvh, int lane, int c0, int pid_lane,
-                                         RowBuf<BWK, BWV>& r, bool live = true, const uint32_t* pg = nullptr) {
+                                         RowBuf<BWK, BWV>& r, bool live = true, const uint64_t* ba = nullptr) {
   constexpr int NBK = 16 * BWK, QB = 4 * BWK, QW = BWK, KW = RowBuf<BWK, BWV>::KW;
   const int smask = (1 << a.log2S) - 1;
   // the tile's 16 tokens share a page (c0 + 16t is a multiple of 16 and S >= 16): a
@@ -977,9 +1007,14 @@ __device__ __forceinline__ void load_k16(const DecodeArgs& a, int kvh, int lane,
   const uint32_t lane_off = live ? uint32_t(tile_token(lane & 15) * NBK + QB * (lane >> 4)) : 0u;
   static_for<0, 4>([&](auto rc) {
     constexpr int t = decltype(rc)::value;
-    const uint32_t pid_t = pg ? pg[t] : __builtin_amdgcn_readlane(pid_lane, 16 * t);  // a live page id, >= 0
-    const uint8_t* blk = a.k_pages + uint64_t(pid_t) * uint64_t(a.ksp) + (kvh >> a.kvshift) * a.ksh +
-                         uint32_t((c0 + 16 * t) & smask) * uint32_t(NBK);
+    const uint8_t* blk;
+    if (ba) {  // the block's address, formed by block_bases
+      blk = global_ptr(ba[t]);
+    } else {
+      const uint32_t pid_t = __builtin_amdgcn_readlane(pid_lane, 16 * t);  // a live page id, >= 0
+      blk = a.k_pages + uint64_t(pid_t) * uint64_t(a.ksp) + (kvh >> a.kvshift) * a.ksh +
+            uint32_t((c0 + 16 * t) & smask) * uint32_t(NBK);
+    }
     const uint8_t* q = blk + lane_off;
     if constexpr (QB == 16) {
       const uint4 x = *reinterpret_cast<const uint4*>(q);
@@ -1270,6 +1305,9 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
   }
   st.gs = 0;
   using Buf = RowBuf<BWK, BWV>;
+  const int smask = (1 << a.log2S) - 1;
+  const uint64_t kbase = uint64_t(a.k_pages) + uint64_t(kvh >> a.kvshift) * uint64_t(a.ksh);
+  const uint64_t vbase = uint64_t(a.v_pages) + uint64_t(kvh >> a.kvshift) * uint64_t(a.vsh);
   int pid_next;
   // The next chunk's loads are issued on every step, the last one included (its
   // addresses clamped into the range's last page, all lanes on one line): with loads
@@ -1280,14 +1318,14 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
     const int c0 = t_lo + 64 * ch;
     const int pid_after = pid_of(ch + 2);
     const bool more = ch + 1 < n;
-    // page ids of the next chunk's four 16-token blocks, for its K and its V rows
-    uint32_t pg[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pg[j] = __builtin_amdgcn_readlane(pid_next, 16 * j);
-    load_k16(a, kvh, lane, c0 + 64, pid_next, Z, more, pg);
+    // addresses of the next chunk's four 16-token blocks, for its K and its V rows
+    uint64_t kb[4], vb[4];
+    block_bases<16 * BWK>(kbase, uint32_t(a.ksp), pid_next, c0 + 64, lane, smask, kb);
+    load_k16(a, kvh, lane, c0 + 64, pid_next, Z, more, kb);
     score_phase_mx<BWK, BWV, NG>(X, cbk, qb, lane, ptile);
     softmax_phase_mx<NG>(sc, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
-    load_v<BWK, BWV, kRawV<BWV>>(a, kvh, lane, c0 + 64, pid_next, X, more, pg);
+    block_bases<16 * BWV>(vbase, uint32_t(a.vsp), pid_next, c0 + 64, lane, smask, vb);
+    load_v<BWK, BWV, kRawV<BWV>>(a, kvh, lane, c0 + 64, pid_next, X, more, vb);
     value_phase_mx<BWK, BWV, NG>(Y, cbv, ptile, lane, st.acc);
     pid_next = pid_after;
   };

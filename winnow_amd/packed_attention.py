@@ -214,6 +214,9 @@ def check_kernel_contract(q: torch.Tensor, kv: PackedKV, *, check_ranges: bool =
         align = 16 if pages.shape[-1] % 16 == 0 else 8
         if pages.data_ptr() % align or pages.stride(0) % align or pages.stride(1) % align:
             raise UnsupportedLayout(f"page base and strides must be {align}-byte aligned")
+        # the scans form a page block's address from page id x page stride in 32 x 32 bits
+        if not 0 <= pages.stride(0) < 2 ** 32:
+            raise UnsupportedLayout("page strides of 2^32 bytes or more")
     for norms in (kv.k_norms, kv.v_norms):
         if norms.stride(-1) != 1:
             raise UnsupportedLayout("norms need a contiguous slot axis")
