@@ -30,6 +30,9 @@ a kv head, and the LDS of a CU serves them at a rate the probe
 scan runs); ``floor_us`` is the time those reads alone need, ``scan_over_floor``
 the scan's time against it. The scan's other LDS traffic (its score tile and p
 words) comes on top.
+``allow_tf32`` times the reference's ``allow_tf32=True`` decode on the same pages
+(the TF32-class scan: single fp16 operands, fp32 accumulation) with its own sampled
+parity; the headline line stays the default, fp32-exact decode.
 """
 from __future__ import annotations
 
@@ -128,7 +131,7 @@ def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
             cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "run", "--",
                    sys.executable, str(ROOT / "bench.py"), "--config", str(cfg), "--steps", "3", "--warmup", "1",
                    "--settle", "0", "--parity", "off", "--cpu-baseline", "off", "--traffic", "off", "--append", "off",
-                   "--configs", "none",
+                   "--configs", "none", "--tf32", "off",
                    "--dequant", "off", "--dense", "off",
                    "--copy-peak", "on"]
             try:
@@ -431,11 +434,12 @@ def dequant_bench(dev, bws=(4, 6), reps: int = 50, check_rows: int = 2048, cpu_r
     return res
 
 
-def parity(w, kv=None, seqs=None):
+def parity(w, kv=None, seqs=None, allow_tf32: bool = False):
     """Same-run checks on the same pages: the first, middle and last sequences' attention
     against the CPU oracle (2e-3 max-abs / 1e-3 relative of the fp32 output) and the
     float64 oracle (relative L2), and sequence 0's first 256 tokens re-quantized by the
-    oracle against the pool bytes (adjudicated flips)."""
+    oracle against the pool bytes (adjudicated flips). ``allow_tf32`` checks the
+    TF32-class decode instead of the default one."""
     import torch
     from cases import to_host
     from oracle import attention as oa
@@ -445,7 +449,7 @@ def parity(w, kv=None, seqs=None):
     B = len(w.lens)
     seqs = seqs or sorted({0, B // 2, B - 1})
     scale = oa.default_scale(w.c["D"])
-    got = pa.packed_decode_attention(w.q, kv, scale, out_dtype=torch.float32).cpu()[seqs]
+    got = pa.packed_decode_attention(w.q, kv, scale, out_dtype=torch.float32, allow_tf32=allow_tf32).cpu()[seqs]
     sub = to_host(kv, seqs)
     qs = w.q.float().cpu()[seqs]
     ref = oa.tiled_compressed_attention(qs, sub, scale)
@@ -469,10 +473,11 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def measure_decode(w, steps: int, warmup: int, settle: float, splits=None):
+def measure_decode(w, steps: int, warmup: int, settle: float, splits=None, allow_tf32: bool = False):
     """Time ``steps`` decode steps of workload ``w`` (pools rotated between steps): the
     step time from events around the calls, the page-scan kernel from HIP events the C
-    ABI records on its stream around every launch."""
+    ABI records on its stream around every launch. ``allow_tf32`` times the TF32-class
+    decode (``wn_decode_attention_tf32``)."""
     import torch
     from winnow_amd import packed_attention as pa
 
@@ -486,7 +491,7 @@ def measure_decode(w, steps: int, warmup: int, settle: float, splits=None):
 
     def step(i, evs=None):
         return pa.packed_decode_attention(q, kvs[i % len(kvs)], scale, workspace=ws, check_ranges=False,
-                                          timing_events=evs, plan=(pps, ns))
+                                          timing_events=evs, plan=(pps, ns), allow_tf32=allow_tf32)
 
     # Bring the GPU to its sustained clocks before the warm-up steps: a few ms of work
     # otherwise times a part-clocked GPU, which a decode server running continuously
@@ -641,6 +646,9 @@ def main(argv=None):
                     help="time the quantize+pack append of 16 new tokens per sequence (BASELINE config 3)")
     ap.add_argument("--traffic", choices=["on", "off"], default="on",
                     help="measure HBM bytes per scan launch with two rocprofv3 --pmc child runs")
+    ap.add_argument("--tf32", choices=["on", "off"], default="on",
+                    help="also time the reference's allow_tf32=True decode on the same pages (scan, "
+                         "fraction of 8 TB/s, tokens/s, sampled parity), beside the default fp32-exact line")
     ap.add_argument("--lds-floor", choices=["on", "off"], default="on",
                     help="measure the LDS lookup rate (wn_probe_lds_lookup_rate, 8 waves per CU as the "
                          "row scans run) and report each scan's LDS floor beside its HBM roofline")
@@ -694,6 +702,20 @@ def main(argv=None):
     par = parity(w) if args.parity == "on" else None
     if par:
         log(f"parity: {par}")
+    tf = None
+    if args.tf32 == "on":
+        # the reference's allow_tf32=True on the same pages: the TF32-class scan where it
+        # is compiled (4-bit K and V, up to four query heads per kv head), else the same scan
+        mt = measure_decode(w, args.config_steps, min(args.warmup, 10), args.settle, args.splits, allow_tf32=True)
+        tf_kern = mt["kernel_ms"] * 1e3
+        tf = {"kernel": "decode_rows_tf_kernel" if c["bwk"] == 4 and c["bwv"] == 4 and Hq // Hkv <= 4
+              else scan_kernel_name(c),
+              "scan_us": tf_kern, "frac": bytes_step / (tf_kern * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+              "us_per_step": mt["ms_per_step"] * 1e3, "tokens_per_s": B / (mt["ms_per_step"] * 1e-3),
+              "steps": args.config_steps,
+              "products": "single fp16 operands (11 significant bits, rounded to nearest), fp32 accumulation",
+              "parity": parity(w, allow_tf32=True) if args.parity == "on" else None}
+        log(f"allow_tf32: {tf}")
     cpu = cpu_baseline(c, lens, q, w.kvs[0], args.cpu_budget) if args.cpu_baseline == "on" else None
     if cpu:
         log(f"cpu baseline: {cpu}")
@@ -752,6 +774,7 @@ def main(argv=None):
         "append": app,
         "dequant": deq,
         "parity": par,
+        "allow_tf32": tf,
     }
     print(json.dumps(result), flush=True)
     return 0

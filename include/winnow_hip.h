@@ -21,6 +21,7 @@
  *   wn_decode_attention      turboquant_kv/packed_attention_triton.py:180-187
  *                            (packed_decode_attention; kernels :51-159,
  *                            host launch :204-262)
+ *   wn_decode_attention_tf32 the same with allow_tf32=True (tl.dot :113, :127)
  *   wn_append_kv             turboquant_kv/packed_backend.py:155-161
  *                            (PagedPackedCache.update: quantize, pack, scatter)
  *   wn_quantize              turboquant_kv/cache.py:108-115 (TurboQuantMSE.quantize)
@@ -43,7 +44,7 @@
 extern "C" {
 #endif
 
-#define WN_ABI_VERSION 6
+#define WN_ABI_VERSION 7
 
 /* element types of floating-point tensors crossing the ABI */
 enum { WN_F32 = 0, WN_F16 = 1, WN_BF16 = 2 };
@@ -106,6 +107,30 @@ int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int pages_per_s
  *   ev_begin / ev_end (hipEvent_t or NULL) are recorded on `stream` around
  *   the split-K page-scan kernel only, for in-situ timing of that kernel. */
 int wn_decode_attention(
+    const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+    const float* pi_k, const float* pi_v,
+    const float* codebook_k, const float* codebook_v,
+    const uint8_t* k_pages, int64_t k_stride_p, int64_t k_stride_h,
+    const uint8_t* v_pages, int64_t v_stride_p, int64_t v_stride_h,
+    const uint16_t* k_norms, int64_t kn_stride_p, int64_t kn_stride_h,
+    const uint16_t* v_norms, int64_t vn_stride_p, int64_t vn_stride_h,
+    const int32_t* page_table, int64_t table_stride_b,
+    const int32_t* seq_lens,
+    void* out, int out_dtype,
+    void* workspace, int64_t workspace_bytes,
+    int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
+    float scale, int pages_per_split, int num_splits,
+    void* stream, void* ev_begin, void* ev_end);
+
+/* wn_decode_attention with TF32-class products: replaces the reference's
+ * packed_decode_attention(..., allow_tf32=True) (packed_attention_triton.py:180-187,
+ * whose kernel passes allow_tf32 to both tl.dot products, :113 and :127). For 4-bit K
+ * and V with up to four query heads per kv head (after the virtual-head split) on
+ * the row scan, the score and value products take single fp16 operands (11
+ * significant bits, rounded to nearest) and accumulate in fp32; every other shape
+ * runs the fp32-exact scan of wn_decode_attention. Same arguments, plan, workspace,
+ * preconditions and errors as wn_decode_attention. */
+int wn_decode_attention_tf32(
     const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
     const float* pi_k, const float* pi_v,
     const float* codebook_k, const float* codebook_v,

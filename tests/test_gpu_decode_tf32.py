@@ -1,0 +1,146 @@
+"""GPU parity of the TF32-class decode (``allow_tf32=True``, ``wn_decode_attention_tf32``)
+against the CPU oracle.
+
+The reference's kernel hands ``allow_tf32`` to both ``tl.dot`` products
+(packed_attention_triton.py:113, 127): with it set, the products take operands of ten
+stored mantissa bits and accumulate in fp32. The TF32-class row scan (4-bit K and V,
+up to four query heads per kv head after the virtual-head split) rounds each operand
+to fp16 (eleven significant bits) and accumulates in fp32. The bar is the north
+star's: within 2e-3 max-abs and 1e-3 relative of the oracle's fp32 tiled path
+(``tiled_compressed_attention``, packed_attention.py:260-311); rows of empty
+sequences are exactly zero. Shapes the TF32-class scan does not cover run the
+fp32-exact scan and give the default call's result bit for bit.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from cases import build, to_device
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+RTOL = 1e-3
+DEV = "cuda"
+RAGGED = (0, 1, 15, 16, 17, 333, 1024)
+RAGGED_WITH_GAPS = (0, 130, 0, 0, 64, 1, 700, 0, 65, 2000, 0)
+
+
+def _pa():
+    from winnow_amd import packed_attention as pa
+    return pa
+
+
+def _check(got, ref, lens):
+    got = got.float().cpu()
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs().max().item()
+    assert torch.allclose(got, ref, atol=ATOL, rtol=RTOL), f"max abs err {err:.3e}"
+    for b, L in enumerate(lens):
+        if L == 0:
+            assert (got[b] == 0).all()
+    return err
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (16, 8), (8, 8), (64, 8), (32, 2)])
+def test_tf32_matches_oracle(Hq, Hkv):
+    """n_rep 4, 2 and 1 on one head group; 8 and 16 as two and four virtual kv heads of
+    four; ragged lengths with an empty sequence, library plan and two fixed splits."""
+    print(f"tf32 Hq={Hq} Hkv={Hkv}", flush=True)
+    q, kv = build(700 + Hq + Hkv, len(RAGGED), Hq, Hkv, 128, RAGGED, 16, 4)
+    scale = oa.default_scale(128)
+    ref = oa.tiled_compressed_attention(q, kv, scale)
+    dkv = to_device(kv, DEV)
+    for splits in (None, 2):
+        got = _pa().packed_decode_attention(q.to(DEV), dkv, scale, num_splits=splits, allow_tf32=True,
+                                            out_dtype=torch.float32)
+        _check(got, ref, RAGGED)
+
+
+@pytest.mark.parametrize("waves", [1, 5, 37])
+def test_tf32_balanced_plan_with_few_waves(waves):
+    """A balanced plan over a handful of waves: each wave scans runs of chunks, crosses
+    (sequence, kv head) boundaries and skips zero-length sequences mid-share."""
+    lens = RAGGED_WITH_GAPS
+    print(f"tf32 balanced {waves} waves", flush=True)
+    q, kv = build(800 + waves, len(lens), 32, 8, 128, lens, 16, 4)
+    scale = oa.default_scale(128)
+    ref = oa.tiled_compressed_attention(q, kv, scale)
+    got = _pa().packed_decode_attention(q.to(DEV), to_device(kv, DEV), scale, plan=(0, waves), allow_tf32=True,
+                                        out_dtype=torch.float32)
+    _check(got, ref, lens)
+
+
+def _round11(x: torch.Tensor) -> torch.Tensor:
+    """x rounded to 11 significant bits, ties to even (fp16's significand, no range limit)."""
+    m, e = torch.frexp(x.double())
+    return torch.ldexp(torch.round(m * 2048) / 2048, e)
+
+
+def tf32_class_reference(q: torch.Tensor, kv, scale: float) -> torch.Tensor:
+    """float64 decode attention whose score and value operands are first rounded as the
+    TF32-class scan rounds them: the rotated, scaled query (in log2 units, as the scan
+    carries it) and both codebooks to 11 significant bits. The p n_V operand's rounding
+    (2^-12 relative per term) is left out; everything else is exact."""
+    B, Hq, _, D = q.shape
+    n_rep = Hq // kv.num_kv_heads
+    log2e = 1.0 / math.log(2.0)
+    ck_t, cv_t = _round11(kv.k_quant.centroids), _round11(kv.v_quant.centroids)
+    q_rot = (q[:, :, 0].double() @ kv.k_quant.Pi.double().T) * scale
+    q_r = _round11(q_rot * log2e) / log2e
+    out = torch.zeros(B, Hq, 1, D, dtype=torch.float64)
+    heads = torch.arange(Hq) // n_rep
+    for b in range(B):
+        if int(kv.seq_lens[b]) == 0:
+            continue
+        pk, nk = oa._gather_history(kv.k_pages, kv.k_norms, kv, b)
+        pv, nv = oa._gather_history(kv.v_pages, kv.v_norms, kv, b)
+        ck = ck_t[oa.unpack_t(pk, kv.k_quant.bit_width, D).long()] * nk.double()[..., None]
+        cv = cv_t[oa.unpack_t(pv, kv.v_quant.bit_width, D).long()] * nv.double()[..., None]
+        s = (q_r[b][:, None, :] @ ck[heads].transpose(-1, -2))[:, 0]          # (Hq, L)
+        a = torch.softmax(s, -1)[:, None, :] @ cv[heads]                        # (Hq, 1, D)
+        out[b] = a @ kv.v_quant.Pi.double()
+    return out
+
+
+def test_tf32_large_scores_and_long_history():
+    """Scores 50 times larger (the lazy maximum moves often) over 4,096 and 2,500 tokens,
+    S=32. Here the TF32-class rounding itself moves scores of several hundred by tenths,
+    beyond the fp32 bar, as the reference's allow_tf32 does; so the result is checked
+    against the float64 decode of operands rounded the same way (tf32_class_reference),
+    at the north-star tolerance. The default call stays within the bar of the fp32
+    oracle, and the two results differ (the TF32-class scan ran)."""
+    lens = (4096, 2500)
+    q, kv = build(901, len(lens), 32, 8, 128, lens, 32, 4, q_scale=50.0)
+    scale = oa.default_scale(128)
+    dkv, qd = to_device(kv, DEV), q.to(DEV)
+    tf = _pa().packed_decode_attention(qd, dkv, scale, allow_tf32=True, out_dtype=torch.float32)
+    exact = _pa().packed_decode_attention(qd, dkv, scale, out_dtype=torch.float32)
+    _check(tf, tf32_class_reference(q, kv, scale).float(), lens)
+    _check(exact, oa.tiled_compressed_attention(q, kv, scale), lens)
+    assert not torch.equal(tf, exact)
+
+
+def test_tf32_matches_the_rounded_operand_reference():
+    """At ordinary scales the TF32-class result also sits within the bar of the decode of
+    rounded operands (the check above, on the ragged batch)."""
+    q, kv = build(902, len(RAGGED), 32, 8, 128, RAGGED, 16, 4)
+    scale = oa.default_scale(128)
+    tf = _pa().packed_decode_attention(q.to(DEV), to_device(kv, DEV), scale, allow_tf32=True,
+                                       out_dtype=torch.float32)
+    _check(tf, tf32_class_reference(q, kv, scale).float(), RAGGED)
+
+
+@pytest.mark.parametrize("bwk,bwv,Hq,Hkv", [(6, 6, 32, 8), (4, 6, 64, 8), (2, 2, 16, 4)])
+def test_tf32_other_shapes_run_the_exact_scan(bwk, bwv, Hq, Hkv):
+    """Widths without a TF32-class scan give the default call's output bit for bit."""
+    q, kv = build(950 + bwk + bwv, len(RAGGED), Hq, Hkv, 128, RAGGED, 16, bwk, bw_v=bwv)
+    scale = oa.default_scale(128)
+    dkv, qd = to_device(kv, DEV), q.to(DEV)
+    tf = _pa().packed_decode_attention(qd, dkv, scale, allow_tf32=True, out_dtype=torch.float32)
+    exact = _pa().packed_decode_attention(qd, dkv, scale, out_dtype=torch.float32)
+    assert torch.equal(tf, exact)

@@ -318,12 +318,15 @@ int valu_groups(int n_rep) {
 // scan where it applies (head_dim 128, page size >= 16, a compiled width pair, any
 // n_rep that 2^s virtual heads bring to <= 8), else the vector-ALU scan (any
 // supported width pair, n_rep split into groups of <= 16).
-SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v) {
+// tf32: the TF32-class row scan where it is compiled (4-bit K and V, up to four query
+// heads per virtual kv head), else the same choice as without it.
+SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v, bool tf32 = false) {
   SplitKernel sk;
   const int n_rep = Hq / Hkv;
   const int shift = row_shift(n_rep);
   if (D == 128 && shift >= 0 && S >= 16 && rows_allowed()) {
-    sk = pick_split_rows(bw_k, bw_v, n_rep >> shift);
+    if (tf32) sk = pick_split_rows_tf(bw_k, bw_v, n_rep >> shift);
+    if (!sk.fn) sk = pick_split_rows(bw_k, bw_v, n_rep >> shift);
     if (sk.fn) {
       sk.kvshift = shift;
       sk.kvdiv = 1 << shift;
@@ -455,7 +458,9 @@ extern "C" int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int 
   return wn::ws_layout(B, Hq, Hkv, D, pages_per_split, num_splits).total;
 }
 
-extern "C" int wn_decode_attention(
+namespace {
+// wn_decode_attention and wn_decode_attention_tf32: tf32 picks the TF32-class scan.
+int decode_attention(
     const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
     const float* pi_k, const float* pi_v, const float* codebook_k, const float* codebook_v,
     const uint8_t* k_pages, int64_t k_stride_p, int64_t k_stride_h,
@@ -466,7 +471,7 @@ extern "C" int wn_decode_attention(
     void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
     int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
     float scale, int pages_per_split, int num_splits,
-    void* stream, void* ev_begin, void* ev_end) {
+    void* stream, void* ev_begin, void* ev_end, bool tf32) {
   using namespace wn;
   clear_error();
   WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, WN_E_INVALID,
@@ -505,7 +510,7 @@ extern "C" int wn_decode_attention(
   WN_REQUIRE(k_stride_p >= 0 && k_stride_p < 2 * lim && v_stride_p >= 0 && v_stride_p < 2 * lim, WN_E_INVALID,
              "decode: page strides of 2^32 bytes or more");
 
-  const SplitKernel sk = choose_scan(Hq, Hkv, D, S, bw_k, bw_v);
+  const SplitKernel sk = choose_scan(Hq, Hkv, D, S, bw_k, bw_v, tf32);
   RotFn rot = pick_rot_d(D, max(sk.nrep, 1));
   WN_REQUIRE(sk.fn && rot, WN_E_UNSUPPORTED, "decode: (D=%d, bw_k=%d, bw_v=%d) not compiled", D, bw_k,
              bw_v);
@@ -571,8 +576,31 @@ extern "C" int wn_decode_attention(
 
   MergeArgs ma{da.part_acc, da.part_ml, pi_v, meta, out, out_dtype, Hq, Hkv_s, n_rep_s, sk.log2_units ? 1 : 0};
   launch_merge(D, dim3(n_rep_s, Hkv_s, B), st, ma);
-  return check_launch("wn_decode_attention");
+  return check_launch(tf32 ? "wn_decode_attention_tf32" : "wn_decode_attention");
 }
+}  // namespace
+
+#define WN_DECODE_PARAMS                                                                                       \
+  const void *q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h, const float *pi_k, const float *pi_v,    \
+      const float *codebook_k, const float *codebook_v, const uint8_t *k_pages, int64_t k_stride_p,            \
+      int64_t k_stride_h, const uint8_t *v_pages, int64_t v_stride_p, int64_t v_stride_h,                      \
+      const uint16_t *k_norms, int64_t kn_stride_p, int64_t kn_stride_h, const uint16_t *v_norms,              \
+      int64_t vn_stride_p, int64_t vn_stride_h, const int32_t *page_table, int64_t table_stride_b,             \
+      const int32_t *seq_lens, void *out, int out_dtype, void *workspace, int64_t workspace_bytes, int B,      \
+      int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages, float scale, int pages_per_split,      \
+      int num_splits, void *stream, void *ev_begin, void *ev_end
+#define WN_DECODE_ARGS                                                                                          \
+  q, q_dtype, q_stride_b, q_stride_h, pi_k, pi_v, codebook_k, codebook_v, k_pages, k_stride_p, k_stride_h,    \
+      v_pages, v_stride_p, v_stride_h, k_norms, kn_stride_p, kn_stride_h, v_norms, vn_stride_p, vn_stride_h,   \
+      page_table, table_stride_b, seq_lens, out, out_dtype, workspace, workspace_bytes, B, Hq, Hkv, D, S,     \
+      bw_k, bw_v, max_pages, scale, pages_per_split, num_splits, stream, ev_begin, ev_end
+
+extern "C" int wn_decode_attention(WN_DECODE_PARAMS) { return decode_attention(WN_DECODE_ARGS, false); }
+
+extern "C" int wn_decode_attention_tf32(WN_DECODE_PARAMS) { return decode_attention(WN_DECODE_ARGS, true); }
+
+#undef WN_DECODE_PARAMS
+#undef WN_DECODE_ARGS
 
 // ------------------------------------------------- allocation-free decode entry
 

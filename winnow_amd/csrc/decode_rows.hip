@@ -1215,6 +1215,225 @@ __device__ __forceinline__ void value_phase_mx(RowBuf<BWK, BWV>& V, Tab<BWV>& cb
   });
 }
 
+// ------------------------------------------------------------------ TF32-class products
+//
+// allow_tf32 (packed_attention_triton.py:113, 127): both products on single fp16
+// operands, 11 significant bits each (the class of TF32's 10 stored bits), accumulated
+// in fp32; 4-bit K and V, one head group. A table entry holds H(2^8 c) of the two
+// codes of a byte (4 bytes), replicated once per lane of the wave (entry (b, r) at
+// byte 256 b + 4 r of a 64 KB slot), so one SDWA move forms its address as in the
+// 16-bit scan and no read waits on a bank conflict. Without the L halves an 8-slot
+// operand carries eight codes: the scores take 4 K-steps per tile (16 MFMAs per
+// chunk) and the values 2 K-steps per M-tile (16 MFMAs), half the 16-bit scan's
+// matrix-core work, and the lookups read 4 bytes instead of 8.
+//   scores  K-step s of tile r: k-slots of group g = dims 32g + 8s + (0..7); column
+//           c < 4 is H(q' head c), the other columns zero.
+//   values  K-step ks: k-slots of group g = tokens 32ks + 4j + g, j = 0..7 (token quads
+//           8ks + j of the V buffer); column c < 4 is H(p n_V 2^-gs) of head c, read
+//           from an fp16 p tile whose 8 halves per (head, ks, g) sit side by side.
+
+constexpr int kTfTableBytes = 256 * 64 * 4;  // 256 byte values x 64 lanes x two fp16
+static_assert(kTfTableBytes == kPairTableBytes, "the TF table takes the 64 KB slot of the 16-bit table");
+
+// Stages the replicated TF table: entry (b, r) holds (H(2^8 c[b & 15]), H(2^8 c[b >> 4])),
+// rounded to nearest.
+__device__ __forceinline__ void stage_table_tf(const float* cb, char* dst, int tid, int nthr) {
+  uint32_t* t = reinterpret_cast<uint32_t*>(dst);
+  for (int i = tid; i < 256 * 64; i += nthr) {
+    const int b = i >> 6;
+    const _Float16 lo = _Float16(cb[b & 15] * kCbScale), hi = _Float16(cb[b >> 4] * kCbScale);
+    t[i] = uint32_t(__builtin_bit_cast(uint16_t, lo)) | uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16;
+  }
+}
+
+// The TF table as one lane reads it: address registers 4 lane | slot << 16, one per
+// byte position of a code word (the code byte goes to bits 8-15).
+struct TabTf {
+  const char* lds;
+  uint32_t r[4];
+  __device__ void init(const char* base, int slot, int lane) {
+    lds = base;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r[k] = uint32_t(4 * lane) | (uint32_t(slot) << 16);
+  }
+};
+
+// Entry of the 4-bit pair in byte K of x: one SDWA move, one 4-byte LDS read.
+template <int K>
+__device__ __forceinline__ uint32_t entry_tf(TabTf& tab, uint32_t x) {
+  tab.r[K] = put_byte1<K>(tab.r[K], x);
+  return *reinterpret_cast<const uint32_t*>(tab.lds + tab.r[K]);
+}
+
+constexpr int kTfLookahead = 4;  // K-steps of table reads in flight ahead of their MFMA
+
+// fp16 p tile of a wave (after its score tile): 4 heads x 64 tokens, token l of the
+// chunk at half 32 (l >> 5) + 8 (l & 3) + ((l >> 2) & 7) of its head's row.
+constexpr int kTfPTileOffset = 4 * kTileStride;  // words
+
+// Scores of a chunk into the score tile (head h of token 16r + 4i + g at word
+// h * kTileStride + 16r + 4g + i), before the 2^-(e+8) scale.
+template <int BWK, int BWV>
+__device__ __forceinline__ void score_phase_tf(const RowBuf<BWK, BWV>& K, TabTf& cbk, const h8 (&qb)[4], int lane,
+                                               uint32_t* pt) {
+  constexpr int LA = kTfLookahead;
+  f32x4 d[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) d[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // step k = 4s + r: word s of the quarter (dims 8s .. 8s+7) of tile r
+  uint32_t e[LA + 1][4];
+  auto look = [&](auto kc, uint32_t (&o)[4]) {
+    constexpr int k = decltype(kc)::value, s = k >> 2, r = k & 3;
+    const uint32_t w = K.w[r * BWK + s];
+    o[0] = entry_tf<0>(cbk, w);
+    o[1] = entry_tf<1>(cbk, w);
+    o[2] = entry_tf<2>(cbk, w);
+    o[3] = entry_tf<3>(cbk, w);
+  };
+  static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
+  __builtin_amdgcn_sched_barrier(0);
+  static_for<0, 16>([&](auto kc) {
+    constexpr int k = decltype(kc)::value, j = k % (LA + 1);
+    if constexpr (k + LA < 16) {
+      look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    d[k & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        __builtin_bit_cast(h8, u32x4{e[j][0], e[j][1], e[j][2], e[j][3]}), qb[k >> 2], d[k & 3], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  const int c = lane & 15, g = lane >> 4;
+  wave_lds_sync();  // the previous chunk's reads of the tile are done
+  if (c < 4) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<float4*>(pt + c * kTileStride + 16 * r + 4 * g) = make_float4(d[r][0], d[r][1], d[r][2], d[r][3]);
+  }
+  wave_lds_sync();
+}
+
+// Online softmax of one chunk (lane = token) from the score tile; H(p n_V 2^-gs) goes to
+// the fp16 p tile. Maxima, the value scale and the rescales as softmax_phase_mx.
+__device__ __forceinline__ void softmax_phase_tf(float sc, uint32_t nk_h, uint32_t nv_h, bool valid, int lane,
+                                                 uint32_t* pt, MxState<1>& st) {
+  constexpr int H = 4;
+  const int off = 16 * (lane >> 4) + 4 * (lane & 3) + ((lane >> 2) & 3);  // word of token lane
+  const float nk = half_lo(nk_h) * sc;
+  const float nv = valid ? half_lo(nv_h) : 0.f;
+  float sv[H];
+#pragma unroll
+  for (int i = 0; i < H; ++i) sv[i] = valid ? __builtin_bit_cast(float, pt[i * kTileStride + off]) * nk : -INFINITY;
+  if (__any(nv >= ldexpf(1.f, 7 + st.gs))) {  // wave-uniform, rare
+    int ge;
+    frexpf(wave_max_nonneg(nv), &ge);
+    const int gs_need = max(0, ge - 7);
+    const float f = ldexpf(1.f, st.gs - gs_need);
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) st.acc[mm] *= f;
+    st.gs = gs_need;
+  }
+  bool move = st.m[0] == -INFINITY;
+#pragma unroll
+  for (int i = 0; i < H; ++i) move = move || __any(sv[i] > st.m[i] + kRescale);
+  if (move) {  // wave-uniform
+    const int hc = (lane & 15) % H;  // head of this lane's accumulator column (columns >= 4 hold zeros)
+    float alpha_c = 1.f;
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const float m_new = fmaxf(st.m[i], wave_max_dpp(sv[i]));
+      const float alpha = __builtin_amdgcn_exp2f(st.m[i] - m_new);  // 0 on the first chunk
+      st.m[i] = m_new;
+      st.l[i] *= alpha;
+      alpha_c = hc == i ? alpha : alpha_c;
+    }
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) st.acc[mm] *= alpha_c;
+  }
+  const float nvs = ldexpf(nv, -st.gs);
+  _Float16* ph = reinterpret_cast<_Float16*>(pt + kTfPTileOffset);
+  const int slot = 32 * (lane >> 5) + 8 * (lane & 3) + ((lane >> 2) & 7);
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const float p = __builtin_amdgcn_exp2f(sv[i] - st.m[i]);  // 0 for masked tokens
+    st.l[i] += p;
+    ph[64 * i + slot] = _Float16(p * nvs);
+  }
+  wave_lds_sync();
+}
+
+// Values of a chunk: 2 K-steps (32 tokens each) x 8 M-tiles (one dim of each lane's
+// eight), one MFMA each; 4-bit V codes of token pairs (j, j+1) merged into bytes.
+template <int BWK, int BWV>
+__device__ __forceinline__ void value_phase_tf(const RowBuf<BWK, BWV>& V, TabTf& cbv, const uint32_t* pt, int lane,
+                                               f32x4 (&acc)[8]) {
+  constexpr int LA = kTfLookahead;
+  const int c = lane & 15, g = lane >> 4;
+  const _Float16* ph = reinterpret_cast<const _Float16*>(pt + kTfPTileOffset);
+  const uint4* prow = reinterpret_cast<const uint4*>(ph + 64 * (c & 3) + 8 * g);
+  const bool live = c < 4;
+  // step k = 8ks + mt
+  auto look = [&](auto kc, uint32_t (&o)[4]) {
+    constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t wa = V.w[8 * ks + 2 * p], wb = V.w[8 * ks + 2 * p + 1];
+      const uint32_t x = (mt & 1) ? (((wa >> 4) & 0x0F0F0F0Fu) | (wb & 0xF0F0F0F0u))
+                                  : ((wa & 0x0F0F0F0Fu) | ((wb << 4) & 0xF0F0F0F0u));
+      o[p] = entry_tf<(mt >> 1)>(cbv, x);
+    }
+  };
+  uint4 wq = prow[0];  // p halves of K-step 0; K-step 1's are read during K-step 0
+  uint32_t e[LA + 1][4];
+  static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
+  h8 bq;
+  __builtin_amdgcn_sched_barrier(0);
+  static_for<0, 16>([&](auto kc) {
+    constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7, j = k % (LA + 1);
+    if constexpr (mt == 0) {
+      bq = __builtin_bit_cast(h8, live ? u32x4{wq.x, wq.y, wq.z, wq.w} : u32x4{0u, 0u, 0u, 0u});
+      if constexpr (ks == 0) wq = prow[4];  // 32 halves further: K-step 1
+    }
+    if constexpr (k + LA < 16) {
+      look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, u32x4{e[j][0], e[j][1], e[j][2], e[j][3]}),
+                                                     bq, acc[mt], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
+// Undoes the value scale and writes the (acc, m, l) partial of each query head h <
+// n_rep to row prow * n_rep + h: lane 16g + h writes dims 32g .. 32g+31 (columns hold
+// whole values: no halves to add).
+__device__ __forceinline__ void write_partial_tf(const DecodeArgs& a, MxState<1>& st, int64_t prow, int lane) {
+  constexpr int D = 128, H = 4;
+  const float f = ldexpf(1.f, st.gs - 8);
+#pragma unroll
+  for (int i = 0; i < H; ++i) st.l[i] = wave_sum(st.l[i]);
+  const int64_t row0 = prow * a.n_rep;
+  const int c = lane & 15, g = lane >> 4;
+  if (c < H && c < a.n_rep) {
+    float* dst = a.part_acc + (row0 + c) * D + 32 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<float4*>(dst + 8 * i) =
+          make_float4(st.acc[0][i] * f, st.acc[1][i] * f, st.acc[2][i] * f, st.acc[3][i] * f);
+      *reinterpret_cast<float4*>(dst + 8 * i + 4) =
+          make_float4(st.acc[4][i] * f, st.acc[5][i] * f, st.acc[6][i] * f, st.acc[7][i] * f);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      if (i < a.n_rep) {
+        a.part_ml[2 * (row0 + i)] = st.m[i];
+        a.part_ml[2 * (row0 + i) + 1] = st.l[i];
+      }
+    }
+  }
+}
+
 // Adds the column halves, undoes the value scale and writes the (acc, m, l) partial of
 // each query head h < n_rep to row prow * n_rep + h: lane 16g + h writes dims
 // 32g .. 32g+31.
@@ -1251,10 +1470,12 @@ __device__ __forceinline__ void write_partial_mx(const DecodeArgs& a, MxState<NG
   }
 }
 
-// scan_range on the 16x16x32 fp16 MFMA.
-template <int BWK, int BWV, int NG>
+// scan_range on the 16x16x32 fp16 MFMA; TF: the TF32-class products (4-bit, one head
+// group, TabTf tables).
+template <int BWK, int BWV, int NG, bool TF, class TabK, class TabV>
 __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh, int t_lo, int t_hi, int64_t prow,
-                                             int lane, Tab<BWK>& cbk, Tab<BWV>& cbv, uint32_t* ptile) {
+                                             int lane, TabK& cbk, TabV& cbv, uint32_t* ptile) {
+  static_assert(!TF || (BWK == 4 && BWV == 4 && NG == 1), "TF32-class scan: 4-bit K and V, one head group");
   constexpr int D = 128, NH = 4 * NG;
   const int page_hi = (t_hi + (1 << a.log2S) - 1) >> a.log2S;
   const int n = (t_hi - t_lo + 63) >> 6;
@@ -1283,12 +1504,20 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
   frexpf(uniform(wave_max(amax)), &qe);
   const int e = 15 - qe;  // |q| < 2^qe, so |q 2^e| < 2^15
   const float sc = ldexpf(1.f, -(e + 8));
-  const uint32_t qsel = c < NH ? 0x01000100u : c < 2 * NH ? 0x03020302u : 0x0c0c0c0cu;
-  h8 qb[8];
+  h8 qb[TF ? 4 : 8];
+  if constexpr (TF) {
+    // K-step s: dims 32g + 8s + (0..7) of q' head c, rounded to nearest; zero past column 3
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
-    qb[s] = dup4(split_word(ldexpf(qv[4 * s], e)), split_word(ldexpf(qv[4 * s + 1], e)),
-                 split_word(ldexpf(qv[4 * s + 2], e)), split_word(ldexpf(qv[4 * s + 3], e)), qsel);
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qb[s][j] = c < NH ? _Float16(ldexpf(qv[8 * s + j], e)) : _Float16(0.f);
+  } else {
+    const uint32_t qsel = c < NH ? 0x01000100u : c < 2 * NH ? 0x03020302u : 0x0c0c0c0cu;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      qb[s] = dup4(split_word(ldexpf(qv[4 * s], e)), split_word(ldexpf(qv[4 * s + 1], e)),
+                   split_word(ldexpf(qv[4 * s + 2], e)), split_word(ldexpf(qv[4 * s + 3], e)), qsel);
+  }
 
   const int32_t* trow = a.table + b * a.tsb;
   auto pid_of = [&](int ch) {
@@ -1322,11 +1551,17 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
     uint64_t kb[4], vb[4];
     block_bases<16 * BWK>(kbase, uint32_t(a.ksp), pid_next, c0 + 64, lane, smask, kb);
     load_k16(a, kvh, lane, c0 + 64, pid_next, Z, more, kb);
-    score_phase_mx<BWK, BWV, NG>(X, cbk, qb, lane, ptile);
-    softmax_phase_mx<NG>(sc, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
+    if constexpr (TF) {
+      score_phase_tf<BWK, BWV>(X, cbk, qb, lane, ptile);
+      softmax_phase_tf(sc, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
+    } else {
+      score_phase_mx<BWK, BWV, NG>(X, cbk, qb, lane, ptile);
+      softmax_phase_mx<NG>(sc, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
+    }
     block_bases<16 * BWV>(vbase, uint32_t(a.vsp), pid_next, c0 + 64, lane, smask, vb);
     load_v<BWK, BWV, kRawV<BWV>>(a, kvh, lane, c0 + 64, pid_next, X, more, vb);
-    value_phase_mx<BWK, BWV, NG>(Y, cbv, ptile, lane, st.acc);
+    if constexpr (TF) value_phase_tf<BWK, BWV>(Y, cbv, ptile, lane, st.acc);
+    else value_phase_mx<BWK, BWV, NG>(Y, cbv, ptile, lane, st.acc);
     pid_next = pid_after;
   };
 
@@ -1345,7 +1580,8 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
   }
   if (ch < n) step(ch, b0, b1, b2);
   if (ch + 1 < n) step(ch + 1, b2, b0, b1);
-  write_partial_mx<NG>(a, st, prow, lane);
+  if constexpr (TF) write_partial_tf(a, st, prow, lane);
+  else write_partial_mx<NG>(a, st, prow, lane);
 }
 
 template <int BWK, int BWV, int NG, int WPB>
@@ -1372,7 +1608,30 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows16_kernel(DecodeArgs a) {
   Tab<BWK> cbk = make_tab<BWK>(lds, Lay::k_off, lane);
   Tab<BWV> cbv = make_tab<BWV>(lds, Lay::v_off, lane);
   for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow) {
-    scan_range16<BWK, BWV, NG>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+    scan_range16<BWK, BWV, NG, false>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+  });
+}
+
+// The TF32-class row scan (allow_tf32): 4-bit K and V, one head group, the 16-bit
+// scan's plan, loads and LDS layout with TF tables in the two 64 KB slots.
+template <int WPB>
+__global__ __launch_bounds__(64 * WPB) void decode_rows_tf_kernel(DecodeArgs a) {
+  using Lay = Rows16Lds<4, 4, 1, WPB>;
+  static_assert(Lay::k_off == 0 && Lay::v_off == kTfTableBytes, "TF tables in slots 0 and 1");
+  static_assert(Lay::tile_bytes >= (kTfPTileOffset + 4 * 64 / 2) * 4, "score and p tiles fit a wave's tile");
+  __shared__ __align__(16) char lds[Lay::total];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
+  stage_table_tf(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
+  stage_table_tf(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
+  __syncthreads();  // the only block-wide barrier: waves run independently from here
+  const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
+  uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);
+  TabTf cbk, cbv;
+  cbk.init(lds, 0, lane);
+  cbv.init(lds, 1, lane);
+  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow) {
+    scan_range16<4, 4, 1, true>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
   });
 }
 
@@ -1459,6 +1718,19 @@ bool rows16_allowed() {
 }
 
 }  // namespace
+
+SplitKernel pick_split_rows_tf(int bw_k, int bw_v, int n_rep) {
+  if (bw_k != 4 || bw_v != 4 || n_rep < 1 || n_rep > 4 || !rows16_allowed()) return SplitKernel{};
+  constexpr int wpb = 8;  // the 16-bit scan's work-group and plan
+  SplitKernel k;
+  k.fn = decode_rows_tf_kernel<wpb>;
+  k.block = 64 * wpb;
+  k.wpb = wpb;
+  k.nrep = 4;
+  k.log2_units = true;
+  k.rows = true;
+  return k;
+}
 
 SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep) {
   const int ng = n_rep <= 4 ? 1 : n_rep <= 8 ? 2 : 0;

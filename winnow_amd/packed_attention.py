@@ -271,8 +271,12 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
     ``num_splits=None`` lets the library plan the split: persistent waves that
     share the batch's chunks equally where the row scan applies, else splits
     sized to fill the GPU; an integer asks for exactly that many splits over the page-table
-    width, as the reference does. ``allow_tf32``, ``num_warps``, ``num_stages``
-    are Triton schedule knobs, accepted for call compatibility and ignored;
+    width, as the reference does. ``allow_tf32=True`` asks, as in the reference
+    (whose kernel hands it to both ``tl.dot`` products), for TF32-class products:
+    ``wn_decode_attention_tf32`` runs 4-bit K and V with up to four query heads per kv
+    head on single fp16 operands (11 significant bits) with fp32 accumulation, and
+    every other shape on the fp32-exact scan. ``num_warps`` and ``num_stages`` are
+    Triton schedule knobs, accepted for call compatibility and ignored;
     ``pages_per_iter`` must still be a power of two. ``out_dtype=torch.float32``
     returns the fp32 result before the cast (for parity checks). ``workspace``
     is an optional caller-owned uint8 buffer of at least ``workspace_bytes``.
@@ -282,7 +286,7 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
     scans several chunks when the batch has more than ``w``), ``(p, n)`` with
     ``p * n >= max_pages`` fixed splits.
     """
-    del allow_tf32, num_warps, num_stages
+    del num_warps, num_stages
     if pages_per_iter < 1 or pages_per_iter & (pages_per_iter - 1):
         raise UnsupportedLayout("pages_per_iter must be a power of two >= 1")
     check_kernel_contract(q, kv, check_ranges=check_ranges)
@@ -300,7 +304,8 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
         raise UnsupportedLayout(f"workspace needs {need} bytes on {q.device}")
     ev0, ev1 = timing_events or (None, None)
     with torch.cuda.device(q.device):
-        _lib.call("wn_decode_attention", *_operands(q, kv), _lib.ptr(out), _lib.DTYPE_CODE[out_dtype],
+        entry = "wn_decode_attention_tf32" if allow_tf32 else "wn_decode_attention"
+        _lib.call(entry, *_operands(q, kv), _lib.ptr(out), _lib.DTYPE_CODE[out_dtype],
                   _lib.ptr(workspace), workspace.numel() * workspace.element_size(),
                   *_sizes(q, kv), float(scale), pps, ns, _lib.stream_of(q.device), ev0, ev1)
     return out
