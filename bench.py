@@ -484,7 +484,7 @@ def measure_decode(w, steps: int, warmup: int, settle: float, splits=None, allow
     q, kvs = w.q, w.kvs
     B, Hq, Hkv, D = len(w.lens), w.c["Hq"], w.c["Hkv"], w.c["D"]
     scale = 1.0 / math.sqrt(D)
-    pps, ns = pa.plan_for(q, kvs[0], splits)
+    pps, ns = pa.plan_for(q, kvs[0], splits, allow_tf32)
     ws = torch.empty(pa.workspace_bytes(B, Hq, Hkv, D, pps, ns), dtype=torch.uint8, device=q.device)
     for kv in kvs:
         pa.check_kernel_contract(q, kv)          # full validation once, outside the timed region

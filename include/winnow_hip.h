@@ -122,14 +122,20 @@ int wn_decode_attention(
     float scale, int pages_per_split, int num_splits,
     void* stream, void* ev_begin, void* ev_end);
 
+/* wn_decode_plan for wn_decode_attention_tf32: its scan may keep more waves resident,
+ * so its balanced plan may have more splits. Same arguments and results. */
+int wn_decode_plan_tf32(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
+                        int requested_splits, int* pages_per_split, int* num_splits);
+
 /* wn_decode_attention with TF32-class products: replaces the reference's
  * packed_decode_attention(..., allow_tf32=True) (packed_attention_triton.py:180-187,
  * whose kernel passes allow_tf32 to both tl.dot products, :113 and :127). For 4-bit K
  * and V with up to four query heads per kv head (after the virtual-head split) on
  * the row scan, the score and value products take single fp16 operands (11
  * significant bits, rounded to nearest) and accumulate in fp32; every other shape
- * runs the fp32-exact scan of wn_decode_attention. Same arguments, plan, workspace,
- * preconditions and errors as wn_decode_attention. */
+ * runs the fp32-exact scan of wn_decode_attention. Same arguments, workspace,
+ * preconditions and errors as wn_decode_attention; the plan comes from
+ * wn_decode_plan_tf32. */
 int wn_decode_attention_tf32(
     const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
     const float* pi_k, const float* pi_v,

@@ -30,6 +30,8 @@ SIGNATURES = {
     "wn_last_error": (ctypes.c_char_p, []),
     "wn_decode_plan": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,
                               ctypes.POINTER(_c_i), ctypes.POINTER(_c_i)]),
+    "wn_decode_plan_tf32": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,
+                                   ctypes.POINTER(_c_i), ctypes.POINTER(_c_i)]),
     "wn_decode_workspace_bytes": (_c_i64, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i]),
     "wn_decode_attention": (_c_i, [
         _c_p, _c_i, _c_i64, _c_i64,                 # q, dtype, strides

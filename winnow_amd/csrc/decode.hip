@@ -425,8 +425,9 @@ static void fixed_plan(int B, int units_per_seq, int mp, int* pages_per_split, i
   *num_splits = int((mp + pps - 1) / pps);
 }
 
-extern "C" int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
-                              int requested_splits, int* pages_per_split, int* num_splits) {
+namespace {
+int decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages, int requested_splits,
+                int* pages_per_split, int* num_splits, bool tf32) {
   using namespace wn;
   clear_error();
   WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && max_pages >= 0, WN_E_INVALID,
@@ -441,7 +442,7 @@ extern "C" int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, in
     *pages_per_split = (mp + ns - 1) / ns;
     return WN_OK;
   }
-  const SplitKernel sk = choose_scan(Hq, Hkv, D, S, bw_k, bw_v);
+  const SplitKernel sk = choose_scan(Hq, Hkv, D, S, bw_k, bw_v, tf32);
   if (sk.fn && sk.rows) {  // row scan: balanced persistent waves
     const int w = resident_waves(sk);
     WN_REQUIRE(w > 0, WN_E_LAUNCH, "wn_decode_plan: cannot query the device occupancy");
@@ -451,6 +452,19 @@ extern "C" int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, in
   }
   fixed_plan(B, Hkv * sk.kvdiv, mp, pages_per_split, num_splits);
   return WN_OK;
+}
+}  // namespace
+
+extern "C" int wn_decode_plan(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
+                              int requested_splits, int* pages_per_split, int* num_splits) {
+  return decode_plan(B, Hq, Hkv, D, S, bw_k, bw_v, max_pages, requested_splits, pages_per_split, num_splits,
+                     false);
+}
+
+extern "C" int wn_decode_plan_tf32(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v, int max_pages,
+                                   int requested_splits, int* pages_per_split, int* num_splits) {
+  return decode_plan(B, Hq, Hkv, D, S, bw_k, bw_v, max_pages, requested_splits, pages_per_split, num_splits,
+                     true);
 }
 
 extern "C" int64_t wn_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int pages_per_split, int num_splits) {

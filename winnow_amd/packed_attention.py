@@ -233,15 +233,18 @@ def check_kernel_contract(q: torch.Tensor, kv: PackedKV, *, check_ranges: bool =
 
 
 def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
-                bits_k: int, bits_v: int, max_pages: int, num_splits: int | None = None):
-    """(pages_per_split, num_splits) the HIP decode uses for this shape (wn_decode_plan).
+                bits_k: int, bits_v: int, max_pages: int, num_splits: int | None = None,
+                allow_tf32: bool = False):
+    """(pages_per_split, num_splits) the HIP decode uses for this shape (wn_decode_plan,
+    or wn_decode_plan_tf32 for the allow_tf32 decode, whose scan may keep more waves).
 
     pages_per_split == 0 is a balanced plan: num_splits persistent waves share
     the batch's 64-token chunks equally.
     """
     pps, ns = ctypes.c_int(0), ctypes.c_int(0)
-    _lib.call("wn_decode_plan", batch, num_q_heads, num_kv_heads, head_dim, page_size, bits_k, bits_v,
-              max_pages, int(num_splits or 0), ctypes.byref(pps), ctypes.byref(ns))
+    _lib.call("wn_decode_plan_tf32" if allow_tf32 else "wn_decode_plan", batch, num_q_heads, num_kv_heads,
+              head_dim, page_size, bits_k, bits_v, max_pages, int(num_splits or 0), ctypes.byref(pps),
+              ctypes.byref(ns))
     return pps.value, ns.value
 
 
@@ -251,12 +254,12 @@ def workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: i
                                                     pages_per_split, num_splits))
 
 
-def plan_for(q: torch.Tensor, kv: PackedKV, num_splits: int | None = None):
+def plan_for(q: torch.Tensor, kv: PackedKV, num_splits: int | None = None, allow_tf32: bool = False):
     """decode_plan for a query and a PackedKV handle, on the query's device."""
     B, Hq, _, D = q.shape
     with torch.cuda.device(q.device):
         return decode_plan(B, Hq, kv.num_kv_heads, D, kv.page_size, kv.k_quant.bit_width,
-                           kv.v_quant.bit_width, kv.page_table.shape[1], num_splits)
+                           kv.v_quant.bit_width, kv.page_table.shape[1], num_splits, allow_tf32)
 
 
 def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
@@ -292,7 +295,7 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
     check_kernel_contract(q, kv, check_ranges=check_ranges)
     B, Hq, _, D = q.shape
     Hkv = kv.num_kv_heads
-    pps, ns = plan if plan is not None else plan_for(q, kv, num_splits)
+    pps, ns = plan if plan is not None else plan_for(q, kv, num_splits, allow_tf32)
     out_dtype = out_dtype or q.dtype
     if out_dtype not in _lib.DTYPE_CODE:
         raise UnsupportedLayout(f"output dtype {out_dtype} is not supported")
