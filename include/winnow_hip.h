@@ -130,7 +130,7 @@ int wn_decode_plan_tf32(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v
 /* wn_decode_attention with TF32-class products: replaces the reference's
  * packed_decode_attention(..., allow_tf32=True) (packed_attention_triton.py:180-187,
  * whose kernel passes allow_tf32 to both tl.dot products, :113 and :127). For 4-bit K
- * and V with up to four query heads per kv head (after the virtual-head split) on
+ * and V with up to four query heads per kv head (n_rep 1-4) on
  * the row scan, the score and value products take single fp16 operands (11
  * significant bits, rounded to nearest) and accumulate in fp32; every other shape
  * runs the fp32-exact scan of wn_decode_attention. Same arguments, workspace,

@@ -4,7 +4,7 @@ against the CPU oracle.
 The reference's kernel hands ``allow_tf32`` to both ``tl.dot`` products
 (packed_attention_triton.py:113, 127): with it set, the products take operands of ten
 stored mantissa bits and accumulate in fp32. The TF32-class row scan (4-bit K and V,
-up to four query heads per kv head after the virtual-head split) rounds each operand
+up to four query heads per kv head) rounds each operand
 to fp16 (eleven significant bits) and accumulates in fp32. The bar is the north
 star's: within 2e-3 max-abs and 1e-3 relative of the oracle's fp32 tiled path
 (``tiled_compressed_attention``, packed_attention.py:260-311); rows of empty
@@ -46,10 +46,10 @@ def _check(got, ref, lens):
     return err
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (16, 8), (8, 8), (64, 8), (32, 2)])
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (16, 8), (8, 8), (24, 8), (8, 2)])
 def test_tf32_matches_oracle(Hq, Hkv):
-    """n_rep 4, 2 and 1 on one head group; 8 and 16 as two and four virtual kv heads of
-    four; ragged lengths with an empty sequence, library plan and two fixed splits."""
+    """n_rep 4, 2, 1 and 3 (one head group, padded columns) and two kv heads of four;
+    ragged lengths with an empty sequence, library plan and two fixed splits."""
     print(f"tf32 Hq={Hq} Hkv={Hkv}", flush=True)
     q, kv = build(700 + Hq + Hkv, len(RAGGED), Hq, Hkv, 128, RAGGED, 16, 4)
     scale = oa.default_scale(128)
@@ -135,9 +135,12 @@ def test_tf32_matches_the_rounded_operand_reference():
     _check(tf, tf32_class_reference(q, kv, scale).float(), RAGGED)
 
 
-@pytest.mark.parametrize("bwk,bwv,Hq,Hkv", [(6, 6, 32, 8), (4, 6, 64, 8), (2, 2, 16, 4)])
+@pytest.mark.parametrize("bwk,bwv,Hq,Hkv", [(6, 6, 32, 8), (4, 6, 64, 8), (2, 2, 16, 4), (4, 4, 64, 8),
+                                             (4, 4, 32, 2)])
 def test_tf32_other_shapes_run_the_exact_scan(bwk, bwv, Hq, Hkv):
-    """Widths without a TF32-class scan give the default call's output bit for bit."""
+    """Widths without a TF32-class scan, and 4-bit pages with n_rep 8 or 16 (one row-scan
+    group of eight, or virtual kv heads of eight), give the default call's output bit
+    for bit."""
     q, kv = build(950 + bwk + bwv, len(RAGGED), Hq, Hkv, 128, RAGGED, 16, bwk, bw_v=bwv)
     scale = oa.default_scale(128)
     dkv, qd = to_device(kv, DEV), q.to(DEV)
