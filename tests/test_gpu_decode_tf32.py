@@ -13,13 +13,12 @@ fp32-exact scan and give the default call's result bit for bit.
 """
 from __future__ import annotations
 
-import math
-
 import pytest
 import torch
 
 from cases import build, to_device
 from oracle import attention as oa
+from tf32_reference import tf32_class_reference
 
 pytestmark = pytest.mark.gpu
 
@@ -73,38 +72,6 @@ def test_tf32_balanced_plan_with_few_waves(waves):
     got = _pa().packed_decode_attention(q.to(DEV), to_device(kv, DEV), scale, plan=(0, waves), allow_tf32=True,
                                         out_dtype=torch.float32)
     _check(got, ref, lens)
-
-
-def _round11(x: torch.Tensor) -> torch.Tensor:
-    """x rounded to 11 significant bits, ties to even (fp16's significand, no range limit)."""
-    m, e = torch.frexp(x.double())
-    return torch.ldexp(torch.round(m * 2048) / 2048, e)
-
-
-def tf32_class_reference(q: torch.Tensor, kv, scale: float) -> torch.Tensor:
-    """float64 decode attention whose score and value operands are first rounded as the
-    TF32-class scan rounds them: the rotated, scaled query (in log2 units, as the scan
-    carries it) and both codebooks to 11 significant bits. The p n_V operand's rounding
-    (2^-12 relative per term) is left out; everything else is exact."""
-    B, Hq, _, D = q.shape
-    n_rep = Hq // kv.num_kv_heads
-    log2e = 1.0 / math.log(2.0)
-    ck_t, cv_t = _round11(kv.k_quant.centroids), _round11(kv.v_quant.centroids)
-    q_rot = (q[:, :, 0].double() @ kv.k_quant.Pi.double().T) * scale
-    q_r = _round11(q_rot * log2e) / log2e
-    out = torch.zeros(B, Hq, 1, D, dtype=torch.float64)
-    heads = torch.arange(Hq) // n_rep
-    for b in range(B):
-        if int(kv.seq_lens[b]) == 0:
-            continue
-        pk, nk = oa._gather_history(kv.k_pages, kv.k_norms, kv, b)
-        pv, nv = oa._gather_history(kv.v_pages, kv.v_norms, kv, b)
-        ck = ck_t[oa.unpack_t(pk, kv.k_quant.bit_width, D).long()] * nk.double()[..., None]
-        cv = cv_t[oa.unpack_t(pv, kv.v_quant.bit_width, D).long()] * nv.double()[..., None]
-        s = (q_r[b][:, None, :] @ ck[heads].transpose(-1, -2))[:, 0]          # (Hq, L)
-        a = torch.softmax(s, -1)[:, None, :] @ cv[heads]                        # (Hq, 1, D)
-        out[b] = a @ kv.v_quant.Pi.double()
-    return out
 
 
 def test_tf32_large_scores_and_long_history():
