@@ -37,7 +37,7 @@ def _prompts(n, seed=1):
 
 
 @torch.no_grad()
-def _generate(model, prompts, max_new, *, backend, bit_width=4, dense_dtype=None, page_size=16):
+def _generate(model, prompts, max_new, *, backend, bit_width=4, dense_dtype=None, page_size=16, allow_tf32=False):
     from winnow_amd import packed_backend as pb
     cfg = model.config
     pool = pb.make_pool(cfg, bit_width=None if dense_dtype else bit_width, num_pages=96, page_size=page_size,
@@ -49,7 +49,8 @@ def _generate(model, prompts, max_new, *, backend, bit_width=4, dense_dtype=None
     last = []
     for o, p in zip(owners, prompts):
         pool.ensure(o, len(p) + max_new)
-        cache = pb.PagedPackedCache(pool, [o], [0], k_quant=kq, v_quant=vq, head_dim=D, decode_backend=backend)
+        cache = pb.PagedPackedCache(pool, [o], [0], k_quant=kq, v_quant=vq, head_dim=D, decode_backend=backend,
+                                    allow_tf32=allow_tf32)
         out = model(input_ids=torch.tensor([p], device=DEV), position_ids=torch.arange(len(p), device=DEV)[None],
                     past_key_values=cache, use_cache=True, logits_to_keep=1)
         last.append(out.logits[0, -1].float())
@@ -58,7 +59,7 @@ def _generate(model, prompts, max_new, *, backend, bit_width=4, dense_dtype=None
     lengths = [len(p) for p in prompts]
     for _ in range(max_new - 1):
         cache = pb.PagedPackedCache(pool, owners, lengths, k_quant=kq, v_quant=vq, head_dim=D,
-                                    decode_backend=backend)
+                                    decode_backend=backend, allow_tf32=allow_tf32)
         ids = torch.tensor([[t[-1]] for t in toks], device=DEV)
         pos = torch.tensor([[L] for L in lengths], device=DEV)
         out = model(input_ids=ids, position_ids=pos, past_key_values=cache, use_cache=True, logits_to_keep=1)
@@ -96,6 +97,29 @@ def test_packed_decode_matches_the_reconstruct_path(model, bw):
     assert pb.BACKEND_COUNTS["hip_packed"] == 11 * 2          # 11 decode steps x 2 layers
     assert pb.BACKEND_COUNTS["prefill_reconstruct_sdpa"] == 3 * 2
     assert pb.BACKEND_COUNTS["native_sdpa"] == 0
+
+
+def test_allow_tf32_decode_keeps_the_greedy_tokens(model):
+    """The cache's allow_tf32 reaches the operator (the TF32-class scan at 4 bits, n_rep
+    2): the logits differ from the fp32-exact decode's, and greedy tokens equal the
+    reconstruct path's. This random-weight model's q and k projections have norms near
+    100, so its attention scores run to hundreds; TF32-class operands (11 significant
+    bits) move such scores by tenths and the first decode step's logits by a few
+    percent of their scale (the fp32-exact decode: 2e-5). The bar here is therefore
+    1e-1 of the logit scale; the operator itself is held to the float64 decode of
+    rounded operands at scores of that size (test_gpu_decode_tf32.py)."""
+    from winnow_amd import packed_backend as pb
+    prompts = _prompts(3, seed=5)
+    ref_toks, ref_steps = _generate(model, prompts, 10, backend="reconstruct_sdpa", bit_width=4)
+    exact_toks, exact_steps = _generate(model, prompts, 10, backend="auto", bit_width=4)
+    pb.BACKEND_COUNTS.clear()
+    toks, steps = _generate(model, prompts, 10, backend="auto", bit_width=4, allow_tf32=True)
+    assert pb.BACKEND_COUNTS["hip_packed"] == 9 * 2
+    assert toks == ref_toks == exact_toks
+    assert not torch.equal(steps[1], exact_steps[1])
+    scale = max(1.0, max(x.abs().max().item() for x in ref_steps))
+    worst = max((a - b).abs().max().item() for a, b in zip(steps, ref_steps))
+    assert worst < 1e-1 * scale, (worst, scale)
 
 
 def test_dense_pages_hip_kernel_matches_dense_sdpa_and_native_generation(model):

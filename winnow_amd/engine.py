@@ -83,6 +83,7 @@ class EngineConfig:
     max_prompt_tokens: int = 8192
     max_new_tokens_cap: int = 512
     decode_backend: str = "auto"
+    allow_tf32: bool = False       # TF32-class products in the packed decode operator
 
 
 # Admission rules in the order they are checked: (reason, refused?, detail).
@@ -238,7 +239,7 @@ class Engine:
         positions = start[:, None] + torch.arange(n, device=self.device)[None, :]
         cache = PagedPackedCache(self.pool, [r.request_id for r in reqs], [r.stored for r in reqs],
                                  k_quant=self.kq, v_quant=self.vq, head_dim=self.head_dim,
-                                 decode_backend=self.cfg.decode_backend)
+                                 decode_backend=self.cfg.decode_backend, allow_tf32=self.cfg.allow_tf32)
         out = self.model(input_ids=ids, position_ids=positions, past_key_values=cache, use_cache=True,
                          logits_to_keep=1)
         for r, stored in zip(reqs, cache.lengths):

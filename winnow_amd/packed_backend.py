@@ -221,7 +221,7 @@ class PagedPackedCache:
     """
 
     def __init__(self, pool: PagePool, owners, lengths, *, k_quant, v_quant,
-                 head_dim: int, decode_backend: str = "auto"):
+                 head_dim: int, decode_backend: str = "auto", allow_tf32: bool = False):
         if len(owners) != len(lengths):
             raise ValueError("one length per owner")
         self.pool = pool
@@ -230,6 +230,9 @@ class PagedPackedCache:
         self.kq, self.vq = k_quant, v_quant
         self.head_dim = head_dim
         self.decode_backend = decode_backend
+        # TF32-class decode products (the operator's allow_tf32; the reference reaches
+        # it through its tuned schedule, packed_backend.py:248-257, which is bypassed)
+        self.allow_tf32 = allow_tf32
         self.meta: PageTable | None = None
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
@@ -270,6 +273,7 @@ class PagedPackedCache:
                                  pa.Quantizer.from_tq(self.vq), D,
                                  seq_lens_host=meta.seq_host, page_table_host=meta.table_host)
         handle.decode_backend = self.decode_backend
+        handle.allow_tf32 = self.allow_tf32
         if layer_idx == pool.num_layers - 1:
             self.lengths = meta.seq_host.tolist()
         return handle, handle
@@ -398,7 +402,7 @@ def _dense_sdpa(query, kv: pa.DenseKV, scaling):
 
 
 def _hip_packed(query, kv, scaling):
-    return pa.packed_decode_attention(query, kv, scaling)
+    return pa.packed_decode_attention(query, kv, scaling, allow_tf32=getattr(kv, "allow_tf32", False))
 
 
 def _hip_dense(query, kv, scaling):
