@@ -454,11 +454,14 @@ def parity(w, kv=None, seqs=None, allow_tf32: bool = False):
     qs = w.q.float().cpu()[seqs]
     ref = oa.tiled_compressed_attention(qs, sub, scale)
     f64 = oa.reconstruct_attention_f64(qs, sub, scale)
-    flips = workloads.requantize_flips(w, kv)
+    rq = workloads.requantize(w, kv)
     return {"sequences": seqs, "attn_max_abs_err": (got - ref).abs().max().item(),
             "attn_within_2e-3_1e-3": bool(torch.allclose(got, ref, atol=2e-3, rtol=1e-3)),
             "rel_l2_vs_f64": ((got.double() - f64).norm() / f64.norm()).item(),
-            "codes_checked": 2 * w.sample[0].shape[2] * w.c["Hkv"] * w.c["D"], "adjudicated_code_flips": flips}
+            "requantized": f"sequence 0 (all {w.sample[0].shape[2]} tokens) and {rq['random_pages']} random "
+                           "pages of three other sequences, K and V",
+            "codes_checked": rq["vectors"] * w.c["D"], "adjudicated_code_flips": rq["code_flips"],
+            "norms_checked": rq["vectors"], "adjudicated_norm_flips": rq["norm_flips"]}
 
 
 def cpu_model() -> str:
@@ -551,7 +554,7 @@ def config_line(cfg: int, dev, steps: int, warmup: int, settle: float, copies: i
     from winnow_amd.packing import packed_bytes
 
     t0 = time.time()
-    w = workloads.build(cfg, dev, copies=copies)
+    w = workloads.build(cfg, dev, copies=copies, full_check=check)
     c = w.c
     log(f"config {cfg} built in {time.time() - t0:.1f} s: B={len(w.lens)} sum(L)={sum(w.lens)}")
     m = measure_decode(w, steps, warmup, settle)
@@ -674,7 +677,7 @@ def main(argv=None):
                           "copy_peak": cp}))
         return 0
     t0 = time.time()
-    w = workloads.build(args.config, dev, copies=args.copies)
+    w = workloads.build(args.config, dev, copies=args.copies, full_check=args.parity == "on")
     c, lens, q = w.c, w.lens, w.q
     log(f"workload config {args.config} built in {time.time() - t0:.1f} s: B={len(lens)} sum(L)={sum(lens)}")
     D, Hkv, Hq = c["D"], c["Hkv"], c["Hq"]

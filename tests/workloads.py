@@ -6,8 +6,9 @@ seconds. The CPU generator seeded with the config seed draws the sequence length
 page order, the outlier channels, the per-head scales and q. K and V (up to 4.4e9
 normals per config) are drawn on the device from a generator seeded with the same
 seed; a CPU draw of that many normals takes minutes. The first ``sample_tokens``
-tokens of sequence 0 are kept on the host so their codes can be recomputed by the
-oracle.
+tokens of sequence 0 (all of it with ``full_check``, plus two random pages of three
+other sequences) are kept on the host so their codes and norms can be recomputed by
+the oracle.
 """
 from __future__ import annotations
 
@@ -45,6 +46,7 @@ class Workload:
     quants: tuple            # (k TurboQuantMSE, v TurboQuantMSE) on the device
     sample: tuple            # host bf16 (1, Hkv, sample_tokens, D) K and V of sequence 0
     table: torch.Tensor      # host (B, max_pages) int32
+    extra: list = None       # (b, page column, host K, host V) of re-checked random pages
 
 
 def lengths(c, g) -> list:
@@ -53,7 +55,7 @@ def lengths(c, g) -> list:
     return [c["L"]] * c["B"]
 
 
-def build(cfg: int, dev, copies: int = 1, sample_tokens: int = 256) -> Workload:
+def build(cfg: int, dev, copies: int = 1, sample_tokens: int = 256, full_check: bool = False) -> Workload:
     from winnow_amd import packed_attention as pa
     from winnow_amd import packed_backend as pb
     from winnow_amd.packing import packed_bytes
@@ -88,6 +90,12 @@ def build(cfg: int, dev, copies: int = 1, sample_tokens: int = 256) -> Workload:
     dtable = table.to(dev)
     zero = torch.zeros(1, dtype=torch.int32)
     sample = None
+    # pages re-checked beside sequence 0, picked by a generator of their own so the
+    # workload's draws are the same with and without the check
+    gx = torch.Generator().manual_seed(c["seed"] + 7)
+    pick = int(torch.randint(B, (1,), generator=gx))
+    extra_b = sorted({B // 2, B - 1, pick} - {0}) if full_check else []
+    extra = []
     for b in range(B):
         L = lens[b]
         k = torch.randn(1, Hkv, L, D, generator=gd, device=dev)
@@ -101,7 +109,12 @@ def build(cfg: int, dev, copies: int = 1, sample_tokens: int = 256) -> Workload:
             v *= head_std[b, :, 1].to(dev)[None, :, None, None]
         k, v = k.bfloat16(), v.bfloat16()
         if b == 0:
-            sample = (k[:, :, :sample_tokens].cpu(), v[:, :, :sample_tokens].cpu())
+            n0 = L if full_check else sample_tokens
+            sample = (k[:, :, :n0].cpu(), v[:, :, :n0].cpu())
+        if b in extra_b:
+            for col in torch.randperm(need[b], generator=gx)[:2].tolist():
+                t0, t1 = col * S, min(col * S + S, L)
+                extra.append((b, col, k[:, :, t0:t1].cpu(), v[:, :, t0:t1].cpu()))
         pb.append_kv(k, v, kq, vq, kp, vp, kn, vn, dtable[b:b + 1], zero.to(dev),
                      page_table_host=table[b:b + 1], start_pos_host=zero)
         del k, v
@@ -112,7 +125,7 @@ def build(cfg: int, dev, copies: int = 1, sample_tokens: int = 256) -> Workload:
         kvs.append(pa.PackedKV(t[0], t[1], t[2], t[3], dtable, seq.to(dev), pa.Quantizer.from_tq(kq),
                                pa.Quantizer.from_tq(vq), D, seq_lens_host=seq, page_table_host=table))
     torch.cuda.synchronize()
-    return Workload(cfg, c, lens, q, kvs, (kq, vq), sample, table)
+    return Workload(cfg, c, lens, q, kvs, (kq, vq), sample, table, extra)
 
 
 def kv_bytes(lens, Hkv, nbk, nbv) -> int:
@@ -121,23 +134,34 @@ def kv_bytes(lens, Hkv, nbk, nbv) -> int:
     return sum(lens) * Hkv * ((nbk + 2) + (nbv + 2))
 
 
-def requantize_flips(w: Workload, kv=None) -> int:
-    """Codes of sequence 0's first sampled tokens recomputed by the CPU oracle against the
-    pool bytes; the number of adjudicated flips (any other difference raises)."""
-    from adjudicate import adjudicate_codes
+def requantize(w: Workload, kv=None) -> dict:
+    """Codes and fp16 norms of the kept tokens (sequence 0's first ones, or all of it and
+    the random pages with ``full_check``) recomputed by the CPU oracle against the pool
+    bytes: counts checked and adjudicated flips (any other difference raises)."""
+    from adjudicate import adjudicate_codes, adjudicate_fp16_norms
     from oracle import packing as opk
     from oracle.quantizer import get_quantizer as oq
 
     kv = kv or w.kvs[0]
     c, D, S = w.c, w.c["D"], w.c["S"]
-    n = w.sample[0].shape[2]
-    flips = 0
-    for src, bw, pages in ((w.sample[0], c["bwk"], kv.k_pages), (w.sample[1], c["bwv"], kv.v_pages)):
-        quant = oq(bw, D, 42)
-        codes, _ = quant.quantize(src)                                   # (1, Hkv, n, D)
-        ids = w.table[0, :-(-n // S)].long()
-        stored = pages[ids.to(pages.device)].cpu()                       # (n/S, Hkv, S, NB)
-        stored = torch.from_numpy(opk.unpack(stored.numpy(), bw, D))
-        stored = stored.permute(1, 0, 2, 3).reshape(1, stored.shape[1], -1, D)[:, :, :n]
-        flips += adjudicate_codes(src, stored, codes, quant)
-    return flips
+    sets = [(0, 0, w.sample[0], w.sample[1])] + list(w.extra or [])
+    out = {"vectors": 0, "code_flips": 0, "norm_flips": 0, "random_pages": len(w.extra or [])}
+    for b, col, ks, vs in sets:
+        n = ks.shape[2]
+        ids = w.table[b, col:col - (-n // S)].long()
+        for src, bw, pages, norms in ((ks, c["bwk"], kv.k_pages, kv.k_norms), (vs, c["bwv"], kv.v_pages, kv.v_norms)):
+            quant = oq(bw, D, 42)
+            codes, n32 = quant.quantize(src)                             # (1, Hkv, n, D), (1, Hkv, n)
+            stored = pages[ids.to(pages.device)].cpu()                   # (pages, Hkv, S, NB)
+            stored = torch.from_numpy(opk.unpack(stored.numpy(), bw, D))
+            stored = stored.permute(1, 0, 2, 3).reshape(1, stored.shape[1], -1, D)[:, :, :n]
+            out["code_flips"] += adjudicate_codes(src, stored, codes, quant)
+            h = norms[ids.to(norms.device)].cpu().permute(1, 0, 2).reshape(1, norms.shape[1], -1)[:, :, :n]
+            out["norm_flips"] += adjudicate_fp16_norms(n32, n32, h, n32.half())
+            out["vectors"] += src.shape[1] * n
+    return out
+
+
+def requantize_flips(w: Workload, kv=None) -> int:
+    """Adjudicated code flips of ``requantize``."""
+    return requantize(w, kv)["code_flips"]
