@@ -210,8 +210,14 @@ def dense_bench(c, lens, q, dev, steps: int = 30, warmup: int = 5, copies: int =
                                   timing_events=(ctypes.c_void_p(e0.cuda_event), ctypes.c_void_p(e1.cuda_event)))
     end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
     kern_ms = statistics.fmean(e0.elapsed_time(e1) for e0, e1 in evs)
+    # the step time without the per-launch events (as measure_decode)
+    start.record()
+    for i in range(steps):
+        pa.dense_decode_attention(q, kvs[i % copies], scale, workspace=ws, check_ranges=False)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
     nbytes = sum(lens) * Hkv * 2 * D * 2
     # parity on two sequences cut to check_len tokens (same pages, shorter seq_lens)
     seqs = [0, B - 1]
@@ -478,9 +484,10 @@ def cpu_model() -> str:
 
 def measure_decode(w, steps: int, warmup: int, settle: float, splits=None, allow_tf32: bool = False):
     """Time ``steps`` decode steps of workload ``w`` (pools rotated between steps): the
-    step time from events around the calls, the page-scan kernel from HIP events the C
-    ABI records on its stream around every launch. ``allow_tf32`` times the TF32-class
-    decode (``wn_decode_attention_tf32``)."""
+    page-scan kernel from HIP events the C ABI records on its stream around every
+    launch, then the step time from events around the same number of calls with
+    nothing recorded between them. ``allow_tf32`` times the TF32-class decode
+    (``wn_decode_attention_tf32``)."""
     import torch
     from winnow_amd import packed_attention as pa
 
@@ -514,6 +521,7 @@ def measure_decode(w, steps: int, warmup: int, settle: float, splits=None, allow
         e0.record()
         e1.record()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # the scan's duration: events recorded on its stream right around every launch
     torch.cuda.synchronize()
     start.record()
     for i in range(steps):
@@ -522,8 +530,18 @@ def measure_decode(w, steps: int, warmup: int, settle: float, splits=None, allow
     end.record()
     torch.cuda.synchronize()
     kern = [e0.elapsed_time(e1) for e0, e1 in ev_pairs]
-    return {"ms_per_step": start.elapsed_time(end) / steps, "kernel_ms": statistics.fmean(kern),
-            "kernel_ms_median": statistics.median(kern), "splits": ns, "pages_per_split": pps}
+    ms_evented = start.elapsed_time(end) / steps
+    # the step time: the same steps with nothing between the launches (the events above
+    # are extra commands in the stream and lengthen each step by a few microseconds)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        step(i)
+    end.record()
+    torch.cuda.synchronize()
+    return {"ms_per_step": start.elapsed_time(end) / steps, "ms_per_step_with_scan_events": ms_evented,
+            "kernel_ms": statistics.fmean(kern), "kernel_ms_median": statistics.median(kern), "splits": ns,
+            "pages_per_split": pps}
 
 
 def lds_lookup_rate(waves_per_cu: int = 8, iters: int = 8192):
@@ -748,6 +766,7 @@ def main(argv=None):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "ms_per_step_with_scan_events": m["ms_per_step_with_scan_events"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
