@@ -114,3 +114,33 @@ def test_tf32_other_shapes_run_the_exact_scan(bwk, bwv, Hq, Hkv):
     tf = _pa().packed_decode_attention(qd, dkv, scale, allow_tf32=True, out_dtype=torch.float32)
     exact = _pa().packed_decode_attention(qd, dkv, scale, out_dtype=torch.float32)
     assert torch.equal(tf, exact)
+
+
+def test_tf32_bf16_query_and_output():
+    """bf16 query in, bf16 output out (the cast after the merge), as the default path."""
+    q, kv = build(960, 2, 32, 8, 128, (300, 77), 16, 4)
+    scale = oa.default_scale(128)
+    got = _pa().packed_decode_attention(q.to(DEV, torch.bfloat16), to_device(kv, DEV), scale, allow_tf32=True)
+    assert got.dtype == torch.bfloat16
+    ref = oa.tiled_compressed_attention(q.bfloat16().float(), kv, scale)
+    assert (got.float().cpu() - ref).abs().max() < 2e-2
+
+
+def test_tf32_strided_pool_layer_view():
+    """Pages handed over as one layer of a (layers, P, ...) pool tensor (a storage offset
+    on every page and norm pointer)."""
+    lens = (450, 200, 0)
+    q, kv = build(961, len(lens), 32, 8, 128, lens, 16, 4)
+    dkv = to_device(kv, DEV)
+
+    def layer(t):
+        return torch.stack([torch.zeros_like(t), t, torch.zeros_like(t)])[1]
+
+    pa = _pa()
+    kv2 = pa.PackedKV(layer(dkv.k_pages), layer(dkv.k_norms), layer(dkv.v_pages), layer(dkv.v_norms),
+                      dkv.page_table, dkv.seq_lens, dkv.k_quant, dkv.v_quant, dkv.head_dim,
+                      seq_lens_host=kv.seq_lens.clone(), page_table_host=kv.page_table.clone())
+    assert kv2.k_pages.storage_offset() > 0
+    scale = oa.default_scale(128)
+    got = pa.packed_decode_attention(q.to(DEV), kv2, scale, allow_tf32=True, out_dtype=torch.float32)
+    _check(got, oa.tiled_compressed_attention(q, kv, scale), lens)
