@@ -105,7 +105,7 @@ def copy_peak(dev, nbytes: int = 1 << 30, reps: int = 10):
     return {"bytes_read": nbytes, "bytes_written": nbytes, "us": t * 1e6, "GBps": 2 * nbytes / t / 1e9}
 
 
-def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
+def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120, tf32: bool = False):
     """HBM bytes one launch of ``kernel`` moves, from two ``rocprofv3 --pmc`` child runs.
 
     Each pass profiles a short run of this script (3 steps plus the 1 GiB device
@@ -113,7 +113,8 @@ def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
     dispatch). Each counter is scaled by what it reads for that copy of known size
     (bytes / counter), so the figure is in real bytes whatever fraction of the
     memory channels the counter samples. Returns None when the profiler is absent
-    or a pass fails; the bench line then carries ``traffic: null``.
+    or a pass fails; the bench line then carries ``traffic: null``. ``tf32`` profiles
+    the allow_tf32 leg of the child run instead of its default decode.
     """
     import csv
     import shutil
@@ -131,7 +132,7 @@ def hbm_traffic(cfg: int, kernel: str, timeout_s: int = 120):
             cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "run", "--",
                    sys.executable, str(ROOT / "bench.py"), "--config", str(cfg), "--steps", "3", "--warmup", "1",
                    "--settle", "0", "--parity", "off", "--cpu-baseline", "off", "--traffic", "off", "--append", "off",
-                   "--configs", "none", "--tf32", "off",
+                   "--configs", "none", "--tf32", "on" if tf32 else "off", "--config-steps", "3",
                    "--dequant", "off", "--dense", "off",
                    "--copy-peak", "on"]
             try:
@@ -745,6 +746,11 @@ def main(argv=None):
     traffic = hbm_traffic(args.config, scan_kernel_name(c)) if args.traffic == "on" else None
     if traffic:
         log(f"traffic: {traffic}")
+    if tf and args.traffic == "on" and tf["kernel"] == "decode_rows_tf_kernel":
+        tt = hbm_traffic(args.config, tf["kernel"], tf32=True)
+        tf["traffic"] = tt["bytes_per_launch"] if tt else None
+        tf["traffic_read_bytes"] = tt["FETCH_SIZE"]["bytes_per_launch"] if tt else None
+        log(f"allow_tf32 traffic: {tt}")
     rate = lds_lookup_rate() if args.lds_floor == "on" else None
     ldsf = None
     if rate:
