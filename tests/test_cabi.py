@@ -65,6 +65,11 @@ def test_plan_reference_semantics(lib):
         pps, ns = decode_plan(B, Hq, Hkv, D, 16, 4, 4, mp)
         assert pps * ns >= mp and pps >= 1 and ns >= 1
         assert (ns - 1) * pps < max(mp, 1)
+        # the allow_tf32 plan: the same scan serves these shapes, so the same plan
+        assert decode_plan(B, Hq, Hkv, D, 16, 4, 4, mp, allow_tf32=True) == (pps, ns)
+    # explicit splits mean the same under allow_tf32
+    assert decode_plan(2, 8, 4, 128, 16, 4, 4, 10, 3, allow_tf32=True) == (4, 3)
+    assert decode_plan(2, 8, 4, 128, 16, 4, 4, 10, 50, allow_tf32=True) == (1, 10)
 
 
 def test_workspace_bytes(lib):
