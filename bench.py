@@ -584,7 +584,8 @@ def config_line(cfg: int, dev, steps: int, warmup: int, settle: float, copies: i
             "table": c["table"], "data": workloads.DATA[c["data"]],
             "tokens_per_s": len(w.lens) / (m["ms_per_step"] * 1e-3), "us_per_step": m["ms_per_step"] * 1e3,
             "scan_kernel": scan_kernel_name(c), "scan_us": m["kernel_ms"] * 1e3, "algorithmic_bytes": nbytes,
-            "scan_GBps": gbps, "frac": gbps / HBM_PEAK_GBPS, "splits": m["splits"],
+            "scan_GBps": gbps, "frac": gbps / HBM_PEAK_GBPS,
+            "step_frac": nbytes / (m["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, "splits": m["splits"],
             "pages_per_split": m["pages_per_split"], "steps": steps}
     if lds_rate:
         fl = lds_floor(w.lens, c, lds_rate, torch.cuda.get_device_properties(dev).multi_processor_count)
@@ -786,6 +787,11 @@ def main(argv=None):
         "kv_tokens_per_s": sum(lens) / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS,
+                     # the same bytes over the whole decode step (rotate + scan + merge), the
+                     # time the reference's traffic model divides by (bench_packed_attention.py:91-110)
+                     "step_achieved": bytes_step / (ms * 1e-3) / 1e9,
+                     "step_frac": bytes_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+                     "target_us_at_0.70": bytes_step / (0.70 * HBM_PEAK_GBPS * 1e9) * 1e6,
                      "traffic": traffic["bytes_per_launch"] if traffic else None,
                      "traffic_read_bytes": traffic["FETCH_SIZE"]["bytes_per_launch"] if traffic else None,
                      "traffic_write_bytes": traffic["WRITE_SIZE"]["bytes_per_launch"] if traffic else None,

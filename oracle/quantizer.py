@@ -24,10 +24,18 @@ Pinned by (``tests/test_oracle_quantizer.py``):
   (2-8 bits): ``tests/golden/reference_constants.json``, written in the build
   container by the reference's own ``TurboQuantMSE`` (``cache.py:84-106``),
   checked by ``tests/test_golden.py``.
+
+The fp32 QR's bits depend on the host's CPU and on LAPACK's thread count, so the
+standard rotations (head_dim 128, seeds 42 and 43) are not rebuilt: ``rotation``
+loads the reference's single-threaded bits from ``winnow_amd/rotations_d128.npz``
+(data the same script writes; the product loads them too), and every host
+quantizes with the same ``Pi``. ``qr_rotation`` is the restated construction; on
+the build container it reproduces those bits exactly (``tests/test_golden.py``).
 """
 from __future__ import annotations
 
 import math
+from pathlib import Path
 
 import numpy as np
 import torch
@@ -59,11 +67,23 @@ def lloyd_max_gaussian(levels: int, sigma: float = 1.0, iters: int = 200, tol: f
     return c, b
 
 
-def rotation(head_dim: int, seed: int) -> torch.Tensor:
-    """Seeded random orthogonal matrix (cache.py:92-97): Q of QR(randn) times sign(diag R).
+_CANONICAL = Path(__file__).resolve().parents[1] / "winnow_amd" / "rotations_d128.npz"
 
-    The QR runs on one thread: its fp32 rounding depends on the thread count, and
-    one thread gives the same bits on every host of this image.
+
+def rotation(head_dim: int, seed: int) -> torch.Tensor:
+    """Seeded random orthogonal matrix (cache.py:92-97): the reference's single-threaded
+    bits for head_dim 128 at seeds 42 and 43, else ``qr_rotation`` on this host."""
+    if head_dim == 128 and seed in (42, 43):
+        with np.load(_CANONICAL) as f:
+            return torch.from_numpy(np.array(f[f"pi_{seed}"], dtype=np.float32)).contiguous()
+    return qr_rotation(head_dim, seed)
+
+
+def qr_rotation(head_dim: int, seed: int) -> torch.Tensor:
+    """Q of QR(randn) times sign(diag R) (cache.py:92-97), the QR on one thread.
+
+    Its fp32 rounding depends on the host's CPU and thread count; one thread gives
+    the same bits on every host of one CPU model.
     """
     gen = torch.Generator(device="cpu").manual_seed(seed)
     G = torch.randn(head_dim, head_dim, generator=gen, dtype=torch.float32)

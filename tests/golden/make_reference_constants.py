@@ -13,11 +13,23 @@ D = 128:
   (42 is ``quantizers_for``'s default, packed_backend.py:298-303; 43 is the V
   seed of test_packed_attention.py:60-61);
 * the fp32 centroids and boundaries as hex bit patterns for every supported
-  width (packing.py:24).
+  width (packing.py:24);
+* the SHA-256 of ``Pi`` as the reference builds it on the thread counts 1, 2, 4
+  and 8, and at this container's default thread count (``pi_sha256_by_threads``,
+  ``default_threads``). ``TurboQuantMSE`` (cache.py:92-97) does not pin the
+  number of threads its fp32 ``torch.linalg.qr`` runs on, and the bits of ``Pi``
+  depend on it: the product and the oracle reproduce the single-threaded
+  construction (``pi_sha256``), which a multi-core host's reference does not.
 
 The file holds data only (hashes and bit patterns). ``tests/test_golden.py``
 checks the oracle and the product's host-side constants against it on the CPU;
 the reference itself is never read at test time or on the GPU box.
+
+It also writes ``winnow_amd/rotations_d128.npz``: the fp32 bits of the reference's
+single-threaded ``Pi`` at D = 128 for seeds 42 and 43. The fp32 QR's bits depend
+on the host's CPU and thread count, so the product and the oracle load these
+standard rotations instead of rebuilding them, and every host encodes with the
+same ``Pi`` (``tests/test_golden.py`` pins the file to the SHAs above).
 """
 from __future__ import annotations
 
@@ -26,6 +38,7 @@ import json
 import sys
 from pathlib import Path
 
+import numpy as np
 import torch
 
 HERE = Path(__file__).resolve().parent
@@ -40,7 +53,7 @@ def _hexbits(t: torch.Tensor) -> list[str]:
 
 
 def main(ref_root: str) -> None:
-    torch.set_num_threads(1)   # the QR runs single-threaded, as the oracle's does
+    default_threads = torch.get_num_threads()
     sys.path.insert(0, str(Path(ref_root) / "turboquant_kv"))
     import cache as ref_cache  # noqa: E402  (the reference module, imported here only)
 
@@ -49,10 +62,23 @@ def main(ref_root: str) -> None:
         "torch": torch.__version__,
         "head_dim": 128,
         "pi_sha256": {},
+        "default_threads": default_threads,
+        "pi_sha256_by_threads": {},
         "codebooks": {},
     }
+    for threads in sorted({1, 2, 4, 8, default_threads}):
+        torch.set_num_threads(threads)
+        out["pi_sha256_by_threads"][str(threads)] = {
+            str(seed): _sha(ref_cache.TurboQuantMSE(4, 128, "cpu", rotation_seed=seed).Pi) for seed in (42, 43)}
+    torch.set_num_threads(1)   # the construction the product and the oracle reproduce
+    rot = {}
     for seed in (42, 43):
-        out["pi_sha256"][str(seed)] = _sha(ref_cache.TurboQuantMSE(4, 128, "cpu", rotation_seed=seed).Pi)
+        pi = ref_cache.TurboQuantMSE(4, 128, "cpu", rotation_seed=seed).Pi.detach().float().contiguous()
+        out["pi_sha256"][str(seed)] = _sha(pi)
+        rot[f"pi_{seed}"] = pi.numpy()
+    rot_path = HERE.parents[1] / "winnow_amd" / "rotations_d128.npz"
+    np.savez(rot_path, **rot)
+    print(f"wrote {rot_path}")
     for bw in (2, 3, 4, 5, 6, 8):
         tq = ref_cache.TurboQuantMSE(bw, 128, "cpu", rotation_seed=42)
         out["codebooks"][str(bw)] = {"centroids": _hexbits(tq.centroids), "boundaries": _hexbits(tq.boundaries)}

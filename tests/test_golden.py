@@ -27,6 +27,7 @@ import torch
 from cases import config1_inputs, config1_kv
 from oracle.quantizer import get_quantizer as oracle_quantizer
 
+ROOT = Path(__file__).resolve().parent.parent
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
@@ -119,6 +120,81 @@ def test_codebooks_match_reference(reference_constants, bw):
     c, b = lloyd_max_gaussian(2 ** bw, sigma=1.0 / math.sqrt(128))
     assert _hex(torch.tensor(c, dtype=torch.float32)) == ref["centroids"]
     assert _hex(torch.tensor(b[1:-1], dtype=torch.float32)) == ref["boundaries"]
+
+
+def _rotation_on_threads(head_dim: int, seed: int, threads: int) -> torch.Tensor:
+    """The reference's Pi construction (cache.py:92-97) with its QR on ``threads`` threads."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    g = torch.randn(head_dim, head_dim, generator=gen, dtype=torch.float32)
+    before = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        q, r = torch.linalg.qr(g)
+    finally:
+        torch.set_num_threads(before)
+    signs = torch.sign(torch.diag(r))
+    signs[signs == 0] = 1.0
+    return (q * signs.unsqueeze(0)).contiguous()
+
+
+@pytest.mark.parametrize("seed", [42, 43])
+def test_shipped_rotations_are_the_reference_bits(reference_constants, seed):
+    """winnow_amd/rotations_d128.npz holds the reference's single-threaded Pi (written by
+    make_reference_constants.py from TurboQuantMSE itself); the product and the oracle
+    load it for head_dim 128 at seeds 42 and 43 on every host."""
+    import numpy as np
+
+    from oracle.quantizer import rotation
+    from winnow_amd.quantizer import seeded_rotation
+    with np.load(ROOT / "winnow_amd" / "rotations_d128.npz") as f:
+        assert f[f"pi_{seed}"].dtype == np.float32 and f[f"pi_{seed}"].shape == (128, 128)
+        assert hashlib.sha256(f[f"pi_{seed}"].tobytes()).hexdigest() == reference_constants["pi_sha256"][str(seed)]
+    assert _sha(rotation(128, seed)) == _sha(seeded_rotation(128, seed)) == reference_constants["pi_sha256"][str(seed)]
+
+
+@pytest.mark.parametrize("seed", [42, 43])
+def test_restated_construction_reproduces_the_shipped_bits(reference_constants, seed):
+    """The oracle's restated construction (seeded randn, single-threaded fp32 QR, sign
+    fix) gives the shipped bits on the build container, where the reference wrote them;
+    another CPU's QR rounds differently (the GPU box's gives another SHA), which is why
+    the standard rotations ship as data."""
+    from oracle.quantizer import qr_rotation
+    got = _sha(qr_rotation(128, seed))
+    if got != reference_constants["pi_sha256"][str(seed)]:
+        pytest.skip(f"this host's fp32 QR rounds differently from the build container's ({got[:12]})")
+    assert got == reference_constants["pi_sha256"][str(seed)]
+
+
+def test_reference_pi_depends_on_its_thread_count(reference_constants):
+    """TurboQuantMSE (cache.py:92-97) leaves LAPACK's thread count free: the fixture records
+    the single-threaded Pi the product and the oracle build and, apart from it, the Pi a
+    multi-threaded host's reference builds. Both SHAs are pinned here."""
+    by = reference_constants["pi_sha256_by_threads"]
+    assert by["1"] == reference_constants["pi_sha256"]
+    multi = {k: v for k, v in by.items() if int(k) > 1}
+    assert multi and all(v == multi[min(multi, key=int)] for v in multi.values())
+    assert multi[min(multi, key=int)]["42"] != by["1"]["42"]
+    assert reference_constants["default_threads"] >= 1
+
+
+def test_multithreaded_reference_pi_flips_only_boundary_codes(reference_constants):
+    """Codes from the single-threaded Pi against the multi-threaded reference Pi: the two
+    differ by at most ~1e-6 per entry, so a code may flip only where y sits within
+    rounding of a bucket boundary. On 20,000 N(0,1) vectors at 4 bits every flip must pass
+    the adjudication protocol, and they must be rare (measured ~2.5e-6 of codes)."""
+    from adjudicate import adjudicate_codes
+    want = reference_constants["pi_sha256_by_threads"]["4"]["42"]
+    pi_mt = _rotation_on_threads(128, 42, 4)
+    if _sha(pi_mt) != want:
+        pytest.skip("this host's multi-threaded QR differs from the one the fixture recorded")
+    tq1 = oracle_quantizer(4, 128, 42)
+    assert _sha(tq1.Pi) == reference_constants["pi_sha256"]["42"]
+    x = torch.randn(20000, 128, generator=torch.Generator().manual_seed(2026))
+    codes1, _ = tq1.quantize(x)
+    flat = x / x.norm(dim=-1, keepdim=True).clamp(min=1e-10)
+    codes_mt = torch.bucketize(flat @ pi_mt.T, tq1.boundaries).to(torch.uint8)
+    flips = adjudicate_codes(x, codes1, codes_mt, tq1)
+    assert flips / codes1.numel() < 2e-5, flips
 
 
 def test_oracle_reproduces_config1(c1, oracle_c1):

@@ -117,6 +117,33 @@ def test_layer_outlier_channels_and_other_widths(D, n_out, bw, bw_out):
         assert err <= 2e-5 * want.abs().max().item(), err
 
 
+@pytest.mark.parametrize("backend", ["triton_fp32", "triton_tf32", "native_cuda_fp32"])
+def test_explicit_backend_with_outlier_channels_takes_the_chunked_path(backend):
+    """The reference uses the requested kernel only without outlier channels and otherwise
+    dequantizes on its chunked path (cache.py:245-246): a caller passing kernel_backend
+    together with num_outlier_channels gets the history, not an error."""
+    from winnow_amd.cache import TQPackedLayer
+    B, H, D, n_out, bw, bw_out = 1, 2, 128, 8, 4, 8
+    g = torch.Generator().manual_seed(77)
+    k0 = torch.randn(B, H, 12, D, generator=g)
+    k0[..., 3] *= 10.0
+    xs_k = [k0, torch.randn(B, H, 1, D, generator=g)]
+    xs_v = [torch.randn(B, H, 12, D, generator=g), torch.randn(B, H, 1, D, generator=g)]
+    layer = TQPackedLayer(D, bw, DEV, max_cache_len=16, num_outlier_channels=n_out, outlier_bits=bw_out,
+                          kernel_backend=backend)
+    k_hist, v_hist = _fill(layer, xs_k, xs_v)
+    assert layer.last_dispatch_decision.backend == "chunked"
+    mask = layer._mask.cpu()
+    for xs, side, hist in ((xs_k, layer._k, k_hist), (xs_v, layer._v, v_hist)):
+        x = torch.cat(xs, dim=2)
+        want = torch.empty(B, H, 13, D, dtype=torch.float64)
+        for chan, w, dim, seed, gi in ((~mask, bw, D - n_out, 42, 0), (mask, bw_out, n_out, 43, 1)):
+            codes, norms = _stored(side[gi], 13, w, dim)
+            want[..., chan] = _closed_form(codes, norms, oracle_quantizer(w, dim, seed))
+        err = (hist.cpu().double() - want).abs().max().item()
+        assert err <= 2e-5 * want.abs().max().item(), err
+
+
 def test_protocol_and_accounting():
     from winnow_amd.cache import TQPackedLayer
     B, H, D, bw, M = 2, 2, 128, 4, 10

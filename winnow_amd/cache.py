@@ -91,6 +91,7 @@ class TQPackedLayer(DynamicLayer):
         self._len = 0
         self._mask = None          # (head_dim,) bool: the outlier channels
         self._k = self._v = None   # lists of _Group: regular, then outlier
+        self._append_table = self._append_start = None   # fused append's (B, 1) table, start positions
         self.is_initialized = False
 
     # ---------------------------------------------------------------- storage
@@ -129,8 +130,14 @@ class TQPackedLayer(DynamicLayer):
         v = v if (v.stride(-1) == 1 and v.dtype == k.dtype) else v.to(k.dtype).contiguous()
         S = 1 << max(self._max - 1, 1).bit_length()   # one power-of-two page holds a whole row
         dev = k.device
-        table = torch.arange(B, dtype=torch.int32, device=dev).view(B, 1)
-        start = torch.full((B,), pos, dtype=torch.int32, device=dev)
+        if self._append_table is None or self._append_table.shape[0] != B:
+            # row b of the cache is "page" b: a (B, 1) identity table, and the start
+            # position of every row, kept on the layer (the steady-state append then
+            # costs the fill of B integers and the append launch)
+            self._append_table = torch.arange(B, dtype=torch.int32, device=dev).view(B, 1)
+            self._append_start = torch.empty(B, dtype=torch.int32, device=dev)
+        table, start = self._append_table, self._append_start
+        start.fill_(pos)
         kg, vg, q = self._k[0], self._v[0], self._tq
         with torch.cuda.device(dev):
             _lib.call("wn_append_kv",
@@ -159,16 +166,20 @@ class TQPackedLayer(DynamicLayer):
 
     # ---------------------------------------------------------------- history
     def _choose(self) -> DequantChoice:
-        fused_ok = not self._out_dim and self._hd == _FUSED_HEAD_DIM
         b = self.kernel_backend
         if b == "torch_fp32":
             return DequantChoice("chunked", False, "kernel_backend torch_fp32")
+        if self._out_dim:
+            # the reference uses its kernels only without outlier channels and otherwise
+            # takes the chunked path whatever kernel_backend asked for (cache.py:245-246)
+            return DequantChoice("chunked", False, f"{b}: outlier channels take the chunked path")
+        fused_ok = self._hd == _FUSED_HEAD_DIM
         if b == "auto":
             if fused_ok:
                 return DequantChoice("fused", self.allow_tf32, "auto: fused kernel (head_dim 128, no outliers)")
-            return DequantChoice("chunked", False, "auto: the fused kernel needs head_dim 128 without outlier channels")
+            return DequantChoice("chunked", False, "auto: the fused kernel needs head_dim 128")
         if not fused_ok:
-            raise RuntimeError(f"requested {b}, but the fused dequant serves head_dim 128 without outlier channels")
+            raise RuntimeError(f"requested {b}, but the fused dequant serves head_dim 128")
         return DequantChoice("fused", b == "triton_tf32", f"kernel_backend {b}")
 
     @torch.no_grad()

@@ -1134,10 +1134,16 @@ __device__ __forceinline__ void softmax_phase_mx(float sc, uint32_t nk_h, uint32
     for (int mm = 0; mm < 8; ++mm) st.acc[mm] *= f;
     st.gs = gs_need;
   }
-  bool move = st.m[0] == -INFINITY;
+  // the reference maxima move when a score exceeds its head's by more than kRescale:
+  // one test of the largest excess over the heads (masked tokens give -inf; the first
+  // chunk, with every maximum at -inf, always moves)
+  float d[H], dmax = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < H; ++i) move = move || __any(sv[i] > st.m[i] + kRescale);
-  if (move) {  // wave-uniform
+  for (int i = 0; i < H; ++i) {
+    d[i] = sv[i] - st.m[i];
+    dmax = fmaxf(dmax, d[i]);
+  }
+  if (st.m[0] == -INFINITY || __any(dmax > kRescale)) {  // wave-uniform
     const int hc = (lane & 15) % H;  // head of this lane's accumulator column
     float alpha_c = 1.f;
 #pragma unroll
@@ -1147,6 +1153,7 @@ __device__ __forceinline__ void softmax_phase_mx(float sc, uint32_t nk_h, uint32
       st.m[i] = m_new;
       st.l[i] *= alpha;
       alpha_c = hc == i ? alpha : alpha_c;
+      d[i] = sv[i] - m_new;
     }
 #pragma unroll
     for (int mm = 0; mm < 8; ++mm) st.acc[mm] *= alpha_c;
@@ -1154,7 +1161,7 @@ __device__ __forceinline__ void softmax_phase_mx(float sc, uint32_t nk_h, uint32
   const float nvs = ldexpf(nv, -st.gs);
 #pragma unroll
   for (int i = 0; i < H; ++i) {
-    const float p = __builtin_amdgcn_exp2f(sv[i] - st.m[i]);  // 0 for masked tokens
+    const float p = __builtin_amdgcn_exp2f(d[i]);  // 0 for masked tokens
     st.l[i] += p;
     pt[i * kTileStride + off] = split_word(p * nvs);
   }
