@@ -226,21 +226,23 @@ def test_split_invariance_and_sampled_oracle_long():
 RAGGED_WITH_GAPS = (0, 130, 0, 0, 64, 1, 700, 0, 65, 2000, 0)
 
 
-@pytest.mark.parametrize("waves", [1, 5, 37])
+@pytest.mark.parametrize("waves", [1, 5, 16, 37, 64])
 @pytest.mark.parametrize("bwk,bwv,Hq,Hkv", [(4, 4, 32, 8), (6, 6, 32, 8), (4, 6, 64, 8), (4, 4, 64, 4)])
 def test_balanced_plan_with_few_waves(waves, bwk, bwv, Hq, Hkv):
     """A balanced plan over a handful of waves (``plan=(0, waves)``): each wave scans a
-    run of 64-token chunks, crosses (sequence, kv head) boundaries, records the
-    partial range of every unit it starts, and skips zero-length sequences in the
-    middle of its share. Covers one and two 4-head groups per wave and the two
-    virtual kv heads of n_rep 16."""
+    run of 64-token chunks, crosses sequence boundaries, records the partial range of
+    every unit it starts, and skips zero-length sequences in the middle of its share.
+    Fewer waves than (virtual) kv heads (1, 5) interleave kv heads in one list; from
+    one group of a wave per kv head up (16, 37 with idle waves, 64) the groups share
+    the chunks and each wave keeps its kv head. Covers one and two 4-head groups per
+    wave and the two virtual kv heads of n_rep 16."""
     lens = RAGGED_WITH_GAPS
     print(f"balanced {waves} waves, {bwk}/{bwv} bits, {Hq}/{Hkv} heads", flush=True)
     q, kv = build(500 + waves + bwk + Hq, len(lens), Hq, Hkv, 128, lens, 16, bwk, bw_v=bwv)
     scale = oa.default_scale(128)
     ref = oa.tiled_compressed_attention(q, kv, scale)
     chunks = Hkv * sum(-(-L // 64) for L in lens)
-    assert chunks > 4 * waves or waves == 37
+    assert chunks > 4 * waves or waves in (37, 64)
     got = _pa().packed_decode_attention(q.to(DEV), to_device(kv, DEV), scale, plan=(0, waves),
                                         out_dtype=torch.float32)
     _check(got, ref, lens)

@@ -651,19 +651,33 @@ __device__ __forceinline__ int xcd_major(int p, int n) {
 // Fixed splits: wave w is unit (split, kv head, sequence) of the flattened
 // num_splits x Hkv x B space and scans pages [split * pages_per_split, ...) of its
 // sequence.
-// Balanced (a.balanced): the W = num_splits waves share the flattened space of
-// 64-token chunks ordered (sequence, kv head, chunk); wave w takes chunks
-// [C w / W', C (w+1) / W') with C the total and W' = min(W, C), and writes one
-// partial per (sequence, kv head) it touches, at row w + b*Hkv + kvh. The wave that
-// scans a unit's first chunk records where the unit's partials start and how many
-// there are (unit_meta), so the merge reads exactly that range.
+// Balanced (a.balanced), grouped (at least Hkv waves): the waves form G = W / Hkv
+// groups of Hkv consecutive waves, wave w = j Hkv + h being kv head h of group j.
+// The groups share the flattened space of 64-token chunks of one kv head, ordered
+// (sequence, chunk), T in all: group j takes [T j / G', T (j+1) / G') with G' =
+// min(G, T), and each of its waves scans that range for its own kv head. So the kv
+// heads of a chunk are scanned side by side by the waves of one work-group, and the
+// 128-byte lines that hold the norms of four kv heads of a page are fetched once
+// for all four, whatever the sequence lengths. The wave writes one partial per
+// sequence it touches, at row h (G' + B) + b + j: a unit's rows are contiguous (its
+// groups are consecutive) and no two (group, sequence) pairs of one kv head share a
+// row (j + b grows with either).
+// Balanced over fewer waves than kv heads: the waves share the flattened space
+// ordered (sequence, kv head, chunk); wave w takes chunks [C w / W', C (w+1) / W')
+// with C the total and W' = min(W, C), and writes one partial per (sequence, kv
+// head) it touches, at row w + b*Hkv + kvh.
+// Either way the wave that scans a unit's first chunk records where the unit's
+// partials start and how many there are (unit_meta), so the merge reads exactly that
+// range.
 template <class Scan>
 __device__ __forceinline__ void for_each_range(const DecodeArgs& a, int64_t w, int lane, Scan&& scan) {
   // One call site of the scan keeps a single copy of its code.
   int b, kvh, t_lo, t_hi;
   int64_t prow;
   int64_t s = 0, e = 0;  // balanced: flattened chunks [s, e) still to do
+  int64_t G = 0, j = 0;  // grouped: groups with work, this wave's group
   const int32_t* pre = a.chunk_prefix;
+  const bool grouped = a.balanced && a.num_splits >= a.Hkv;
   if (!a.balanced) {
     if (w >= int64_t(a.num_splits) * a.Hkv * a.B) return;
     const int split = int(w % a.num_splits);
@@ -681,25 +695,61 @@ __device__ __forceinline__ void for_each_range(const DecodeArgs& a, int64_t w, i
     if (split == 0 && lane == 0)  // the merge reads the group's partial rows from here
       a.unit_meta[b * a.Hkv + kvh] = make_int2(int(prow), (n_pages + a.pages_per_split - 1) / a.pages_per_split);
   } else {
-    const int64_t C = int64_t(a.Hkv) * pre[a.B];
-    const int64_t Wp = min(int64_t(a.num_splits), C);
-    if (w >= Wp) return;
-    s = C * w / Wp;
-    e = C * (w + 1) / Wp;
-    // sequence holding flattened chunk s: the largest b with Hkv * pre[b] <= s
+    const int64_t T = pre[a.B];
+    int64_t key;  // the flattened position to find the sequence of, in units of pre[]
+    int64_t mult; // pre[] -> flattened position
+    if (grouped) {
+      G = min(int64_t(a.num_splits / a.Hkv), T);
+      j = w / a.Hkv;
+      if (j >= G) return;
+      s = T * j / G;
+      e = T * (j + 1) / G;
+      key = s;
+      mult = 1;
+      kvh = int(w % a.Hkv);
+    } else {
+      const int64_t C = int64_t(a.Hkv) * T;
+      const int64_t Wp = min(int64_t(a.num_splits), C);
+      if (w >= Wp) return;
+      s = C * w / Wp;
+      e = C * (w + 1) / Wp;
+      key = s;
+      mult = a.Hkv;
+      kvh = 0;
+    }
+    // sequence holding flattened chunk s: the largest b with mult * pre[b] <= s
     int lo = 0, hi = a.B;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (int64_t(a.Hkv) * pre[mid] <= s) lo = mid;
+      if (mult * pre[mid] <= key) lo = mid;
       else hi = mid;
     }
     b = lo;
-    kvh = t_lo = t_hi = 0;
+    t_lo = t_hi = 0;
     prow = 0;
   }
   while (true) {
     int nb = 0, c_hi = 0;
-    if (a.balanced) {
+    if (grouped) {
+      nb = pre[b + 1] - pre[b];
+      while (nb == 0) {  // sequences without tokens own no chunks
+        ++b;
+        nb = pre[b + 1] - pre[b];
+      }
+      const int c_lo = int(s - pre[b]);
+      c_hi = int(min(int64_t(nb), c_lo + (e - s)));
+      t_lo = 64 * c_lo;
+      t_hi = min(64 * c_hi, a.seq_lens[b]);
+      prow = int64_t(kvh) * (G + a.B) + b + j;
+      if (c_lo == 0 && lane == 0) {
+        // the unit's first group: its partials are rows prow .. prow + n - 1, one per
+        // group up to the last group starting before the sequence's end pre[b + 1]
+        const int64_t T = pre[a.B];
+        const int64_t jl = (int64_t(pre[b + 1]) * G + T - 1) / T - 1;
+        a.unit_meta[b * a.Hkv + kvh] = make_int2(int(prow), int(jl - j + 1));
+      }
+      s += c_hi - c_lo;
+    } else if (a.balanced) {
       nb = pre[b + 1] - pre[b];
       while (nb == 0) {  // sequences without tokens own no chunks
         ++b;
@@ -725,7 +775,8 @@ __device__ __forceinline__ void for_each_range(const DecodeArgs& a, int64_t w, i
     }
     scan(b, kvh, t_lo, t_hi, prow);
     if (!a.balanced || s >= e) break;
-    if (kvh + 1 == a.Hkv && c_hi == nb) ++b;
+    if (grouped) ++b;  // the group's range continues in the next sequence
+    else if (kvh + 1 == a.Hkv && c_hi == nb) ++b;
   }
 }
 
