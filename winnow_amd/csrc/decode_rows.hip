@@ -884,6 +884,16 @@ __device__ __forceinline__ float wave_max_dpp(float x) {
   return __builtin_bit_cast(float, (k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
 }
 
+// Tile words read by every lane whether or not its token is valid: the empty asm uses
+// each value unconditionally, so the compiler cannot sink a read into a branch on
+// `valid` (it had: one exec-masked branch per head around a read and a full LDS wait,
+// eight serialised round trips per chunk with two head groups).
+template <int N>
+__device__ __forceinline__ void read_unconditionally(float (&x)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(x[i]));
+}
+
 // H | L << 16 of x with H = fp16(x) and L = fp16(x - H), both rounded toward zero.
 __device__ __forceinline__ uint32_t split_word(float x) {
   typedef __fp16 h2 __attribute__((ext_vector_type(2)));
@@ -1164,15 +1174,20 @@ __device__ __forceinline__ void softmax_phase_mx(float sc, uint32_t nk_h, uint32
   const float nk = half_lo(nk_h) * sc;
   const float nv = valid ? half_lo(nv_h) : 0.f;
   float sv[H];
+  if constexpr (kTileHalves<NG>) {
 #pragma unroll
-  for (int i = 0; i < H; ++i) {
-    if constexpr (kTileHalves<NG>) {
+    for (int i = 0; i < H; ++i) {
       const float x = __builtin_bit_cast(float, pt[i * kTileStride + off]) +
                       __builtin_bit_cast(float, pt[(i + H) * kTileStride + off]);
       sv[i] = valid ? x * nk : -INFINITY;
-    } else {
-      sv[i] = valid ? __builtin_bit_cast(float, pt[i * kTileStride + off]) * nk : -INFINITY;
     }
+  } else {
+    float x[H];
+#pragma unroll
+    for (int i = 0; i < H; ++i) x[i] = __builtin_bit_cast(float, pt[i * kTileStride + off]);
+    read_unconditionally(x);
+#pragma unroll
+    for (int i = 0; i < H; ++i) sv[i] = valid ? x[i] * nk : -INFINITY;
   }
   // value scale: 2^kRescale * max(n_V) * 2^-gs < 2^15, i.e. every n_V < 2^(7 + gs); the
   // scale only grows, so the wave's maximum is taken only when a norm reaches the limit
@@ -1378,9 +1393,12 @@ __device__ __forceinline__ void softmax_phase_tf(float sc, uint32_t nk_h, uint32
   const int off = 16 * (lane >> 4) + 4 * (lane & 3) + ((lane >> 2) & 3);  // word of token lane
   const float nk = half_lo(nk_h) * sc;
   const float nv = valid ? half_lo(nv_h) : 0.f;
-  float sv[H];
+  float x[H], sv[H];
 #pragma unroll
-  for (int i = 0; i < H; ++i) sv[i] = valid ? __builtin_bit_cast(float, pt[i * kTileStride + off]) * nk : -INFINITY;
+  for (int i = 0; i < H; ++i) x[i] = __builtin_bit_cast(float, pt[i * kTileStride + off]);
+  read_unconditionally(x);
+#pragma unroll
+  for (int i = 0; i < H; ++i) sv[i] = valid ? x[i] * nk : -INFINITY;
   if (__any(nv >= ldexpf(1.f, 7 + st.gs))) {  // wave-uniform, rare
     int ge;
     frexpf(wave_max_nonneg(nv), &ge);
