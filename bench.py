@@ -78,6 +78,14 @@ def scan_kernel_name(c) -> str:
     return "decode_split_kernel"
 
 
+def tf_kernel_name(c) -> str:
+    """Symbol of the page-scan kernel wn_decode_attention_tf32 launches for this shape:
+    the TF32-class row scan for 4 and 6-bit K and V on the row scan, else the default's."""
+    if (scan_kernel_name(c) == "decode_rows16_kernel" and c["bwk"] in (4, 6) and c["bwv"] in (4, 6)):
+        return "decode_rows_tf_kernel"
+    return scan_kernel_name(c)
+
+
 kv_bytes = workloads.kv_bytes
 
 
@@ -462,7 +470,14 @@ def parity(w, kv=None, seqs=None, allow_tf32: bool = False):
     ref = oa.tiled_compressed_attention(qs, sub, scale)
     f64 = oa.reconstruct_attention_f64(qs, sub, scale)
     rq = workloads.requantize(w, kv)
-    return {"sequences": seqs, "attn_max_abs_err": (got - ref).abs().max().item(),
+    tf = {}
+    if allow_tf32:
+        # also against the float64 decode of operands rounded as the TF32-class scan rounds them
+        from tf32_reference import tf32_class_reference
+        rr = tf32_class_reference(qs, sub, scale).float()
+        tf = {"rounded_operand_ref_max_abs_err": (got - rr).abs().max().item(),
+              "rounded_operand_ref_within_2e-3_1e-3": bool(torch.allclose(got, rr, atol=2e-3, rtol=1e-3))}
+    return {"sequences": seqs, **tf, "attn_max_abs_err": (got - ref).abs().max().item(),
             "attn_within_2e-3_1e-3": bool(torch.allclose(got, ref, atol=2e-3, rtol=1e-3)),
             "rel_l2_vs_f64": ((got.double() - f64).norm() / f64.norm()).item(),
             "requantized": f"sequence 0 (all {w.sample[0].shape[2]} tokens) and {rq['random_pages']} random "
@@ -566,9 +581,23 @@ def lds_floor(lens, c, rate, cus):
             "floor_us": chunks * c["D"] / (cus * rate)}
 
 
+def tf32_leg(w, bytes_step: int, steps: int, warmup: int, settle: float, splits, check: bool):
+    """The reference's allow_tf32=True decode on the same pages: scan time, fraction of
+    8 TB/s, tokens/s and sampled parity (against the oracle's fp32 path at the north-star
+    bar)."""
+    mt = measure_decode(w, steps, warmup, settle, splits, allow_tf32=True)
+    us = mt["kernel_ms"] * 1e3
+    return {"kernel": tf_kernel_name(w.c), "scan_us": us, "frac": bytes_step / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+            "us_per_step": mt["ms_per_step"] * 1e3, "tokens_per_s": len(w.lens) / (mt["ms_per_step"] * 1e-3),
+            "step_frac": bytes_step / (mt["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, "steps": steps,
+            "products": "single fp16 operands (11 significant bits, rounded to nearest), fp32 accumulation",
+            "parity": parity(w, allow_tf32=True) if check else None}
+
+
 def config_line(cfg: int, dev, steps: int, warmup: int, settle: float, copies: int, check: bool,
-                lds_rate: float | None = None):
-    """Decode throughput, roofline fraction of the scan and same-run parity at config ``cfg``."""
+                lds_rate: float | None = None, tf32: bool = False):
+    """Decode throughput, roofline fraction of the scan and same-run parity at config
+    ``cfg``; ``tf32`` adds the allow_tf32 leg on the same pages."""
     import torch
     from winnow_amd.packing import packed_bytes
 
@@ -593,6 +622,8 @@ def config_line(cfg: int, dev, steps: int, warmup: int, settle: float, copies: i
         line["scan_over_lds_floor"] = line["scan_us"] / fl["floor_us"]
     if check:
         line["parity"] = parity(w)
+    if tf32:
+        line["allow_tf32"] = tf32_leg(w, nbytes, steps, warmup, settle, None, check)
     log(f"config {cfg}: {line}")
     del w
     torch.cuda.empty_cache()
@@ -728,16 +759,9 @@ def main(argv=None):
     tf = None
     if args.tf32 == "on":
         # the reference's allow_tf32=True on the same pages: the TF32-class scan where it
-        # is compiled (4-bit K and V, up to four query heads per kv head), else the same scan
-        mt = measure_decode(w, args.config_steps, min(args.warmup, 10), args.settle, args.splits, allow_tf32=True)
-        tf_kern = mt["kernel_ms"] * 1e3
-        tf = {"kernel": "decode_rows_tf_kernel" if c["bwk"] == 4 and c["bwv"] == 4 and Hq // Hkv <= 4
-              else scan_kernel_name(c),
-              "scan_us": tf_kern, "frac": bytes_step / (tf_kern * 1e-6) / 1e9 / HBM_PEAK_GBPS,
-              "us_per_step": mt["ms_per_step"] * 1e3, "tokens_per_s": B / (mt["ms_per_step"] * 1e-3),
-              "steps": args.config_steps,
-              "products": "single fp16 operands (11 significant bits, rounded to nearest), fp32 accumulation",
-              "parity": parity(w, allow_tf32=True) if args.parity == "on" else None}
+        # is compiled (4 and 6-bit K and V on the row scan), else the same scan
+        tf = tf32_leg(w, bytes_step, args.config_steps, min(args.warmup, 10), args.settle, args.splits,
+                      args.parity == "on")
         log(f"allow_tf32: {tf}")
     cpu = cpu_baseline(c, lens, q, w.kvs[0], args.cpu_budget) if args.cpu_baseline == "on" else None
     if cpu:
@@ -763,7 +787,7 @@ def main(argv=None):
     for cfg in extra:
         if cfg != args.config:
             others[str(cfg)] = config_line(cfg, dev, args.config_steps, min(args.warmup, 10), args.settle,
-                                           args.copies, args.parity == "on", rate)
+                                           args.copies, args.parity == "on", rate, args.tf32 == "on")
 
     result = {
         "metric": METRIC,

@@ -129,11 +129,11 @@ int wn_decode_plan_tf32(int B, int Hq, int Hkv, int D, int S, int bw_k, int bw_v
 
 /* wn_decode_attention with TF32-class products: replaces the reference's
  * packed_decode_attention(..., allow_tf32=True) (packed_attention_triton.py:180-187,
- * whose kernel passes allow_tf32 to both tl.dot products, :113 and :127). For 4-bit K
- * and V with up to four query heads per kv head (n_rep 1-4) on
- * the row scan, the score and value products take single fp16 operands (11
- * significant bits, rounded to nearest) and accumulate in fp32; every other shape
- * runs the fp32-exact scan of wn_decode_attention. Same arguments, workspace,
+ * whose kernel passes allow_tf32 to both tl.dot products, :113 and :127). For 4 and
+ * 6-bit K and V (alike or mixed) on the row scan (head_dim 128, page size >= 16, n_rep
+ * up to 8, or up to 16 in virtual kv heads of eight), the score and value products
+ * take single fp16 operands (11 significant bits, rounded to nearest) and accumulate
+ * in fp32; every other shape runs the fp32-exact scan of wn_decode_attention. Same arguments, workspace,
  * preconditions and errors as wn_decode_attention; the plan comes from
  * wn_decode_plan_tf32. */
 int wn_decode_attention_tf32(

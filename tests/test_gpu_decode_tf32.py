@@ -3,8 +3,8 @@ against the CPU oracle.
 
 The reference's kernel hands ``allow_tf32`` to both ``tl.dot`` products
 (packed_attention_triton.py:113, 127): with it set, the products take operands of ten
-stored mantissa bits and accumulate in fp32. The TF32-class row scan (4-bit K and V,
-up to four query heads per kv head) rounds each operand
+stored mantissa bits and accumulate in fp32. The TF32-class row scan (4 or 6-bit K
+and V, alike or mixed, up to eight query heads per kv head) rounds each operand
 to fp16 (eleven significant bits) and accumulates in fp32. The bar is the north
 star's: within 2e-3 max-abs and 1e-3 relative of the oracle's fp32 tiled path
 (``tiled_compressed_attention``, packed_attention.py:260-311); rows of empty
@@ -45,12 +45,17 @@ def _check(got, ref, lens):
     return err
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (16, 8), (8, 8), (24, 8), (8, 2)])
-def test_tf32_matches_oracle(Hq, Hkv):
-    """n_rep 4, 2, 1 and 3 (one head group, padded columns) and two kv heads of four;
-    ragged lengths with an empty sequence, library plan and two fixed splits."""
-    print(f"tf32 Hq={Hq} Hkv={Hkv}", flush=True)
-    q, kv = build(700 + Hq + Hkv, len(RAGGED), Hq, Hkv, 128, RAGGED, 16, 4)
+@pytest.mark.parametrize("bwk,bwv,Hq,Hkv", [
+    (4, 4, 32, 8), (4, 4, 16, 8), (4, 4, 8, 8), (4, 4, 24, 8), (4, 4, 8, 2),
+    (6, 6, 32, 8), (6, 6, 8, 8), (4, 6, 32, 8), (6, 4, 32, 8),
+    (4, 4, 64, 8), (4, 6, 64, 8), (6, 6, 64, 8), (6, 4, 64, 8), (4, 6, 40, 8), (6, 6, 56, 8),
+    (4, 4, 32, 2), (4, 6, 64, 4)])
+def test_tf32_matches_oracle(bwk, bwv, Hq, Hkv):
+    """4 and 6-bit K and V, alike and mixed: n_rep 4, 2, 1 and 3 (one head group,
+    padded columns), n_rep 8, 5 and 7 (two groups), n_rep 16 (virtual kv heads of
+    eight); ragged lengths with an empty sequence, library plan and two fixed splits."""
+    print(f"tf32 {bwk}/{bwv} Hq={Hq} Hkv={Hkv}", flush=True)
+    q, kv = build(700 + Hq + Hkv + 10 * bwk + bwv, len(RAGGED), Hq, Hkv, 128, RAGGED, 16, bwk, bw_v=bwv)
     scale = oa.default_scale(128)
     ref = oa.tiled_compressed_attention(q, kv, scale)
     dkv = to_device(kv, DEV)
@@ -60,13 +65,14 @@ def test_tf32_matches_oracle(Hq, Hkv):
         _check(got, ref, RAGGED)
 
 
-@pytest.mark.parametrize("waves", [1, 5, 37])
-def test_tf32_balanced_plan_with_few_waves(waves):
+@pytest.mark.parametrize("waves,bwk,bwv,Hq", [(1, 4, 4, 32), (5, 4, 4, 32), (37, 4, 4, 32), (5, 6, 6, 32),
+                                              (37, 4, 6, 64), (8, 4, 6, 64)])
+def test_tf32_balanced_plan_with_few_waves(waves, bwk, bwv, Hq):
     """A balanced plan over a handful of waves: each wave scans runs of chunks, crosses
     (sequence, kv head) boundaries and skips zero-length sequences mid-share."""
     lens = RAGGED_WITH_GAPS
-    print(f"tf32 balanced {waves} waves", flush=True)
-    q, kv = build(800 + waves, len(lens), 32, 8, 128, lens, 16, 4)
+    print(f"tf32 balanced {waves} waves {bwk}/{bwv} Hq={Hq}", flush=True)
+    q, kv = build(800 + waves + bwk + bwv, len(lens), Hq, 8, 128, lens, 16, bwk, bw_v=bwv)
     scale = oa.default_scale(128)
     ref = oa.tiled_compressed_attention(q, kv, scale)
     got = _pa().packed_decode_attention(q.to(DEV), to_device(kv, DEV), scale, plan=(0, waves), allow_tf32=True,
@@ -74,7 +80,8 @@ def test_tf32_balanced_plan_with_few_waves(waves):
     _check(got, ref, lens)
 
 
-def test_tf32_large_scores_and_long_history():
+@pytest.mark.parametrize("bwk,bwv,Hq", [(4, 4, 32), (6, 6, 32), (4, 6, 64)])
+def test_tf32_large_scores_and_long_history(bwk, bwv, Hq):
     """Scores 50 times larger (the lazy maximum moves often) over 4,096 and 2,500 tokens,
     S=32. Here the TF32-class rounding itself moves scores of several hundred by tenths,
     beyond the fp32 bar, as the reference's allow_tf32 does; so the result is checked
@@ -82,7 +89,8 @@ def test_tf32_large_scores_and_long_history():
     at the north-star tolerance. The default call stays within the bar of the fp32
     oracle, and the two results differ (the TF32-class scan ran)."""
     lens = (4096, 2500)
-    q, kv = build(901, len(lens), 32, 8, 128, lens, 32, 4, q_scale=50.0)
+    print(f"tf32 large scores {bwk}/{bwv} Hq={Hq}", flush=True)
+    q, kv = build(901 + bwk + bwv + Hq, len(lens), Hq, 8, 128, lens, 32, bwk, bw_v=bwv, q_scale=50.0)
     scale = oa.default_scale(128)
     dkv, qd = to_device(kv, DEV), q.to(DEV)
     tf = _pa().packed_decode_attention(qd, dkv, scale, allow_tf32=True, out_dtype=torch.float32)
@@ -92,22 +100,21 @@ def test_tf32_large_scores_and_long_history():
     assert not torch.equal(tf, exact)
 
 
-def test_tf32_matches_the_rounded_operand_reference():
+@pytest.mark.parametrize("bwk,bwv,Hq", [(4, 4, 32), (6, 6, 32), (4, 6, 64)])
+def test_tf32_matches_the_rounded_operand_reference(bwk, bwv, Hq):
     """At ordinary scales the TF32-class result also sits within the bar of the decode of
     rounded operands (the check above, on the ragged batch)."""
-    q, kv = build(902, len(RAGGED), 32, 8, 128, RAGGED, 16, 4)
+    q, kv = build(902 + bwk + bwv + Hq, len(RAGGED), Hq, 8, 128, RAGGED, 16, bwk, bw_v=bwv)
     scale = oa.default_scale(128)
     tf = _pa().packed_decode_attention(q.to(DEV), to_device(kv, DEV), scale, allow_tf32=True,
                                        out_dtype=torch.float32)
     _check(tf, tf32_class_reference(q, kv, scale).float(), RAGGED)
 
 
-@pytest.mark.parametrize("bwk,bwv,Hq,Hkv", [(6, 6, 32, 8), (4, 6, 64, 8), (2, 2, 16, 4), (4, 4, 64, 8),
-                                             (4, 4, 32, 2)])
+@pytest.mark.parametrize("bwk,bwv,Hq,Hkv", [(2, 2, 16, 4), (5, 5, 32, 8), (3, 3, 64, 8), (4, 8, 32, 8)])
 def test_tf32_other_shapes_run_the_exact_scan(bwk, bwv, Hq, Hkv):
-    """Widths without a TF32-class scan, and 4-bit pages with n_rep 8 or 16 (one row-scan
-    group of eight, or virtual kv heads of eight), give the default call's output bit
-    for bit."""
+    """Width pairs without a TF32-class scan (2, 3 and 5 bits, 8-bit values) give the
+    default call's output bit for bit."""
     q, kv = build(950 + bwk + bwv, len(RAGGED), Hq, Hkv, 128, RAGGED, 16, bwk, bw_v=bwv)
     scale = oa.default_scale(128)
     dkv, qd = to_device(kv, DEV), q.to(DEV)

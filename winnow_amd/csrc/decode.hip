@@ -318,9 +318,9 @@ int valu_groups(int n_rep) {
 // scan where it applies (head_dim 128, page size >= 16, a compiled width pair, any
 // n_rep that 2^s virtual heads bring to <= 8), else the vector-ALU scan (any
 // supported width pair, n_rep split into groups of <= 16).
-// tf32: the TF32-class row scan where it is compiled (4-bit K and V, a row scan with
-// one group of up to four query heads per kv head: n_rep 1-4), else the same choice
-// as without it (larger n_rep would need virtual kv heads that read the pages again).
+// tf32: the TF32-class row scan where it is compiled (4 and 6-bit K and V, alike or
+// mixed, on the row scan: n_rep up to 8, or up to 16 in virtual kv heads of eight),
+// else the same choice as without it.
 SplitKernel choose_scan(int Hq, int Hkv, int D, int S, int bw_k, int bw_v, bool tf32 = false) {
   SplitKernel sk;
   const int n_rep = Hq / Hkv;

@@ -949,19 +949,19 @@ __device__ __forceinline__ uint2 entry4(Tab<4>& tab, uint32_t x) {
   return *reinterpret_cast<const uint2*>(tab.lds + tab.r[K]);
 }
 
-// Byte offset (8 x index) of the pair-table entry whose 2 BW-bit index starts at bit
-// BIT of the little-endian words w: the index is cut out already multiplied by 8
-// (a shift or alignbit, then one mask), two instructions per lookup.
-template <int BW, int BIT>
+// Byte offset (2^SC x index; entries of 2^SC bytes) of the pair-table entry whose
+// 2 BW-bit index starts at bit BIT of the little-endian words w: the index is cut out
+// already multiplied (a shift or alignbit, then one mask), two instructions per lookup.
+template <int BW, int BIT, int SC = 3>
 __device__ __forceinline__ uint32_t pair_offset(const uint32_t* w) {
-  constexpr uint32_t m8 = ((1u << (2 * BW)) - 1u) << 3;
-  constexpr int s = BIT - 3;  // the index's bit 0 lands on bit 3
+  constexpr uint32_t m = ((1u << (2 * BW)) - 1u) << SC;
+  constexpr int s = BIT - SC;  // the index's bit 0 lands on bit SC
   if constexpr (s < 0) {
-    return (w[0] << (-s)) & m8;
+    return (w[0] << (-s)) & m;
   } else {
     constexpr int wi = s >> 5, sh = s & 31;
-    if constexpr (sh + 2 * BW + 3 <= 32) return (w[wi] >> sh) & m8;
-    else return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & m8;
+    if constexpr (sh + 2 * BW + SC <= 32) return (w[wi] >> sh) & m;
+    else return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & m;
   }
 }
 
@@ -1292,76 +1292,134 @@ __device__ __forceinline__ void value_phase_mx(RowBuf<BWK, BWV>& V, Tab<BWV>& cb
 //
 // allow_tf32 (packed_attention_triton.py:113, 127): both products on single fp16
 // operands, 11 significant bits each (the class of TF32's 10 stored bits), accumulated
-// in fp32; 4-bit K and V, one head group. A table entry holds H(2^8 c) of the two
-// codes of a byte (4 bytes), replicated once per lane of the wave (entry (b, r) at
-// byte 256 b + 4 r of a 64 KB slot), so one SDWA move forms its address as in the
-// 16-bit scan and no read waits on a bank conflict. Without the L halves an 8-slot
-// operand carries eight codes: the scores take 4 K-steps per tile (16 MFMAs per
-// chunk) and the values 2 K-steps per M-tile (16 MFMAs), half the 16-bit scan's
-// matrix-core work, and the lookups read 4 bytes instead of 8.
+// in fp32; 4 or 6-bit K and V, one or two head groups. A table entry holds H(2^8 c) of
+// two codes (4 bytes). The 4-bit table is replicated once per lane of the wave (entry
+// (b, r) at byte 256 b + 4 r of a 64 KB slot), so one SDWA move forms its address as
+// in the 16-bit scan and no read waits on a bank conflict; the 6-bit table holds the
+// 4096 code pairs (16 KB) and is read at 4 x the 12-bit pair index. Without the L
+// halves an 8-slot operand carries eight codes: the scores take 4 K-steps per tile (16
+// MFMAs per chunk) and the values 2 K-steps per M-tile (16 MFMAs), half the 16-bit
+// scan's matrix-core work, and the lookups read 4 bytes instead of 8.
 //   scores  K-step s of tile r: k-slots of group g = dims 32g + 8s + (0..7); column
-//           c < 4 is H(q' head c), the other columns zero.
+//           c < NH is H(q' head c), the other columns zero.
 //   values  K-step ks: k-slots of group g = tokens 32ks + 4j + g, j = 0..7 (token quads
-//           8ks + j of the V buffer); column c < 4 is H(p n_V 2^-gs) of head c, read
+//           8ks + j of the V buffer); column c < NH is H(p n_V 2^-gs) of head c, read
 //           from an fp16 p tile whose 8 halves per (head, ks, g) sit side by side.
 
 constexpr int kTfTableBytes = 256 * 64 * 4;  // 256 byte values x 64 lanes x two fp16
 static_assert(kTfTableBytes == kPairTableBytes, "the TF table takes the 64 KB slot of the 16-bit table");
 
-// Stages the replicated TF table: entry (b, r) holds (H(2^8 c[b & 15]), H(2^8 c[b >> 4])),
-// rounded to nearest.
+template <int BW>
+constexpr int tf_table_bytes() { return BW == 4 ? kTfTableBytes : 4 << (2 * BW); }
+
+// Two fp16 values rounded to nearest, lo in the low half.
+__device__ __forceinline__ uint32_t tf_word(float lo, float hi) {
+  return uint32_t(__builtin_bit_cast(uint16_t, _Float16(lo))) | uint32_t(__builtin_bit_cast(uint16_t, _Float16(hi))) << 16;
+}
+
+// Stages a TF table: 4-bit, the replicated byte table (entry (b, r) holds
+// (H(2^8 c[b & 15]), H(2^8 c[b >> 4]))); 6-bit, entry i holds (H(2^8 c[i mod 64]),
+// H(2^8 c[i >> 6])), two consecutive codes read as one 12-bit index.
+template <int BW>
 __device__ __forceinline__ void stage_table_tf(const float* cb, char* dst, int tid, int nthr) {
+  static_assert(BW == 4 || BW == 6, "TF tables: 4 and 6-bit codes");
   uint32_t* t = reinterpret_cast<uint32_t*>(dst);
-  for (int i = tid; i < 256 * 64; i += nthr) {
-    const int b = i >> 6;
-    const _Float16 lo = _Float16(cb[b & 15] * kCbScale), hi = _Float16(cb[b >> 4] * kCbScale);
-    t[i] = uint32_t(__builtin_bit_cast(uint16_t, lo)) | uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16;
+  if constexpr (BW == 4) {
+    for (int i = tid; i < 256 * 64; i += nthr) {
+      const int b = i >> 6;
+      t[i] = tf_word(cb[b & 15] * kCbScale, cb[b >> 4] * kCbScale);
+    }
+  } else {
+    for (int i = tid; i < (1 << (2 * BW)); i += nthr) t[i] = tf_word(cb[i & 63] * kCbScale, cb[i >> 6] * kCbScale);
   }
 }
 
-// The TF table as one lane reads it: address registers 4 lane | slot << 16, one per
-// byte position of a code word (the code byte goes to bits 8-15).
+// A TF table as one lane reads it: the 6-bit table's base; the 4-bit table's address
+// registers 4 lane | slot << 16, one per byte position of a code word (the code byte
+// goes to bits 8-15).
+template <int BW>
 struct TabTf {
+  const char* t;
+};
+template <>
+struct TabTf<4> {
   const char* lds;
   uint32_t r[4];
-  __device__ void init(const char* base, int slot, int lane) {
-    lds = base;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) r[k] = uint32_t(4 * lane) | (uint32_t(slot) << 16);
-  }
 };
+
+template <int BW>
+__device__ __forceinline__ TabTf<BW> make_tab_tf(const char* lds, int off, int lane) {
+  TabTf<BW> tab;
+  if constexpr (BW == 4) {
+    tab.lds = lds;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) tab.r[k] = uint32_t(4 * lane) | (uint32_t(off >> 16) << 16);
+  } else {
+    tab.t = lds + off;
+  }
+  return tab;
+}
 
 // Entry of the 4-bit pair in byte K of x: one SDWA move, one 4-byte LDS read.
 template <int K>
-__device__ __forceinline__ uint32_t entry_tf(TabTf& tab, uint32_t x) {
+__device__ __forceinline__ uint32_t entry_tf(TabTf<4>& tab, uint32_t x) {
   tab.r[K] = put_byte1<K>(tab.r[K], x);
   return *reinterpret_cast<const uint32_t*>(tab.lds + tab.r[K]);
 }
 
+// Entry of the 6-bit pair table at byte offset off.
+__device__ __forceinline__ uint32_t pair_entry_tf(const TabTf<6>& tab, uint32_t off) {
+  return *reinterpret_cast<const uint32_t*>(tab.t + off);
+}
+
+// Entry of pair N (codes 2N, 2N+1) of a packed piece held as words.
+template <int BW, int N>
+__device__ __forceinline__ uint32_t piece_pair_tf(const uint32_t* w, TabTf<BW>& tab) {
+  if constexpr (BW == 4) return entry_tf<N & 3>(tab, w[N >> 2]);
+  else return pair_entry_tf(tab, pair_offset<BW, 2 * BW * N, 2>(w));
+}
+
 constexpr int kTfLookahead = 4;  // K-steps of table reads in flight ahead of their MFMA
 
-// fp16 p tile of a wave (after its score tile): 4 heads x 64 tokens, token l of the
+// fp16 p tile of a wave (after its score tile): NH heads x 64 tokens, token l of the
 // chunk at half 32 (l >> 5) + 8 (l & 3) + ((l >> 2) & 7) of its head's row.
-constexpr int kTfPTileOffset = 4 * kTileStride;  // words
+template <int NG>
+constexpr int tf_ptile_offset() { return 4 * NG * kTileStride; }  // words
+
+// LDS of a TF work-group: the two tables (a 4-bit table in a 64 KB slot of its own,
+// slot 1 beside a 6-bit table, whose reads then need no base add: the read's 16-bit
+// offset field holds its offsets), then a score tile and a p tile per wave.
+template <int BWK, int BWV, int NG, int WPB>
+struct TfLds {
+  static constexpr bool k4 = BWK == 4, v4 = BWV == 4;
+  static constexpr int k_off = k4 && !v4 ? kTfTableBytes : 0;
+  static constexpr int v_off = v4 ? kTfTableBytes : k4 ? 0 : tf_table_bytes<BWK>();
+  static constexpr int tiles = k_off + tf_table_bytes<BWK>() > v_off + tf_table_bytes<BWV>()
+                                   ? k_off + tf_table_bytes<BWK>()
+                                   : v_off + tf_table_bytes<BWV>();
+  static constexpr int tile_bytes = (tf_ptile_offset<NG>() + 4 * NG * 64 / 2) * 4;
+  static constexpr int total = tiles + WPB * tile_bytes;
+  static_assert(tile_bytes % 16 == 0, "tiles stay 16-byte aligned");
+  static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
+};
 
 // Scores of a chunk into the score tile (head h of token 16r + 4i + g at word
 // h * kTileStride + 16r + 4g + i), before the 2^-(e+8) scale.
-template <int BWK, int BWV>
-__device__ __forceinline__ void score_phase_tf(const RowBuf<BWK, BWV>& K, TabTf& cbk, const h8 (&qb)[4], int lane,
-                                               uint32_t* pt) {
-  constexpr int LA = kTfLookahead;
+template <int BWK, int BWV, int NG>
+__device__ __forceinline__ void score_phase_tf(const RowBuf<BWK, BWV>& K, TabTf<BWK>& cbk, const h8 (&qb)[4],
+                                               int lane, uint32_t* pt) {
+  constexpr int NH = 4 * NG, QW = BWK, LA = kTfLookahead;
   f32x4 d[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) d[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // step k = 4s + r: word s of the quarter (dims 8s .. 8s+7) of tile r
+  // step k = 4s + r: pairs 4s .. 4s+3 (dims 8s .. 8s+7) of the quarter of tile r
   uint32_t e[LA + 1][4];
   auto look = [&](auto kc, uint32_t (&o)[4]) {
     constexpr int k = decltype(kc)::value, s = k >> 2, r = k & 3;
-    const uint32_t w = K.w[r * BWK + s];
-    o[0] = entry_tf<0>(cbk, w);
-    o[1] = entry_tf<1>(cbk, w);
-    o[2] = entry_tf<2>(cbk, w);
-    o[3] = entry_tf<3>(cbk, w);
+    o[0] = piece_pair_tf<BWK, 4 * s>(K.w + r * QW, cbk);
+    o[1] = piece_pair_tf<BWK, 4 * s + 1>(K.w + r * QW, cbk);
+    o[2] = piece_pair_tf<BWK, 4 * s + 2>(K.w + r * QW, cbk);
+    o[3] = piece_pair_tf<BWK, 4 * s + 3>(K.w + r * QW, cbk);
   };
   static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
   __builtin_amdgcn_sched_barrier(0);
@@ -1377,7 +1435,7 @@ __device__ __forceinline__ void score_phase_tf(const RowBuf<BWK, BWV>& K, TabTf&
   });
   const int c = lane & 15, g = lane >> 4;
   wave_lds_sync();  // the previous chunk's reads of the tile are done
-  if (c < 4) {
+  if (c < NH) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       *reinterpret_cast<float4*>(pt + c * kTileStride + 16 * r + 4 * g) = make_float4(d[r][0], d[r][1], d[r][2], d[r][3]);
@@ -1387,9 +1445,10 @@ __device__ __forceinline__ void score_phase_tf(const RowBuf<BWK, BWV>& K, TabTf&
 
 // Online softmax of one chunk (lane = token) from the score tile; H(p n_V 2^-gs) goes to
 // the fp16 p tile. Maxima, the value scale and the rescales as softmax_phase_mx.
+template <int NG>
 __device__ __forceinline__ void softmax_phase_tf(float sc, uint32_t nk_h, uint32_t nv_h, bool valid, int lane,
-                                                 uint32_t* pt, MxState<1>& st) {
-  constexpr int H = 4;
+                                                 uint32_t* pt, MxState<NG>& st) {
+  constexpr int H = 4 * NG;
   const int off = 16 * (lane >> 4) + 4 * (lane & 3) + ((lane >> 2) & 3);  // word of token lane
   const float nk = half_lo(nk_h) * sc;
   const float nv = valid ? half_lo(nv_h) : 0.f;
@@ -1408,11 +1467,14 @@ __device__ __forceinline__ void softmax_phase_tf(float sc, uint32_t nk_h, uint32
     for (int mm = 0; mm < 8; ++mm) st.acc[mm] *= f;
     st.gs = gs_need;
   }
-  bool move = st.m[0] == -INFINITY;
+  float d[H], dmax = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < H; ++i) move = move || __any(sv[i] > st.m[i] + kRescale);
-  if (move) {  // wave-uniform
-    const int hc = (lane & 15) % H;  // head of this lane's accumulator column (columns >= 4 hold zeros)
+  for (int i = 0; i < H; ++i) {
+    d[i] = sv[i] - st.m[i];
+    dmax = fmaxf(dmax, d[i]);
+  }
+  if (st.m[0] == -INFINITY || __any(dmax > kRescale)) {  // wave-uniform
+    const int hc = (lane & 15) % H;  // head of this lane's accumulator column (columns >= H hold zeros)
     float alpha_c = 1.f;
 #pragma unroll
     for (int i = 0; i < H; ++i) {
@@ -1421,16 +1483,17 @@ __device__ __forceinline__ void softmax_phase_tf(float sc, uint32_t nk_h, uint32
       st.m[i] = m_new;
       st.l[i] *= alpha;
       alpha_c = hc == i ? alpha : alpha_c;
+      d[i] = sv[i] - m_new;
     }
 #pragma unroll
     for (int mm = 0; mm < 8; ++mm) st.acc[mm] *= alpha_c;
   }
   const float nvs = ldexpf(nv, -st.gs);
-  _Float16* ph = reinterpret_cast<_Float16*>(pt + kTfPTileOffset);
+  _Float16* ph = reinterpret_cast<_Float16*>(pt + tf_ptile_offset<NG>());
   const int slot = 32 * (lane >> 5) + 8 * (lane & 3) + ((lane >> 2) & 7);
 #pragma unroll
   for (int i = 0; i < H; ++i) {
-    const float p = __builtin_amdgcn_exp2f(sv[i] - st.m[i]);  // 0 for masked tokens
+    const float p = __builtin_amdgcn_exp2f(d[i]);  // 0 for masked tokens
     st.l[i] += p;
     ph[64 * i + slot] = _Float16(p * nvs);
   }
@@ -1438,24 +1501,31 @@ __device__ __forceinline__ void softmax_phase_tf(float sc, uint32_t nk_h, uint32
 }
 
 // Values of a chunk: 2 K-steps (32 tokens each) x 8 M-tiles (one dim of each lane's
-// eight), one MFMA each; 4-bit V codes of token pairs (j, j+1) merged into bytes.
-template <int BWK, int BWV>
-__device__ __forceinline__ void value_phase_tf(const RowBuf<BWK, BWV>& V, TabTf& cbv, const uint32_t* pt, int lane,
+// eight), one MFMA each. 4-bit V codes of token pairs (j, j+1) are merged into bytes;
+// 6-bit ones into 12-bit pair indices by merge_value_pairs.
+template <int BWK, int BWV, int NG>
+__device__ __forceinline__ void value_phase_tf(RowBuf<BWK, BWV>& V, TabTf<BWV>& cbv, const uint32_t* pt, int lane,
                                                f32x4 (&acc)[8]) {
-  constexpr int LA = kTfLookahead;
+  constexpr int NH = 4 * NG, VW = VWords<BWV>::N, LA = kTfLookahead;
   const int c = lane & 15, g = lane >> 4;
-  const _Float16* ph = reinterpret_cast<const _Float16*>(pt + kTfPTileOffset);
-  const uint4* prow = reinterpret_cast<const uint4*>(ph + 64 * (c & 3) + 8 * g);
-  const bool live = c < 4;
-  // step k = 8ks + mt
+  if constexpr (BWV != 4) merge_value_pairs<BWK, BWV>(V, lane);
+  const _Float16* ph = reinterpret_cast<const _Float16*>(pt + tf_ptile_offset<NG>());
+  const uint4* prow = reinterpret_cast<const uint4*>(ph + 64 * (c % NH) + 8 * g);
+  const bool live = c < NH;
+  // step k = 8ks + mt; pair p = tokens (8ks + 2p, 8ks + 2p + 1) of the V buffer
   auto look = [&](auto kc, uint32_t (&o)[4]) {
     constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const uint32_t wa = V.w[8 * ks + 2 * p], wb = V.w[8 * ks + 2 * p + 1];
-      const uint32_t x = (mt & 1) ? (((wa >> 4) & 0x0F0F0F0Fu) | (wb & 0xF0F0F0F0u))
-                                  : ((wa & 0x0F0F0F0Fu) | ((wb << 4) & 0xF0F0F0F0u));
-      o[p] = entry_tf<(mt >> 1)>(cbv, x);
+      if constexpr (BWV == 4) {
+        const uint32_t wa = V.w[8 * ks + 2 * p], wb = V.w[8 * ks + 2 * p + 1];
+        const uint32_t x = (mt & 1) ? (((wa >> 4) & 0x0F0F0F0Fu) | (wb & 0xF0F0F0F0u))
+                                    : ((wa & 0x0F0F0F0Fu) | ((wb << 4) & 0xF0F0F0F0u));
+        o[p] = entry_tf<(mt >> 1)>(cbv, x);
+      } else {
+        // Ce in the first token's slot (even dims), Co in the second's (odd dims)
+        o[p] = pair_entry_tf(cbv, pair_offset<BWV, BWV * mt, 2>(V.w + (8 * ks + 2 * p + (mt & 1)) * VW));
+      }
     }
   };
   uint4 wq = prow[0];  // p halves of K-step 0; K-step 1's are read during K-step 0
@@ -1482,8 +1552,9 @@ __device__ __forceinline__ void value_phase_tf(const RowBuf<BWK, BWV>& V, TabTf&
 // Undoes the value scale and writes the (acc, m, l) partial of each query head h <
 // n_rep to row prow * n_rep + h: lane 16g + h writes dims 32g .. 32g+31 (columns hold
 // whole values: no halves to add).
-__device__ __forceinline__ void write_partial_tf(const DecodeArgs& a, MxState<1>& st, int64_t prow, int lane) {
-  constexpr int D = 128, H = 4;
+template <int NG>
+__device__ __forceinline__ void write_partial_tf(const DecodeArgs& a, MxState<NG>& st, int64_t prow, int lane) {
+  constexpr int D = 128, H = 4 * NG;
   const float f = ldexpf(1.f, st.gs - 8);
 #pragma unroll
   for (int i = 0; i < H; ++i) st.l[i] = wave_sum(st.l[i]);
@@ -1546,12 +1617,12 @@ __device__ __forceinline__ void write_partial_mx(const DecodeArgs& a, MxState<NG
   }
 }
 
-// scan_range on the 16x16x32 fp16 MFMA; TF: the TF32-class products (4-bit, one head
-// group, TabTf tables).
+// scan_range on the 16x16x32 fp16 MFMA; TF: the TF32-class products (4 or 6-bit
+// codes, TabTf tables).
 template <int BWK, int BWV, int NG, bool TF, class TabK, class TabV>
 __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh, int t_lo, int t_hi, int64_t prow,
                                              int lane, TabK& cbk, TabV& cbv, uint32_t* ptile) {
-  static_assert(!TF || (BWK == 4 && BWV == 4 && NG == 1), "TF32-class scan: 4-bit K and V, one head group");
+  static_assert(!TF || ((BWK == 4 || BWK == 6) && (BWV == 4 || BWV == 6)), "TF32-class scan: 4 or 6-bit K and V");
   constexpr int D = 128, NH = 4 * NG;
   const int page_hi = (t_hi + (1 << a.log2S) - 1) >> a.log2S;
   const int n = (t_hi - t_lo + 63) >> 6;
@@ -1628,15 +1699,15 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
     block_bases<16 * BWK>(kbase, uint32_t(a.ksp), pid_next, c0 + 64, lane, smask, kb);
     load_k16(a, kvh, lane, c0 + 64, pid_next, Z, more, kb);
     if constexpr (TF) {
-      score_phase_tf<BWK, BWV>(X, cbk, qb, lane, ptile);
-      softmax_phase_tf(sc, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
+      score_phase_tf<BWK, BWV, NG>(X, cbk, qb, lane, ptile);
+      softmax_phase_tf<NG>(sc, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
     } else {
       score_phase_mx<BWK, BWV, NG>(X, cbk, qb, lane, ptile);
       softmax_phase_mx<NG>(sc, X.w[Buf::KW], X.w[Buf::KW + 1], c0 + lane < t_hi, lane, ptile, st);
     }
     block_bases<16 * BWV>(vbase, uint32_t(a.vsp), pid_next, c0 + 64, lane, smask, vb);
     load_v<BWK, BWV, kRawV<BWV>>(a, kvh, lane, c0 + 64, pid_next, X, more, vb);
-    if constexpr (TF) value_phase_tf<BWK, BWV>(Y, cbv, ptile, lane, st.acc);
+    if constexpr (TF) value_phase_tf<BWK, BWV, NG>(Y, cbv, ptile, lane, st.acc);
     else value_phase_mx<BWK, BWV, NG>(Y, cbv, ptile, lane, st.acc);
     pid_next = pid_after;
   };
@@ -1656,7 +1727,7 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
   }
   if (ch < n) step(ch, b0, b1, b2);
   if (ch + 1 < n) step(ch + 1, b2, b0, b1);
-  if constexpr (TF) write_partial_tf(a, st, prow, lane);
+  if constexpr (TF) write_partial_tf<NG>(a, st, prow, lane);
   else write_partial_mx<NG>(a, st, prow, lane);
 }
 
@@ -1688,26 +1759,23 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows16_kernel(DecodeArgs a) {
   });
 }
 
-// The TF32-class row scan (allow_tf32): 4-bit K and V, one head group, the 16-bit
-// scan's plan, loads and LDS layout with TF tables in the two 64 KB slots.
-template <int WPB>
+// The TF32-class row scan (allow_tf32): 4 or 6-bit K and V, one or two head groups,
+// the 16-bit scan's plan and loads with TF tables (TfLds).
+template <int BWK, int BWV, int NG, int WPB>
 __global__ __launch_bounds__(64 * WPB) void decode_rows_tf_kernel(DecodeArgs a) {
-  using Lay = Rows16Lds<4, 4, 1, WPB>;
-  static_assert(Lay::k_off == 0 && Lay::v_off == kTfTableBytes, "TF tables in slots 0 and 1");
-  static_assert(Lay::tile_bytes >= (kTfPTileOffset + 4 * 64 / 2) * 4, "score and p tiles fit a wave's tile");
+  using Lay = TfLds<BWK, BWV, NG, WPB>;
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_table_tf(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
-  stage_table_tf(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
+  stage_table_tf<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
+  stage_table_tf<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);
-  TabTf cbk, cbv;
-  cbk.init(lds, 0, lane);
-  cbv.init(lds, 1, lane);
+  TabTf<BWK> cbk = make_tab_tf<BWK>(lds, Lay::k_off, lane);
+  TabTf<BWV> cbv = make_tab_tf<BWV>(lds, Lay::v_off, lane);
   for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow) {
-    scan_range16<4, 4, 1, true>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+    scan_range16<BWK, BWV, NG, true>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
   });
 }
 
@@ -1782,6 +1850,31 @@ SplitKernel rows16_for(int bw_k, int bw_v) {
   return SplitKernel{};
 }
 
+template <int BWK, int BWV, int NG>
+SplitKernel rows_tf_kernel() {
+  // the 16-bit scan's work-group: twelve waves (three per SIMD, in 167 VGPRs with one K
+  // and one V buffer) measured 106.5 us at config 2 against 103.0 us for eight
+  constexpr int wpb = 8;
+  SplitKernel k;
+  k.fn = decode_rows_tf_kernel<BWK, BWV, NG, wpb>;
+  k.block = 64 * wpb;
+  k.wpb = wpb;
+  k.nrep = 4 * NG;
+  k.log2_units = true;
+  k.rows = true;
+  return k;
+}
+
+// The TF32-class scan's width pairs: 4 and 6 bits, alike or mixed.
+template <int NG>
+SplitKernel rows_tf_for(int bw_k, int bw_v) {
+  if (bw_k == 4 && bw_v == 4) return rows_tf_kernel<4, 4, NG>();
+  if (bw_k == 6 && bw_v == 6) return rows_tf_kernel<6, 6, NG>();
+  if (bw_k == 4 && bw_v == 6) return rows_tf_kernel<4, 6, NG>();
+  if (bw_k == 6 && bw_v == 4) return rows_tf_kernel<6, 4, NG>();
+  return SplitKernel{};
+}
+
 // WN_DECODE_SCAN=rows32 keeps the fp32-product row scan for every width (the two
 // compute the same result to fp32 rounding; the knob exists to compare them on one
 // machine). Read once.
@@ -1796,18 +1889,9 @@ bool rows16_allowed() {
 }  // namespace
 
 SplitKernel pick_split_rows_tf(int bw_k, int bw_v, int n_rep) {
-  if (bw_k != 4 || bw_v != 4 || n_rep < 1 || n_rep > 4 || !rows16_allowed()) return SplitKernel{};
-  // the 16-bit scan's work-group: twelve waves (three per SIMD, in 167 VGPRs with one K
-  // and one V buffer) measured 106.5 us at config 2 against 103.0 us for eight
-  constexpr int wpb = 8;
-  SplitKernel k;
-  k.fn = decode_rows_tf_kernel<wpb>;
-  k.block = 64 * wpb;
-  k.wpb = wpb;
-  k.nrep = 4;
-  k.log2_units = true;
-  k.rows = true;
-  return k;
+  const int ng = n_rep >= 1 && n_rep <= 4 ? 1 : n_rep >= 5 && n_rep <= 8 ? 2 : 0;
+  if (ng == 0 || !rows16_allowed()) return SplitKernel{};
+  return ng == 1 ? rows_tf_for<1>(bw_k, bw_v) : rows_tf_for<2>(bw_k, bw_v);
 }
 
 SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep) {

@@ -50,7 +50,8 @@ struct SplitKernel {
 SplitKernel pick_split_rows(int bw_k, int bw_v, int n_rep);
 
 // The TF32-class row scan (single fp16 operands, fp32 accumulation; allow_tf32) for
-// 4-bit K and V and up to four query heads per kv head, or an empty SplitKernel.
+// 4 and 6-bit K and V (alike or mixed) and up to eight query heads per kv head, or an
+// empty SplitKernel.
 SplitKernel pick_split_rows_tf(int bw_k, int bw_v, int n_rep);
 
 // Dense-page scan (bf16 or fp16 pages of head_dim 64 or 128, up to 16 query heads

@@ -276,8 +276,8 @@ def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
     sized to fill the GPU; an integer asks for exactly that many splits over the page-table
     width, as the reference does. ``allow_tf32=True`` asks, as in the reference
     (whose kernel hands it to both ``tl.dot`` products), for TF32-class products:
-    ``wn_decode_attention_tf32`` runs 4-bit K and V with up to four query heads per kv
-    head on single fp16 operands (11 significant bits) with fp32 accumulation, and
+    ``wn_decode_attention_tf32`` runs 4 and 6-bit K and V (alike or mixed) on the row
+    scan on single fp16 operands (11 significant bits) with fp32 accumulation, and
     every other shape on the fp32-exact scan. ``num_warps`` and ``num_stages`` are
     Triton schedule knobs, accepted for call compatibility and ignored;
     ``pages_per_iter`` must still be a power of two. ``out_dtype=torch.float32``
