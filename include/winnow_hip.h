@@ -30,6 +30,10 @@
  *                            (TurboQuantMSE.dequantize_into)
  *   wn_tq_dequant            turboquant_kv/kernel.py:78-115, csrc/tq_dequant.cu:186-215
  *   wn_dequantize_history    turboquant_kv/packed_backend.py:192-208
+ *   wn_prefill_attention     turboquant_kv/packed_backend.py:211-226
+ *                            (_reconstruct_sdpa, the Q > 1 route at :278-280:
+ *                            dequantize the history, then SDPA with the offset
+ *                            causal mask of packed_attention.py:198-206)
  *   wn_dense_decode_attention turboquant_kv/packed_attention_triton.py:190-201
  *                            (dense_decode_attention, the matched unquantized
  *                            baseline; DENSE branch of the kernel :101-127)
@@ -44,7 +48,7 @@
 extern "C" {
 #endif
 
-#define WN_ABI_VERSION 7
+#define WN_ABI_VERSION 8
 
 /* element types of floating-point tensors crossing the ABI */
 enum { WN_F32 = 0, WN_F16 = 1, WN_BF16 = 2 };
@@ -254,6 +258,52 @@ int wn_dequantize_history(const uint8_t* pages, int64_t page_stride, int64_t hea
                           const int32_t* table_row, int L, int Hkv, int S,
                           const float* centroids, const float* pi, int bw, int D,
                           void* out, int out_dtype, int fast, void* stream);
+
+/* Split count of wn_prefill_attention for this shape: about two waves per resident
+ * scan slot on the current device over the (sequence, kv head, 32-row query block)
+ * items, and at most a quarter of the 64-token chunks of max_len (the longest
+ * sequence; any count >= 1 is valid whatever the lengths). head_dim 128, S a power
+ * of two >= 16, widths 4 and 6 bits (alike or mixed); WN_E_UNSUPPORTED otherwise. */
+int wn_prefill_plan(int B, int Hq, int Hkv, int Q, int D, int S, int bw_k, int bw_v, int max_len,
+                    int* num_splits);
+
+/* Bytes of scratch wn_prefill_attention needs: the rotated queries (rows n_rep * Q
+ * per kv head rounded up to 64) and num_splits (acc, m, l) partials per row. -1 for
+ * invalid sizes. */
+int64_t wn_prefill_workspace_bytes(int B, int Hq, int Hkv, int Q, int D, int num_splits);
+
+/* Prefill attention over paged packed K/V, Q >= 1 query tokens per sequence, read in
+ * the packed form (no history is written to HBM). Replaces the reference's Q > 1
+ * route _reconstruct_sdpa (packed_backend.py:211-226): query i of sequence b, whose
+ * seq_lens[b] = L already counts the Q new tokens, attends to keys j <= L - Q + i
+ * (packed_attention.py:198-206); a query that sees no key gives 0.
+ *   q    (B, Hq, Q, D) with element strides q_stride_b, q_stride_h, q_stride_q
+ *        (last dim contiguous), element type q_dtype
+ *   out  (B, Hq, Q, D) contiguous, element type out_dtype
+ * The algebra of wn_decode_attention, with single fp16 operands (11 significant bits,
+ * rounded to nearest) in both products and fp32 accumulation: finer than the
+ * reference's bf16 history and bf16 SDPA for bf16 queries. head_dim 128, S a power of
+ * two >= 16, 4 and 6-bit K and V (alike or mixed; WN_E_UNSUPPORTED otherwise). K
+ * pages 16-byte (4-bit) or 8-byte aligned in base and strides, V pages 4-byte; norm
+ * bases 8-byte aligned, norm strides multiples of 4 elements. num_splits from
+ * wn_prefill_plan (any value 1..4096 is valid); the page-id and length
+ * preconditions of wn_decode_attention hold here too (unchecked on the device).
+ * ev_begin / ev_end (hipEvent_t or NULL) are recorded around the scan kernel. */
+int wn_prefill_attention(
+    const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_q,
+    const float* pi_k, const float* pi_v,
+    const float* codebook_k, const float* codebook_v,
+    const uint8_t* k_pages, int64_t k_stride_p, int64_t k_stride_h,
+    const uint8_t* v_pages, int64_t v_stride_p, int64_t v_stride_h,
+    const uint16_t* k_norms, int64_t kn_stride_p, int64_t kn_stride_h,
+    const uint16_t* v_norms, int64_t vn_stride_p, int64_t vn_stride_h,
+    const int32_t* page_table, int64_t table_stride_b,
+    const int32_t* seq_lens,
+    void* out, int out_dtype,
+    void* workspace, int64_t workspace_bytes,
+    int B, int Hq, int Hkv, int Q, int D, int S, int bw_k, int bw_v,
+    float scale, int num_splits,
+    void* stream, void* ev_begin, void* ev_end);
 
 /* Plan of wn_dense_decode_attention (as wn_decode_plan: requested_splits > 0 gives
  * the reference's cdiv split of max_pages; 0 lets the library choose: a balanced

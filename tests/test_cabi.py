@@ -47,7 +47,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.wn_abi_version() == 7
+    assert lib.wn_abi_version() == 8
     assert isinstance(lib.wn_last_error(), bytes)
 
 

@@ -107,7 +107,9 @@ def test_allow_tf32_decode_keeps_the_greedy_tokens(model):
     bits) move such scores by tenths and the first decode step's logits by a few
     percent of their scale (the fp32-exact decode: 2e-5). The bar here is therefore
     1e-1 of the logit scale; the operator itself is held to the float64 decode of
-    rounded operands at scores of that size (test_gpu_decode_tf32.py)."""
+    rounded operands at scores of that size (test_gpu_decode_tf32.py). The prompts'
+    Q > 1 steps run the fused prefill over the packed pages, which allow_tf32 opens to
+    fp32 queries (the same operand class)."""
     from winnow_amd import packed_backend as pb
     prompts = _prompts(3, seed=5)
     ref_toks, ref_steps = _generate(model, prompts, 10, backend="reconstruct_sdpa", bit_width=4)
@@ -115,6 +117,7 @@ def test_allow_tf32_decode_keeps_the_greedy_tokens(model):
     pb.BACKEND_COUNTS.clear()
     toks, steps = _generate(model, prompts, 10, backend="auto", bit_width=4, allow_tf32=True)
     assert pb.BACKEND_COUNTS["hip_packed"] == 9 * 2
+    assert pb.BACKEND_COUNTS["prefill_hip_packed"] == 3 * 2
     assert toks == ref_toks == exact_toks
     assert not torch.equal(steps[1], exact_steps[1])
     scale = max(1.0, max(x.abs().max().item() for x in ref_steps))

@@ -58,3 +58,25 @@ def test_rounding_matters_where_it_should():
     q, kv = build(12, len(lens), 32, 8, 128, lens, 16, 4)
     ordinary = (tf32_class_reference(q, kv, scale).float() - oa.tiled_compressed_attention(q, kv, scale))
     assert torch.allclose(ordinary, torch.zeros_like(ordinary), atol=2e-3)
+
+
+def test_prefill_queries_follow_the_offset_causal_mask():
+    """Q > 1: with the rounding off it is the oracle's fp32 reconstruct attention
+    (offset causal mask, rows without a key = 0) to fp32 rounding, the queries of a
+    sequence shorter than Q included; query i of one row, alone as a Q = 1 decode of
+    the history cut at L - Q + i + 1, gives the same row."""
+    lens = (0, 3, 17, 130, 300)
+    Q = 5
+    q, kv = build(21, len(lens), 12, 4, 128, lens, 16, 4)
+    q = torch.randn(len(lens), 12, Q, 128, generator=torch.Generator().manual_seed(22))
+    scale = oa.default_scale(128)
+    got = tf32_class_reference(q, kv, scale, rnd=lambda x: x.double())
+    want = oa.reconstruct_attention(q, kv, scale)
+    assert (got.float() - want).abs().max().item() < 1e-5
+    assert (got[1, :, :2] == 0).all()            # L = 3 < Q: queries 0 and 1 see no key
+    b, i = 3, 2
+    cut = oa.OracleKV(kv.k_pages, kv.k_norms, kv.v_pages, kv.v_norms, kv.page_table,
+                      torch.tensor([lens[b] - Q + i + 1 if j == b else 0 for j in range(len(lens))],
+                                   dtype=torch.int32), kv.k_quant, kv.v_quant, kv.head_dim)
+    one = tf32_class_reference(q[:, :, i:i + 1], cut, scale, rnd=lambda x: x.double())
+    assert (one[b, :, 0] - got[b, :, i]).abs().max().item() < 1e-12

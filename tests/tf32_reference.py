@@ -19,31 +19,42 @@ def round11(x: torch.Tensor, bits: int = 11) -> torch.Tensor:
     return torch.ldexp(torch.round(m * (1 << bits)) / (1 << bits), e)
 
 
-def tf32_class_reference(q: torch.Tensor, kv, scale: float, rnd=round11) -> torch.Tensor:
-    """float64 decode attention whose score and value operands are first rounded as the
-    TF32-class scan rounds them (``rnd``): the rotated, scaled query (in log2 units, as
-    the scan carries it) and both codebooks to 11 significant bits. The p n_V
-    operand's rounding (2^-12 relative per term) is left out; everything else is exact.
-    The query is rotated in float64 before its rounding, the scan rounds its fp32
-    rotation: the two can differ by one step of the 11-bit grid where they fall on
-    either side of a halfway point. The algebra is the oracle's decode
-    (packed_attention.py:260-334 in float64)."""
-    B, Hq, _, D = q.shape
-    n_rep = Hq // kv.num_kv_heads
+def tf32_class_reference(q: torch.Tensor, kv, scale: float, rnd=round11,
+                         q_log2: torch.Tensor | None = None) -> torch.Tensor:
+    """float64 attention whose score and value operands are first rounded as the
+    TF32-class scans (decode with ``allow_tf32=True``, and the fused prefill) round
+    them (``rnd``): the rotated, scaled query (in log2 units, as the scans carry it)
+    and both codebooks to 11 significant bits. The p n_V operand's rounding (2^-12
+    relative per term) is left out; everything else is exact. The query is rotated in
+    float64 before its rounding, the scans round their fp32 rotation: the two can
+    differ by one step of the 11-bit grid where they fall on either side of a halfway
+    point. q is (B, Hq, Q, D): query i of a sequence of length L sees keys
+    j <= L - Q + i and a query that sees none gives 0, as in the oracle's
+    reconstruct_attention (packed_attention.py:198-231, here in float64). ``q_log2``
+    (B, Hq, Q, D), when given, replaces the float64 rotation: the scan's own fp32
+    rotated query in log2 units (scale log2(e) q Pi_K^T), which the scan rounds as
+    ``rnd`` does, so that no component can round the other way."""
+    B, Hq, Q, D = q.shape
     log2e = 1.0 / math.log(2.0)
     ck_t, cv_t = rnd(kv.k_quant.centroids), rnd(kv.v_quant.centroids)
-    q_rot = (q[:, :, 0].double() @ kv.k_quant.Pi.double().T) * scale
-    q_r = rnd(q_rot * log2e) / log2e
-    out = torch.zeros(B, Hq, 1, D, dtype=torch.float64)
+    if q_log2 is None:
+        q_log2 = (q.double() @ kv.k_quant.Pi.double().T) * (scale * log2e)    # (B, Hq, Q, D)
+    q_r = rnd(q_log2.double()) / log2e
+    out = torch.zeros(B, Hq, Q, D, dtype=torch.float64)
+    n_rep = Hq // kv.num_kv_heads
     heads = torch.arange(Hq) // n_rep
     for b in range(B):
-        if int(kv.seq_lens[b]) == 0:
+        L = int(kv.seq_lens[b])
+        if L == 0:
             continue
         pk, nk = oa._gather_history(kv.k_pages, kv.k_norms, kv, b)
         pv, nv = oa._gather_history(kv.v_pages, kv.v_norms, kv, b)
         ck = ck_t[oa.unpack_t(pk, kv.k_quant.bit_width, D).long()] * nk.double()[..., None]
         cv = cv_t[oa.unpack_t(pv, kv.v_quant.bit_width, D).long()] * nv.double()[..., None]
-        s = (q_r[b][:, None, :] @ ck[heads].transpose(-1, -2))[:, 0]          # (Hq, L)
-        a = torch.softmax(s, -1)[:, None, :] @ cv[heads]                        # (Hq, 1, D)
-        out[b] = a @ kv.v_quant.Pi.double()
+        s = q_r[b] @ ck[heads].transpose(-1, -2)                                # (Hq, Q, L)
+        allowed = torch.arange(L)[None, :] <= (L - Q + torch.arange(Q))[:, None]
+        s = s.masked_fill(~allowed[None], float("-inf"))
+        p = torch.softmax(s, -1).nan_to_num(0.0)
+        a = p @ cv[heads]                                                       # (Hq, Q, D)
+        out[b] = (a @ kv.v_quant.Pi.double()) * allowed.any(-1)[None, :, None]
     return out

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libwinnow_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 WN_F32, WN_F16, WN_BF16 = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 32 << 20          # WN_NOALLOC_SCRATCH_BYTES
@@ -103,6 +103,20 @@ SIGNATURES = {
         _c_p, _c_i, _c_i, _c_i,                     # table row, L, Hkv, S
         _c_p, _c_p, _c_i, _c_i,                     # centroids, Pi, bw, D
         _c_p, _c_i, _c_i, _c_p]),                   # out, out dtype, fast, stream
+    "wn_prefill_plan": (_c_i, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, ctypes.POINTER(_c_i)]),
+    "wn_prefill_workspace_bytes": (_c_i64, [_c_i, _c_i, _c_i, _c_i, _c_i, _c_i]),
+    "wn_prefill_attention": (_c_i, [
+        _c_p, _c_i, _c_i64, _c_i64, _c_i64,         # q, dtype, strides (b, h, q)
+        _c_p, _c_p, _c_p, _c_p,                     # pi_k, pi_v, codebooks
+        _c_p, _c_i64, _c_i64,                       # k pages
+        _c_p, _c_i64, _c_i64,                       # v pages
+        _c_p, _c_i64, _c_i64,                       # k norms
+        _c_p, _c_i64, _c_i64,                       # v norms
+        _c_p, _c_i64, _c_p,                         # table, stride, seq_lens
+        _c_p, _c_i, _c_p, _c_i64,                   # out, out dtype, workspace
+        _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,   # B Hq Hkv Q D S bwk bwv
+        _c_f, _c_i,                                 # scale, num_splits
+        _c_p, _c_p, _c_p]),                         # stream, ev_begin, ev_end
     "wn_probe_lds_lookup_rate": (_c_i, [_c_i, _c_i, ctypes.POINTER(ctypes.c_double)]),
 }
 

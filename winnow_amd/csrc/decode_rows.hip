@@ -41,23 +41,15 @@
 #include <utility>
 
 #include "wn_decode.h"
+#include "wn_tables.h"
 
 namespace wn {
 namespace {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 
 constexpr float kRescale = 8.0f;
 constexpr int kPStride = 20;  // floats per (head, token group) row of the p tile (16 + pad, 16-B rows)
-
-template <int I, int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
 
 template <int K>
 __device__ __forceinline__ float comp(const float4& x) {
@@ -71,22 +63,6 @@ __device__ __forceinline__ float comp(const float4& x) {
 // p(head 4g+i, token c0+4q+G) * n_V sits at row 16g + 4i + G, column q.
 __device__ __forceinline__ const float4* tile_row(const float* pt, int g, int lane) {
   return reinterpret_cast<const float4*>(pt + (16 * g + (lane & 3) * 4 + (lane >> 4)) * kPStride);
-}
-
-// Byte K of x written into byte 1 of r, the other bytes of r kept: one VOP2 SDWA
-// move. With r = 8*(lane % 32) | slot << 16 this is the LDS byte address of entry
-// (byte K of x, lane % 32) of the replicated pair table in 64 KB slot `slot`.
-template <int K>
-__device__ __forceinline__ uint32_t put_byte1(uint32_t r, uint32_t x) {
-  if constexpr (K == 0)
-    asm("v_mov_b32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0" : "+v"(r) : "v"(x));
-  else if constexpr (K == 1)
-    asm("v_mov_b32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1" : "+v"(r) : "v"(x));
-  else if constexpr (K == 2)
-    asm("v_mov_b32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_2" : "+v"(r) : "v"(x));
-  else
-    asm("v_mov_b32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3" : "+v"(r) : "v"(x));
-  return r;
 }
 
 constexpr int kPairTableBytes = 256 * 32 * 8;  // 256 byte values x 32 lanes x float2
@@ -843,9 +819,6 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
 //            with an exact rescale of the accumulators, when a chunk needs it); the
 //            partials are multiplied by 2^(gs-8) when written.
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-constexpr float kCbScale = 256.0f;  // codebook values scaled by 2^8 before the split
 // One head group: the score tile keeps both column halves (q' H and L parts) and the
 // softmax adds them as it reads (four adds per lane) instead of a row rotate and add
 // on the sixteen output registers; two groups keep the rotate, for LDS room.
@@ -949,22 +922,6 @@ __device__ __forceinline__ uint2 entry4(Tab<4>& tab, uint32_t x) {
   return *reinterpret_cast<const uint2*>(tab.lds + tab.r[K]);
 }
 
-// Byte offset (2^SC x index; entries of 2^SC bytes) of the pair-table entry whose
-// 2 BW-bit index starts at bit BIT of the little-endian words w: the index is cut out
-// already multiplied (a shift or alignbit, then one mask), two instructions per lookup.
-template <int BW, int BIT, int SC = 3>
-__device__ __forceinline__ uint32_t pair_offset(const uint32_t* w) {
-  constexpr uint32_t m = ((1u << (2 * BW)) - 1u) << SC;
-  constexpr int s = BIT - SC;  // the index's bit 0 lands on bit SC
-  if constexpr (s < 0) {
-    return (w[0] << (-s)) & m;
-  } else {
-    constexpr int wi = s >> 5, sh = s & 31;
-    if constexpr (sh + 2 * BW + SC <= 32) return (w[wi] >> sh) & m;
-    else return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & m;
-  }
-}
-
 template <int BW>
 __device__ __forceinline__ uint2 pair_entry(const Tab<BW>& tab, uint32_t off) {
   return *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(tab.t) + off);
@@ -983,20 +940,6 @@ __device__ __forceinline__ uint2 piece_pair(const uint32_t* w, Tab<BW>& tab) {
 // one field into the gaps, Co the same for the odd ones, so the index of dim m is the
 // 2 BW bits of Ce (m even) or Co (m odd) from bit BW m, and each lookup costs two
 // instructions (pair_offset). RAW windows are unshifted on the way.
-template <int BW>
-constexpr uint64_t field_mask(int parity) {
-  uint64_t m = 0;
-  for (int k = parity; k < 8; k += 2) m |= ((uint64_t(1) << BW) - 1) << (BW * k);
-  return m;
-}
-
-// (a & m) | (b & ~m) in one instruction whatever the compiler knows of a's and b's bits.
-__device__ __forceinline__ uint32_t bitsel(uint32_t m, uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(a), "v"(b));
-  return r;
-}
-
 template <int BWK, int BWV>
 __device__ __forceinline__ void merge_value_pairs(RowBuf<BWK, BWV>& V, int lane) {
   constexpr int VW = VWords<BWV>::N;
@@ -1306,78 +1249,7 @@ __device__ __forceinline__ void value_phase_mx(RowBuf<BWK, BWV>& V, Tab<BWV>& cb
 //           8ks + j of the V buffer); column c < NH is H(p n_V 2^-gs) of head c, read
 //           from an fp16 p tile whose 8 halves per (head, ks, g) sit side by side.
 
-constexpr int kTfTableBytes = 256 * 64 * 4;  // 256 byte values x 64 lanes x two fp16
 static_assert(kTfTableBytes == kPairTableBytes, "the TF table takes the 64 KB slot of the 16-bit table");
-
-template <int BW>
-constexpr int tf_table_bytes() { return BW == 4 ? kTfTableBytes : 4 << (2 * BW); }
-
-// Two fp16 values rounded to nearest, lo in the low half.
-__device__ __forceinline__ uint32_t tf_word(float lo, float hi) {
-  return uint32_t(__builtin_bit_cast(uint16_t, _Float16(lo))) | uint32_t(__builtin_bit_cast(uint16_t, _Float16(hi))) << 16;
-}
-
-// Stages a TF table: 4-bit, the replicated byte table (entry (b, r) holds
-// (H(2^8 c[b & 15]), H(2^8 c[b >> 4]))); 6-bit, entry i holds (H(2^8 c[i mod 64]),
-// H(2^8 c[i >> 6])), two consecutive codes read as one 12-bit index.
-template <int BW>
-__device__ __forceinline__ void stage_table_tf(const float* cb, char* dst, int tid, int nthr) {
-  static_assert(BW == 4 || BW == 6, "TF tables: 4 and 6-bit codes");
-  uint32_t* t = reinterpret_cast<uint32_t*>(dst);
-  if constexpr (BW == 4) {
-    for (int i = tid; i < 256 * 64; i += nthr) {
-      const int b = i >> 6;
-      t[i] = tf_word(cb[b & 15] * kCbScale, cb[b >> 4] * kCbScale);
-    }
-  } else {
-    for (int i = tid; i < (1 << (2 * BW)); i += nthr) t[i] = tf_word(cb[i & 63] * kCbScale, cb[i >> 6] * kCbScale);
-  }
-}
-
-// A TF table as one lane reads it: the 6-bit table's base; the 4-bit table's address
-// registers 4 lane | slot << 16, one per byte position of a code word (the code byte
-// goes to bits 8-15).
-template <int BW>
-struct TabTf {
-  const char* t;
-};
-template <>
-struct TabTf<4> {
-  const char* lds;
-  uint32_t r[4];
-};
-
-template <int BW>
-__device__ __forceinline__ TabTf<BW> make_tab_tf(const char* lds, int off, int lane) {
-  TabTf<BW> tab;
-  if constexpr (BW == 4) {
-    tab.lds = lds;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) tab.r[k] = uint32_t(4 * lane) | (uint32_t(off >> 16) << 16);
-  } else {
-    tab.t = lds + off;
-  }
-  return tab;
-}
-
-// Entry of the 4-bit pair in byte K of x: one SDWA move, one 4-byte LDS read.
-template <int K>
-__device__ __forceinline__ uint32_t entry_tf(TabTf<4>& tab, uint32_t x) {
-  tab.r[K] = put_byte1<K>(tab.r[K], x);
-  return *reinterpret_cast<const uint32_t*>(tab.lds + tab.r[K]);
-}
-
-// Entry of the 6-bit pair table at byte offset off.
-__device__ __forceinline__ uint32_t pair_entry_tf(const TabTf<6>& tab, uint32_t off) {
-  return *reinterpret_cast<const uint32_t*>(tab.t + off);
-}
-
-// Entry of pair N (codes 2N, 2N+1) of a packed piece held as words.
-template <int BW, int N>
-__device__ __forceinline__ uint32_t piece_pair_tf(const uint32_t* w, TabTf<BW>& tab) {
-  if constexpr (BW == 4) return entry_tf<N & 3>(tab, w[N >> 2]);
-  else return pair_entry_tf(tab, pair_offset<BW, 2 * BW * N, 2>(w));
-}
 
 constexpr int kTfLookahead = 4;  // K-steps of table reads in flight ahead of their MFMA
 

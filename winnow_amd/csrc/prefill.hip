@@ -1,0 +1,770 @@
+// Fused prefill attention over paged packed K/V for gfx950: Q > 1 queries per
+// sequence under the offset causal mask, head_dim 128, 4 and 6-bit K and V.
+//
+// Replaces the reference's Q > 1 route, _reconstruct_sdpa
+// (turboquant_kv/packed_backend.py:211-226, reached at :278-280), which writes each
+// history back to HBM dequantized and then runs SDPA. Here the pages are read in
+// their packed form and the history is never expanded: the algebra is the
+// compressed-domain one of the decode (turboquant_kv/packed_attention.py:260-334)
+// with a query block per wave, and the mask is the reference's: query i of a
+// sequence of length L (the cache already holds the Q new tokens) sees keys
+// j <= L - Q + i (packed_attention.py:198-206); a query that sees no key gives 0.
+//
+// Three launches on the caller's stream:
+//   1. pf_rotate_kernel  q_rot = scale log2(e) q Pi_K^T, one row per (sequence, kv
+//                        head, r) with r = qi n_rep + h (query qi, head h of the
+//                        group), rows padded to kRowPad per kv head with zeros;
+//   2. pf_scan_kernel    one wave per (sequence, kv head, column block, split): the
+//                        block's 16 NCT query rows against the split's share of the
+//                        64-token chunks the block can see, on
+//                        v_mfma_f32_16x16x32_f16 with single fp16 operands (11
+//                        significant bits, rounded to nearest) and fp32 accumulation;
+//                        writes an (acc, m, l) partial per row;
+//   3. pf_merge_kernel   per row, the max-stable merge of its splits, 1/l, Pi_V, cast.
+//
+// The scan, per 64-token chunk (lane 16g + c):
+//   scores  S[token, row] with A = K table entries (row c of tile t = token 16t + c,
+//           k-slots of group g in K-step s = dims 32g + 8s + 0..7: quarter g of the
+//           token's packed row, four pair lookups) and B = q' (column c = query row c
+//           of column tile ct, the same dims). One A operand feeds NCT MFMAs. Output
+//           lane (g, c) register i holds token 16t + 4g + i of column c.
+//   softmax per column (query row), log2 units, lazy reference maximum (moves only
+//           when a score exceeds it by more than kPfRescale): the column maximum is
+//           the lane's sixteen scores, then two cross-lane steps over g.
+//   values  O[dim, row] with A = V table entries (row c of M-tile mt = dim 8c + mt;
+//           k-slots of group g in K-step ks = tokens 32ks + 4g + 0..3 and 32ks + 16 +
+//           4g + 0..3, the token pairs' codes merged into pair indices) and B = the
+//           fp16 p n_V 2^-gs of the same tokens, which are this lane's own score
+//           registers: P never leaves the registers. Output lane (g, c) register i of
+//           M-tile mt holds dim 32g + 8i + mt of column c.
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "wn_common.h"
+#include "wn_tables.h"
+
+namespace wn {
+namespace {
+
+constexpr float kPfRescale = 8.0f;
+constexpr int kRowPad = 64;    // q_rot rows per (sequence, kv head) are a multiple of this
+constexpr int kRotRows = 32;   // rows per work-group of the rotate and merge kernels
+
+struct PrefillArgs {
+  const float* q_rot;  // (B*Hkv*nrp, 128)
+  const uint8_t* k_pages;
+  const uint8_t* v_pages;
+  const uint16_t* k_norms;
+  const uint16_t* v_norms;
+  const float* cb_k;
+  const float* cb_v;
+  const int32_t* table;
+  const int32_t* seq_lens;
+  float* part_acc;  // (items * 16 NCT, 128), item = ((b*Hkv + kvh)*nsplit + s)*ncb + cb
+  float* part_ml;   // (items * 16 NCT, 2): maximum (log2 units), sum
+  int64_t ksp, ksh, vsp, vsh;  // page strides, bytes
+  int64_t knp, knh, vnp, vnh;  // norm strides, elements
+  int64_t tsb;                 // page-table row stride, elements
+  int B, Hkv, n_rep, Q, nrp, ncb, nsplit, log2S;
+};
+
+// Packed rows of one chunk as a lane holds them.
+template <int BWK, int BWV>
+struct PfBuf {
+  static constexpr int VW = BWV == 4 ? 1 : 2;
+  uint32_t k[4 * BWK];  // tile t: quarter g of token c0 + 16t + c, words [t BWK, t BWK + BWK)
+  uint32_t v[16 * VW];  // token (t, i) = c0 + 16t + 4g + i: codes of dims 8c .. 8c+7 (6-bit: raw window)
+  uint32_t nk[8];       // fp16 K norms of tokens (t, i): half i & 1 of word 2t + (i >> 1)
+  uint32_t nv[8];       // fp16 V norms, the same tokens
+};
+
+// The loads of chunk [c0, c0+64): tile t's 16 tokens share a page (16 | c0 and S >= 16),
+// whose page-table column is clamped to col_hi, the range's last page (tokens past the
+// range are loaded from real pages and masked).
+template <int BWK, int BWV>
+__device__ __forceinline__ void pf_load(const PrefillArgs& a, const int32_t* trow, int kvh, int c0, int col_hi,
+                                        int lane, PfBuf<BWK, BWV>& o) {
+  constexpr int NBK = 16 * BWK, NBV = 16 * BWV, VW = PfBuf<BWK, BWV>::VW;
+  const int g = lane >> 4, c = lane & 15;
+  const int smask = (1 << a.log2S) - 1;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int t0 = c0 + 16 * t;
+    const uint32_t pid = uint32_t(__builtin_amdgcn_readfirstlane(trow[min(t0 >> a.log2S, col_hi)]));
+    const uint32_t slot = uint32_t(t0 & smask);
+    const uint8_t* kb = a.k_pages + uint64_t(pid) * uint64_t(a.ksp) + uint64_t(kvh) * uint64_t(a.ksh);
+    const uint8_t* kp = kb + (slot + uint32_t(c)) * uint32_t(NBK) + uint32_t(4 * BWK * g);
+    if constexpr (BWK == 4) {
+      const uint4 x = *reinterpret_cast<const uint4*>(kp);
+      o.k[4 * t] = x.x;
+      o.k[4 * t + 1] = x.y;
+      o.k[4 * t + 2] = x.z;
+      o.k[4 * t + 3] = x.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const uint2 x = reinterpret_cast<const uint2*>(kp)[j];
+        o.k[6 * t + 2 * j] = x.x;
+        o.k[6 * t + 2 * j + 1] = x.y;
+      }
+    }
+    const uint8_t* vb = a.v_pages + uint64_t(pid) * uint64_t(a.vsp) + uint64_t(kvh) * uint64_t(a.vsh) +
+                        (slot + uint32_t(4 * g)) * uint32_t(NBV);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (BWV == 4) {
+        o.v[4 * t + i] = *reinterpret_cast<const uint32_t*>(vb + i * NBV + 4 * c);
+      } else {
+        // bytes [6c, 6c + 6) of the row inside the 8 bytes from 6c rounded down to 4
+        uint2 x;
+        __builtin_memcpy(&x, __builtin_assume_aligned(vb + i * NBV + ((6 * c) & ~3), 4), 8);
+        o.v[VW * (4 * t + i)] = x.x;
+        o.v[VW * (4 * t + i) + 1] = x.y;
+      }
+    }
+    const uint32_t ns = slot + uint32_t(4 * g);
+    const uint2 nk = *reinterpret_cast<const uint2*>(a.k_norms + uint64_t(pid) * uint64_t(a.knp) +
+                                                     uint64_t(kvh) * uint64_t(a.knh) + ns);
+    const uint2 nv = *reinterpret_cast<const uint2*>(a.v_norms + uint64_t(pid) * uint64_t(a.vnp) +
+                                                     uint64_t(kvh) * uint64_t(a.vnh) + ns);
+    o.nk[2 * t] = nk.x;
+    o.nk[2 * t + 1] = nk.y;
+    o.nv[2 * t] = nv.x;
+    o.nv[2 * t + 1] = nv.y;
+  }
+}
+
+__device__ __forceinline__ float half_at(const uint32_t* w, int k) {
+  return f16_to_f32(uint16_t(w[k >> 1] >> (16 * (k & 1))));
+}
+
+// 6-bit V: the raw windows moved down to the codes, then each token pair's words
+// rewritten in place as (Ce, Co): Ce holds the first token's even-numbered codes with
+// the second's shifted up one field into the gaps, Co the same for the odd ones, so
+// the pair index of dim m is the 12 bits of Ce (m even) or Co (m odd) from bit 6 m.
+template <int BWK, int BWV>
+__device__ __forceinline__ void pf_merge_pairs(PfBuf<BWK, BWV>& o, int lane) {
+  static_assert(BWV == 6, "pair merges are for 6-bit values");
+  constexpr uint64_t E = 0x03F03F03F03Full & 0xFFFFFFFFFFFFull;  // fields 0, 2, 4, 6 of 6 bits
+  constexpr uint64_t O = ~E & 0xFFFFFFFFFFFFull;                // fields 1, 3, 5, 7
+  const uint32_t sh = 16u * uint32_t(lane & 1);
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    uint32_t* x = o.v + 2 * (2 * p);
+    uint32_t* y = o.v + 2 * (2 * p + 1);
+    const uint64_t a = (uint64_t(x[1]) << 32 | x[0]) >> sh;
+    const uint64_t b = (uint64_t(y[1]) << 32 | y[0]) >> sh;
+    const uint64_t bs = b << 6;
+    const uint64_t ce = (a & E) | (bs & ~E);
+    const uint64_t co = (a & O) | (bs & ~O);
+    x[0] = uint32_t(ce);
+    x[1] = uint32_t(ce >> 32);
+    y[0] = uint32_t(co);
+    y[1] = uint32_t(co >> 32);
+  }
+}
+
+template <int NCT>
+struct PfState {
+  f32x4 acc[NCT][8];  // acc[ct][mt] register i: dim 32g + 8i + mt of column c, scaled by 2^(8-gs)
+  float m[NCT];       // reference maximum of column c (log2 units; -inf before its first key)
+  float l[NCT];       // sum of 2^(s - m) over this lane's tokens
+  int lim[NCT];       // last visible token of column c (padding rows: no limit)
+  int gs;             // value scale shift (wave-uniform)
+};
+
+// One chunk. lim_hi: tokens past it (the range end) are masked for every column;
+// full: every token of the chunk is visible to every column (no masks).
+template <int BWK, int BWV, int NCT>
+__device__ __forceinline__ void pf_chunk(PfBuf<BWK, BWV>& X, TabTf<BWK>& cbk, TabTf<BWV>& cbv,
+                                         const h8 (&qb)[NCT][4], float sc, int c0, int t_hi, bool full,
+                                         int lane, PfState<NCT>& st) {
+  constexpr int LA = 4;
+  const int g = lane >> 4;
+  // ---- scores: step k = 4s + t (K-step s of tile t)
+  f32x4 d[NCT][4];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) d[ct][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  {
+    uint32_t e[LA + 1][4];
+    auto look = [&](auto kc, uint32_t (&o)[4]) {
+      constexpr int k = decltype(kc)::value, s = k >> 2, t = k & 3;
+      o[0] = piece_pair_tf<BWK, 4 * s>(X.k + t * BWK, cbk);
+      o[1] = piece_pair_tf<BWK, 4 * s + 1>(X.k + t * BWK, cbk);
+      o[2] = piece_pair_tf<BWK, 4 * s + 2>(X.k + t * BWK, cbk);
+      o[3] = piece_pair_tf<BWK, 4 * s + 3>(X.k + t * BWK, cbk);
+    };
+    static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
+    static_for<0, 16>([&](auto kc) {
+      constexpr int k = decltype(kc)::value, s = k >> 2, t = k & 3, j = k % (LA + 1);
+      if constexpr (k + LA < 16) look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
+      const h8 av = __builtin_bit_cast(h8, u32x4{e[j][0], e[j][1], e[j][2], e[j][3]});
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) d[ct][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qb[ct][s], d[ct][t], 0, 0, 0);
+    });
+  }
+
+  // ---- value scale: every n_V < 2^(7 + gs), so 2^kPfRescale n_V 2^-gs < 2^15 in fp16
+  float nvr[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) nvr[k] = half_at(X.nv, k);
+  float nvmax = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) nvmax = fmaxf(nvmax, nvr[k]);
+  if (__any(nvmax >= ldexpf(1.f, 7 + st.gs))) {  // wave-uniform, rare
+    int ge;
+    frexpf(wave_max(nvmax), &ge);
+    const int gs_need = max(0, ge - 7);
+    const float f = ldexpf(1.f, st.gs - gs_need);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) st.acc[ct][mt] *= f;
+    st.gs = gs_need;
+  }
+  const float vsc = ldexpf(1.f, -st.gs);
+  float nks[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) nks[k] = half_at(X.nk, k) * sc;
+
+  // ---- softmax per column tile; p n_V 2^-gs into the value B operands
+  h8 pb[NCT][2];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    float s[16];
+    // token (t, i) = c0 + 16t + 4g + i sits at s[4t + i]
+    const int lim = min(st.lim[ct], t_hi - 1) - (c0 + 4 * g);  // visible: 16t + i <= lim
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = d[ct][t][i] * nks[4 * t + i];
+        s[4 * t + i] = (full || 16 * t + i <= lim) ? x : -INFINITY;
+        mx = fmaxf(mx, s[4 * t + i]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (__any(mx > st.m[ct] + kPfRescale)) {  // wave-uniform
+      const float m_new = mx > st.m[ct] + kPfRescale ? mx : st.m[ct];
+      const float alpha = m_new == st.m[ct] ? 1.f : __builtin_amdgcn_exp2f(st.m[ct] - m_new);  // 0 from -inf
+      st.m[ct] = m_new;
+      st.l[ct] *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) st.acc[ct][mt] *= alpha;
+    }
+    const float m0 = st.m[ct] == -INFINITY ? 0.f : st.m[ct];  // a column with no key yet: every s is -inf
+    float p[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      p[k] = __builtin_amdgcn_exp2f(s[k] - m0);  // 0 for masked tokens
+      st.l[ct] += p[k];
+    }
+    // K-step ks: k-slots 0..3 = tile 2ks, 4..7 = tile 2ks+1, registers i = 0..3
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      h8 v;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int k = 8 * ks + j;  // tile 2ks + j/4, register j%4: s index 4(2ks + j/4) + j%4 = 8ks + j
+        v[j] = _Float16(p[k] * nvr[k] * vsc);
+      }
+      pb[ct][ks] = v;
+    }
+  }
+
+  // ---- values: step k = 8ks + mt
+  if constexpr (BWV == 6) pf_merge_pairs<BWK, BWV>(X, lane);
+  {
+    uint32_t e[LA + 1][4];
+    auto look = [&](auto kc, uint32_t (&o)[4]) {
+      constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7;
+      // pair q of K-step ks: tokens (j, j+1) with j = 2q of the k-slots: tile 2ks + (q >> 1), registers 2(q & 1), +1
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int ta = 4 * (2 * ks + (q >> 1)) + 2 * (q & 1);  // token index (t, i) of the first of the pair
+        if constexpr (BWV == 4) {
+          const uint32_t wa = X.v[ta], wb = X.v[ta + 1];
+          const uint32_t x = (mt & 1) ? (((wa >> 4) & 0x0F0F0F0Fu) | (wb & 0xF0F0F0F0u))
+                                      : ((wa & 0x0F0F0F0Fu) | ((wb << 4) & 0xF0F0F0F0u));
+          o[q] = entry_tf<(mt >> 1)>(cbv, x);
+        } else {
+          o[q] = pair_entry_tf(cbv, pair_offset<6, 6 * mt, 2>(X.v + 2 * (ta + (mt & 1))));
+        }
+      }
+    };
+    static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
+    static_for<0, 16>([&](auto kc) {
+      constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7, j = k % (LA + 1);
+      if constexpr (k + LA < 16) look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
+      const h8 av = __builtin_bit_cast(h8, u32x4{e[j][0], e[j][1], e[j][2], e[j][3]});
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        st.acc[ct][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[ct][ks], st.acc[ct][mt], 0, 0, 0);
+    });
+  }
+}
+
+// Writes the (acc, m, l) partial of each column (query row) of the block: lane (g, c)
+// writes dims 32g .. 32g+31 of row 16 ct + c.
+template <int NCT>
+__device__ __forceinline__ void pf_write(const PrefillArgs& a, PfState<NCT>& st, int64_t row0, int lane) {
+  const int g = lane >> 4, c = lane & 15;
+  const float f = ldexpf(1.f, st.gs - 8);
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    float l = st.l[ct];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int64_t row = row0 + 16 * ct + c;
+    float* dst = a.part_acc + row * 128 + 32 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<float4*>(dst + 8 * i) = make_float4(st.acc[ct][0][i] * f, st.acc[ct][1][i] * f,
+                                                            st.acc[ct][2][i] * f, st.acc[ct][3][i] * f);
+      *reinterpret_cast<float4*>(dst + 8 * i + 4) = make_float4(st.acc[ct][4][i] * f, st.acc[ct][5][i] * f,
+                                                                st.acc[ct][6][i] * f, st.acc[ct][7][i] * f);
+    }
+    if (g == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * row) = make_float2(st.m[ct], l);
+  }
+}
+
+// Logical index of work-group p of n when groups go to the 8 XCDs round robin: XCD x
+// holds groups x, x+8, ...; they become a contiguous run of logical indices, so the
+// waves of neighbouring items (the column blocks of one split) share an XCD's L2.
+__device__ __forceinline__ int pf_xcd_major(int p, int n) {
+  const int q = n >> 3, r = n & 7, x = p & 7, s = p >> 3;
+  return x * q + min(x, r) + s;
+}
+
+template <int BWK, int BWV>
+struct PfLds {
+  static constexpr bool k4 = BWK == 4, v4 = BWV == 4;
+  static constexpr int k_off = k4 && !v4 ? kTfTableBytes : 0;
+  static constexpr int v_off = v4 ? kTfTableBytes : k4 ? 0 : tf_table_bytes<BWK>();
+  static constexpr int total = k_off + tf_table_bytes<BWK>() > v_off + tf_table_bytes<BWV>()
+                                   ? k_off + tf_table_bytes<BWK>()
+                                   : v_off + tf_table_bytes<BWV>();
+  static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
+};
+
+template <int BWK, int BWV, int NCT, int WPB>
+__global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
+  using Lay = PfLds<BWK, BWV>;
+  __shared__ __align__(16) char lds[Lay::total];
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+  const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
+  stage_table_tf<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
+  stage_table_tf<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
+  __syncthreads();  // the only block-wide barrier: waves run independently from here
+  const int64_t w = int64_t(pf_xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
+  const int64_t items = int64_t(a.B) * a.Hkv * a.nsplit * a.ncb;
+  if (w >= items) return;
+  const int cb = int(w % a.ncb);
+  int64_t u = w / a.ncb;
+  const int s = int(u % a.nsplit);
+  u /= a.nsplit;
+  const int kvh = int(u % a.Hkv);
+  const int b = int(u / a.Hkv);
+  constexpr int NR = 16 * NCT;
+  const int64_t row0 = w * NR;
+
+  PfState<NCT> st;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) st.acc[ct][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m[ct] = -INFINITY;
+    st.l[ct] = 0.f;
+  }
+  st.gs = 0;
+
+  // visible tokens of the block: query qi sees keys j <= L - Q + qi
+  const int L = a.seq_lens[b];
+  const int rows = a.n_rep * a.Q;
+  const int r_first = cb * NR, r_last = min(r_first + NR, rows) - 1;
+  int T = r_first < rows ? min(L, L - a.Q + r_last / a.n_rep + 1) : 0;
+  T = max(T, 0);
+  const int nch = (T + 63) >> 6;
+  const int ch_lo = int(int64_t(nch) * s / a.nsplit), ch_hi = int(int64_t(nch) * (s + 1) / a.nsplit);
+  if (ch_lo < ch_hi) {
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const int r = r_first + 16 * ct + c;
+      st.lim[ct] = r < rows ? L - a.Q + r / a.n_rep : INT32_MAX;  // padding rows: no mask (never written)
+    }
+    // every column of the block sees at least tokens <= lim_min
+    const int lim_min = L - a.Q + r_first / a.n_rep;
+    const int t_lo = 64 * ch_lo, t_hi = min(64 * ch_hi, T);
+    const int col_hi = (t_hi - 1) >> a.log2S;
+    const int32_t* trow = a.table + int64_t(b) * a.tsb;
+
+    // B operands of the scores: column c of tile ct = row r_first + 16 ct + c, K-step
+    // s = dims 32g + 8s + 0..7 of q' = q_rot 2^e, rounded to nearest (e per wave:
+    // |q'| < 2^15)
+    float qv[NCT][32];
+    float amax = 0.f;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const float4* qp = reinterpret_cast<const float4*>(
+          a.q_rot + ((int64_t(b) * a.Hkv + kvh) * a.nrp + r_first + 16 * ct + c) * 128 + 32 * g);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float4 x = qp[k];
+        qv[ct][4 * k] = x.x;
+        qv[ct][4 * k + 1] = x.y;
+        qv[ct][4 * k + 2] = x.z;
+        qv[ct][4 * k + 3] = x.w;
+      }
+#pragma unroll
+      for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(qv[ct][k]));
+    }
+    int qe;
+    frexpf(wave_max(amax), &qe);
+    const int e = 15 - qe;
+    const float sc = ldexpf(1.f, -(e + 8));
+    h8 qb[NCT][4];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qb[ct][k][j] = _Float16(ldexpf(qv[ct][8 * k + j], e));
+
+    TabTf<BWK> cbk = make_tab_tf<BWK>(lds, Lay::k_off, lane);
+    TabTf<BWV> cbv = make_tab_tf<BWV>(lds, Lay::v_off, lane);
+    PfBuf<BWK, BWV> x0, x1;
+    pf_load<BWK, BWV>(a, trow, kvh, t_lo, col_hi, lane, x0);
+    const int n = ch_hi - ch_lo;
+    auto step = [&](int ch, PfBuf<BWK, BWV>& X, PfBuf<BWK, BWV>& Y) {
+      const int c0 = t_lo + 64 * ch;
+      // the next chunk's rows load while this one computes (clamped into the range on the last)
+      pf_load<BWK, BWV>(a, trow, kvh, min(c0 + 64, t_lo + 64 * (n - 1)), col_hi, lane, Y);
+      const bool full = c0 + 63 <= lim_min && c0 + 64 <= t_hi;
+      pf_chunk<BWK, BWV, NCT>(X, cbk, cbv, qb, sc, c0, t_hi, full, lane, st);
+    };
+    int ch = 0;
+    for (; ch + 2 <= n; ch += 2) {
+      step(ch, x0, x1);
+      step(ch + 1, x1, x0);
+    }
+    if (ch < n) step(ch, x0, x1);
+  }
+  pf_write<NCT>(a, st, row0, lane);
+}
+
+// ---------------------------------------------------------------- rotate and merge
+
+struct PfRotArgs {
+  const void* q;
+  int64_t qsb, qsh, qsq;  // element strides of q (B, Hq, Q, D)
+  const float* pi;
+  float* q_rot;
+  float scale;
+  int Hkv, n_rep, Q, nrp, q_dtype;
+};
+
+// y[r][j] = sum_k x[r][k] M[k][j] for the kRotRows rows of a work-group: xt = x
+// transposed in LDS ([k][r]), m = M in LDS ([k][j]); thread t makes rows 4 (t / 32)
+// .. +3 and columns 4 (t % 32) .. +3.
+__device__ __forceinline__ void rows_times(const float* xt, const float* m, int tid, float (&y)[4][4]) {
+  const int rb = 4 * (tid >> 5), jb = 4 * (tid & 31);
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) y[r][j] = 0.f;
+#pragma unroll 8
+  for (int k = 0; k < 128; ++k) {
+    const float4 xv = *reinterpret_cast<const float4*>(xt + k * kRotRows + rb);
+    const float4 mv = *reinterpret_cast<const float4*>(m + k * 128 + jb);
+    const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, ma[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[r][j] = fmaf(xa[r], ma[j], y[r][j]);
+  }
+}
+
+// q_rot rows (sequence blockIdx.z, kv head blockIdx.y, rows 32 blockIdx.x .. +31):
+// scale * q Pi_K^T, zero for rows past n_rep Q.
+__global__ __launch_bounds__(256) void pf_rotate_kernel(PfRotArgs a) {
+  __shared__ __align__(16) float pit[128 * 128];      // Pi_K^T: [k][j] = Pi_K[j][k]
+  __shared__ __align__(16) float xt[128 * kRotRows];  // q rows transposed
+  const int tid = threadIdx.x, kvh = blockIdx.y, b = blockIdx.z, r0 = blockIdx.x * kRotRows;
+  for (int i = tid; i < 128 * 128; i += 256) {  // j fastest: conflict-free LDS writes, reads from L2
+    const int k = i >> 7, j = i & 127;
+    pit[i] = a.pi[j * 128 + k];
+  }
+  const int rows = a.n_rep * a.Q;
+  for (int i = tid; i < kRotRows * 128; i += 256) {
+    const int rr = i >> 7, k = i & 127, r = r0 + rr;
+    float v = 0.f;
+    if (r < rows) {
+      const int qi = r / a.n_rep, h = kvh * a.n_rep + r % a.n_rep;
+      v = load_elem(a.q, b * a.qsb + h * a.qsh + qi * a.qsq + k, a.q_dtype);
+    }
+    xt[k * kRotRows + rr] = v;
+  }
+  __syncthreads();
+  float y[4][4];
+  rows_times(xt, pit, tid, y);
+  const int rb = 4 * (tid >> 5), jb = 4 * (tid & 31);
+  float* out = a.q_rot + ((int64_t(b) * a.Hkv + kvh) * a.nrp + r0) * 128;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    *reinterpret_cast<float4*>(out + (rb + r) * 128 + jb) =
+        make_float4(y[r][0] * a.scale, y[r][1] * a.scale, y[r][2] * a.scale, y[r][3] * a.scale);
+}
+
+struct PfMergeArgs {
+  const float* part_acc;
+  const float* part_ml;
+  const float* pi_v;
+  void* out;  // (B, Hq, Q, D) contiguous
+  int out_dtype, Hkv, n_rep, Q, nrp, ncb, nsplit, nr;  // nr: rows per column block
+};
+
+// Rows (sequence blockIdx.z, kv head blockIdx.y, rows 32 blockIdx.x .. +31): the
+// max-stable merge of each row's split partials (weights 2^(m_s - max m)), 1 / l,
+// then Pi_V and the cast; rows that saw no key are 0 (packed_attention.py:206).
+__global__ __launch_bounds__(256) void pf_merge_kernel(PfMergeArgs a) {
+  __shared__ __align__(16) float pv[128 * 128];
+  __shared__ __align__(16) float xt[128 * kRotRows];
+  const int tid = threadIdx.x, kvh = blockIdx.y, b = blockIdx.z, r0 = blockIdx.x * kRotRows;
+  for (int i = tid; i < 128 * 128 / 4; i += 256)
+    reinterpret_cast<float4*>(pv)[i] = reinterpret_cast<const float4*>(a.pi_v)[i];
+  {
+    // thread: row rr = tid / 8, dims 16 (tid % 8) .. +15
+    const int rr = tid >> 3, d0 = 16 * (tid & 7), r = r0 + rr;
+    const int cb = r / a.nr, ri = r % a.nr;
+    float M = -INFINITY, den = 0.f, num[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) num[k] = 0.f;
+    for (int s = 0; s < a.nsplit; ++s) {
+      const int64_t row = (((int64_t(b) * a.Hkv + kvh) * a.nsplit + s) * a.ncb + cb) * a.nr + ri;
+      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * row);
+      if (ml.x == -INFINITY) continue;  // the split saw no key of this row
+      const float Mn = fmaxf(M, ml.x);
+      const float ro = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+      const float w = __builtin_amdgcn_exp2f(ml.x - Mn);
+      den = den * ro + w * ml.y;
+      const float4* src = reinterpret_cast<const float4*>(a.part_acc + row * 128 + d0);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float4 x = src[k];
+        num[4 * k] = num[4 * k] * ro + w * x.x;
+        num[4 * k + 1] = num[4 * k + 1] * ro + w * x.y;
+        num[4 * k + 2] = num[4 * k + 2] * ro + w * x.z;
+        num[4 * k + 3] = num[4 * k + 3] * ro + w * x.w;
+      }
+      M = Mn;
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) xt[(d0 + k) * kRotRows + rr] = num[k] * inv;
+  }
+  __syncthreads();
+  float y[4][4];
+  rows_times(xt, pv, tid, y);
+  const int rb = 4 * (tid >> 5), jb = 4 * (tid & 31);
+  const int rows = a.n_rep * a.Q, Hq = a.Hkv * a.n_rep;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int rg = r0 + rb + r;
+    if (rg >= rows) continue;
+    const int qi = rg / a.n_rep, h = kvh * a.n_rep + rg % a.n_rep;
+    const int64_t o = ((int64_t(b) * Hq + h) * a.Q + qi) * 128 + jb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_elem(a.out, o + j, a.out_dtype, y[r][j]);
+  }
+}
+
+// ---------------------------------------------------------------- host side
+
+using PfScanFn = void (*)(PrefillArgs);
+
+struct PfKernel {
+  PfScanFn fn = nullptr;
+  int wpb = 0, nct = 0;
+};
+
+template <int BWK, int BWV>
+PfKernel pf_kernel() {
+  // four column tiles (64 query rows) per wave: one K or V lookup feeds four MFMAs;
+  // the accumulators take 128 registers, so one wave per SIMD
+  constexpr int NCT = 2, WPB = 4;
+  return PfKernel{pf_scan_kernel<BWK, BWV, NCT, WPB>, WPB, NCT};
+}
+
+PfKernel pick_prefill(int bw_k, int bw_v) {
+  if (bw_k == 4 && bw_v == 4) return pf_kernel<4, 4>();
+  if (bw_k == 6 && bw_v == 6) return pf_kernel<6, 6>();
+  if (bw_k == 4 && bw_v == 6) return pf_kernel<4, 6>();
+  if (bw_k == 6 && bw_v == 4) return pf_kernel<6, 4>();
+  return PfKernel{};
+}
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+int pf_nrp(int n_rep, int Q) { return int((int64_t(n_rep) * Q + kRowPad - 1) / kRowPad * kRowPad); }
+
+struct PfLayout {
+  int64_t qrot, acc, ml, total;
+};
+
+PfLayout pf_layout(int B, int Hq, int Hkv, int Q, int num_splits) {
+  PfLayout l;
+  const int64_t rows = int64_t(B) * Hkv * pf_nrp(Hq / Hkv, Q);
+  l.qrot = 0;
+  l.acc = align256(rows * 128 * 4);
+  l.ml = l.acc + align256(rows * num_splits * 128 * 4);
+  l.total = l.ml + align256(rows * num_splits * 2 * 4);
+  return l;
+}
+
+int resident_waves_pf(const PfKernel& k) {
+  static std::mutex mu;
+  static std::map<std::pair<int, PfScanFn>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find({dev, k.fn});
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k.fn), 64 * k.wpb, 0) !=
+          hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  const int w = per_cu * cus * k.wpb;
+  cache[{dev, k.fn}] = w;
+  return w;
+}
+
+}  // namespace
+}  // namespace wn
+
+extern "C" int wn_prefill_plan(int B, int Hq, int Hkv, int Q, int D, int S, int bw_k, int bw_v, int max_len,
+                               int* num_splits) {
+  using namespace wn;
+  clear_error();
+  WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Q > 0 && max_len >= 0 && num_splits, WN_E_INVALID,
+             "wn_prefill_plan: bad sizes B=%d Hq=%d Hkv=%d Q=%d max_len=%d", B, Hq, Hkv, Q, max_len);
+  const PfKernel k = pick_prefill(bw_k, bw_v);
+  WN_REQUIRE(D == 128 && S >= 16 && is_pow2(S) && k.fn, WN_E_UNSUPPORTED,
+             "wn_prefill_plan: (D=%d, S=%d, bw_k=%d, bw_v=%d) not compiled", D, S, bw_k, bw_v);
+  const int w = resident_waves_pf(k);
+  WN_REQUIRE(w > 0, WN_E_LAUNCH, "wn_prefill_plan: cannot query the device occupancy");
+  // about two waves per resident slot over the (sequence, kv head, column block)
+  // items, each split keeping at least four chunks of the longest history
+  const int64_t units = int64_t(B > 0 ? B : 1) * Hkv * (pf_nrp(Hq / Hkv, Q) / (16 * k.nct));
+  int64_t ns = (2 * int64_t(w) + units - 1) / units;
+  const int64_t chunks = (int64_t(max_len) + 63) / 64;
+  ns = std::min<int64_t>(ns, std::max<int64_t>(1, chunks / 4));
+  *num_splits = int(std::max<int64_t>(1, std::min<int64_t>(ns, 256)));
+  return WN_OK;
+}
+
+extern "C" int64_t wn_prefill_workspace_bytes(int B, int Hq, int Hkv, int Q, int D, int num_splits) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Q <= 0 || D != 128 || num_splits <= 0) return -1;
+  return wn::pf_layout(B, Hq, Hkv, Q, num_splits).total;
+}
+
+extern "C" int wn_prefill_attention(
+    const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_q,
+    const float* pi_k, const float* pi_v, const float* codebook_k, const float* codebook_v,
+    const uint8_t* k_pages, int64_t k_stride_p, int64_t k_stride_h,
+    const uint8_t* v_pages, int64_t v_stride_p, int64_t v_stride_h,
+    const uint16_t* k_norms, int64_t kn_stride_p, int64_t kn_stride_h,
+    const uint16_t* v_norms, int64_t vn_stride_p, int64_t vn_stride_h,
+    const int32_t* page_table, int64_t table_stride_b, const int32_t* seq_lens,
+    void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
+    int B, int Hq, int Hkv, int Q, int D, int S, int bw_k, int bw_v,
+    float scale, int num_splits, void* stream, void* ev_begin, void* ev_end) {
+  using namespace wn;
+  clear_error();
+  WN_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Q > 0, WN_E_INVALID,
+             "prefill: need B>=0, Q>0, Hq%%Hkv==0 (B=%d Hq=%d Hkv=%d Q=%d)", B, Hq, Hkv, Q);
+  const PfKernel k = pick_prefill(bw_k, bw_v);
+  WN_REQUIRE(D == 128 && k.fn, WN_E_UNSUPPORTED, "prefill: (D=%d, bw_k=%d, bw_v=%d) not compiled", D, bw_k, bw_v);
+  WN_REQUIRE(is_pow2(S) && S >= 16, WN_E_INVALID, "prefill: page size %d is not a power of two >= 16", S);
+  WN_REQUIRE(q_dtype >= WN_F32 && q_dtype <= WN_BF16 && out_dtype >= WN_F32 && out_dtype <= WN_BF16,
+             WN_E_INVALID, "prefill: dtype codes %d/%d", q_dtype, out_dtype);
+  WN_REQUIRE(num_splits > 0 && num_splits <= 4096, WN_E_INVALID, "prefill: num_splits %d", num_splits);
+  const int n_rep = Hq / Hkv;
+  WN_REQUIRE(int64_t(n_rep) * Q <= (int64_t(1) << 24), WN_E_INVALID, "prefill: n_rep * Q too large");
+  if (B == 0) return WN_OK;
+  WN_REQUIRE(q && pi_k && pi_v && codebook_k && codebook_v && k_pages && v_pages && k_norms && v_norms &&
+                 page_table && seq_lens && out,
+             WN_E_INVALID, "prefill: null operand");
+  const int nbk = D * bw_k / 8, nbv = D * bw_v / 8;
+  WN_REQUIRE(aligned(k_pages, 8) && k_stride_p % 8 == 0 && k_stride_h % 8 == 0 &&
+                 (bw_k != 4 || (aligned(k_pages, 16) && k_stride_p % 16 == 0 && k_stride_h % 16 == 0)),
+             WN_E_INVALID, "prefill: K pages need 16 (4-bit) or 8-byte aligned base and strides");
+  WN_REQUIRE(aligned(v_pages, 4) && v_stride_p % 4 == 0 && v_stride_h % 4 == 0, WN_E_INVALID,
+             "prefill: V pages need 4-byte aligned base and strides");
+  WN_REQUIRE(k_stride_h >= int64_t(S) * nbk && v_stride_h >= int64_t(S) * nbv && k_stride_p >= 0 &&
+                 v_stride_p >= 0,
+             WN_E_INVALID, "prefill: head stride smaller than one (S, NB) page block");
+  // the scan reads four norms of a token quad with one 8-byte load
+  WN_REQUIRE(aligned(k_norms, 8) && aligned(v_norms, 8) && kn_stride_p % 4 == 0 && kn_stride_h % 4 == 0 &&
+                 vn_stride_p % 4 == 0 && vn_stride_h % 4 == 0 && kn_stride_p >= 0 && kn_stride_h >= 0 &&
+                 vn_stride_p >= 0 && vn_stride_h >= 0,
+             WN_E_INVALID, "prefill: norm bases 8-byte aligned and strides multiples of 4 elements");
+  WN_REQUIRE(aligned(pi_v, 16) && aligned(out, 4), WN_E_INVALID, "prefill: Pi_V 16-byte aligned");
+  const PfLayout lay = pf_layout(B, Hq, Hkv, Q, num_splits);
+  WN_REQUIRE(workspace && workspace_bytes >= lay.total && aligned(workspace, 256), WN_E_WORKSPACE,
+             "prefill: workspace needs %lld bytes, 256-aligned (got %lld)", (long long)lay.total,
+             (long long)workspace_bytes);
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nrp = pf_nrp(n_rep, Q);
+  const int nr = 16 * k.nct, ncb = nrp / nr;
+
+  PfRotArgs ra{q, q_stride_b, q_stride_h, q_stride_q, pi_k, reinterpret_cast<float*>(ws + lay.qrot),
+               float(double(scale) * 1.4426950408889634), Hkv, n_rep, Q, nrp, q_dtype};
+  hipLaunchKernelGGL(pf_rotate_kernel, dim3(nrp / kRotRows, Hkv, B), dim3(256), 0, st, ra);
+
+  PrefillArgs pa;
+  pa.q_rot = ra.q_rot;
+  pa.k_pages = k_pages;
+  pa.v_pages = v_pages;
+  pa.k_norms = k_norms;
+  pa.v_norms = v_norms;
+  pa.cb_k = codebook_k;
+  pa.cb_v = codebook_v;
+  pa.table = page_table;
+  pa.seq_lens = seq_lens;
+  pa.part_acc = reinterpret_cast<float*>(ws + lay.acc);
+  pa.part_ml = reinterpret_cast<float*>(ws + lay.ml);
+  pa.ksp = k_stride_p;
+  pa.ksh = k_stride_h;
+  pa.vsp = v_stride_p;
+  pa.vsh = v_stride_h;
+  pa.knp = kn_stride_p;
+  pa.knh = kn_stride_h;
+  pa.vnp = vn_stride_p;
+  pa.vnh = vn_stride_h;
+  pa.tsb = table_stride_b;
+  pa.B = B;
+  pa.Hkv = Hkv;
+  pa.n_rep = n_rep;
+  pa.Q = Q;
+  pa.nrp = nrp;
+  pa.ncb = ncb;
+  pa.nsplit = num_splits;
+  pa.log2S = ilog2(S);
+  const int64_t waves = int64_t(B) * Hkv * num_splits * ncb;
+  WN_REQUIRE(waves / k.wpb < (int64_t(1) << 31), WN_E_INVALID, "prefill: grid too large");
+  if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
+  hipLaunchKernelGGL(k.fn, dim3(unsigned((waves + k.wpb - 1) / k.wpb)), dim3(64 * k.wpb), 0, st, pa);
+  if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
+
+  PfMergeArgs ma{pa.part_acc, pa.part_ml, pi_v, out, out_dtype, Hkv, n_rep, Q, nrp, ncb, num_splits, nr};
+  hipLaunchKernelGGL(pf_merge_kernel, dim3(nrp / kRotRows, Hkv, B), dim3(256), 0, st, ma);
+  return check_launch("wn_prefill_attention");
+}

@@ -360,6 +360,99 @@ def packed_decode_attention_noalloc(q: torch.Tensor, kv: PackedKV, scale: float,
     return out
 
 
+PREFILL_WIDTHS = (4, 6)
+
+
+def prefill_supported(q: torch.Tensor, kv: PackedKV) -> bool:
+    """Whether ``packed_prefill_attention`` compiles this shape: head_dim 128, page size a
+    power of two >= 16, 4 and 6-bit K and V (alike or mixed), a fp32/fp16/bf16 query on
+    a HIP device with a contiguous head_dim, norms whose rows the scan reads four at a
+    time (bases 8-byte aligned, strides multiples of 4 elements)."""
+    if q.dim() != 4 or q.shape[-1] != 128 or kv.head_dim != 128 or not _lib.is_hip(q):
+        return False
+    if kv.k_quant.bit_width not in PREFILL_WIDTHS or kv.v_quant.bit_width not in PREFILL_WIDTHS:
+        return False
+    if not _pow2(kv.page_size) or q.dtype not in _lib.DTYPE_CODE or q.stride(-1) != 1:
+        return False
+    for quant in (kv.k_quant, kv.v_quant):
+        if not quant.Pi.is_contiguous() or quant.Pi.data_ptr() % 16 or not quant.centroids.is_contiguous():
+            return False
+    if kv.page_table.stride(-1) != 1 or not kv.seq_lens.is_contiguous():
+        return False
+    for n in (kv.k_norms, kv.v_norms):
+        if n.stride(-1) != 1 or n.data_ptr() % 8 or n.stride(0) % 4 or n.stride(1) % 4:
+            return False
+    for pages, align in ((kv.k_pages, 16 if kv.k_quant.bit_width == 4 else 8), (kv.v_pages, 4)):
+        if pages.stride(-1) != 1 or pages.stride(-2) != pages.shape[-1] or pages.data_ptr() % align \
+                or pages.stride(0) % align or pages.stride(1) % align:
+            return False
+    return True
+
+
+def prefill_plan_for(q: torch.Tensor, kv: PackedKV) -> int:
+    """Split count of the fused prefill for this query and handle (wn_prefill_plan)."""
+    B, Hq, Q, D = q.shape
+    lens = kv.seq_lens_host if kv.seq_lens_host is not None else kv.seq_lens.cpu()
+    max_len = int(lens.max()) if lens.numel() else 0
+    ns = ctypes.c_int(0)
+    with torch.cuda.device(q.device):
+        _lib.call("wn_prefill_plan", B, Hq, kv.num_kv_heads, Q, D, kv.page_size, kv.k_quant.bit_width,
+                  kv.v_quant.bit_width, max_len, ctypes.byref(ns))
+    return ns.value
+
+
+def prefill_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, q_len: int, head_dim: int,
+                            num_splits: int) -> int:
+    return int(_lib.lib().wn_prefill_workspace_bytes(batch, num_q_heads, num_kv_heads, q_len, head_dim,
+                                                     num_splits))
+
+
+def packed_prefill_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,
+                             num_splits: int | None = None, out_dtype: torch.dtype | None = None,
+                             workspace: torch.Tensor | None = None, check_ranges: bool = True,
+                             timing_events=None) -> torch.Tensor:
+    """q (B, Hq, Q, D) -> (B, Hq, Q, D) in q.dtype, read from the packed pages
+    (``wn_prefill_attention``): the reference's Q > 1 route (packed_backend.py:211-226,
+    dequantize the history and run SDPA with the offset causal mask of
+    packed_attention.py:198-206) without writing the history to HBM. Query i of a
+    sequence of length L (the cache already holds the Q new tokens) sees keys
+    j <= L - Q + i; a query that sees none gives 0.
+
+    Both products take single fp16 operands (11 significant bits, rounded to nearest)
+    and accumulate in fp32. ``num_splits`` replaces the library's split count;
+    ``out_dtype=torch.float32`` returns the fp32 result before the cast;
+    ``workspace`` is an optional caller-owned uint8 buffer of at least
+    ``prefill_workspace_bytes``; ``timing_events`` a pair of raw ``hipEvent_t``
+    handles recorded around the scan kernel. Raises ``UnsupportedLayout`` where
+    ``prefill_supported`` is false."""
+    check_contract(q, kv, check_ranges=check_ranges)
+    if not prefill_supported(q, kv):
+        raise UnsupportedLayout("the fused prefill needs head_dim 128, 4 or 6-bit K and V, page size a power "
+                                "of two >= 16, a HIP device and 4-aligned norm rows")
+    B, Hq, Q, D = q.shape
+    Hkv = kv.num_kv_heads
+    ns = int(num_splits) if num_splits else prefill_plan_for(q, kv)
+    out_dtype = out_dtype or q.dtype
+    if out_dtype not in _lib.DTYPE_CODE:
+        raise UnsupportedLayout(f"output dtype {out_dtype} is not supported")
+    out = torch.empty(B, Hq, Q, D, dtype=out_dtype, device=q.device)
+    need = prefill_workspace_bytes(B, Hq, Hkv, Q, D, ns)
+    if need < 0:
+        raise UnsupportedLayout(f"bad prefill sizes B={B} Hq={Hq} Hkv={Hkv} Q={Q} splits={ns}")
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    elif workspace.numel() * workspace.element_size() < need or workspace.device != q.device:
+        raise UnsupportedLayout(f"workspace needs {need} bytes on {q.device}")
+    ev0, ev1 = timing_events or (None, None)
+    with torch.cuda.device(q.device):
+        _lib.call("wn_prefill_attention", _lib.ptr(q), _lib.DTYPE_CODE[q.dtype], q.stride(0), q.stride(1),
+                  q.stride(2), *_operands(q, kv)[4:], _lib.ptr(out), _lib.DTYPE_CODE[out_dtype],
+                  _lib.ptr(workspace), workspace.numel() * workspace.element_size(),
+                  B, Hq, Hkv, Q, D, kv.page_size, kv.k_quant.bit_width, kv.v_quant.bit_width,
+                  float(scale), ns, _lib.stream_of(q.device), ev0, ev1)
+    return out
+
+
 DENSE_PAGE_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 

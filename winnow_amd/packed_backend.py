@@ -309,6 +309,20 @@ def select_decode_backend(query: torch.Tensor, kv, requested: str) -> str:
     return requested
 
 
+def prefill_fused(query: torch.Tensor, kv) -> bool:
+    """Whether a Q > 1 step runs the fused prefill over the packed pages
+    (``packed_prefill_attention``) instead of the reference's dequantize-then-SDPA
+    route (packed_backend.py:278-280). The fused scan takes single fp16 operands: it
+    serves bf16 and fp16 queries, whose reference route computes in bf16 / fp16 SDPA
+    over a history dequantized to that type, and fp32 queries only when the handle
+    allows TF32-class products (``allow_tf32``); otherwise an fp32 query keeps the
+    fp32 reconstruct route, as in the reference. Shapes the scan does not compile
+    (``prefill_supported``) keep the reconstruct route too."""
+    if query.dtype == torch.float32 and not getattr(kv, "allow_tf32", False):
+        return False
+    return pa.prefill_supported(query, kv)
+
+
 def _host_lens(kv) -> torch.Tensor:
     return kv.seq_lens_host if kv.seq_lens_host is not None else kv.seq_lens.cpu()
 
@@ -409,10 +423,15 @@ def _hip_dense(query, kv, scaling):
     return pa.dense_decode_attention(query, kv, scaling)
 
 
+def _hip_prefill(query, kv, scaling):
+    return pa.packed_prefill_attention(query, kv, scaling)
+
+
 _ROUTES = {
     "hip_packed": _hip_packed,
     "reconstruct_sdpa": _reconstruct_sdpa,
     "prefill_reconstruct_sdpa": _reconstruct_sdpa,
+    "prefill_hip_packed": _hip_prefill,
     "hip_dense": _hip_dense,
     "dense_sdpa": _dense_sdpa,
     "prefill_dense_sdpa": _dense_sdpa,
@@ -421,7 +440,9 @@ _ROUTES = {
 
 def _route(query, kv) -> str:
     if query.shape[2] > 1:
-        return "prefill_dense_sdpa" if isinstance(kv, pa.DenseKV) else "prefill_reconstruct_sdpa"
+        if isinstance(kv, pa.DenseKV):
+            return "prefill_dense_sdpa"
+        return "prefill_hip_packed" if prefill_fused(query, kv) else "prefill_reconstruct_sdpa"
     return select_decode_backend(query, kv, getattr(kv, "decode_backend", "auto"))
 
 
