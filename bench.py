@@ -30,6 +30,10 @@ a kv head, and the LDS of a CU serves them at a rate the probe
 scan runs); ``floor_us`` is the time those reads alone need, ``scan_over_floor``
 the scan's time against it. The scan's other LDS traffic (its score tile and p
 words) comes on top.
+``prefill`` times the fused prefill over the packed pages (Q = 16 new tokens per
+sequence, and Q = 512 for two sequences) beside the reference's Q > 1 route on the same
+pages and GPU (dequantize each history, then SDPA), with the scan's HBM and MFMA
+fractions and sampled parity against the oracle.
 ``allow_tf32`` times the reference's ``allow_tf32=True`` decode on the same pages
 (the TF32-class scan: single fp16 operands, fp32 accumulation) with its own sampled
 parity; the headline line stays the default, fp32-exact decode.
@@ -594,10 +598,140 @@ def tf32_leg(w, bytes_step: int, steps: int, warmup: int, settle: float, splits,
             "parity": parity(w, allow_tf32=True) if check else None}
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 matrix-core peak
+
+
+def _sub_kv(kv, n: int, cut: int | None = None):
+    """The first ``n`` sequences of a device PackedKV, lengths optionally cut to ``cut``."""
+    from winnow_amd import packed_attention as pa
+    lens = kv.seq_lens_host[:n].clone()
+    if cut is not None:
+        lens = lens.clamp(max=cut)
+    return pa.PackedKV(kv.k_pages, kv.k_norms, kv.v_pages, kv.v_norms, kv.page_table[:n],
+                       lens.to(kv.seq_lens.device), kv.k_quant, kv.v_quant, kv.head_dim,
+                       seq_lens_host=lens, page_table_host=kv.page_table_host[:n])
+
+
+def _pick(kv, seqs):
+    """A device PackedKV restricted to sequences ``seqs`` (same pool)."""
+    from winnow_amd import packed_attention as pa
+    idx = torch_index(seqs, kv.page_table.device)
+    return pa.PackedKV(kv.k_pages, kv.k_norms, kv.v_pages, kv.v_norms, kv.page_table[idx], kv.seq_lens[idx],
+                       kv.k_quant, kv.v_quant, kv.head_dim, seq_lens_host=kv.seq_lens_host[list(seqs)],
+                       page_table_host=kv.page_table_host[list(seqs)])
+
+
+def torch_index(seqs, dev):
+    import torch
+    return torch.tensor(list(seqs), dtype=torch.long, device=dev)
+
+
+def prefill_bench(w, Q: int, nseq: int | None = None, steps: int = 10, warmup: int = 3, ref_steps: int = 2,
+                  check: bool = True, check_len: int = 4096):
+    """The fused prefill (``packed_prefill_attention``, wn_prefill_attention) of Q new
+    tokens per sequence on the workload's pages, the first ``nseq`` sequences: their
+    lengths count the Q tokens (the cache holds them before attention, as on the
+    reference's Q > 1 route), query bf16 ~N(0, 1) seeded, output bf16. Beside it the
+    reference's route on the same pages and GPU: each history dequantized to bf16, then
+    SDPA with the offset causal mask (``_reconstruct_sdpa``, packed_backend.py:211-226).
+
+    The scan is timed with HIP events on its stream; the call (rotate + scan + merge)
+    with events around the calls. Its roofline, both ways: HBM, the packed K/V rows and
+    norms of each history read once (the decode's algorithmic bytes); MFMA, 4 Hq D flops
+    per visible (query, key) pair (query i of a sequence of length L sees L - Q + i + 1
+    keys) against the 2.5 PFLOP/s dense fp16 peak. Parity: two sequences cut to
+    ``check_len`` tokens against the oracle's fp32 reconstruct_attention."""
+    import torch
+    from cases import to_host
+    from oracle import attention as oa
+    from winnow_amd import packed_attention as pa
+    from winnow_amd import packed_backend as pb
+    from winnow_amd.packing import packed_bytes
+
+    c = w.c
+    kv = _sub_kv(w.kvs[0], nseq or len(w.lens))
+    lens = [int(x) for x in kv.seq_lens_host]
+    B, Hq, D = len(lens), c["Hq"], c["D"]
+    g = torch.Generator(device=w.q.device).manual_seed(1000 + Q)
+    q = torch.randn(B, Hq, Q, D, generator=g, device=w.q.device).bfloat16()
+    scale = 1.0 / math.sqrt(D)
+    ns = pa.prefill_plan_for(q, kv)
+    ws = torch.empty(pa.prefill_workspace_bytes(B, Hq, c["Hkv"], Q, D, ns), dtype=torch.uint8, device=q.device)
+    call = lambda evs=None: pa.packed_prefill_attention(q, kv, scale, num_splits=ns, workspace=ws,  # noqa: E731
+                                                        check_ranges=False, timing_events=evs)
+    for _ in range(warmup):
+        call()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in evs:
+        e0.record()
+        e1.record()
+    torch.cuda.synchronize()
+    for e0, e1 in evs:
+        call((ctypes.c_void_p(e0.cuda_event), ctypes.c_void_p(e1.cuda_event)))
+    torch.cuda.synchronize()
+    scan_ms = statistics.fmean(e0.elapsed_time(e1) for e0, e1 in evs)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        call()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    pb._reconstruct_sdpa(q, kv, scale)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(ref_steps):
+        pb._reconstruct_sdpa(q, kv, scale)
+    end.record()
+    torch.cuda.synchronize()
+    ref_ms = start.elapsed_time(end) / ref_steps
+    nbytes = kv_bytes(lens, c["Hkv"], packed_bytes(D, c["bwk"]), packed_bytes(D, c["bwv"]))
+    pairs = sum(max(0, min(L, L - Q + i + 1)) for L in lens for i in range(Q))
+    flops = 4 * Hq * D * pairs
+    out = {"Q": Q, "batch": B, "q_heads": Hq, "kv_heads": c["Hkv"], "seq_lens": f"{min(lens)}..{max(lens)}",
+           "bits_k": c["bwk"], "bits_v": c["bwv"], "splits": ns, "kernel": "pf_scan_kernel",
+           "scan_us": scan_ms * 1e3, "us_per_call": ms * 1e3, "prefill_tokens_per_s": B * Q / (ms * 1e-3),
+           "hbm": {"algorithmic_bytes": nbytes, "achieved_GBps": nbytes / (scan_ms * 1e-3) / 1e9,
+                   "frac": nbytes / (scan_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS},
+           "mfma": {"flops": flops, "achieved_TFLOPs": flops / (scan_ms * 1e-3) / 1e12,
+                    "frac": flops / (scan_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS},
+           "reference_route": "history dequantized to bf16, then SDPA with the offset causal mask "
+                              "(_reconstruct_sdpa, packed_backend.py:211-226)",
+           "reference_route_us": ref_ms * 1e3, "speedup_vs_reference_route": ref_ms / ms,
+           "products": "single fp16 operands (11 significant bits, rounded to nearest), fp32 accumulation"}
+    if check:
+        from tf32_reference import prefill_q_log2, tf32_class_reference
+        seqs = sorted({0, B - 1})
+        sub = _sub_kv(kv, B, cut=check_len)
+        qs = q[seqs].contiguous()
+        sub2 = _pick(sub, seqs)
+        wsc = torch.empty(pa.prefill_workspace_bytes(len(seqs), Hq, c["Hkv"], Q, D, 3), dtype=torch.uint8,
+                          device=q.device)
+        got = pa.packed_prefill_attention(qs, sub2, scale, num_splits=3, workspace=wsc,
+                                          out_dtype=torch.float32).cpu()
+        host = to_host(sub2, list(range(len(seqs))))
+        ref = oa.reconstruct_attention(qs.float().cpu(), host, scale)
+        rr = tf32_class_reference(qs.float().cpu(), host, scale,
+                                  q_log2=prefill_q_log2(wsc, len(seqs), Hq, c["Hkv"], Q)).float()
+        route = pb._reconstruct_sdpa(qs, sub2, scale).float().cpu()
+        out["parity"] = {
+            "sequences": seqs, "cut_to": check_len,
+            "rounded_operand_ref_max_abs_err": (got - rr).abs().max().item(),
+            "rounded_operand_ref_within_2e-3_1e-3": bool(torch.allclose(got, rr, atol=2e-3, rtol=1e-3)),
+            "fp32_oracle_max_abs_err": (got - ref).abs().max().item(),
+            "fp32_oracle_within_2e-3_1e-3": bool(torch.allclose(got, ref, atol=2e-3, rtol=1e-3)),
+            "reference_route_fp32_oracle_max_abs_err": (route - ref).abs().max().item(),
+            "note": "the TF32-class operand rounding itself moves this data (1 % outlier channels, 1,024 "
+                    "query rows) up to ~4e-3 from the fp32 oracle; the reference's bf16 route moves it more"}
+    del ws
+    return out
+
+
 def config_line(cfg: int, dev, steps: int, warmup: int, settle: float, copies: int, check: bool,
-                lds_rate: float | None = None, tf32: bool = False):
+                lds_rate: float | None = None, tf32: bool = False, prefill: bool = False):
     """Decode throughput, roofline fraction of the scan and same-run parity at config
-    ``cfg``; ``tf32`` adds the allow_tf32 leg on the same pages."""
+    ``cfg``; ``tf32`` adds the allow_tf32 leg on the same pages, ``prefill`` the fused
+    prefill of 16 new tokens per sequence."""
     import torch
     from winnow_amd.packing import packed_bytes
 
@@ -624,6 +758,8 @@ def config_line(cfg: int, dev, steps: int, warmup: int, settle: float, copies: i
         line["parity"] = parity(w)
     if tf32:
         line["allow_tf32"] = tf32_leg(w, nbytes, steps, warmup, settle, None, check)
+    if prefill and c["bwk"] in (4, 6) and c["bwv"] in (4, 6):
+        line["prefill"] = [prefill_bench(w, 16, check=check)]
     log(f"config {cfg}: {line}")
     del w
     torch.cuda.empty_cache()
@@ -703,6 +839,10 @@ def main(argv=None):
     ap.add_argument("--tf32", choices=["on", "off"], default="on",
                     help="also time the reference's allow_tf32=True decode on the same pages (scan, "
                          "fraction of 8 TB/s, tokens/s, sampled parity), beside the default fp32-exact line")
+    ap.add_argument("--prefill", choices=["on", "off"], default="on",
+                    help="time the fused prefill over the packed pages (16 new tokens per sequence; "
+                         "512 for the first two sequences) against the reference's dequantize + SDPA "
+                         "route on the same pages, with its HBM and MFMA roofline and sampled parity")
     ap.add_argument("--lds-floor", choices=["on", "off"], default="on",
                     help="measure the LDS lookup rate (wn_probe_lds_lookup_rate, 8 waves per CU as the "
                          "row scans run) and report each scan's LDS floor beside its HBM roofline")
@@ -763,6 +903,11 @@ def main(argv=None):
         tf = tf32_leg(w, bytes_step, args.config_steps, min(args.warmup, 10), args.settle, args.splits,
                       args.parity == "on")
         log(f"allow_tf32: {tf}")
+    pre = None
+    if args.prefill == "on":
+        pre = [prefill_bench(w, 16, check=args.parity == "on"),
+               prefill_bench(w, 512, nseq=2, check=args.parity == "on")]
+        log(f"prefill: {pre}")
     cpu = cpu_baseline(c, lens, q, w.kvs[0], args.cpu_budget) if args.cpu_baseline == "on" else None
     if cpu:
         log(f"cpu baseline: {cpu}")
@@ -787,7 +932,8 @@ def main(argv=None):
     for cfg in extra:
         if cfg != args.config:
             others[str(cfg)] = config_line(cfg, dev, args.config_steps, min(args.warmup, 10), args.settle,
-                                           args.copies, args.parity == "on", rate, args.tf32 == "on")
+                                           args.copies, args.parity == "on", rate, args.tf32 == "on",
+                                           args.prefill == "on")
 
     result = {
         "metric": METRIC,
@@ -833,6 +979,7 @@ def main(argv=None):
         "dequant": deq,
         "parity": par,
         "allow_tf32": tf,
+        "prefill": pre,
     }
     print(json.dumps(result), flush=True)
     return 0

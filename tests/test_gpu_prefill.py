@@ -21,7 +21,7 @@ import torch
 
 from cases import build, to_device
 from oracle import attention as oa
-from tf32_reference import tf32_class_reference
+from tf32_reference import prefill_q_log2, tf32_class_reference
 
 pytestmark = pytest.mark.gpu
 
@@ -100,13 +100,10 @@ def test_prefill_large_scores_against_the_rounded_operand_reference(bwk, bwv, Hq
     ws = torch.empty(pa.prefill_workspace_bytes(B, Hq, Hkv, Q, 128, 3), dtype=torch.uint8, device=DEV)
     got = pa.packed_prefill_attention(q.to(DEV), to_device(kv, DEV), scale, num_splits=3, workspace=ws,
                                       out_dtype=torch.float32)
-    # the scan's fp32 rotated queries, rows (sequence, kv head, qi n_rep + h) at the
-    # workspace's start: one ulp of a query component near a rounding halfway point
-    # moves these outputs by ~5e-3, so the reference rounds the scan's own values
-    n_rep = Hq // Hkv
-    nrp = -(-n_rep * Q // 64) * 64
-    rows = ws[:B * Hkv * nrp * 128 * 4].view(torch.float32).view(B, Hkv, nrp, 128)[:, :, :n_rep * Q]
-    q_log2 = rows.reshape(B, Hkv, Q, n_rep, 128).permute(0, 1, 3, 2, 4).reshape(B, Hq, Q, 128).cpu()
+    # the scan's fp32 rotated queries: one ulp of a query component near a rounding
+    # halfway point moves these outputs by ~5e-3, so the reference rounds the scan's
+    # own values
+    q_log2 = prefill_q_log2(ws, B, Hq, Hkv, Q)
     assert torch.allclose(q_log2.double(), (q.double() @ kv.k_quant.Pi.double().T) * scale / math.log(2.0),
                           rtol=1e-5, atol=1e-4)
     _check(got, tf32_class_reference(q, kv, scale, q_log2=q_log2).float(), lens, Q)

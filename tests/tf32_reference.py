@@ -58,3 +58,14 @@ def tf32_class_reference(q: torch.Tensor, kv, scale: float, rnd=round11,
         a = p @ cv[heads]                                                       # (Hq, Q, D)
         out[b] = (a @ kv.v_quant.Pi.double()) * allowed.any(-1)[None, :, None]
     return out
+
+
+def prefill_q_log2(workspace: torch.Tensor, B: int, Hq: int, Hkv: int, Q: int) -> torch.Tensor:
+    """The fused prefill's own fp32 rotated queries (log2 units), (B, Hq, Q, D) on the
+    CPU, read back from the start of the caller-owned workspace of a
+    ``packed_prefill_attention`` call: rows (sequence, kv head, qi n_rep + h), padded
+    to a multiple of 64 per kv head."""
+    n_rep = Hq // Hkv
+    nrp = -(-n_rep * Q // 64) * 64
+    rows = workspace[:B * Hkv * nrp * 128 * 4].view(torch.float32).view(B, Hkv, nrp, 128)[:, :, :n_rep * Q]
+    return rows.reshape(B, Hkv, Q, n_rep, 128).permute(0, 1, 3, 2, 4).reshape(B, Hq, Q, 128).cpu()

@@ -71,64 +71,99 @@ struct PrefillArgs {
   int B, Hkv, n_rep, Q, nrp, ncb, nsplit, log2S;
 };
 
-// Packed rows of one chunk as a lane holds them.
-template <int BWK, int BWV>
-struct PfBuf {
-  static constexpr int VW = BWV == 4 ? 1 : 2;
-  uint32_t k[4 * BWK];  // tile t: quarter g of token c0 + 16t + c, words [t BWK, t BWK + BWK)
-  uint32_t v[16 * VW];  // token (t, i) = c0 + 16t + 4g + i: codes of dims 8c .. 8c+7 (6-bit: raw window)
-  uint32_t nk[8];       // fp16 K norms of tokens (t, i): half i & 1 of word 2t + (i >> 1)
-  uint32_t nv[8];       // fp16 V norms, the same tokens
+// The four 16-token tiles of chunk [c0, c0+64): page ids (wave-uniform) and in-page
+// slots. A tile's 16 tokens share a page (16 | c0 and S >= 16); its page-table column
+// is clamped to col_hi, the range's last page (tokens past the range are read from
+// real pages and masked).
+struct PfTiles {
+  uint32_t pid[4];
+  uint32_t slot[4];
 };
 
-// The loads of chunk [c0, c0+64): tile t's 16 tokens share a page (16 | c0 and S >= 16),
-// whose page-table column is clamped to col_hi, the range's last page (tokens past the
-// range are loaded from real pages and masked).
-template <int BWK, int BWV>
-__device__ __forceinline__ void pf_load(const PrefillArgs& a, const int32_t* trow, int kvh, int c0, int col_hi,
-                                        int lane, PfBuf<BWK, BWV>& o) {
-  constexpr int NBK = 16 * BWK, NBV = 16 * BWV, VW = PfBuf<BWK, BWV>::VW;
-  const int g = lane >> 4, c = lane & 15;
+__device__ __forceinline__ PfTiles pf_tiles(const PrefillArgs& a, const int32_t* trow, int c0, int col_hi) {
+  PfTiles o;
   const int smask = (1 << a.log2S) - 1;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int t0 = c0 + 16 * t;
-    const uint32_t pid = uint32_t(__builtin_amdgcn_readfirstlane(trow[min(t0 >> a.log2S, col_hi)]));
-    const uint32_t slot = uint32_t(t0 & smask);
-    const uint8_t* kb = a.k_pages + uint64_t(pid) * uint64_t(a.ksp) + uint64_t(kvh) * uint64_t(a.ksh);
-    const uint8_t* kp = kb + (slot + uint32_t(c)) * uint32_t(NBK) + uint32_t(4 * BWK * g);
+    o.pid[t] = uint32_t(__builtin_amdgcn_readfirstlane(trow[min(t0 >> a.log2S, col_hi)]));
+    o.slot[t] = uint32_t(t0 & smask);
+  }
+  return o;
+}
+
+// K rows: tile t, quarter g of token c0 + 16t + c (words [t BWK, t BWK + BWK)).
+template <int BWK>
+struct PfK {
+  uint32_t w[4 * BWK];
+};
+// V rows: token (t, i) = c0 + 16t + 4g + i, codes of dims 8c .. 8c+7 (6-bit: the raw
+// 8-byte window from 6c rounded down to 4), VW words each.
+template <int BWV>
+struct PfV {
+  static constexpr int VW = BWV == 4 ? 1 : 2;
+  uint32_t w[16 * VW];
+};
+// fp16 norms of tokens (t, i): half i & 1 of word 2t + (i >> 1).
+struct PfN {
+  uint32_t nk[8], nv[8];
+};
+
+template <int BWK>
+__device__ __forceinline__ void pf_load_k(const PrefillArgs& a, const PfTiles& tl, int kvh, int lane, PfK<BWK>& o) {
+  constexpr int NBK = 16 * BWK;
+  const int g = lane >> 4, c = lane & 15;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint8_t* kp = a.k_pages + uint64_t(tl.pid[t]) * uint64_t(a.ksp) + uint64_t(kvh) * uint64_t(a.ksh) +
+                        (tl.slot[t] + uint32_t(c)) * uint32_t(NBK) + uint32_t(4 * BWK * g);
     if constexpr (BWK == 4) {
       const uint4 x = *reinterpret_cast<const uint4*>(kp);
-      o.k[4 * t] = x.x;
-      o.k[4 * t + 1] = x.y;
-      o.k[4 * t + 2] = x.z;
-      o.k[4 * t + 3] = x.w;
+      o.w[4 * t] = x.x;
+      o.w[4 * t + 1] = x.y;
+      o.w[4 * t + 2] = x.z;
+      o.w[4 * t + 3] = x.w;
     } else {
 #pragma unroll
       for (int j = 0; j < 3; ++j) {
         const uint2 x = reinterpret_cast<const uint2*>(kp)[j];
-        o.k[6 * t + 2 * j] = x.x;
-        o.k[6 * t + 2 * j + 1] = x.y;
+        o.w[6 * t + 2 * j] = x.x;
+        o.w[6 * t + 2 * j + 1] = x.y;
       }
     }
-    const uint8_t* vb = a.v_pages + uint64_t(pid) * uint64_t(a.vsp) + uint64_t(kvh) * uint64_t(a.vsh) +
-                        (slot + uint32_t(4 * g)) * uint32_t(NBV);
+  }
+}
+
+template <int BWV>
+__device__ __forceinline__ void pf_load_v(const PrefillArgs& a, const PfTiles& tl, int kvh, int lane, PfV<BWV>& o) {
+  constexpr int NBV = 16 * BWV, VW = PfV<BWV>::VW;
+  const int g = lane >> 4, c = lane & 15;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint8_t* vb = a.v_pages + uint64_t(tl.pid[t]) * uint64_t(a.vsp) + uint64_t(kvh) * uint64_t(a.vsh) +
+                        (tl.slot[t] + uint32_t(4 * g)) * uint32_t(NBV);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (BWV == 4) {
-        o.v[4 * t + i] = *reinterpret_cast<const uint32_t*>(vb + i * NBV + 4 * c);
+        o.w[4 * t + i] = *reinterpret_cast<const uint32_t*>(vb + i * NBV + 4 * c);
       } else {
-        // bytes [6c, 6c + 6) of the row inside the 8 bytes from 6c rounded down to 4
         uint2 x;
         __builtin_memcpy(&x, __builtin_assume_aligned(vb + i * NBV + ((6 * c) & ~3), 4), 8);
-        o.v[VW * (4 * t + i)] = x.x;
-        o.v[VW * (4 * t + i) + 1] = x.y;
+        o.w[VW * (4 * t + i)] = x.x;
+        o.w[VW * (4 * t + i) + 1] = x.y;
       }
     }
-    const uint32_t ns = slot + uint32_t(4 * g);
-    const uint2 nk = *reinterpret_cast<const uint2*>(a.k_norms + uint64_t(pid) * uint64_t(a.knp) +
+  }
+}
+
+__device__ __forceinline__ void pf_load_n(const PrefillArgs& a, const PfTiles& tl, int kvh, int lane, PfN& o) {
+  const int g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t ns = tl.slot[t] + uint32_t(4 * g);
+    const uint2 nk = *reinterpret_cast<const uint2*>(a.k_norms + uint64_t(tl.pid[t]) * uint64_t(a.knp) +
                                                      uint64_t(kvh) * uint64_t(a.knh) + ns);
-    const uint2 nv = *reinterpret_cast<const uint2*>(a.v_norms + uint64_t(pid) * uint64_t(a.vnp) +
+    const uint2 nv = *reinterpret_cast<const uint2*>(a.v_norms + uint64_t(tl.pid[t]) * uint64_t(a.vnp) +
                                                      uint64_t(kvh) * uint64_t(a.vnh) + ns);
     o.nk[2 * t] = nk.x;
     o.nk[2 * t + 1] = nk.y;
@@ -141,31 +176,44 @@ __device__ __forceinline__ float half_at(const uint32_t* w, int k) {
   return f16_to_f32(uint16_t(w[k >> 1] >> (16 * (k & 1))));
 }
 
-// 6-bit V: the raw windows moved down to the codes, then each token pair's words
-// rewritten in place as (Ce, Co): Ce holds the first token's even-numbered codes with
-// the second's shifted up one field into the gaps, Co the same for the odd ones, so
-// the pair index of dim m is the 12 bits of Ce (m even) or Co (m odd) from bit 6 m.
-template <int BWK, int BWV>
-__device__ __forceinline__ void pf_merge_pairs(PfBuf<BWK, BWV>& o, int lane) {
-  static_assert(BWV == 6, "pair merges are for 6-bit values");
-  constexpr uint64_t E = 0x03F03F03F03Full & 0xFFFFFFFFFFFFull;  // fields 0, 2, 4, 6 of 6 bits
-  constexpr uint64_t O = ~E & 0xFFFFFFFFFFFFull;                // fields 1, 3, 5, 7
-  const uint32_t sh = 16u * uint32_t(lane & 1);
+// The V rows' token pairs (2p, 2p+1) rewritten in place so that one word per (pair,
+// dim parity) holds the pair indices: 4-bit, the byte of dims (2j, 2j+1) becomes
+// (first token's code of dim 2j, second's) in the first word and the same for dim
+// 2j+1 in the second; 6-bit, the raw windows are moved down to the codes and the pair
+// becomes (Ce, Co), Ce holding the first token's even-numbered codes with the second's
+// shifted up one field into the gaps, Co the same for the odd ones (pair index of dim
+// m: the 12 bits of Ce (m even) or Co (m odd) from bit 6 m).
+template <int BWV>
+__device__ __forceinline__ void pf_merge_pairs(PfV<BWV>& o, int lane) {
+  if constexpr (BWV == 4) {
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    uint32_t* x = o.v + 2 * (2 * p);
-    uint32_t* y = o.v + 2 * (2 * p + 1);
-    const uint64_t a = (uint64_t(x[1]) << 32 | x[0]) >> sh;
-    const uint64_t b = (uint64_t(y[1]) << 32 | y[0]) >> sh;
-    const uint64_t bs = b << 6;
-    const uint64_t ce = (a & E) | (bs & ~E);
-    const uint64_t co = (a & O) | (bs & ~O);
-    x[0] = uint32_t(ce);
-    x[1] = uint32_t(ce >> 32);
-    y[0] = uint32_t(co);
-    y[1] = uint32_t(co >> 32);
+    for (int p = 0; p < 8; ++p) {
+      const uint32_t wa = o.w[2 * p], wb = o.w[2 * p + 1];
+      o.w[2 * p] = bitsel(0x0F0F0F0Fu, wa, wb << 4);
+      o.w[2 * p + 1] = bitsel(0x0F0F0F0Fu, wa >> 4, wb);
+    }
+  } else {
+    constexpr uint64_t E = 0x03F03F03F03Full;    // fields 0, 2, 4, 6 of 6 bits
+    constexpr uint64_t O = ~E & 0xFFFFFFFFFFFFull;  // fields 1, 3, 5, 7
+    const uint32_t sh = 16u * uint32_t(lane & 1);
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      uint32_t* x = o.w + 2 * (2 * p);
+      uint32_t* y = o.w + 2 * (2 * p + 1);
+      const uint64_t a = (uint64_t(x[1]) << 32 | x[0]) >> sh;
+      const uint64_t b = (uint64_t(y[1]) << 32 | y[0]) >> sh;
+      const uint64_t bs = b << 6;
+      const uint64_t ce = (a & E) | (bs & ~E);
+      const uint64_t co = (a & O) | (bs & ~O);
+      x[0] = uint32_t(ce);
+      x[1] = uint32_t(ce >> 32);
+      y[0] = uint32_t(co);
+      y[1] = uint32_t(co >> 32);
+    }
   }
 }
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 template <int NCT>
 struct PfState {
@@ -176,46 +224,62 @@ struct PfState {
   int gs;             // value scale shift (wave-uniform)
 };
 
-// One chunk. lim_hi: tokens past it (the range end) are masked for every column;
-// full: every token of the chunk is visible to every column (no masks).
-template <int BWK, int BWV, int NCT>
-__device__ __forceinline__ void pf_chunk(PfBuf<BWK, BWV>& X, TabTf<BWK>& cbk, TabTf<BWV>& cbv,
-                                         const h8 (&qb)[NCT][4], float sc, int c0, int t_hi, bool full,
-                                         int lane, PfState<NCT>& st) {
-  constexpr int LA = 4;
-  const int g = lane >> 4;
-  // ---- scores: step k = 4s + t (K-step s of tile t)
-  f32x4 d[NCT][4];
+constexpr int kPfLookahead = 4;  // K-steps of table reads in flight ahead of their MFMA
+
+// Scores of the chunk: d[ct][t] register i = token 16t + 4g + i of column c, before
+// the n_K 2^-(e+8) scale. Step k = 4s + t (K-step s of tile t); one A operand (four
+// pair lookups) feeds NCT MFMAs.
+template <int BWK, int NCT>
+__device__ __forceinline__ void pf_scores(const PfK<BWK>& K, TabTf<BWK>& cbk, const h8 (&qb)[NCT][4],
+                                          f32x4 (&d)[NCT][4]) {
+  constexpr int LA = kPfLookahead;
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
     for (int t = 0; t < 4; ++t) d[ct][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  {
-    uint32_t e[LA + 1][4];
-    auto look = [&](auto kc, uint32_t (&o)[4]) {
-      constexpr int k = decltype(kc)::value, s = k >> 2, t = k & 3;
-      o[0] = piece_pair_tf<BWK, 4 * s>(X.k + t * BWK, cbk);
-      o[1] = piece_pair_tf<BWK, 4 * s + 1>(X.k + t * BWK, cbk);
-      o[2] = piece_pair_tf<BWK, 4 * s + 2>(X.k + t * BWK, cbk);
-      o[3] = piece_pair_tf<BWK, 4 * s + 3>(X.k + t * BWK, cbk);
-    };
-    static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
-    static_for<0, 16>([&](auto kc) {
-      constexpr int k = decltype(kc)::value, s = k >> 2, t = k & 3, j = k % (LA + 1);
-      if constexpr (k + LA < 16) look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
-      const h8 av = __builtin_bit_cast(h8, u32x4{e[j][0], e[j][1], e[j][2], e[j][3]});
+  // the four entries of a step land in one 4-register operand (no moves to assemble it)
+  u32x4 e[LA + 1];
+  auto look = [&](auto kc, u32x4& o) {
+    constexpr int k = decltype(kc)::value, s = k >> 2, t = k & 3;
+    o[0] = piece_pair_tf<BWK, 4 * s>(K.w + t * BWK, cbk);
+    o[1] = piece_pair_tf<BWK, 4 * s + 1>(K.w + t * BWK, cbk);
+    o[2] = piece_pair_tf<BWK, 4 * s + 2>(K.w + t * BWK, cbk);
+    o[3] = piece_pair_tf<BWK, 4 * s + 3>(K.w + t * BWK, cbk);
+  };
+  // the schedule is pinned step by step (sched_barrier): left free, the compiler
+  // hoists every table read to the top and runs out of registers
+  static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
+  __builtin_amdgcn_sched_barrier(0);
+  static_for<0, 16>([&](auto kc) {
+    constexpr int k = decltype(kc)::value, s = k >> 2, t = k & 3, j = k % (LA + 1);
+    if constexpr (k + LA < 16) {
+      look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const h8 av = __builtin_bit_cast(h8, e[j]);
 #pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) d[ct][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qb[ct][s], d[ct][t], 0, 0, 0);
-    });
-  }
+    for (int ct = 0; ct < NCT; ++ct) d[ct][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qb[ct][s], d[ct][t], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+}
 
-  // ---- value scale: every n_V < 2^(7 + gs), so 2^kPfRescale n_V 2^-gs < 2^15 in fp16
-  float nvr[16];
+// Online softmax of the chunk per column, p n_V 2^-gs into the value B operands:
+// K-step ks of column tile ct takes tokens (2ks, i) at k-slots i and (2ks + 1, i) at
+// k-slots 4 + i, this lane's own score registers. full: every token of the chunk is
+// visible to every column (no masks); else token 16t + 4g + i of column c is visible
+// when it is <= min(lim[c], t_hi - 1).
+template <int NCT>
+__device__ __forceinline__ void pf_softmax(const f32x4 (&d)[NCT][4], const PfN& N, float sc, int c0, int t_hi,
+                                           bool full, int lane, PfState<NCT>& st, h8 (&pb)[NCT][2]) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const int g = lane >> 4;
+  // value scale: every n_V < 2^(7 + gs), so 2^kPfRescale n_V 2^-gs < 2^15 in fp16.
+  // Norms are non-negative fp16, which order as their bit patterns: a packed u16 max.
+  uint32_t nvm = N.nv[0];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) nvr[k] = half_at(X.nv, k);
-  float nvmax = 0.f;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) nvmax = fmaxf(nvmax, nvr[k]);
+  for (int w = 1; w < 8; ++w) nvm = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(
+                                        __builtin_bit_cast(u16x2, nvm), __builtin_bit_cast(u16x2, N.nv[w])));
+  const float nvmax = fmaxf(half_at(&nvm, 0), half_at(&nvm, 1));
   if (__any(nvmax >= ldexpf(1.f, 7 + st.gs))) {  // wave-uniform, rare
     int ge;
     frexpf(wave_max(nvmax), &ge);
@@ -227,87 +291,99 @@ __device__ __forceinline__ void pf_chunk(PfBuf<BWK, BWV>& X, TabTf<BWK>& cbk, Ta
       for (int mt = 0; mt < 8; ++mt) st.acc[ct][mt] *= f;
     st.gs = gs_need;
   }
-  const float vsc = ldexpf(1.f, -st.gs);
+  // n_V 2^-gs of tokens (k, k+1), k even, as an fp16 pair (the stored pair, scaled exactly)
+  const _Float16 vsc = _Float16(ldexpf(1.f, -st.gs));
+  h2 nv2[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) nv2[w] = __builtin_bit_cast(h2, N.nv[w]) * h2{vsc, vsc};
   float nks[16];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) nks[k] = half_at(X.nk, k) * sc;
-
-  // ---- softmax per column tile; p n_V 2^-gs into the value B operands
-  h8 pb[NCT][2];
+  for (int k = 0; k < 16; ++k) nks[k] = half_at(N.nk, k) * sc;
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) {
-    float s[16];
-    // token (t, i) = c0 + 16t + 4g + i sits at s[4t + i]
-    const int lim = min(st.lim[ct], t_hi - 1) - (c0 + 4 * g);  // visible: 16t + i <= lim
-    float mx = -INFINITY;
+    // u = s - m0 with m0 the reference maximum (0 before the column's first key)
+    const bool fresh = st.m[ct] == -INFINITY;
+    const float m0 = fresh ? 0.f : st.m[ct];
+    const int lim = min(st.lim[ct], t_hi - 1) - (c0 + 4 * g);  // token (t, i) visible: 16t + i <= lim
+    float u[16], umax = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float x = d[ct][t][i] * nks[4 * t + i];
-        s[4 * t + i] = (full || 16 * t + i <= lim) ? x : -INFINITY;
-        mx = fmaxf(mx, s[4 * t + i]);
+        const float x = fmaf(d[ct][t][i], nks[4 * t + i], -m0);
+        u[4 * t + i] = (full || 16 * t + i <= lim) ? x : -INFINITY;
+        umax = fmaxf(umax, u[4 * t + i]);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    if (__any(mx > st.m[ct] + kPfRescale)) {  // wave-uniform
-      const float m_new = mx > st.m[ct] + kPfRescale ? mx : st.m[ct];
-      const float alpha = m_new == st.m[ct] ? 1.f : __builtin_amdgcn_exp2f(st.m[ct] - m_new);  // 0 from -inf
-      st.m[ct] = m_new;
+    umax = fmaxf(umax, __shfl_xor(umax, 16, 64));
+    umax = fmaxf(umax, __shfl_xor(umax, 32, 64));
+    // the reference moves to the chunk's maximum when a score exceeds it by more than
+    // kPfRescale, and on the column's first key
+    const bool move = umax > kPfRescale || (fresh && umax > -INFINITY);
+    if (__any(move)) {  // wave-uniform
+      const float shift = move ? umax : 0.f;
+      const float alpha = move ? (fresh ? 0.f : __builtin_amdgcn_exp2f(-umax)) : 1.f;
+      st.m[ct] = move ? m0 + umax : st.m[ct];
       st.l[ct] *= alpha;
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) st.acc[ct][mt] *= alpha;
-    }
-    const float m0 = st.m[ct] == -INFINITY ? 0.f : st.m[ct];  // a column with no key yet: every s is -inf
-    float p[16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      p[k] = __builtin_amdgcn_exp2f(s[k] - m0);  // 0 for masked tokens
-      st.l[ct] += p[k];
+      for (int k = 0; k < 16; ++k) u[k] -= shift;
     }
-    // K-step ks: k-slots 0..3 = tile 2ks, 4..7 = tile 2ks+1, registers i = 0..3
+    // p (fp32, into l) and p n_V 2^-gs: p rounded to fp16, times the fp16 norm pair
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      h8 v;
+      u32x4 v;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int k = 8 * ks + j;  // tile 2ks + j/4, register j%4: s index 4(2ks + j/4) + j%4 = 8ks + j
-        v[j] = _Float16(p[k] * nvr[k] * vsc);
+      for (int j = 0; j < 4; ++j) {
+        const int k = 8 * ks + 2 * j;
+        const float p0 = __builtin_amdgcn_exp2f(u[k]), p1 = __builtin_amdgcn_exp2f(u[k + 1]);  // 0 if masked
+        st.l[ct] += p0 + p1;
+        v[j] = __builtin_bit_cast(uint32_t, h2{_Float16(p0), _Float16(p1)} * nv2[k >> 1]);
       }
-      pb[ct][ks] = v;
+      pb[ct][ks] = __builtin_bit_cast(h8, v);
     }
   }
+}
 
-  // ---- values: step k = 8ks + mt
-  if constexpr (BWV == 6) pf_merge_pairs<BWK, BWV>(X, lane);
-  {
-    uint32_t e[LA + 1][4];
-    auto look = [&](auto kc, uint32_t (&o)[4]) {
-      constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7;
-      // pair q of K-step ks: tokens (j, j+1) with j = 2q of the k-slots: tile 2ks + (q >> 1), registers 2(q & 1), +1
+// Entry of the 4-bit pair in byte J of x: the address 4 lane | byte << 8 | slot << 16
+// formed by one byte permute of x and the table register (a fresh register per read,
+// where entry_tf rewrites the shared one in place).
+template <int J>
+__device__ __forceinline__ uint32_t entry_perm(const TabTf<4>& tab, uint32_t x) {
+  const uint32_t addr = __builtin_amdgcn_perm(x, tab.r[0], 0x03020000u | uint32_t(4 + J) << 8);
+  return *reinterpret_cast<const uint32_t*>(tab.lds + addr);
+}
+
+// Values of the chunk: step k = 8ks + mt; pair q of K-step ks = tokens (8ks + 2q,
+// 8ks + 2q + 1) of the V rows, merged by pf_merge_pairs.
+template <int BWV, int NCT>
+__device__ __forceinline__ void pf_values(const PfV<BWV>& V, TabTf<BWV>& cbv, const h8 (&pb)[NCT][2],
+                                          PfState<NCT>& st) {
+  constexpr int LA = kPfLookahead, VW = PfV<BWV>::VW;
+  u32x4 e[LA + 1];
+  auto look = [&](auto kc, u32x4& o) {
+    constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int ta = 4 * (2 * ks + (q >> 1)) + 2 * (q & 1);  // token index (t, i) of the first of the pair
-        if constexpr (BWV == 4) {
-          const uint32_t wa = X.v[ta], wb = X.v[ta + 1];
-          const uint32_t x = (mt & 1) ? (((wa >> 4) & 0x0F0F0F0Fu) | (wb & 0xF0F0F0F0u))
-                                      : ((wa & 0x0F0F0F0Fu) | ((wb << 4) & 0xF0F0F0F0u));
-          o[q] = entry_tf<(mt >> 1)>(cbv, x);
-        } else {
-          o[q] = pair_entry_tf(cbv, pair_offset<6, 6 * mt, 2>(X.v + 2 * (ta + (mt & 1))));
-        }
-      }
-    };
-    static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
-    static_for<0, 16>([&](auto kc) {
-      constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7, j = k % (LA + 1);
-      if constexpr (k + LA < 16) look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
-      const h8 av = __builtin_bit_cast(h8, u32x4{e[j][0], e[j][1], e[j][2], e[j][3]});
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t* w = V.w + VW * (8 * ks + 2 * q + (mt & 1));
+      if constexpr (BWV == 4) o[q] = entry_perm<(mt >> 1)>(cbv, w[0]);
+      else o[q] = pair_entry_tf(cbv, pair_offset<6, 6 * mt, 2>(w));
+    }
+  };
+  static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
+  __builtin_amdgcn_sched_barrier(0);
+  static_for<0, 16>([&](auto kc) {
+    constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7, j = k % (LA + 1);
+    if constexpr (k + LA < 16) {
+      look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const h8 av = __builtin_bit_cast(h8, e[j]);
 #pragma unroll
-      for (int ct = 0; ct < NCT; ++ct)
-        st.acc[ct][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[ct][ks], st.acc[ct][mt], 0, 0, 0);
-    });
-  }
+    for (int ct = 0; ct < NCT; ++ct)
+      st.acc[ct][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[ct][ks], st.acc[ct][mt], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  });
 }
 
 // Writes the (acc, m, l) partial of each column (query row) of the block: lane (g, c)
@@ -438,22 +514,35 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
 
     TabTf<BWK> cbk = make_tab_tf<BWK>(lds, Lay::k_off, lane);
     TabTf<BWV> cbv = make_tab_tf<BWV>(lds, Lay::v_off, lane);
-    PfBuf<BWK, BWV> x0, x1;
-    pf_load<BWK, BWV>(a, trow, kvh, t_lo, col_hi, lane, x0);
-    const int n = ch_hi - ch_lo;
-    auto step = [&](int ch, PfBuf<BWK, BWV>& X, PfBuf<BWK, BWV>& Y) {
-      const int c0 = t_lo + 64 * ch;
-      // the next chunk's rows load while this one computes (clamped into the range on the last)
-      pf_load<BWK, BWV>(a, trow, kvh, min(c0 + 64, t_lo + 64 * (n - 1)), col_hi, lane, Y);
-      const bool full = c0 + 63 <= lim_min && c0 + 64 <= t_hi;
-      pf_chunk<BWK, BWV, NCT>(X, cbk, cbv, qb, sc, c0, t_hi, full, lane, st);
-    };
-    int ch = 0;
-    for (; ch + 2 <= n; ch += 2) {
-      step(ch, x0, x1);
-      step(ch + 1, x1, x0);
+    // one buffer each for the K rows, the V rows and the norms: the next chunk's K rows
+    // load once the scores have read this chunk's, its norms after the softmax, its V
+    // rows after the values, each about two thirds of a chunk ahead of its use
+    PfK<BWK> K;
+    PfV<BWV> V;
+    PfN N;
+    {
+      const PfTiles tl = pf_tiles(a, trow, t_lo, col_hi);
+      pf_load_k<BWK>(a, tl, kvh, lane, K);
+      pf_load_n(a, tl, kvh, lane, N);
+      pf_load_v<BWV>(a, tl, kvh, lane, V);
     }
-    if (ch < n) step(ch, x0, x1);
+    const int n = ch_hi - ch_lo;
+    for (int ch = 0; ch < n; ++ch) {
+      const int c0 = t_lo + 64 * ch;
+      // the next chunk's tiles (the last chunk's again on the last step: its loads are
+      // issued on every step, so each step's waits count the same loads)
+      const PfTiles nx = pf_tiles(a, trow, min(c0 + 64, t_lo + 64 * (n - 1)), col_hi);
+      const bool full = c0 + 63 <= lim_min && c0 + 64 <= t_hi;
+      f32x4 d[NCT][4];
+      pf_scores<BWK, NCT>(K, cbk, qb, d);
+      pf_load_k<BWK>(a, nx, kvh, lane, K);
+      h8 pb[NCT][2];
+      pf_softmax<NCT>(d, N, sc, c0, t_hi, full, lane, st, pb);
+      pf_load_n(a, nx, kvh, lane, N);
+      pf_merge_pairs<BWV>(V, lane);
+      pf_values<BWV, NCT>(V, cbv, pb, st);
+      pf_load_v<BWV>(a, nx, kvh, lane, V);
+    }
   }
   pf_write<NCT>(a, st, row0, lane);
 }
@@ -597,7 +686,7 @@ template <int BWK, int BWV>
 PfKernel pf_kernel() {
   // four column tiles (64 query rows) per wave: one K or V lookup feeds four MFMAs;
   // the accumulators take 128 registers, so one wave per SIMD
-  constexpr int NCT = 2, WPB = 4;
+  constexpr int NCT = 2, WPB = 8;
   return PfKernel{pf_scan_kernel<BWK, BWV, NCT, WPB>, WPB, NCT};
 }
 
