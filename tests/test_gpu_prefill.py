@@ -56,12 +56,14 @@ def _check(got, ref, lens, Q):
 @pytest.mark.parametrize("bwk,bwv,Hq,Hkv,Q", [
     (4, 4, 32, 8, 16), (4, 4, 32, 8, 7), (4, 4, 8, 8, 40), (4, 4, 16, 8, 33), (4, 4, 12, 4, 5),
     (6, 6, 32, 8, 16), (6, 6, 8, 8, 3), (4, 6, 64, 8, 16), (6, 4, 32, 8, 9), (4, 6, 40, 8, 2),
-    (4, 4, 64, 4, 24)])
+    (4, 4, 64, 4, 24), (4, 4, 32, 8, 64), (6, 6, 32, 8, 100), (4, 6, 64, 8, 40), (6, 4, 16, 8, 70)])
 def test_prefill_matches_the_oracle(bwk, bwv, Hq, Hkv, Q):
     """Widths 4/4, 6/6, 4/6 and 6/4; n_rep 1 to 16 (query blocks that cut through a
     query's heads); ragged lengths with an empty sequence, a sequence shorter than Q
     (its first queries see no key), one of exactly Q tokens and long ones; library
-    split count and fixed counts of 1 and 5."""
+    split count and fixed counts of 1 and 5. Shapes of at least eight 32-row query
+    blocks per kv head (n_rep Q >= 225) run the shared-tile scan, the 6/6 case with a
+    last work-group of six blocks; the others the per-wave scan."""
     lens = (0, 3, Q, 17 + Q, 700, 1500)
     print(f"prefill {bwk}/{bwv} Hq={Hq} Hkv={Hkv} Q={Q}", flush=True)
     q, kv = _case(1000 + Hq + 7 * Q + 10 * bwk + bwv, lens, Hq, Hkv, Q, bwk, bwv)
@@ -85,15 +87,17 @@ def test_prefill_page_sizes(S):
     _check(got, oa.reconstruct_attention(q, kv, scale), lens, Q)
 
 
-@pytest.mark.parametrize("bwk,bwv,Hq", [(4, 4, 32), (6, 6, 32), (4, 6, 64)])
-def test_prefill_large_scores_against_the_rounded_operand_reference(bwk, bwv, Hq):
+@pytest.mark.parametrize("bwk,bwv,Hq,Q", [(4, 4, 32, 20), (6, 6, 32, 20), (4, 6, 64, 20), (4, 4, 32, 96),
+                                          (4, 6, 64, 48)])
+def test_prefill_large_scores_against_the_rounded_operand_reference(bwk, bwv, Hq, Q):
     """Scores 50 times larger (the lazy maximum moves often) over 2,500 and 4,096
     tokens: the TF32-class rounding itself moves scores of several hundred by tenths,
-    so the result is held to the float64 attention of operands rounded the same way."""
+    so the result is held to the float64 attention of operands rounded the same way.
+    Q = 96 and 48 run the shared-tile scan."""
     lens = (2500, 4096)
-    Q, Hkv = 20, 8
+    Hkv = 8
     print(f"prefill large scores {bwk}/{bwv} Hq={Hq}", flush=True)
-    q, kv = _case(1200 + bwk + bwv + Hq, lens, Hq, Hkv, Q, bwk, bwv, S=32, q_scale=50.0)
+    q, kv = _case(1200 + bwk + bwv + Hq + Q, lens, Hq, Hkv, Q, bwk, bwv, S=32, q_scale=50.0)
     scale = oa.default_scale(128)
     pa = _pa()
     B = len(lens)

@@ -265,10 +265,12 @@ __device__ __forceinline__ void pf_scores(const PfK<BWK>& K, TabTf<BWK>& cbk, co
 
 // Online softmax of the chunk per column, p n_V 2^-gs into the value B operands:
 // K-step ks of column tile ct takes tokens (2ks, i) at k-slots i and (2ks + 1, i) at
-// k-slots 4 + i, this lane's own score registers. full: every token of the chunk is
-// visible to every column (no masks); else token 16t + 4g + i of column c is visible
-// when it is <= min(lim[c], t_hi - 1).
-template <int NCT>
+// k-slots 4 + i, this lane's own score registers. Score register i of tile t is token
+// c0 + 16t + 4g + i, or with TILED (the shared-tile scan's order) c0 + 32(t >> 1) +
+// 8g + 4(t & 1) + i; norms word 2t + (i >> 1) holds its n_K, n_V either way. full:
+// every token of the chunk is visible to every column (no masks); else a token of
+// column c is visible when it is <= min(lim[c], t_hi - 1).
+template <int NCT, bool TILED = false>
 __device__ __forceinline__ void pf_softmax(const f32x4 (&d)[NCT][4], const PfN& N, float sc, int c0, int t_hi,
                                            bool full, int lane, PfState<NCT>& st, h8 (&pb)[NCT][2]) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -304,14 +306,16 @@ __device__ __forceinline__ void pf_softmax(const f32x4 (&d)[NCT][4], const PfN& 
     // u = s - m0 with m0 the reference maximum (0 before the column's first key)
     const bool fresh = st.m[ct] == -INFINITY;
     const float m0 = fresh ? 0.f : st.m[ct];
-    const int lim = min(st.lim[ct], t_hi - 1) - (c0 + 4 * g);  // token (t, i) visible: 16t + i <= lim
+    // token (t, i) visible: its offset from the lane's base is <= lim
+    const int lim = min(st.lim[ct], t_hi - 1) - (c0 + (TILED ? 8 : 4) * g);
     float u[16], umax = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float x = fmaf(d[ct][t][i], nks[4 * t + i], -m0);
-        u[4 * t + i] = (full || 16 * t + i <= lim) ? x : -INFINITY;
+        const int off = TILED ? 32 * (t >> 1) + 4 * (t & 1) + i : 16 * t + i;
+        u[4 * t + i] = (full || off <= lim) ? x : -INFINITY;
         umax = fmaxf(umax, u[4 * t + i]);
       }
     umax = fmaxf(umax, __shfl_xor(umax, 16, 64));
@@ -406,6 +410,25 @@ __device__ __forceinline__ void pf_write(const PrefillArgs& a, PfState<NCT>& st,
       *reinterpret_cast<float4*>(dst + 8 * i + 4) = make_float4(st.acc[ct][4][i] * f, st.acc[ct][5][i] * f,
                                                                 st.acc[ct][6][i] * f, st.acc[ct][7][i] * f);
     }
+    if (g == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * row) = make_float2(st.m[ct], l);
+  }
+}
+
+// pf_write for the shared-tile scan, whose value M-tile mt row c is dim 16 mt + c:
+// lane (g, c) writes dims 16 mt + 4g .. +3 of row 16 ct + c.
+template <int NCT>
+__device__ __forceinline__ void pf_write_tiled(const PrefillArgs& a, PfState<NCT>& st, int64_t row0, int lane) {
+  const int g = lane >> 4, c = lane & 15;
+  const float f = ldexpf(1.f, st.gs - 8);
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    float l = st.l[ct];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int64_t row = row0 + 16 * ct + c;
+    float* dst = a.part_acc + row * 128 + 4 * g;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<f32x4*>(dst + 16 * mt) = st.acc[ct][mt] * f;
     if (g == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * row) = make_float2(st.m[ct], l);
   }
 }
@@ -547,6 +570,351 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
   pf_write<NCT>(a, st, row0, lane);
 }
 
+// ---------------------------------------------------------------- shared-tile scan
+//
+// For query blocks of many rows per kv head (n_rep Q >= 8 blocks of 16 NCT rows) the
+// eight waves of a work-group take eight neighbouring blocks of the same (sequence,
+// kv head, split) and share the chunk's dequantization: all threads turn the chunk's
+// packed K and V rows into fp16 tiles in LDS (each code looked up once per work-group
+// instead of once per wave), one barrier per chunk, and each wave reads its MFMA A
+// operands from the tiles with one 16-byte LDS read per step. Scores, softmax and
+// values are those of the per-wave scan with one change of token order: row c of
+// score tile t is token tile_row(t, c), so that the 8 k-slots of lane group g in value
+// K-step ks (score tiles 2ks and 2ks + 1, registers 0..3) are the consecutive tokens
+// 32ks + 8g .. +7, which one read of the transposed V tile returns.
+//
+//   K tile   [64 tokens][128 dims] fp16, rows of 272 bytes, the 16-byte column
+//            quads of rows 16..31 and 48..63 swapped by XOR 4 (the 16 rows that 16
+//            lanes read together fall in 16 different bank quads)
+//   V tile   [128 dims][64 tokens] fp16 (transposed), rows of 144 bytes
+//   norms    n_K, n_V of the 64 tokens, fp16
+// Two sets (chunk n is read from set n & 1 while chunk n + 1 is written to the other);
+// the codebooks sit beside them as plain pair tables of fp16 pairs (4-bit: 256
+// entries, 6-bit: 4096).
+
+constexpr int kKRow = 272;                       // bytes per K tile row (256 + 16)
+constexpr int kVRow = 144;                       // bytes per V tile row (128 + 16)
+constexpr int kKTile = 64 * kKRow;               // 17,408
+constexpr int kVTile = 128 * kVRow;              // 18,432
+constexpr int kTileSet = kKTile + kVTile + 256;  // + 64 K and 64 V norms
+
+template <int BW>
+constexpr int plain_tf_bytes() { return 4 << (2 * BW); }
+
+// Byte offset of 16-byte column quad q of K tile row r.
+__device__ __forceinline__ uint32_t ktile_off(int r, int q) { return uint32_t(r * kKRow + ((q ^ ((r & 16) >> 2)) << 4)); }
+
+// Token of row c of score tile t (see above).
+__device__ __forceinline__ int tile_row(int t, int c) { return 32 * (t >> 1) + 8 * (c >> 2) + 4 * (t & 1) + (c & 3); }
+
+// Stages a plain pair table of fp16 pairs: entry i = (H(2^8 c[i mod 2^BW]), H(2^8 c[i >> BW])).
+template <int BW>
+__device__ __forceinline__ void stage_plain_tf(const float* cb, char* dst, int tid, int nthr) {
+  uint32_t* t = reinterpret_cast<uint32_t*>(dst);
+  for (int i = tid; i < (1 << (2 * BW)); i += nthr)
+    t[i] = tf_word(cb[i & ((1 << BW) - 1)] * kCbScale, cb[i >> BW] * kCbScale);
+}
+
+template <int BW>
+__device__ __forceinline__ uint32_t plain_entry(const char* tab, uint32_t idx) {
+  return *reinterpret_cast<const uint32_t*>(tab + (idx << 2));
+}
+
+// The raw bytes one thread dequantizes per chunk, loaded a chunk ahead.
+// K items (token, 8-dim group dg), dg fastest: 1024 / (64 WPB) per thread.
+// V items (token pair tp, 8-dim group dg), tp fastest: 512 / (64 WPB) per thread.
+// Norms: threads 0..31 take K norms of tokens 2i, 2i+1; threads 32..63 the V norms.
+template <int BWK, int BWV, int WPB>
+struct PfRaw {
+  static constexpr int NK = 1024 / (64 * WPB), NV = 512 / (64 * WPB);
+  static constexpr int KW = BWK == 4 ? 1 : 2, VW = BWV == 4 ? 1 : 2;
+  uint32_t k[NK][KW];
+  uint32_t v[NV][2][VW];
+  uint32_t n;
+};
+
+template <int BWK, int BWV, int WPB>
+__device__ __forceinline__ void pf_raw_load(const PrefillArgs& a, const int32_t* trow, int kvh, int c0, int col_hi,
+                                            int tid, PfRaw<BWK, BWV, WPB>& o) {
+  using R = PfRaw<BWK, BWV, WPB>;
+  const int smask = (1 << a.log2S) - 1;
+  auto row_of = [&](const uint8_t* base, int64_t sp, int64_t sh, int nb, int tok) {
+    const int t = c0 + tok;
+    const uint32_t pid = uint32_t(trow[min(t >> a.log2S, col_hi)]);
+    return base + uint64_t(pid) * uint64_t(sp) + uint64_t(kvh) * uint64_t(sh) + uint32_t(t & smask) * uint32_t(nb);
+  };
+#pragma unroll
+  for (int j = 0; j < R::NK; ++j) {
+    const int it = tid + 64 * WPB * j, tok = it >> 4, dg = it & 15;
+    const uint8_t* p = row_of(a.k_pages, a.ksp, a.ksh, 16 * BWK, tok);
+    if constexpr (BWK == 4) {
+      o.k[j][0] = *reinterpret_cast<const uint32_t*>(p + 4 * dg);
+    } else {
+      uint2 x;
+      __builtin_memcpy(&x, __builtin_assume_aligned(p + ((6 * dg) & ~3), 4), 8);
+      o.k[j][0] = x.x;
+      o.k[j][1] = x.y;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < R::NV; ++j) {
+    const int it = tid + 64 * WPB * j, tp = it & 31, dg = it >> 5;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint8_t* p = row_of(a.v_pages, a.vsp, a.vsh, 16 * BWV, 2 * tp + h);
+      if constexpr (BWV == 4) {
+        o.v[j][h][0] = *reinterpret_cast<const uint32_t*>(p + 4 * dg);
+      } else {
+        uint2 x;
+        __builtin_memcpy(&x, __builtin_assume_aligned(p + ((6 * dg) & ~3), 4), 8);
+        o.v[j][h][0] = x.x;
+        o.v[j][h][1] = x.y;
+      }
+    }
+  }
+  if (tid < 64) {
+    const int tok = 2 * (tid & 31);
+    const int t = c0 + tok;
+    const uint32_t pid = uint32_t(trow[min(t >> a.log2S, col_hi)]);
+    const uint16_t* nb = tid < 32 ? a.k_norms + uint64_t(pid) * uint64_t(a.knp) + uint64_t(kvh) * uint64_t(a.knh)
+                                  : a.v_norms + uint64_t(pid) * uint64_t(a.vnp) + uint64_t(kvh) * uint64_t(a.vnh);
+    o.n = *reinterpret_cast<const uint32_t*>(nb + (t & smask));
+  }
+}
+
+// Dequantizes the raw bytes into tile set `set`.
+template <int BWK, int BWV, int WPB>
+__device__ __forceinline__ void pf_raw_store(const PfRaw<BWK, BWV, WPB>& r, const char* tabk, const char* tabv,
+                                             char* set, int tid) {
+  using R = PfRaw<BWK, BWV, WPB>;
+#pragma unroll
+  for (int j = 0; j < R::NK; ++j) {
+    const int it = tid + 64 * WPB * j, tok = it >> 4, dg = it & 15;
+    u32x4 e;
+    if constexpr (BWK == 4) {
+      const uint32_t w = r.k[j][0];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) e[p] = plain_entry<4>(tabk, (w >> (8 * p)) & 0xFFu);
+    } else {
+      const uint32_t sh = 16u * uint32_t(dg & 1);
+      const uint64_t x = (uint64_t(r.k[j][1]) << 32 | r.k[j][0]) >> sh;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) e[p] = plain_entry<6>(tabk, uint32_t(x >> (12 * p)) & 0xFFFu);
+    }
+    *reinterpret_cast<u32x4*>(set + ktile_off(tok, dg)) = e;
+  }
+  char* vt = set + kKTile;
+#pragma unroll
+  for (int j = 0; j < R::NV; ++j) {
+    const int it = tid + 64 * WPB * j, tp = it & 31, dg = it >> 5;
+    // pair index of dim 8dg + m: (code of token 2tp, code of token 2tp + 1)
+    uint32_t idx[8];
+    if constexpr (BWV == 4) {
+      const uint32_t wa = r.v[j][0][0], wb = r.v[j][1][0];
+      const uint32_t xe = bitsel(0x0F0F0F0Fu, wa, wb << 4), xo = bitsel(0x0F0F0F0Fu, wa >> 4, wb);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) idx[m] = ((m & 1 ? xo : xe) >> (8 * (m >> 1))) & 0xFFu;
+    } else {
+      const uint32_t sh = 16u * uint32_t(dg & 1);
+      const uint64_t xa = (uint64_t(r.v[j][0][1]) << 32 | r.v[j][0][0]) >> sh;
+      const uint64_t xb = (uint64_t(r.v[j][1][1]) << 32 | r.v[j][1][0]) >> sh;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) idx[m] = uint32_t((xa >> (6 * m)) & 63u) | uint32_t((xb >> (6 * m)) & 63u) << 6;
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+      *reinterpret_cast<uint32_t*>(vt + (8 * dg + m) * kVRow + 4 * tp) = plain_entry<BWV>(tabv, idx[m]);
+  }
+  if (tid < 64) *reinterpret_cast<uint32_t*>(set + kKTile + kVTile + 128 * (tid >> 5) + 4 * (tid & 31)) = r.n;
+}
+
+template <int BWK, int BWV, int WPB>
+struct PfTileLds {
+  static constexpr int tabk = 0, tabv = plain_tf_bytes<BWK>();
+  static constexpr int sets = tabv + plain_tf_bytes<BWV>();
+  static constexpr int total = sets + 2 * kTileSet;
+  static_assert(sets % 16 == 0 && kTileSet % 16 == 0, "tile sets 16-byte aligned");
+  static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
+};
+
+template <int BWK, int BWV, int NCT, int WPB>
+__global__ __launch_bounds__(64 * WPB) void pf_tile_kernel(PrefillArgs a) {
+  using Lay = PfTileLds<BWK, BWV, WPB>;
+  constexpr int NR = 16 * NCT, LA = kPfLookahead;
+  __shared__ __align__(16) char lds[Lay::total];
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+  const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
+  stage_plain_tf<BWK>(a.cb_k, lds + Lay::tabk, tid, 64 * WPB);
+  stage_plain_tf<BWV>(a.cb_v, lds + Lay::tabv, tid, 64 * WPB);
+  // work-group unit: (sequence, kv head, split, column group of WPB blocks)
+  const int ncg = (a.ncb + WPB - 1) / WPB;
+  const int64_t unit = pf_xcd_major(blockIdx.x, gridDim.x);
+  const int cg = int(unit % ncg);
+  int64_t u = unit / ncg;
+  const int s = int(u % a.nsplit);
+  u /= a.nsplit;
+  const int kvh = int(u % a.Hkv);
+  const int b = int(u / a.Hkv);
+  const bool unit_live = b < a.B;  // grid rounding
+  const int cb = cg * WPB + wig;
+  const bool wave_live = unit_live && cb < a.ncb;
+
+  PfState<NCT> st;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) st.acc[ct][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m[ct] = -INFINITY;
+    st.l[ct] = 0.f;
+  }
+  st.gs = 0;
+  const int L = unit_live ? a.seq_lens[b] : 0;
+  const int rows = a.n_rep * a.Q;
+  // the group's chunks: those its last row sees (the other rows mask what they must not see)
+  const int g_first = cg * WPB * NR, g_last = min(g_first + WPB * NR, rows) - 1;
+  const int T = max(0, g_first < rows ? min(L, L - a.Q + g_last / a.n_rep + 1) : 0);
+  const int nch = (T + 63) >> 6;
+  const int ch_lo = int(int64_t(nch) * s / a.nsplit), ch_hi = int(int64_t(nch) * (s + 1) / a.nsplit);
+  const int n = ch_hi - ch_lo;  // work-group uniform
+  const int r_first = cb * NR;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int r = r_first + 16 * ct + c;
+    st.lim[ct] = r < rows ? L - a.Q + r / a.n_rep : INT32_MAX;
+  }
+  const int lim_min = L - a.Q + min(r_first, rows - 1) / a.n_rep;
+
+  // B operands of the scores (as in pf_scan_kernel); a wave past the last block keeps zeros
+  h8 qb[NCT][4];
+  float sc = 1.f;
+  {
+    float qv[NCT][32];
+    float amax = 0.f;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const int64_t row = (int64_t(b) * a.Hkv + kvh) * a.nrp + min(r_first + 16 * ct + c, a.nrp - 1);
+      const float4* qp = reinterpret_cast<const float4*>(a.q_rot + row * 128 + 32 * g);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float4 x = wave_live ? qp[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+        qv[ct][4 * k] = x.x;
+        qv[ct][4 * k + 1] = x.y;
+        qv[ct][4 * k + 2] = x.z;
+        qv[ct][4 * k + 3] = x.w;
+      }
+#pragma unroll
+      for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(qv[ct][k]));
+    }
+    int qe;
+    frexpf(wave_max(amax), &qe);
+    const int e = 15 - qe;
+    sc = ldexpf(1.f, -(e + 8));
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qb[ct][k][j] = _Float16(ldexpf(qv[ct][8 * k + j], e));
+  }
+
+  if (n > 0) {
+    const int t_lo = 64 * ch_lo, t_hi = min(64 * ch_hi, T);
+    const int col_hi = (t_hi - 1) >> a.log2S;
+    const int32_t* trow = a.table + int64_t(b) * a.tsb;
+    const char* tabk = lds + Lay::tabk;
+    const char* tabv = lds + Lay::tabv;
+    PfRaw<BWK, BWV, WPB> raw;
+    pf_raw_load<BWK, BWV, WPB>(a, trow, kvh, t_lo, col_hi, tid, raw);
+    __syncthreads();  // the tables are staged
+    pf_raw_store<BWK, BWV, WPB>(raw, tabk, tabv, lds + Lay::sets, tid);
+    if (n > 1) pf_raw_load<BWK, BWV, WPB>(a, trow, kvh, t_lo + 64, col_hi, tid, raw);
+    // this lane's score A rows (token tile_row(t, c)) and value A row (dim 16 mt + c)
+    uint32_t krow[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) krow[t] = uint32_t(tile_row(t, c));
+    for (int ch = 0; ch < n; ++ch) {
+      __syncthreads();  // chunk ch is in set ch & 1; set (ch + 1) & 1 is free
+      const char* cur = lds + Lay::sets + (ch & 1) * kTileSet;
+      if (ch + 1 < n) {
+        pf_raw_store<BWK, BWV, WPB>(raw, tabk, tabv, lds + Lay::sets + ((ch + 1) & 1) * kTileSet, tid);
+        if (ch + 2 < n) pf_raw_load<BWK, BWV, WPB>(a, trow, kvh, t_lo + 64 * (ch + 2), col_hi, tid, raw);
+      }
+      if (!wave_live) continue;
+      const int c0 = t_lo + 64 * ch;
+      const bool full = c0 + 63 <= lim_min && c0 + 64 <= t_hi;
+      // scores: step k = 4s + t, A = 8 dims 32g + 8s .. of token tile_row(t, c)
+      f32x4 d[NCT][4];
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) d[ct][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      {
+        h8 e[LA + 1];
+        auto look = [&](auto kc, h8& o) {
+          constexpr int k = decltype(kc)::value, s4 = k >> 2, t = k & 3;
+          o = *reinterpret_cast<const h8*>(cur + ktile_off(int(krow[t]), 4 * g + s4));
+        };
+        static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<0, 16>([&](auto kc) {
+          constexpr int k = decltype(kc)::value, s4 = k >> 2, t = k & 3, j = k % (LA + 1);
+          if constexpr (k + LA < 16) {
+            look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct)
+            d[ct][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(e[j], qb[ct][s4], d[ct][t], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+      }
+      // norms of this lane's score registers: tile t register i = token tile_row(t, 4g + i),
+      // i.e. tokens 32ks + 8g + 4h + i for t = 2ks + h: two 16-byte reads per side
+      PfN nrm;
+      {
+        const uint4* nk = reinterpret_cast<const uint4*>(cur + kKTile + kVTile);
+        const uint4* nv = reinterpret_cast<const uint4*>(cur + kKTile + kVTile + 128);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const uint4 x = nk[4 * ks + g], y = nv[4 * ks + g];
+          nrm.nk[4 * ks] = x.x;
+          nrm.nk[4 * ks + 1] = x.y;
+          nrm.nk[4 * ks + 2] = x.z;
+          nrm.nk[4 * ks + 3] = x.w;
+          nrm.nv[4 * ks] = y.x;
+          nrm.nv[4 * ks + 1] = y.y;
+          nrm.nv[4 * ks + 2] = y.z;
+          nrm.nv[4 * ks + 3] = y.w;
+        }
+      }
+      h8 pb[NCT][2];
+      pf_softmax<NCT, true>(d, nrm, sc, c0, t_hi, full, lane, st, pb);
+      // values: step k = 8ks + mt, A = tokens 32ks + 8g .. +7 of dim 16 mt + c
+      {
+        h8 e[LA + 1];
+        auto look = [&](auto kc, h8& o) {
+          constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7;
+          o = *reinterpret_cast<const h8*>(cur + kKTile + (16 * mt + c) * kVRow + 16 * (4 * ks + g));
+        };
+        static_for<0, LA>([&](auto kc) { look(kc, e[decltype(kc)::value]); });
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<0, 16>([&](auto kc) {
+          constexpr int k = decltype(kc)::value, ks = k >> 3, mt = k & 7, j = k % (LA + 1);
+          if constexpr (k + LA < 16) {
+            look(std::integral_constant<int, k + LA>{}, e[(k + LA) % (LA + 1)]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct)
+            st.acc[ct][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(e[j], pb[ct][ks], st.acc[ct][mt], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+      }
+    }
+  }
+  if (wave_live) pf_write_tiled<NCT>(a, st, ((((int64_t(b) * a.Hkv + kvh) * a.nsplit + s) * a.ncb + cb) * NR), lane);
+}
+
 // ---------------------------------------------------------------- rotate and merge
 
 struct PfRotArgs {
@@ -678,8 +1046,9 @@ __global__ __launch_bounds__(256) void pf_merge_kernel(PfMergeArgs a) {
 using PfScanFn = void (*)(PrefillArgs);
 
 struct PfKernel {
-  PfScanFn fn = nullptr;
-  int wpb = 0, nct = 0;
+  PfScanFn fn = nullptr;   // per-wave scan (few query blocks per kv head)
+  PfScanFn tile = nullptr;  // shared-tile scan (work-groups of tile_wpb blocks)
+  int wpb = 0, nct = 0, tile_wpb = 0;
 };
 
 template <int BWK, int BWV>
@@ -687,7 +1056,7 @@ PfKernel pf_kernel() {
   // four column tiles (64 query rows) per wave: one K or V lookup feeds four MFMAs;
   // the accumulators take 128 registers, so one wave per SIMD
   constexpr int NCT = 2, WPB = 8;
-  return PfKernel{pf_scan_kernel<BWK, BWV, NCT, WPB>, WPB, NCT};
+  return PfKernel{pf_scan_kernel<BWK, BWV, NCT, WPB>, pf_tile_kernel<BWK, BWV, NCT, 8>, WPB, NCT, 8};
 }
 
 PfKernel pick_prefill(int bw_k, int bw_v) {
@@ -716,23 +1085,27 @@ PfLayout pf_layout(int B, int Hq, int Hkv, int Q, int num_splits) {
   return l;
 }
 
-int resident_waves_pf(const PfKernel& k) {
+// Resident work-groups of `fn` (wpb waves each) on the current device.
+int resident_groups_pf(PfScanFn fn, int wpb) {
   static std::mutex mu;
   static std::map<std::pair<int, PfScanFn>, int> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   std::lock_guard<std::mutex> lock(mu);
-  auto it = cache.find({dev, k.fn});
+  auto it = cache.find({dev, fn});
   if (it != cache.end()) return it->second;
   int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k.fn), 64 * k.wpb, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), 64 * wpb, 0) !=
           hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return 0;
-  const int w = per_cu * cus * k.wpb;
-  cache[{dev, k.fn}] = w;
+  const int w = per_cu * cus;
+  cache[{dev, fn}] = w;
   return w;
 }
+
+// The shared-tile scan serves shapes with at least tile_wpb query blocks per kv head.
+bool use_tile(const PfKernel& k, int n_rep, int Q) { return pf_nrp(n_rep, Q) / (16 * k.nct) >= k.tile_wpb; }
 
 }  // namespace
 }  // namespace wn
@@ -746,12 +1119,16 @@ extern "C" int wn_prefill_plan(int B, int Hq, int Hkv, int Q, int D, int S, int 
   const PfKernel k = pick_prefill(bw_k, bw_v);
   WN_REQUIRE(D == 128 && S >= 16 && is_pow2(S) && k.fn, WN_E_UNSUPPORTED,
              "wn_prefill_plan: (D=%d, S=%d, bw_k=%d, bw_v=%d) not compiled", D, S, bw_k, bw_v);
-  const int w = resident_waves_pf(k);
+  // about two work-groups per resident slot over the (sequence, kv head, column block
+  // or group of blocks) units, each split keeping at least four chunks of the longest
+  // history
+  const bool tile = use_tile(k, Hq / Hkv, Q);
+  const int wpb = tile ? k.tile_wpb : k.wpb;
+  const int w = resident_groups_pf(tile ? k.tile : k.fn, wpb);
   WN_REQUIRE(w > 0, WN_E_LAUNCH, "wn_prefill_plan: cannot query the device occupancy");
-  // about two waves per resident slot over the (sequence, kv head, column block)
-  // items, each split keeping at least four chunks of the longest history
-  const int64_t units = int64_t(B > 0 ? B : 1) * Hkv * (pf_nrp(Hq / Hkv, Q) / (16 * k.nct));
-  int64_t ns = (2 * int64_t(w) + units - 1) / units;
+  const int ncb = pf_nrp(Hq / Hkv, Q) / (16 * k.nct);
+  const int64_t units = int64_t(B > 0 ? B : 1) * Hkv * (tile ? (ncb + wpb - 1) / wpb : ncb);
+  int64_t ns = (2 * int64_t(tile ? w : w * wpb) + units - 1) / units;
   const int64_t chunks = (int64_t(max_len) + 63) / 64;
   ns = std::min<int64_t>(ns, std::max<int64_t>(1, chunks / 4));
   *num_splits = int(std::max<int64_t>(1, std::min<int64_t>(ns, 256)));
@@ -847,10 +1224,13 @@ extern "C" int wn_prefill_attention(
   pa.ncb = ncb;
   pa.nsplit = num_splits;
   pa.log2S = ilog2(S);
-  const int64_t waves = int64_t(B) * Hkv * num_splits * ncb;
-  WN_REQUIRE(waves / k.wpb < (int64_t(1) << 31), WN_E_INVALID, "prefill: grid too large");
+  const bool tile = use_tile(k, n_rep, Q);
+  const int64_t groups = tile ? int64_t(B) * Hkv * num_splits * ((ncb + k.tile_wpb - 1) / k.tile_wpb)
+                              : (int64_t(B) * Hkv * num_splits * ncb + k.wpb - 1) / k.wpb;
+  WN_REQUIRE(groups < (int64_t(1) << 31), WN_E_INVALID, "prefill: grid too large");
   if (ev_begin) hipEventRecord(static_cast<hipEvent_t>(ev_begin), st);
-  hipLaunchKernelGGL(k.fn, dim3(unsigned((waves + k.wpb - 1) / k.wpb)), dim3(64 * k.wpb), 0, st, pa);
+  if (tile) hipLaunchKernelGGL(k.tile, dim3(unsigned(groups)), dim3(64 * k.tile_wpb), 0, st, pa);
+  else hipLaunchKernelGGL(k.fn, dim3(unsigned(groups)), dim3(64 * k.wpb), 0, st, pa);
   if (ev_end) hipEventRecord(static_cast<hipEvent_t>(ev_end), st);
 
   PfMergeArgs ma{pa.part_acc, pa.part_ml, pi_v, out, out_dtype, Hkv, n_rep, Q, nrp, ncb, num_splits, nr};
