@@ -916,6 +916,14 @@ __global__ __launch_bounds__(64 * WPB) void pf_tile_kernel(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------- rotate and merge
+//
+// Both are a kRotRows-row tile times a 128 x 128 rotation per work-group: the matrix
+// M^T ([j][k], 132-float rows) and the rows ([r][k], 132-float rows) in LDS, thread t
+// making rows RT (t >> 4) .. and columns (t & 15) + 16 jj, jj = 0..7, from 16-byte
+// reads along k (the 16 lanes of a column group read 16 different M^T rows whose 4-bank
+// spans do not overlap; lanes sharing rows read the same addresses).
+
+constexpr int kRotStride = 132;  // floats per LDS row (16-byte aligned, bank-skewed)
 
 struct PfRotArgs {
   const void* q;
@@ -926,36 +934,43 @@ struct PfRotArgs {
   int Hkv, n_rep, Q, nrp, q_dtype;
 };
 
-// y[r][j] = sum_k x[r][k] M[k][j] for the kRotRows rows of a work-group: xt = x
-// transposed in LDS ([k][r]), m = M in LDS ([k][j]); thread t makes rows 4 (t / 32)
-// .. +3 and columns 4 (t % 32) .. +3.
-__device__ __forceinline__ void rows_times(const float* xt, const float* m, int tid, float (&y)[4][4]) {
-  const int rb = 4 * (tid >> 5), jb = 4 * (tid & 31);
+// y[r][jj] = sum_k x[rb + r][k] mt[(t & 15) + 16 jj][k], rb = RT (t >> 4).
+constexpr int RT = kRotRows / 16;  // rows per thread
+__device__ __forceinline__ void rows_times_t(const float* x, const float* mt, int tid, float (&y)[RT][8]) {
+  const int rb = RT * (tid >> 4), jc = tid & 15;
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int r = 0; r < RT; ++r)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) y[r][j] = 0.f;
-#pragma unroll 8
-  for (int k = 0; k < 128; ++k) {
-    const float4 xv = *reinterpret_cast<const float4*>(xt + k * kRotRows + rb);
-    const float4 mv = *reinterpret_cast<const float4*>(m + k * 128 + jb);
-    const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, ma[4] = {mv.x, mv.y, mv.z, mv.w};
+    for (int jj = 0; jj < 8; ++jj) y[r][jj] = 0.f;
+#pragma unroll 2
+  for (int k = 0; k < 128; k += 4) {
+    float4 xv[RT], mv[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < RT; ++r) xv[r] = *reinterpret_cast<const float4*>(x + (rb + r) * kRotStride + k);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) y[r][j] = fmaf(xa[r], ma[j], y[r][j]);
+    for (int jj = 0; jj < 8; ++jj) mv[jj] = *reinterpret_cast<const float4*>(mt + (jc + 16 * jj) * kRotStride + k);
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        y[r][jj] = fmaf(xv[r].x, mv[jj].x, y[r][jj]);
+        y[r][jj] = fmaf(xv[r].y, mv[jj].y, y[r][jj]);
+        y[r][jj] = fmaf(xv[r].z, mv[jj].z, y[r][jj]);
+        y[r][jj] = fmaf(xv[r].w, mv[jj].w, y[r][jj]);
+      }
   }
 }
 
-// q_rot rows (sequence blockIdx.z, kv head blockIdx.y, rows 32 blockIdx.x .. +31):
-// scale * q Pi_K^T, zero for rows past n_rep Q.
+// q_rot rows (sequence blockIdx.z, kv head blockIdx.y, rows kRotRows blockIdx.x ..):
+// scale * q Pi_K^T, zero for rows past n_rep Q. Pi_K is [j][k] already: its rows are
+// staged as they are, with coalesced 16-byte loads.
 __global__ __launch_bounds__(256) void pf_rotate_kernel(PfRotArgs a) {
-  __shared__ __align__(16) float pit[128 * 128];      // Pi_K^T: [k][j] = Pi_K[j][k]
-  __shared__ __align__(16) float xt[128 * kRotRows];  // q rows transposed
+  __shared__ __align__(16) float mt[128 * kRotStride];
+  __shared__ __align__(16) float x[kRotRows * kRotStride];
   const int tid = threadIdx.x, kvh = blockIdx.y, b = blockIdx.z, r0 = blockIdx.x * kRotRows;
-  for (int i = tid; i < 128 * 128; i += 256) {  // j fastest: conflict-free LDS writes, reads from L2
-    const int k = i >> 7, j = i & 127;
-    pit[i] = a.pi[j * 128 + k];
+  for (int i = tid; i < 128 * 32; i += 256) {
+    const int j = i >> 5, k4 = 4 * (i & 31);
+    *reinterpret_cast<float4*>(mt + j * kRotStride + k4) = reinterpret_cast<const float4*>(a.pi)[i];
   }
   const int rows = a.n_rep * a.Q;
   for (int i = tid; i < kRotRows * 128; i += 256) {
@@ -965,17 +980,17 @@ __global__ __launch_bounds__(256) void pf_rotate_kernel(PfRotArgs a) {
       const int qi = r / a.n_rep, h = kvh * a.n_rep + r % a.n_rep;
       v = load_elem(a.q, b * a.qsb + h * a.qsh + qi * a.qsq + k, a.q_dtype);
     }
-    xt[k * kRotRows + rr] = v;
+    x[rr * kRotStride + k] = v;
   }
   __syncthreads();
-  float y[4][4];
-  rows_times(xt, pit, tid, y);
-  const int rb = 4 * (tid >> 5), jb = 4 * (tid & 31);
+  float y[RT][8];
+  rows_times_t(x, mt, tid, y);
+  const int rb = RT * (tid >> 4), jc = tid & 15;
   float* out = a.q_rot + ((int64_t(b) * a.Hkv + kvh) * a.nrp + r0) * 128;
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    *reinterpret_cast<float4*>(out + (rb + r) * 128 + jb) =
-        make_float4(y[r][0] * a.scale, y[r][1] * a.scale, y[r][2] * a.scale, y[r][3] * a.scale);
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) out[(rb + r) * 128 + jc + 16 * jj] = y[r][jj] * a.scale;
 }
 
 struct PfMergeArgs {
@@ -986,9 +1001,43 @@ struct PfMergeArgs {
   int out_dtype, Hkv, n_rep, Q, nrp, ncb, nsplit, nr;  // nr: rows per column block
 };
 
-// Rows (sequence blockIdx.z, kv head blockIdx.y, rows 32 blockIdx.x .. +31): the
+// y[r][j] = sum_k xt[k][rb + r] m[k][jb + j] for the kRotRows rows of a work-group:
+// xt = the rows transposed ([k][r]), m = M as it is stored ([k][j]); thread t makes
+// rows 4 (t / 32) .. +3 (RT2 of them) and columns 4 (t % 32) .. +3.
+constexpr int RT2 = kRotRows / 8;
+__device__ __forceinline__ void rows_times_n(const float* xt, const float* m, int tid, float (&y)[RT2][4]) {
+  const int rb = RT2 * (tid >> 5), jb = 4 * (tid & 31);
+#pragma unroll
+  for (int r = 0; r < RT2; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) y[r][j] = 0.f;
+#pragma unroll 4
+  for (int k = 0; k < 128; ++k) {
+    float xa[RT2];
+#pragma unroll
+    for (int r = 0; r < RT2; r += 4) {
+      const float4 xv = *reinterpret_cast<const float4*>(xt + k * kRotRows + rb + r);
+      xa[r] = xv.x;
+      xa[r + 1] = xv.y;
+      xa[r + 2] = xv.z;
+      xa[r + 3] = xv.w;
+    }
+    const float4 mv = *reinterpret_cast<const float4*>(m + k * 128 + jb);
+#pragma unroll
+    for (int r = 0; r < RT2; ++r) {
+      y[r][0] = fmaf(xa[r], mv.x, y[r][0]);
+      y[r][1] = fmaf(xa[r], mv.y, y[r][1]);
+      y[r][2] = fmaf(xa[r], mv.z, y[r][2]);
+      y[r][3] = fmaf(xa[r], mv.w, y[r][3]);
+    }
+  }
+}
+
+// Rows (sequence blockIdx.z, kv head blockIdx.y, rows kRotRows blockIdx.x ..): the
 // max-stable merge of each row's split partials (weights 2^(m_s - max m)), 1 / l,
-// then Pi_V and the cast; rows that saw no key are 0 (packed_attention.py:206).
+// then Pi_V ([k][j], staged as stored) and the cast; rows that saw no key are 0
+// (packed_attention.py:206). The splits' maxima are read in one pass and their
+// weighted rows in a second, so neither pass chains a load behind another.
 __global__ __launch_bounds__(256) void pf_merge_kernel(PfMergeArgs a) {
   __shared__ __align__(16) float pv[128 * 128];
   __shared__ __align__(16) float xt[128 * kRotRows];
@@ -996,42 +1045,47 @@ __global__ __launch_bounds__(256) void pf_merge_kernel(PfMergeArgs a) {
   for (int i = tid; i < 128 * 128 / 4; i += 256)
     reinterpret_cast<float4*>(pv)[i] = reinterpret_cast<const float4*>(a.pi_v)[i];
   {
-    // thread: row rr = tid / 8, dims 16 (tid % 8) .. +15
-    const int rr = tid >> 3, d0 = 16 * (tid & 7), r = r0 + rr;
+    // thread: row rr = tid / TPR, dims DPT (tid % TPR) .. (TPR threads per row)
+    constexpr int TPR = 256 / kRotRows, DPT = 128 / TPR;
+    const int rr = tid / TPR, d0 = DPT * (tid % TPR), r = r0 + rr;
     const int cb = r / a.nr, ri = r % a.nr;
-    float M = -INFINITY, den = 0.f, num[16];
+    const int64_t row0 = (((int64_t(b) * a.Hkv + kvh) * a.nsplit) * a.ncb + cb) * a.nr + ri;
+    const int64_t srow = int64_t(a.ncb) * a.nr;  // rows between a row's consecutive splits
+    float M = -INFINITY;
+#pragma unroll 8
+    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[2 * (row0 + s * srow)]);
+    float den = 0.f, num[DPT];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) num[k] = 0.f;
-    for (int s = 0; s < a.nsplit; ++s) {
-      const int64_t row = (((int64_t(b) * a.Hkv + kvh) * a.nsplit + s) * a.ncb + cb) * a.nr + ri;
-      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * row);
-      if (ml.x == -INFINITY) continue;  // the split saw no key of this row
-      const float Mn = fmaxf(M, ml.x);
-      const float ro = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
-      const float w = __builtin_amdgcn_exp2f(ml.x - Mn);
-      den = den * ro + w * ml.y;
-      const float4* src = reinterpret_cast<const float4*>(a.part_acc + row * 128 + d0);
+    for (int k = 0; k < DPT; ++k) num[k] = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll 4
+      for (int s = 0; s < a.nsplit; ++s) {
+        const int64_t row = row0 + s * srow;
+        const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * row);
+        const float w = __builtin_amdgcn_exp2f(ml.x - M);  // 0 for a split without keys (m = -inf)
+        den = fmaf(w, ml.y, den);
+        const float4* src = reinterpret_cast<const float4*>(a.part_acc + row * 128 + d0);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float4 x = src[k];
-        num[4 * k] = num[4 * k] * ro + w * x.x;
-        num[4 * k + 1] = num[4 * k + 1] * ro + w * x.y;
-        num[4 * k + 2] = num[4 * k + 2] * ro + w * x.z;
-        num[4 * k + 3] = num[4 * k + 3] * ro + w * x.w;
+        for (int k = 0; k < DPT / 4; ++k) {
+          const float4 v = src[k];
+          num[4 * k] = fmaf(w, v.x, num[4 * k]);
+          num[4 * k + 1] = fmaf(w, v.y, num[4 * k + 1]);
+          num[4 * k + 2] = fmaf(w, v.z, num[4 * k + 2]);
+          num[4 * k + 3] = fmaf(w, v.w, num[4 * k + 3]);
+        }
       }
-      M = Mn;
     }
     const float inv = den > 0.f ? 1.f / den : 0.f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) xt[(d0 + k) * kRotRows + rr] = num[k] * inv;
+    for (int k = 0; k < DPT; ++k) xt[(d0 + k) * kRotRows + rr] = num[k] * inv;
   }
   __syncthreads();
-  float y[4][4];
-  rows_times(xt, pv, tid, y);
-  const int rb = 4 * (tid >> 5), jb = 4 * (tid & 31);
+  float y[RT2][4];
+  rows_times_n(xt, pv, tid, y);
+  const int rb = RT2 * (tid >> 5), jb = 4 * (tid & 31);
   const int rows = a.n_rep * a.Q, Hq = a.Hkv * a.n_rep;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+  for (int r = 0; r < RT2; ++r) {
     const int rg = r0 + rb + r;
     if (rg >= rows) continue;
     const int qi = rg / a.n_rep, h = kvh * a.n_rep + rg % a.n_rep;
