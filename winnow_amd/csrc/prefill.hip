@@ -598,8 +598,12 @@ constexpr int kKTile = 64 * kKRow;               // 17,408
 constexpr int kVTile = 128 * kVRow;              // 18,432
 constexpr int kTileSet = kKTile + kVTile + 256;  // + 64 K and 64 V norms
 
+// Dequantization tables of the shared-tile scan: the 4-bit pair table replicated once
+// per lane of a half-wave (entry i of copy r at word 32 i + r, 32 KB), so that a wave's
+// reads fall in distinct banks but for lanes l and l + 32; the 6-bit pair table plain
+// (4,096 entries, 16 KB).
 template <int BW>
-constexpr int plain_tf_bytes() { return 4 << (2 * BW); }
+constexpr int plain_tf_bytes() { return BW == 4 ? 256 * 32 * 4 : 4 << (2 * BW); }
 
 // Byte offset of 16-byte column quad q of K tile row r.
 __device__ __forceinline__ uint32_t ktile_off(int r, int q) { return uint32_t(r * kKRow + ((q ^ ((r & 16) >> 2)) << 4)); }
@@ -607,17 +611,23 @@ __device__ __forceinline__ uint32_t ktile_off(int r, int q) { return uint32_t(r 
 // Token of row c of score tile t (see above).
 __device__ __forceinline__ int tile_row(int t, int c) { return 32 * (t >> 1) + 8 * (c >> 2) + 4 * (t & 1) + (c & 3); }
 
-// Stages a plain pair table of fp16 pairs: entry i = (H(2^8 c[i mod 2^BW]), H(2^8 c[i >> BW])).
+// Stages a pair table of fp16 pairs: entry i = (H(2^8 c[i mod 2^BW]), H(2^8 c[i >> BW])).
 template <int BW>
 __device__ __forceinline__ void stage_plain_tf(const float* cb, char* dst, int tid, int nthr) {
   uint32_t* t = reinterpret_cast<uint32_t*>(dst);
-  for (int i = tid; i < (1 << (2 * BW)); i += nthr)
-    t[i] = tf_word(cb[i & ((1 << BW) - 1)] * kCbScale, cb[i >> BW] * kCbScale);
+  if constexpr (BW == 4) {
+    for (int i = tid; i < 256 * 32; i += nthr) t[i] = tf_word(cb[(i >> 5) & 15] * kCbScale, cb[i >> 9] * kCbScale);
+  } else {
+    for (int i = tid; i < (1 << (2 * BW)); i += nthr)
+      t[i] = tf_word(cb[i & ((1 << BW) - 1)] * kCbScale, cb[i >> BW] * kCbScale);
+  }
 }
 
+// Entry idx; lane_off = 4 (lane % 32), the lane's copy of a replicated 4-bit table.
 template <int BW>
-__device__ __forceinline__ uint32_t plain_entry(const char* tab, uint32_t idx) {
-  return *reinterpret_cast<const uint32_t*>(tab + (idx << 2));
+__device__ __forceinline__ uint32_t plain_entry(const char* tab, uint32_t idx, uint32_t lane_off) {
+  if constexpr (BW == 4) return *reinterpret_cast<const uint32_t*>(tab + ((idx << 7) | lane_off));
+  else return *reinterpret_cast<const uint32_t*>(tab + (idx << 2));
 }
 
 // The raw bytes one thread dequantizes per chunk, loaded a chunk ahead.
@@ -687,6 +697,7 @@ template <int BWK, int BWV, int WPB>
 __device__ __forceinline__ void pf_raw_store(const PfRaw<BWK, BWV, WPB>& r, const char* tabk, const char* tabv,
                                              char* set, int tid) {
   using R = PfRaw<BWK, BWV, WPB>;
+  const uint32_t lo = uint32_t(tid & 31) << 2;
 #pragma unroll
   for (int j = 0; j < R::NK; ++j) {
     const int it = tid + 64 * WPB * j, tok = it >> 4, dg = it & 15;
@@ -694,12 +705,12 @@ __device__ __forceinline__ void pf_raw_store(const PfRaw<BWK, BWV, WPB>& r, cons
     if constexpr (BWK == 4) {
       const uint32_t w = r.k[j][0];
 #pragma unroll
-      for (int p = 0; p < 4; ++p) e[p] = plain_entry<4>(tabk, (w >> (8 * p)) & 0xFFu);
+      for (int p = 0; p < 4; ++p) e[p] = plain_entry<4>(tabk, (w >> (8 * p)) & 0xFFu, lo);
     } else {
       const uint32_t sh = 16u * uint32_t(dg & 1);
       const uint64_t x = (uint64_t(r.k[j][1]) << 32 | r.k[j][0]) >> sh;
 #pragma unroll
-      for (int p = 0; p < 4; ++p) e[p] = plain_entry<6>(tabk, uint32_t(x >> (12 * p)) & 0xFFFu);
+      for (int p = 0; p < 4; ++p) e[p] = plain_entry<6>(tabk, uint32_t(x >> (12 * p)) & 0xFFFu, lo);
     }
     *reinterpret_cast<u32x4*>(set + ktile_off(tok, dg)) = e;
   }
@@ -723,7 +734,7 @@ __device__ __forceinline__ void pf_raw_store(const PfRaw<BWK, BWV, WPB>& r, cons
     }
 #pragma unroll
     for (int m = 0; m < 8; ++m)
-      *reinterpret_cast<uint32_t*>(vt + (8 * dg + m) * kVRow + 4 * tp) = plain_entry<BWV>(tabv, idx[m]);
+      *reinterpret_cast<uint32_t*>(vt + (8 * dg + m) * kVRow + 4 * tp) = plain_entry<BWV>(tabv, idx[m], lo);
   }
   if (tid < 64) *reinterpret_cast<uint32_t*>(set + kKTile + kVTile + 128 * (tid >> 5) + 4 * (tid & 31)) = r.n;
 }
@@ -784,26 +795,25 @@ __global__ __launch_bounds__(64 * WPB) void pf_tile_kernel(PrefillArgs a) {
   }
   const int lim_min = L - a.Q + min(r_first, rows - 1) / a.n_rep;
 
-  // B operands of the scores (as in pf_scan_kernel); a wave past the last block keeps zeros
+  // B operands of the scores (as in pf_scan_kernel); a wave past the last block keeps
+  // zeros. The rows are read twice (the maximum, then the conversion) rather than held
+  // as floats meanwhile.
   h8 qb[NCT][4];
   float sc = 1.f;
   {
-    float qv[NCT][32];
-    float amax = 0.f;
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
+    auto qrow = [&](int ct) {
       const int64_t row = (int64_t(b) * a.Hkv + kvh) * a.nrp + min(r_first + 16 * ct + c, a.nrp - 1);
-      const float4* qp = reinterpret_cast<const float4*>(a.q_rot + row * 128 + 32 * g);
+      return reinterpret_cast<const float4*>(a.q_rot + row * 128 + 32 * g);
+    };
+    float amax = 0.f;
+    if (wave_live) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float4 x = wave_live ? qp[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-        qv[ct][4 * k] = x.x;
-        qv[ct][4 * k + 1] = x.y;
-        qv[ct][4 * k + 2] = x.z;
-        qv[ct][4 * k + 3] = x.w;
-      }
+      for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
-      for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(qv[ct][k]));
+        for (int k = 0; k < 8; ++k) {
+          const float4 x = qrow(ct)[k];
+          amax = fmaxf(amax, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+        }
     }
     int qe;
     frexpf(wave_max(amax), &qe);
@@ -812,9 +822,13 @@ __global__ __launch_bounds__(64 * WPB) void pf_tile_kernel(PrefillArgs a) {
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
+      for (int k = 0; k < 4; ++k) {
+        const float4 x0 = wave_live ? qrow(ct)[2 * k] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 x1 = wave_live ? qrow(ct)[2 * k + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qb[ct][k][j] = _Float16(ldexpf(qv[ct][8 * k + j], e));
+        for (int j = 0; j < 8; ++j) qb[ct][k][j] = _Float16(ldexpf(v[j], e));
+      }
   }
 
   if (n > 0) {
