@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void rotate_q_kernel(RotArgs a) {
     return;
   }
   const float4* src = reinterpret_cast<const float4*>(a.pi_k + z * JQ * D);
-  for (int i = tid; i < JQ * D / 4; i += 256) {
+  for_strided<JQ * D / 4, 256>(tid, [&](int i) {
     const float4 v = src[i];
     const int r = (4 * i) / D, c = (4 * i) % D;
     float* dst = pis + r * LDP + c;
@@ -97,11 +97,11 @@ __global__ __launch_bounds__(256) void rotate_q_kernel(RotArgs a) {
     dst[1] = v.y;
     dst[2] = v.z;
     dst[3] = v.w;
-  }
-  for (int i = tid; i < NREP * D; i += 256) {
+  });
+  for_strided<NREP * D, 256>(tid, [&](int i) {
     const int h = i / D, d = i % D;
     qs[h][d] = h < a.n_rep ? load_elem(a.q, b * a.qsb + int64_t(kvh * a.n_rep + h) * a.qsh + d, a.q_dtype) : 0.f;
-  }
+  });
   __syncthreads();
   float* out = a.q_rot + (int64_t(b) * a.Hkv + kvh) * NREP * D + z * JQ;
   for (int i = tid; i < NREP * JQ; i += 256) {

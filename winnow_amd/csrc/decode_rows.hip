@@ -102,20 +102,20 @@ struct Tab<4> {
 // (c[b & 15], c[b >> 4])), the pair table of pair_coded widths (entry i holds
 // (c[i mod 2^BW], c[i >> BW]): two consecutive codes, LSB first, read as one
 // 2*BW-bit index), else the plain table.
-template <int BW>
-__device__ __forceinline__ void stage_table(const float* cb, char* dst, int tid, int nthr) {
+template <int BW, int NTHR>
+__device__ __forceinline__ void stage_table(const float* cb, char* dst, int tid) {
   if constexpr (BW == 4) {
     float2* t = reinterpret_cast<float2*>(dst);
-    for (int i = tid; i < 256 * 32; i += nthr) {
+    for_strided<256 * 32, NTHR>(tid, [&](int i) {
       const int b = i >> 5;
       t[i] = make_float2(cb[b & 15], cb[b >> 4]);
-    }
+    });
   } else if constexpr (pair_coded<BW>()) {
     float2* t = reinterpret_cast<float2*>(dst);
-    for (int i = tid; i < (1 << (2 * BW)); i += nthr) t[i] = make_float2(cb[i & ((1 << BW) - 1)], cb[i >> BW]);
+    for_strided<(1 << (2 * BW)), NTHR>(tid, [&](int i) { t[i] = make_float2(cb[i & ((1 << BW) - 1)], cb[i >> BW]); });
   } else {
     float* t = reinterpret_cast<float*>(dst);
-    for (int i = tid; i < (1 << BW); i += nthr) t[i] = cb[i];
+    for_strided<(1 << BW), NTHR>(tid, [&](int i) { t[i] = cb[i]; });
   }
 }
 
@@ -764,8 +764,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_table<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
-  stage_table<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
+  stage_table<BWK, 64 * WPB>(a.cb_k, lds + Lay::k_off, tid);
+  stage_table<BWV, 64 * WPB>(a.cb_v, lds + Lay::v_off, tid);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   // Work-groups are dealt to the eight XCDs round robin (group p on XCD p % 8); the
   // logical group index gives each XCD a contiguous stretch of the flattened work,
@@ -882,17 +882,17 @@ __device__ __forceinline__ uint2 split_pair(float lo, float hi) {
 
 // The pair tables of stage_table with 16-bit split entries (4-bit: replicated and
 // byte-indexed; 2, 3, 5, 6 bits: 2^(2 BW) entries).
-template <int BW>
-__device__ __forceinline__ void stage_table16(const float* cb, char* dst, int tid, int nthr) {
+template <int BW, int NTHR>
+__device__ __forceinline__ void stage_table16(const float* cb, char* dst, int tid) {
   static_assert(BW == 4 || pair_coded<BW>(), "16-bit tables are pair tables");
   uint2* t = reinterpret_cast<uint2*>(dst);
   if constexpr (BW == 4) {
-    for (int i = tid; i < 256 * 32; i += nthr) {
+    for_strided<256 * 32, NTHR>(tid, [&](int i) {
       const int b = i >> 5;
       t[i] = split_pair(cb[b & 15], cb[b >> 4]);
-    }
+    });
   } else {
-    for (int i = tid; i < (1 << (2 * BW)); i += nthr) t[i] = split_pair(cb[i & ((1 << BW) - 1)], cb[i >> BW]);
+    for_strided<(1 << (2 * BW)), NTHR>(tid, [&](int i) { t[i] = split_pair(cb[i & ((1 << BW) - 1)], cb[i >> BW]); });
   }
 }
 
@@ -1619,8 +1619,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows16_kernel(DecodeArgs a) {
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_table16<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
-  stage_table16<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
+  stage_table16<BWK, 64 * WPB>(a.cb_k, lds + Lay::k_off, tid);
+  stage_table16<BWV, 64 * WPB>(a.cb_v, lds + Lay::v_off, tid);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);
@@ -1639,8 +1639,8 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_tf_kernel(DecodeArgs a) 
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_table_tf<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
-  stage_table_tf<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
+  stage_table_tf<BWK, 64 * WPB>(a.cb_k, lds + Lay::k_off, tid);
+  stage_table_tf<BWV, 64 * WPB>(a.cb_v, lds + Lay::v_off, tid);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);

@@ -259,7 +259,7 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
   __shared__ DqTab<BW> tab;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Pi^T planes: pit[h][pit_row(n) * kPiRow + k] = split(Pi[k][n])
-  for (int i = tid; i < D * D / 2; i += kDqWaves * 64) {
+  for_strided<D * D / 2, kDqWaves * 64>(tid, [&](int i) {
     const int k = i / (D / 2), n2 = 2 * (i % (D / 2));  // two columns of row k
     const float2 x = *reinterpret_cast<const float2*>(a.pi + k * D + n2);
     const int m = pit_row(n2);  // n2 even: dims n2, n2 + 1 sit in rows m, m + 1
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
       pit[PLANES - 1][m * kPiRow + k] = uint16_t(l & 0xffffu);
       pit[PLANES - 1][(m + 1) * kPiRow + k] = uint16_t(l >> 16);
     }
-  }
+  });
   stage_dq_tab<BW, FAST>(a.cb, tab, tid);
   __syncthreads();
 

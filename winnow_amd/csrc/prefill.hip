@@ -458,8 +458,8 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_table_tf<BWK>(a.cb_k, lds + Lay::k_off, tid, 64 * WPB);
-  stage_table_tf<BWV>(a.cb_v, lds + Lay::v_off, tid, 64 * WPB);
+  stage_table_tf<BWK, 64 * WPB>(a.cb_k, lds + Lay::k_off, tid);
+  stage_table_tf<BWV, 64 * WPB>(a.cb_v, lds + Lay::v_off, tid);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   const int64_t w = int64_t(pf_xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   const int64_t items = int64_t(a.B) * a.Hkv * a.nsplit * a.ncb;
@@ -612,14 +612,14 @@ __device__ __forceinline__ uint32_t ktile_off(int r, int q) { return uint32_t(r 
 __device__ __forceinline__ int tile_row(int t, int c) { return 32 * (t >> 1) + 8 * (c >> 2) + 4 * (t & 1) + (c & 3); }
 
 // Stages a pair table of fp16 pairs: entry i = (H(2^8 c[i mod 2^BW]), H(2^8 c[i >> BW])).
-template <int BW>
-__device__ __forceinline__ void stage_plain_tf(const float* cb, char* dst, int tid, int nthr) {
+template <int BW, int NTHR>
+__device__ __forceinline__ void stage_plain_tf(const float* cb, char* dst, int tid) {
   uint32_t* t = reinterpret_cast<uint32_t*>(dst);
   if constexpr (BW == 4) {
-    for (int i = tid; i < 256 * 32; i += nthr) t[i] = tf_word(cb[(i >> 5) & 15] * kCbScale, cb[i >> 9] * kCbScale);
+    for_strided<256 * 32, NTHR>(tid, [&](int i) { t[i] = tf_word(cb[(i >> 5) & 15] * kCbScale, cb[i >> 9] * kCbScale); });
   } else {
-    for (int i = tid; i < (1 << (2 * BW)); i += nthr)
-      t[i] = tf_word(cb[i & ((1 << BW) - 1)] * kCbScale, cb[i >> BW] * kCbScale);
+    for_strided<(1 << (2 * BW)), NTHR>(
+        tid, [&](int i) { t[i] = tf_word(cb[i & ((1 << BW) - 1)] * kCbScale, cb[i >> BW] * kCbScale); });
   }
 }
 
@@ -755,8 +755,8 @@ __global__ __launch_bounds__(64 * WPB) void pf_tile_kernel(PrefillArgs a) {
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_plain_tf<BWK>(a.cb_k, lds + Lay::tabk, tid, 64 * WPB);
-  stage_plain_tf<BWV>(a.cb_v, lds + Lay::tabv, tid, 64 * WPB);
+  stage_plain_tf<BWK, 64 * WPB>(a.cb_k, lds + Lay::tabk, tid);
+  stage_plain_tf<BWV, 64 * WPB>(a.cb_v, lds + Lay::tabv, tid);
   // work-group unit: (sequence, kv head, split, column group of WPB blocks)
   const int ncg = (a.ncb + WPB - 1) / WPB;
   const int64_t unit = pf_xcd_major(blockIdx.x, gridDim.x);
@@ -982,12 +982,12 @@ __global__ __launch_bounds__(256) void pf_rotate_kernel(PfRotArgs a) {
   __shared__ __align__(16) float mt[128 * kRotStride];
   __shared__ __align__(16) float x[kRotRows * kRotStride];
   const int tid = threadIdx.x, kvh = blockIdx.y, b = blockIdx.z, r0 = blockIdx.x * kRotRows;
-  for (int i = tid; i < 128 * 32; i += 256) {
+  for_strided<128 * 32, 256>(tid, [&](int i) {
     const int j = i >> 5, k4 = 4 * (i & 31);
     *reinterpret_cast<float4*>(mt + j * kRotStride + k4) = reinterpret_cast<const float4*>(a.pi)[i];
-  }
+  });
   const int rows = a.n_rep * a.Q;
-  for (int i = tid; i < kRotRows * 128; i += 256) {
+  for_strided<kRotRows * 128, 256>(tid, [&](int i) {
     const int rr = i >> 7, k = i & 127, r = r0 + rr;
     float v = 0.f;
     if (r < rows) {
@@ -995,7 +995,7 @@ __global__ __launch_bounds__(256) void pf_rotate_kernel(PfRotArgs a) {
       v = load_elem(a.q, b * a.qsb + h * a.qsh + qi * a.qsq + k, a.q_dtype);
     }
     x[rr * kRotStride + k] = v;
-  }
+  });
   __syncthreads();
   float y[RT][8];
   rows_times_t(x, mt, tid, y);
@@ -1056,8 +1056,8 @@ __global__ __launch_bounds__(256) void pf_merge_kernel(PfMergeArgs a) {
   __shared__ __align__(16) float pv[128 * 128];
   __shared__ __align__(16) float xt[128 * kRotRows];
   const int tid = threadIdx.x, kvh = blockIdx.y, b = blockIdx.z, r0 = blockIdx.x * kRotRows;
-  for (int i = tid; i < 128 * 128 / 4; i += 256)
-    reinterpret_cast<float4*>(pv)[i] = reinterpret_cast<const float4*>(a.pi_v)[i];
+  for_strided<128 * 128 / 4, 256>(
+      tid, [&](int i) { reinterpret_cast<float4*>(pv)[i] = reinterpret_cast<const float4*>(a.pi_v)[i]; });
   {
     // thread: row rr = tid / TPR, dims DPT (tid % TPR) .. (TPR threads per row)
     constexpr int TPR = 256 / kRotRows, DPT = 128 / TPR;

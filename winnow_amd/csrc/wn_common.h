@@ -77,6 +77,19 @@ __device__ __forceinline__ uint32_t code_at(const uint32_t (&w)[NW], int d) {
   return v & ((1u << BW) - 1u);
 }
 
+// f(i) for i = tid + NTHR k in [0, N), for the staging loops of a work-group's
+// prologue: the trip count is known at compile time, so the loop unrolls and every
+// iteration's loads are issued before the first wait (a loop on i < N waits for each
+// iteration's loads in turn, a chain of cache round trips before the work starts).
+template <int N, int NTHR, class F>
+__device__ __forceinline__ void for_strided(int tid, F&& f) {
+#pragma unroll
+  for (int k = 0; k < (N + NTHR - 1) / NTHR; ++k) {
+    const int i = tid + NTHR * k;
+    if (N % NTHR == 0 || i < N) f(i);
+  }
+}
+
 // Wave-wide (64 lanes) reductions.
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -90,17 +90,17 @@ __device__ __forceinline__ uint32_t tf_word(float lo, float hi) {
 // Stages a TF table: 4-bit, the replicated byte table (entry (b, r) holds
 // (H(2^8 c[b & 15]), H(2^8 c[b >> 4]))); 6-bit, entry i holds (H(2^8 c[i mod 64]),
 // H(2^8 c[i >> 6])), two consecutive codes read as one 12-bit index.
-template <int BW>
-__device__ __forceinline__ void stage_table_tf(const float* cb, char* dst, int tid, int nthr) {
+template <int BW, int NTHR>
+__device__ __forceinline__ void stage_table_tf(const float* cb, char* dst, int tid) {
   static_assert(BW == 4 || BW == 6, "TF tables: 4 and 6-bit codes");
   uint32_t* t = reinterpret_cast<uint32_t*>(dst);
   if constexpr (BW == 4) {
-    for (int i = tid; i < 256 * 64; i += nthr) {
+    for_strided<256 * 64, NTHR>(tid, [&](int i) {
       const int b = i >> 6;
       t[i] = tf_word(cb[b & 15] * kCbScale, cb[b >> 4] * kCbScale);
-    }
+    });
   } else {
-    for (int i = tid; i < (1 << (2 * BW)); i += nthr) t[i] = tf_word(cb[i & 63] * kCbScale, cb[i >> 6] * kCbScale);
+    for_strided<(1 << (2 * BW)), NTHR>(tid, [&](int i) { t[i] = tf_word(cb[i & 63] * kCbScale, cb[i >> 6] * kCbScale); });
   }
 }
 
