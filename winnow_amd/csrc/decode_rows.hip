@@ -622,8 +622,8 @@ __device__ __forceinline__ int xcd_major(int p, int n) {
   return x * q + min(x, r) + s;
 }
 
-// The work list of wave w, one scan(b, kvh, t_lo, t_hi, prow) call per (sequence,
-// kv head, token range) it owns.
+// The work list of wave w, one scan(b, kvh, t_lo, t_hi, prow, left) call per
+// (sequence, kv head, token range) it owns; left = the wave's chunks after the range.
 // Fixed splits: wave w is unit (split, kv head, sequence) of the flattened
 // num_splits x Hkv x B space and scans pages [split * pages_per_split, ...) of its
 // sequence.
@@ -749,7 +749,7 @@ __device__ __forceinline__ void for_each_range(const DecodeArgs& a, int64_t w, i
       }
       s += c_hi - c_lo;
     }
-    scan(b, kvh, t_lo, t_hi, prow);
+    scan(b, kvh, t_lo, t_hi, prow, uint32_t(a.balanced ? e - s : 0));
     if (!a.balanced || s >= e) break;
     if (grouped) ++b;  // the group's range continues in the next sequence
     else if (kvh + 1 == a.Hkv && c_hi == nb) ++b;
@@ -775,7 +775,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_kernel(DecodeArgs a) {
   float* ptile = reinterpret_cast<float*>(lds + Lay::tiles + wig * Lay::tile_bytes);
   Tab<BWK> cbk = make_tab<BWK>(lds, Lay::k_off, lane);
   Tab<BWV> cbv = make_tab<BWV>(lds, Lay::v_off, lane);
-  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow) {
+  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow, uint32_t) {
     scan_range<BWK, BWV, NG>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
   });
 }
@@ -1270,7 +1270,8 @@ struct TfLds {
                                    ? k_off + tf_table_bytes<BWK>()
                                    : v_off + tf_table_bytes<BWV>();
   static constexpr int tile_bytes = (tf_ptile_offset<NG>() + 4 * NG * 64 / 2) * 4;
-  static constexpr int total = tiles + WPB * tile_bytes;
+  static constexpr int pace = tiles + WPB * tile_bytes;  // one word per wave (Pace)
+  static constexpr int total = pace + 4 * WPB;
   static_assert(tile_bytes % 16 == 0, "tiles stay 16-byte aligned");
   static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
 };
@@ -1489,11 +1490,48 @@ __device__ __forceinline__ void write_partial_mx(const DecodeArgs& a, MxState<NG
   }
 }
 
+// Pacing of the two waves that share a SIMD. A work-group's eight waves are dealt to
+// the CU's four SIMDs in turn, so waves k and k ^ 4 share one, and its issue arbiter
+// favours the older wave of the two: with equal shares of chunks, wave k ran ahead
+// and wave k ^ 4 scanned the last fifth of its chunks alone, latency-bound (per-wave
+// timestamps at config 2: waves 0-3 of every work-group ended at ~106 us, waves 4-7
+// at ~129 us). Each wave publishes the chunks it has left in an LDS word once per
+// chunk and raises its priority while it has more left than its partner. No chunk
+// moves between waves, so the results are those of the unpaced scan.
+// The words are read and written with relaxed work-group-scope atomics: a stale
+// value only delays the priority change by a chunk.
+struct Pace {
+  uint32_t* mine;     // this wave's word
+  uint32_t* partner;  // the word of the other wave on its SIMD
+  __device__ void publish(uint32_t left, int lane) const {
+    if (lane == 0) __hip_atomic_store(mine, left, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __device__ uint32_t partner_left() const {
+    return __hip_atomic_load(partner, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+};
+
+template <int WPB>
+__device__ __forceinline__ Pace make_pace(uint32_t* words, int wig, int lane) {
+  static_assert(WPB == 8, "pacing pairs waves k and k ^ 4: two waves per SIMD");
+  const Pace p{words + wig, words + (wig ^ 4)};
+  p.publish(0, lane);  // before the work-group barrier
+  return p;
+}
+
+// Priority for the next chunk: raised while this wave has more chunks left than its
+// partner (a partner without work, or done, shows 0).
+__device__ __forceinline__ void pace_step(uint32_t left, uint32_t partner_left) {
+  if (__builtin_amdgcn_readfirstlane(partner_left) < left) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // scan_range on the 16x16x32 fp16 MFMA; TF: the TF32-class products (4 or 6-bit
-// codes, TabTf tables).
+// codes, TabTf tables). left_after: the wave's chunks after this range (pacing).
 template <int BWK, int BWV, int NG, bool TF, class TabK, class TabV>
 __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh, int t_lo, int t_hi, int64_t prow,
-                                             int lane, TabK& cbk, TabV& cbv, uint32_t* ptile) {
+                                             int lane, TabK& cbk, TabV& cbv, uint32_t* ptile, const Pace& pace,
+                                             uint32_t left_after) {
   static_assert(!TF || ((BWK == 4 || BWK == 6) && (BWV == 4 || BWV == 6)), "TF32-class scan: 4 or 6-bit K and V");
   constexpr int D = 128, NH = 4 * NG;
   const int page_hi = (t_hi + (1 << a.log2S) - 1) >> a.log2S;
@@ -1566,6 +1604,9 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
     const int c0 = t_lo + 64 * ch;
     const int pid_after = pid_of(ch + 2);
     const bool more = ch + 1 < n;
+    const uint32_t left = uint32_t(n - ch) + left_after;
+    pace.publish(left, lane);
+    const uint32_t partner_left = pace.partner_left();
     // addresses of the next chunk's four 16-token blocks, for its K and its V rows
     uint64_t kb[4], vb[4];
     block_bases<16 * BWK>(kbase, uint32_t(a.ksp), pid_next, c0 + 64, lane, smask, kb);
@@ -1582,6 +1623,7 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
     if constexpr (TF) value_phase_tf<BWK, BWV, NG>(Y, cbv, ptile, lane, st.acc);
     else value_phase_mx<BWK, BWV, NG>(Y, cbv, ptile, lane, st.acc);
     pid_next = pid_after;
+    pace_step(left, partner_left);
   };
 
   Buf b0, b1, b2;
@@ -1609,7 +1651,8 @@ struct Rows16Lds {
   static constexpr int v_off = RowsLds<BWK, BWV, NG, WPB>::v_off;
   static constexpr int tiles = RowsLds<BWK, BWV, NG, WPB>::tiles;
   static constexpr int tile_bytes = (kTileHalves<NG> ? 2 : 1) * 4 * NG * kTileStride * 4;
-  static constexpr int total = tiles + WPB * tile_bytes;
+  static constexpr int pace = tiles + WPB * tile_bytes;  // one word per wave (Pace)
+  static constexpr int total = pace + 4 * WPB;
   static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
 };
 
@@ -1621,14 +1664,16 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows16_kernel(DecodeArgs a) {
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
   stage_table16<BWK, 64 * WPB>(a.cb_k, lds + Lay::k_off, tid);
   stage_table16<BWV, 64 * WPB>(a.cb_v, lds + Lay::v_off, tid);
+  const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig, lane);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);
   Tab<BWK> cbk = make_tab<BWK>(lds, Lay::k_off, lane);
   Tab<BWV> cbv = make_tab<BWV>(lds, Lay::v_off, lane);
-  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow) {
-    scan_range16<BWK, BWV, NG, false>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow, uint32_t left) {
+    scan_range16<BWK, BWV, NG, false>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile, pace, left);
   });
+  pace.publish(0, lane);
 }
 
 // The TF32-class row scan (allow_tf32): 4 or 6-bit K and V, one or two head groups,
@@ -1641,14 +1686,16 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_tf_kernel(DecodeArgs a) 
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
   stage_table_tf<BWK, 64 * WPB>(a.cb_k, lds + Lay::k_off, tid);
   stage_table_tf<BWV, 64 * WPB>(a.cb_v, lds + Lay::v_off, tid);
+  const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig, lane);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);
   TabTf<BWK> cbk = make_tab_tf<BWK>(lds, Lay::k_off, lane);
   TabTf<BWV> cbv = make_tab_tf<BWV>(lds, Lay::v_off, lane);
-  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow) {
-    scan_range16<BWK, BWV, NG, true>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile);
+  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow, uint32_t left) {
+    scan_range16<BWK, BWV, NG, true>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile, pace, left);
   });
+  pace.publish(0, lane);
 }
 
 // Waves per work-group: three per SIMD where the scan fits in 168 VGPRs, else two.
