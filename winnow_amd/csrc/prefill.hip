@@ -446,9 +446,10 @@ struct PfLds {
   static constexpr bool k4 = BWK == 4, v4 = BWV == 4;
   static constexpr int k_off = k4 && !v4 ? kTfTableBytes : 0;
   static constexpr int v_off = v4 ? kTfTableBytes : k4 ? 0 : tf_table_bytes<BWK>();
-  static constexpr int total = k_off + tf_table_bytes<BWK>() > v_off + tf_table_bytes<BWV>()
-                                   ? k_off + tf_table_bytes<BWK>()
-                                   : v_off + tf_table_bytes<BWV>();
+  static constexpr int pace = k_off + tf_table_bytes<BWK>() > v_off + tf_table_bytes<BWV>()
+                                  ? k_off + tf_table_bytes<BWK>()
+                                  : v_off + tf_table_bytes<BWV>();  // one word per wave (Pace)
+  static constexpr int total = pace + 4 * 8;
   static_assert(total <= 160 * 1024, "LDS of a work-group exceeds 160 KB");
 };
 
@@ -460,6 +461,7 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
   stage_table_tf<BWK, 64 * WPB>(a.cb_k, lds + Lay::k_off, tid);
   stage_table_tf<BWV, 64 * WPB>(a.cb_v, lds + Lay::v_off, tid);
+  const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig, lane);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   const int64_t w = int64_t(pf_xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   const int64_t items = int64_t(a.B) * a.Hkv * a.nsplit * a.ncb;
@@ -552,6 +554,9 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
     const int n = ch_hi - ch_lo;
     for (int ch = 0; ch < n; ++ch) {
       const int c0 = t_lo + 64 * ch;
+      const uint32_t left = uint32_t(n - ch);
+      pace.publish(left, lane);
+      const uint32_t partner_left = pace.partner_left();
       // the next chunk's tiles (the last chunk's again on the last step: its loads are
       // issued on every step, so each step's waits count the same loads)
       const PfTiles nx = pf_tiles(a, trow, min(c0 + 64, t_lo + 64 * (n - 1)), col_hi);
@@ -565,7 +570,9 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
       pf_merge_pairs<BWV>(V, lane);
       pf_values<BWV, NCT>(V, cbv, pb, st);
       pf_load_v<BWV>(a, nx, kvh, lane, V);
+      pace_step(left, partner_left);
     }
+    pace.publish(0, lane);
   }
   pf_write<NCT>(a, st, row0, lane);
 }
