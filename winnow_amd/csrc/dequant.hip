@@ -42,7 +42,10 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kDqD = 128;
-constexpr int kDqWaves = 4;
+// Waves per work-group: the accurate mode runs one work-group of eight per CU (two
+// waves per SIMD, paced: Pace); the fast mode, at four waves per SIMD, four.
+template <bool FAST>
+constexpr int dq_waves() { return FAST ? 4 : 8; }
 constexpr int kDqTU = 2;  // output tiles per MFMA group
 constexpr int kPiRow = 136;  // bf16 per row of a Pi^T plane: 128 + 8 pad (272 B rows)
 
@@ -176,10 +179,10 @@ __device__ __forceinline__ void stage_dq_tab(const float* cb, DqTab<BW>& t, int 
     }
   };
   if constexpr (BW == 4) {
-    for (int b = tid; b < 256; b += kDqWaves * 64) put(b, cb[b & 15], cb[b >> 4]);
+    for (int b = tid; b < 256; b += dq_waves<FAST>() * 64) put(b, cb[b & 15], cb[b >> 4]);
   } else {
     constexpr int L = 1 << BW;
-    for (int i = tid; i < (L + 1) / 2; i += kDqWaves * 64) put(i, cb[2 * i], 2 * i + 1 < L ? cb[2 * i + 1] : 0.f);
+    for (int i = tid; i < (L + 1) / 2; i += dq_waves<FAST>() * 64) put(i, cb[2 * i], 2 * i + 1 < L ? cb[2 * i + 1] : 0.f);
   }
 }
 
@@ -249,7 +252,9 @@ __device__ __forceinline__ int pit_row(int d) {
 }
 
 template <int BW, bool FAST, int OUT, bool PAGED>
-__global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void tq_dequant_kernel(DqArgs a) {
+__global__ __launch_bounds__(dq_waves<FAST>() * 64) __attribute__((amdgpu_waves_per_eu(2))) void tq_dequant_kernel(
+    DqArgs a) {
+  constexpr int kDqWaves = dq_waves<FAST>();
   constexpr int D = kDqD, NB = D * BW / 8, PLANES = FAST ? 1 : 2;
   // 16-row tiles per pass: each Pi^T operand read from LDS feeds RT MFMAs; four in the
   // accurate mode (half the LDS reads per row), two in the fast mode, whose registers
@@ -257,6 +262,7 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
   constexpr int RT = FAST ? 2 : 3, kRows = 16 * RT;
   __shared__ __align__(16) uint16_t pit[PLANES][D * kPiRow];  // Pi^T: bf16 hi and lo, or fp16
   __shared__ DqTab<BW> tab;
+  __shared__ uint32_t pace_words[8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Pi^T planes: pit[h][pit_row(n) * kPiRow + k] = split(Pi[k][n])
   for_strided<D * D / 2, kDqWaves * 64>(tid, [&](int i) {
@@ -277,6 +283,9 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     }
   });
   stage_dq_tab<BW, FAST>(a.cb, tab, tid);
+  // the accurate mode paces the two waves of a SIMD (Pace); the fast mode's four
+  // waves per SIMD come from two work-groups and are not paced
+  const Pace pace = make_pace<8>(pace_words, __builtin_amdgcn_readfirstlane(wave) & 7, lane);
   __syncthreads();
 
   const int g = lane >> 4, c16 = lane & 15;
@@ -373,17 +382,26 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
         store8<OUT>(a.out, row * D + 32 * c + 8 * g, acc[rt][2 * c] * nv, acc[rt][2 * c + 1] * nv);
     }
   };
+  // the wave's passes still to do, this one included (pacing of the two waves of a SIMD)
+  int64_t pass = int64_t(blockIdx.x) * kDqWaves + wave;
+  uint32_t left = pass < passes ? uint32_t((passes - pass + stride - 1) / stride) : 0u;
   // One pass: page ids two passes ahead, codes of the next pass, then this pass.
   auto half = [&](int64_t pass, const uint32_t (&cur)[RT][BW], const uint32_t (&ncur)[RT], uint32_t (&nxt)[RT][BW],
                   uint32_t (&nnxt)[RT], const int32_t (&pg_nxt)[RT], int32_t (&pg_after)[RT]) {
+    uint32_t partner_left = 0;
+    if constexpr (!FAST) {
+      pace.publish(left, lane);
+      partner_left = pace.partner_left();
+    }
     page_ids(pass + 2 * stride, pg_after);
     load_pass(pass + stride, pg_nxt, nxt, nnxt);
     f32x4 acc[RT][8];
     compute_pass(cur, acc);
     store_pass(pass, ncur, acc);
+    if constexpr (!FAST) pace_step(left, partner_left);
+    --left;
   };
 
-  int64_t pass = int64_t(blockIdx.x) * kDqWaves + wave;
   if (pass >= passes) return;
   uint32_t b0[RT][BW], b1[RT][BW];
   uint32_t n0[RT], n1[RT];  // fp16 bits, one register each (a packed pair would wait for both loads)
@@ -401,6 +419,7 @@ __global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     half(pass, b0, n0, b1, n1, pb, pa);
     pass += stride;
   }
+  if constexpr (!FAST) pace.publish(0, lane);
 }
 
 using DqFn = void (*)(DqArgs);
@@ -448,13 +467,14 @@ int launch_dq(DqArgs& a, int bw, int fast, int out_dtype, hipStream_t st, const 
   (void)hipGetDevice(&dev);
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (cus <= 0) cus = 256;
+  const int waves = fast ? dq_waves<true>() : dq_waves<false>();
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDqWaves * 64, 0) != hipSuccess || per_cu < 1)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, waves * 64, 0) != hipSuccess || per_cu < 1)
     per_cu = 1;
   const int64_t rows = fast ? 32 : 48;  // rows per pass (16 * RT of the kernel)
-  const int64_t want = (a.N + rows * kDqWaves - 1) / (rows * kDqWaves);
+  const int64_t want = (a.N + rows * waves - 1) / (rows * waves);
   const int64_t grid = want < int64_t(per_cu) * cus ? want : int64_t(per_cu) * cus;
-  hipLaunchKernelGGL(fn, dim3(unsigned(grid)), dim3(kDqWaves * 64), 0, st, a);
+  hipLaunchKernelGGL(fn, dim3(unsigned(grid)), dim3(waves * 64), 0, st, a);
   return check_launch(what);
 }
 

@@ -149,42 +149,5 @@ __device__ __forceinline__ uint32_t piece_pair_tf(const uint32_t* w, TabTf<BW>& 
   else return pair_entry_tf(tab, pair_offset<BW, 2 * BW * N, 2>(w));
 }
 
-// Pacing of the two waves that share a SIMD. A work-group's eight waves are dealt to
-// the CU's four SIMDs in turn, so waves k and k ^ 4 share one, and its issue arbiter
-// favours the older wave of the two: with equal shares of chunks, wave k ran ahead
-// and wave k ^ 4 scanned the last fifth of its chunks alone, latency-bound (per-wave
-// timestamps of the decode row scan at BASELINE config 2: waves 0-3 of every
-// work-group ended at ~106 us, waves 4-7 at ~129 us). Each wave publishes the chunks
-// it has left in an LDS word once per chunk and raises its priority while it has
-// more left than its partner. No chunk moves between waves, so the results are those
-// of an unpaced scan.
-// The words are read and written with relaxed work-group-scope atomics: a stale
-// value only delays the priority change by a chunk.
-struct Pace {
-  uint32_t* mine;     // this wave's word
-  uint32_t* partner;  // the word of the other wave on its SIMD
-  __device__ void publish(uint32_t left, int lane) const {
-    if (lane == 0) __hip_atomic_store(mine, left, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  __device__ uint32_t partner_left() const {
-    return __hip_atomic_load(partner, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-};
-
-template <int WPB>
-__device__ __forceinline__ Pace make_pace(uint32_t* words, int wig, int lane) {
-  static_assert(WPB == 8, "pacing pairs waves k and k ^ 4: two waves per SIMD");
-  const Pace p{words + wig, words + (wig ^ 4)};
-  p.publish(0, lane);  // before the work-group barrier
-  return p;
-}
-
-// Priority for the next chunk: raised while this wave has more chunks left than its
-// partner (a partner without work, or done, shows 0).
-__device__ __forceinline__ void pace_step(uint32_t left, uint32_t partner_left) {
-  if (__builtin_amdgcn_readfirstlane(partner_left) < left) __builtin_amdgcn_s_setprio(1);
-  else __builtin_amdgcn_s_setprio(0);
-}
-
 }  // namespace
 }  // namespace wn
