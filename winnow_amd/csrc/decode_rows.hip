@@ -1501,6 +1501,13 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
   const int page_hi = (t_hi + (1 << a.log2S) - 1) >> a.log2S;
   const int n = (t_hi - t_lo + 63) >> 6;
   const int c = lane & 15, g = lane >> 4;
+  const int32_t* trow = a.table + b * a.tsb;
+  auto pid_of = [&](int ch) {
+    const int col = min((t_lo + 64 * ch + lane) >> a.log2S, page_hi - 1);
+    return trow[col];
+  };
+  // the first two chunks' page ids are loaded together with the query below
+  const int pid0 = pid_of(0), pid1 = pid_of(1);
 
   // B operands of the scores: column c, K-step s, k-slots of group g = dims
   // 32g + 4s + (0..3), each twice; H (c < NH) or L (c >= NH) of q' = q 2^e, zero
@@ -1540,11 +1547,6 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
                    split_word(ldexpf(qv[4 * s + 2], e)), split_word(ldexpf(qv[4 * s + 3], e)), qsel);
   }
 
-  const int32_t* trow = a.table + b * a.tsb;
-  auto pid_of = [&](int ch) {
-    const int col = min((t_lo + 64 * ch + lane) >> a.log2S, page_hi - 1);
-    return trow[col];
-  };
   MxState<NG> st;
 #pragma unroll
   for (int mm = 0; mm < 8; ++mm) st.acc[mm] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1591,9 +1593,9 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
   };
 
   Buf b0, b1, b2;
-  load_k16(a, kvh, lane, t_lo, pid_of(0), b0);
-  load_v<BWK, BWV, kRawV<BWV>>(a, kvh, lane, t_lo, pid_of(0), b1);
-  pid_next = pid_of(1);
+  load_k16(a, kvh, lane, t_lo, pid0, b0);
+  load_v<BWK, BWV, kRawV<BWV>>(a, kvh, lane, t_lo, pid0, b1);
+  pid_next = pid1;
   wait_vmem_all();
   // whole turns of the three buffers in a loop without early exits (a loop header
   // reached from an exit path gets its wait counts from that path), then the rest
