@@ -456,6 +456,10 @@ struct PfLds {
 template <int BWK, int BWV, int NCT, int WPB>
 __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
   using Lay = PfLds<BWK, BWV>;
+  // the two waves of a SIMD are paced (Pace) with 4-bit V; with 6-bit V the pacing's
+  // registers made the compiler spill in the chunk loop (at Q 16: 6/6 365 -> 522 us,
+  // 4/6 561 -> 795 us), so those scans run unpaced
+  constexpr bool kPace = BWV == 4;
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -555,8 +559,11 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
     for (int ch = 0; ch < n; ++ch) {
       const int c0 = t_lo + 64 * ch;
       const uint32_t left = uint32_t(n - ch);
-      pace.publish(left, lane);
-      const uint32_t partner_left = pace.partner_left();
+      uint32_t partner_left = 0;
+      if constexpr (kPace) {
+        pace.publish(left, lane);
+        partner_left = pace.partner_left();
+      }
       // the next chunk's tiles (the last chunk's again on the last step: its loads are
       // issued on every step, so each step's waits count the same loads)
       const PfTiles nx = pf_tiles(a, trow, min(c0 + 64, t_lo + 64 * (n - 1)), col_hi);
@@ -570,9 +577,9 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
       pf_merge_pairs<BWV>(V, lane);
       pf_values<BWV, NCT>(V, cbv, pb, st);
       pf_load_v<BWV>(a, nx, kvh, lane, V);
-      pace_step(left, partner_left);
+      if constexpr (kPace) pace_step(left, partner_left);
     }
-    pace.publish(0, lane);
+    if constexpr (kPace) pace.publish(0, lane);
   }
   pf_write<NCT>(a, st, row0, lane);
 }
