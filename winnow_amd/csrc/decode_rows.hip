@@ -645,115 +645,137 @@ __device__ __forceinline__ int xcd_major(int p, int n) {
 // Either way the wave that scans a unit's first chunk records where the unit's
 // partials start and how many there are (unit_meta), so the merge reads exactly that
 // range.
-template <class Scan>
-__device__ __forceinline__ void for_each_range(const DecodeArgs& a, int64_t w, int lane, Scan&& scan) {
-  // One call site of the scan keeps a single copy of its code.
-  int b, kvh, t_lo, t_hi;
-  int64_t prow;
+// The walk is split in two: init() finds the wave's first range (the plan's lookups
+// and divisions, which a kernel can run while its tables load) and run() scans the
+// ranges one call site at a time (one copy of the scan's code).
+struct RangeWalk {
+  int b = 0, kvh = 0, t_lo = 0, t_hi = 0;
+  int64_t prow = 0;
   int64_t s = 0, e = 0;  // balanced: flattened chunks [s, e) still to do
   int64_t G = 0, j = 0;  // grouped: groups with work, this wave's group
-  const int32_t* pre = a.chunk_prefix;
-  const bool grouped = a.balanced && a.num_splits >= a.Hkv;
-  if (!a.balanced) {
-    if (w >= int64_t(a.num_splits) * a.Hkv * a.B) return;
-    const int split = int(w % a.num_splits);
-    kvh = int((w / a.num_splits) % a.Hkv);
-    b = int(w / (int64_t(a.num_splits) * a.Hkv));
-    const int L = a.seq_lens[b];
-    const int S = 1 << a.log2S;
-    const int n_pages = (L + S - 1) >> a.log2S;
-    const int page_lo = split * a.pages_per_split;
-    if (page_lo >= n_pages) return;  // wave-uniform: this split is past the sequence
-    const int page_hi = min(page_lo + a.pages_per_split, n_pages);
-    t_lo = page_lo << a.log2S;
-    t_hi = min(page_hi << a.log2S, L);
-    prow = (int64_t(b) * a.Hkv + kvh) * a.num_splits + split;
-    if (split == 0 && lane == 0)  // the merge reads the group's partial rows from here
-      a.unit_meta[b * a.Hkv + kvh] = make_int2(int(prow), (n_pages + a.pages_per_split - 1) / a.pages_per_split);
-  } else {
-    const int64_t T = pre[a.B];
-    int64_t key;  // the flattened position to find the sequence of, in units of pre[]
-    int64_t mult; // pre[] -> flattened position
-    if (grouped) {
-      G = min(int64_t(a.num_splits / a.Hkv), T);
-      j = w / a.Hkv;
-      if (j >= G) return;
-      s = T * j / G;
-      e = T * (j + 1) / G;
-      key = s;
-      mult = 1;
-      kvh = int(w % a.Hkv);
+  bool grouped = false;
+
+  // The chunk prefix and the lengths do not change while a scan runs (the rotate
+  // launch writes the prefix before it): const_view makes their reads scalar loads.
+  // false: the wave has no work
+  __device__ __forceinline__ bool init(const DecodeArgs& a, int64_t w, int lane) {
+    const auto* pre = const_view(a.chunk_prefix);
+    const auto* seq_lens = const_view(a.seq_lens);
+    grouped = a.balanced && a.num_splits >= a.Hkv;
+    if (!a.balanced) {
+      if (w >= int64_t(a.num_splits) * a.Hkv * a.B) return false;
+      const int split = int(w % a.num_splits);
+      kvh = int((w / a.num_splits) % a.Hkv);
+      b = int(w / (int64_t(a.num_splits) * a.Hkv));
+      const int L = seq_lens[b];
+      const int S = 1 << a.log2S;
+      const int n_pages = (L + S - 1) >> a.log2S;
+      const int page_lo = split * a.pages_per_split;
+      if (page_lo >= n_pages) return false;  // wave-uniform: this split is past the sequence
+      const int page_hi = min(page_lo + a.pages_per_split, n_pages);
+      t_lo = page_lo << a.log2S;
+      t_hi = min(page_hi << a.log2S, L);
+      prow = (int64_t(b) * a.Hkv + kvh) * a.num_splits + split;
+      if (split == 0 && lane == 0)  // the merge reads the group's partial rows from here
+        a.unit_meta[b * a.Hkv + kvh] = make_int2(int(prow), (n_pages + a.pages_per_split - 1) / a.pages_per_split);
     } else {
-      const int64_t C = int64_t(a.Hkv) * T;
-      const int64_t Wp = min(int64_t(a.num_splits), C);
-      if (w >= Wp) return;
-      s = C * w / Wp;
-      e = C * (w + 1) / Wp;
-      key = s;
-      mult = a.Hkv;
-      kvh = 0;
-    }
-    // sequence holding flattened chunk s: the largest b with mult * pre[b] <= s
-    int lo = 0, hi = a.B;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (mult * pre[mid] <= key) lo = mid;
-      else hi = mid;
-    }
-    b = lo;
-    t_lo = t_hi = 0;
-    prow = 0;
-  }
-  while (true) {
-    int nb = 0, c_hi = 0;
-    if (grouped) {
-      nb = pre[b + 1] - pre[b];
-      while (nb == 0) {  // sequences without tokens own no chunks
-        ++b;
-        nb = pre[b + 1] - pre[b];
-      }
-      const int c_lo = int(s - pre[b]);
-      c_hi = int(min(int64_t(nb), c_lo + (e - s)));
-      t_lo = 64 * c_lo;
-      t_hi = min(64 * c_hi, a.seq_lens[b]);
-      prow = int64_t(kvh) * (G + a.B) + b + j;
-      if (c_lo == 0 && lane == 0) {
-        // the unit's first group: its partials are rows prow .. prow + n - 1, one per
-        // group up to the last group starting before the sequence's end pre[b + 1]
-        const int64_t T = pre[a.B];
-        const int64_t jl = (int64_t(pre[b + 1]) * G + T - 1) / T - 1;
-        a.unit_meta[b * a.Hkv + kvh] = make_int2(int(prow), int(jl - j + 1));
-      }
-      s += c_hi - c_lo;
-    } else if (a.balanced) {
-      nb = pre[b + 1] - pre[b];
-      while (nb == 0) {  // sequences without tokens own no chunks
-        ++b;
-        nb = pre[b + 1] - pre[b];
-      }
-      const int64_t base = int64_t(a.Hkv) * pre[b];
-      kvh = int((s - base) / nb);
-      const int c_lo = int((s - base) % nb);
-      c_hi = int(min(int64_t(nb), c_lo + (e - s)));
-      t_lo = 64 * c_lo;
-      t_hi = min(64 * c_hi, a.seq_lens[b]);
-      prow = w + int64_t(b) * a.Hkv + kvh;
-      if (c_lo == 0 && lane == 0) {
-        // the unit's first wave: its partials are rows prow .. prow + n - 1, one per
-        // wave up to the last wave starting before the unit's end U1
-        const int64_t C = int64_t(a.Hkv) * pre[a.B];
+      const int64_t T = pre[a.B];
+      int64_t key;  // the flattened position to find the sequence of, in units of pre[]
+      int64_t mult; // pre[] -> flattened position
+      if (grouped) {
+        G = min(int64_t(a.num_splits / a.Hkv), T);
+        j = w / a.Hkv;
+        if (j >= G) return false;
+        s = T * j / G;
+        e = T * (j + 1) / G;
+        key = s;
+        mult = 1;
+        kvh = int(w % a.Hkv);
+      } else {
+        const int64_t C = int64_t(a.Hkv) * T;
         const int64_t Wp = min(int64_t(a.num_splits), C);
-        const int64_t U1 = base + int64_t(kvh + 1) * nb;
-        const int64_t wl = (U1 * Wp + C - 1) / C - 1;
-        a.unit_meta[b * a.Hkv + kvh] = make_int2(int(prow), int(wl - w + 1));
+        if (w >= Wp) return false;
+        s = C * w / Wp;
+        e = C * (w + 1) / Wp;
+        key = s;
+        mult = a.Hkv;
+        kvh = 0;
       }
-      s += c_hi - c_lo;
+      // sequence holding flattened chunk s: the largest b with mult * pre[b] <= s
+      int lo = 0, hi = a.B;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (mult * pre[mid] <= key) lo = mid;
+        else hi = mid;
+      }
+      b = lo;
+      t_lo = t_hi = 0;
+      prow = 0;
     }
-    scan(b, kvh, t_lo, t_hi, prow, uint32_t(a.balanced ? e - s : 0));
-    if (!a.balanced || s >= e) break;
-    if (grouped) ++b;  // the group's range continues in the next sequence
-    else if (kvh + 1 == a.Hkv && c_hi == nb) ++b;
+    return true;
   }
+
+  template <class Scan>
+  __device__ __forceinline__ void run(const DecodeArgs& a, int64_t w, int lane, Scan&& scan) {
+    const auto* pre = const_view(a.chunk_prefix);
+    const auto* seq_lens = const_view(a.seq_lens);
+    while (true) {
+      int nb = 0, c_hi = 0;
+      if (grouped) {
+        nb = pre[b + 1] - pre[b];
+        while (nb == 0) {  // sequences without tokens own no chunks
+          ++b;
+          nb = pre[b + 1] - pre[b];
+        }
+        const int c_lo = int(s - pre[b]);
+        c_hi = int(min(int64_t(nb), c_lo + (e - s)));
+        t_lo = 64 * c_lo;
+        t_hi = min(64 * c_hi, seq_lens[b]);
+        prow = int64_t(kvh) * (G + a.B) + b + j;
+        if (c_lo == 0 && lane == 0) {
+          // the unit's first group: its partials are rows prow .. prow + n - 1, one per
+          // group up to the last group starting before the sequence's end pre[b + 1]
+          const int64_t T = pre[a.B];
+          const int64_t jl = (int64_t(pre[b + 1]) * G + T - 1) / T - 1;
+          a.unit_meta[b * a.Hkv + kvh] = make_int2(int(prow), int(jl - j + 1));
+        }
+        s += c_hi - c_lo;
+      } else if (a.balanced) {
+        nb = pre[b + 1] - pre[b];
+        while (nb == 0) {  // sequences without tokens own no chunks
+          ++b;
+          nb = pre[b + 1] - pre[b];
+        }
+        const int64_t base = int64_t(a.Hkv) * pre[b];
+        kvh = int((s - base) / nb);
+        const int c_lo = int((s - base) % nb);
+        c_hi = int(min(int64_t(nb), c_lo + (e - s)));
+        t_lo = 64 * c_lo;
+        t_hi = min(64 * c_hi, seq_lens[b]);
+        prow = w + int64_t(b) * a.Hkv + kvh;
+        if (c_lo == 0 && lane == 0) {
+          // the unit's first wave: its partials are rows prow .. prow + n - 1, one per
+          // wave up to the last wave starting before the unit's end U1
+          const int64_t C = int64_t(a.Hkv) * pre[a.B];
+          const int64_t Wp = min(int64_t(a.num_splits), C);
+          const int64_t U1 = base + int64_t(kvh + 1) * nb;
+          const int64_t wl = (U1 * Wp + C - 1) / C - 1;
+          a.unit_meta[b * a.Hkv + kvh] = make_int2(int(prow), int(wl - w + 1));
+        }
+        s += c_hi - c_lo;
+      }
+      scan(b, kvh, t_lo, t_hi, prow, uint32_t(a.balanced ? e - s : 0));
+      if (!a.balanced || s >= e) break;
+      if (grouped) ++b;  // the group's range continues in the next sequence
+      else if (kvh + 1 == a.Hkv && c_hi == nb) ++b;
+    }
+  }
+};
+
+template <class Scan>
+__device__ __forceinline__ void for_each_range(const DecodeArgs& a, int64_t w, int lane, Scan&& scan) {
+  RangeWalk rw;
+  if (rw.init(a, w, lane)) rw.run(a, w, lane, scan);
 }
 
 // Work-group of WPB independent waves sharing the codebook tables; wave w =
@@ -882,18 +904,24 @@ __device__ __forceinline__ uint2 split_pair(float lo, float hi) {
 
 // The pair tables of stage_table with 16-bit split entries (4-bit: replicated and
 // byte-indexed; 2, 3, 5, 6 bits: 2^(2 BW) entries).
+template <int BW>
+constexpr int table16_entries() { return BW == 4 ? 256 * 32 : 1 << (2 * BW); }
+// codes of entry i: 4-bit, byte i >> 5 (lane copy i & 31); else a code pair
+template <int BW>
+__device__ __forceinline__ int2 table16_codes(int i) {
+  if constexpr (BW == 4) return make_int2((i >> 5) & 15, i >> 9);
+  else return make_int2(i & ((1 << BW) - 1), i >> BW);
+}
 template <int BW, int NTHR>
-__device__ __forceinline__ void stage_table16(const float* cb, char* dst, int tid) {
+using Table16Loads = CodePairs<table16_entries<BW>(), NTHR>;
+template <int BW, int NTHR>
+__device__ __forceinline__ Table16Loads<BW, NTHR> load_table16(const float* cb, int tid) {
   static_assert(BW == 4 || pair_coded<BW>(), "16-bit tables are pair tables");
-  uint2* t = reinterpret_cast<uint2*>(dst);
-  if constexpr (BW == 4) {
-    for_strided<256 * 32, NTHR>(tid, [&](int i) {
-      const int b = i >> 5;
-      t[i] = split_pair(cb[b & 15], cb[b >> 4]);
-    });
-  } else {
-    for_strided<(1 << (2 * BW)), NTHR>(tid, [&](int i) { t[i] = split_pair(cb[i & ((1 << BW) - 1)], cb[i >> BW]); });
-  }
+  return load_code_pairs<table16_entries<BW>(), NTHR>(cb, tid, [](int i) { return table16_codes<BW>(i); });
+}
+template <int BW, int NTHR>
+__device__ __forceinline__ void store_table16(const Table16Loads<BW, NTHR>& p, char* dst, int tid) {
+  store_code_pairs(p, reinterpret_cast<uint2*>(dst), tid, [](float lo, float hi) { return split_pair(lo, hi); });
 }
 
 // Table reads in flight ahead of their MFMA in the 16-bit scan: eight steps where
@@ -1628,17 +1656,25 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows16_kernel(DecodeArgs a) {
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_table16<BWK, 64 * WPB>(a.cb_k, lds + Lay::k_off, tid);
-  stage_table16<BWV, 64 * WPB>(a.cb_v, lds + Lay::v_off, tid);
+  const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
+  // the tables' codebook loads travel while the wave looks up its first range (the
+  // plan's dependent scalar loads and divisions); the entries are stored after
+  const auto lk = load_table16<BWK, 64 * WPB>(a.cb_k, tid);
+  const auto lv = load_table16<BWV, 64 * WPB>(a.cb_v, tid);
+  RangeWalk rw;
+  const bool live = rw.init(a, w, lane);
+  store_table16<BWK, 64 * WPB>(lk, lds + Lay::k_off, tid);
+  store_table16<BWV, 64 * WPB>(lv, lds + Lay::v_off, tid);
   const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig, lane);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
-  const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);
   Tab<BWK> cbk = make_tab<BWK>(lds, Lay::k_off, lane);
   Tab<BWV> cbv = make_tab<BWV>(lds, Lay::v_off, lane);
-  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow, uint32_t left) {
-    scan_range16<BWK, BWV, NG, false>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile, pace, left);
-  });
+  if (live) {
+    rw.run(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow, uint32_t left) {
+      scan_range16<BWK, BWV, NG, false>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile, pace, left);
+    });
+  }
   pace.publish(0, lane);
 }
 
@@ -1650,17 +1686,24 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_tf_kernel(DecodeArgs a) 
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_table_tf<BWK, 64 * WPB>(a.cb_k, lds + Lay::k_off, tid);
-  stage_table_tf<BWV, 64 * WPB>(a.cb_v, lds + Lay::v_off, tid);
+  const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
+  // table loads travel while the wave looks up its first range (as in decode_rows16_kernel)
+  const auto lk = load_table_tf<BWK, 64 * WPB>(a.cb_k, tid);
+  const auto lv = load_table_tf<BWV, 64 * WPB>(a.cb_v, tid);
+  RangeWalk rw;
+  const bool live = rw.init(a, w, lane);
+  store_table_tf<BWK, 64 * WPB>(lk, lds + Lay::k_off, tid);
+  store_table_tf<BWV, 64 * WPB>(lv, lds + Lay::v_off, tid);
   const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig, lane);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
-  const int64_t w = int64_t(xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);
   TabTf<BWK> cbk = make_tab_tf<BWK>(lds, Lay::k_off, lane);
   TabTf<BWV> cbv = make_tab_tf<BWV>(lds, Lay::v_off, lane);
-  for_each_range(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow, uint32_t left) {
-    scan_range16<BWK, BWV, NG, true>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile, pace, left);
-  });
+  if (live) {
+    rw.run(a, w, lane, [&](int b, int kvh, int t_lo, int t_hi, int64_t prow, uint32_t left) {
+      scan_range16<BWK, BWV, NG, true>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile, pace, left);
+    });
+  }
   pace.publish(0, lane);
 }
 

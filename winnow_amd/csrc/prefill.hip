@@ -490,7 +490,7 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
   st.gs = 0;
 
   // visible tokens of the block: query qi sees keys j <= L - Q + qi
-  const int L = a.seq_lens[b];
+  const int L = const_view(a.seq_lens)[b];  // a scalar load (const_view)
   const int rows = a.n_rep * a.Q;
   const int r_first = cb * NR, r_last = min(r_first + NR, rows) - 1;
   int T = r_first < rows ? min(L, L - a.Q + r_last / a.n_rep + 1) : 0;
@@ -793,7 +793,7 @@ __global__ __launch_bounds__(64 * WPB) void pf_tile_kernel(PrefillArgs a) {
     st.l[ct] = 0.f;
   }
   st.gs = 0;
-  const int L = unit_live ? a.seq_lens[b] : 0;
+  const int L = unit_live ? const_view(a.seq_lens)[b] : 0;
   const int rows = a.n_rep * a.Q;
   // the group's chunks: those its last row sees (the other rows mask what they must not see)
   const int g_first = cg * WPB * NR, g_last = min(g_first + WPB * NR, rows) - 1;

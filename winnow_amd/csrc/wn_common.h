@@ -77,6 +77,16 @@ __device__ __forceinline__ uint32_t code_at(const uint32_t (&w)[NW], int d) {
   return v & ((1u << BW) - 1u);
 }
 
+// A read-only view through the constant address space, for buffers no launch writes
+// while it reads them (plans, lengths, prefixes): their wave-uniform reads become
+// scalar loads, which wait on their own counter rather than behind the wave's vector
+// loads (through a plain pointer the compiler cannot rule out a store by the kernel,
+// and reads uniform values with vector loads).
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* const_view(const T* p) {
+  return (const __attribute__((address_space(4))) T*)(p);
+}
+
 // f(i) for i = tid + NTHR k in [0, N), for the staging loops of a work-group's
 // prologue: the trip count is known at compile time, so the loop unrolls and every
 // iteration's loads are issued before the first wait (a loop on i < N waits for each

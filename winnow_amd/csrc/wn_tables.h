@@ -82,6 +82,37 @@ constexpr int kTfTableBytes = 256 * 64 * 4;  // 256 byte values x 64 lanes x two
 template <int BW>
 constexpr int tf_table_bytes() { return BW == 4 ? kTfTableBytes : 4 << (2 * BW); }
 
+// Codebook values behind the table entries one thread stages: entry i = tid + NTHR k
+// (k < K) holds the values of codes (lo, hi) = codes(i). Loaded apart from the stores,
+// so that a kernel can issue a table's loads, do other work while they travel (the
+// row scans look up their plan), and store the entries after.
+template <int N, int NTHR>
+struct CodePairs {
+  static constexpr int K = (N + NTHR - 1) / NTHR;
+  float lo[K], hi[K];
+};
+
+template <int N, int NTHR, class Codes>
+__device__ __forceinline__ CodePairs<N, NTHR> load_code_pairs(const float* cb, int tid, Codes&& codes) {
+  CodePairs<N, NTHR> p;
+#pragma unroll
+  for (int k = 0; k < CodePairs<N, NTHR>::K; ++k) {
+    const int2 c = codes(min(tid + NTHR * k, N - 1));  // entries past N: loaded clamped, not stored
+    p.lo[k] = cb[c.x];
+    p.hi[k] = cb[c.y];
+  }
+  return p;
+}
+
+template <int N, int NTHR, class T, class Entry>
+__device__ __forceinline__ void store_code_pairs(const CodePairs<N, NTHR>& p, T* t, int tid, Entry&& entry) {
+#pragma unroll
+  for (int k = 0; k < CodePairs<N, NTHR>::K; ++k) {
+    const int i = tid + NTHR * k;
+    if (N % NTHR == 0 || i < N) t[i] = entry(p.lo[k], p.hi[k]);
+  }
+}
+
 // Two fp16 values rounded to nearest, lo in the low half.
 __device__ __forceinline__ uint32_t tf_word(float lo, float hi) {
   return uint32_t(__builtin_bit_cast(uint16_t, _Float16(lo))) | uint32_t(__builtin_bit_cast(uint16_t, _Float16(hi))) << 16;
@@ -90,18 +121,29 @@ __device__ __forceinline__ uint32_t tf_word(float lo, float hi) {
 // Stages a TF table: 4-bit, the replicated byte table (entry (b, r) holds
 // (H(2^8 c[b & 15]), H(2^8 c[b >> 4]))); 6-bit, entry i holds (H(2^8 c[i mod 64]),
 // H(2^8 c[i >> 6])), two consecutive codes read as one 12-bit index.
+template <int BW>
+constexpr int tf_entries() { return BW == 4 ? 256 * 64 : 1 << (2 * BW); }
+// codes of TF table entry i: 4-bit, byte i >> 6 (lane copy i & 63); 6-bit, a code pair
+template <int BW>
+__device__ __forceinline__ int2 tf_codes(int i) {
+  if constexpr (BW == 4) return make_int2((i >> 6) & 15, i >> 10);
+  else return make_int2(i & 63, i >> 6);
+}
+template <int BW, int NTHR>
+using TfLoads = CodePairs<tf_entries<BW>(), NTHR>;
+template <int BW, int NTHR>
+__device__ __forceinline__ TfLoads<BW, NTHR> load_table_tf(const float* cb, int tid) {
+  static_assert(BW == 4 || BW == 6, "TF tables: 4 and 6-bit codes");
+  return load_code_pairs<tf_entries<BW>(), NTHR>(cb, tid, [](int i) { return tf_codes<BW>(i); });
+}
+template <int BW, int NTHR>
+__device__ __forceinline__ void store_table_tf(const TfLoads<BW, NTHR>& p, char* dst, int tid) {
+  store_code_pairs(p, reinterpret_cast<uint32_t*>(dst), tid,
+                   [](float lo, float hi) { return tf_word(lo * kCbScale, hi * kCbScale); });
+}
 template <int BW, int NTHR>
 __device__ __forceinline__ void stage_table_tf(const float* cb, char* dst, int tid) {
-  static_assert(BW == 4 || BW == 6, "TF tables: 4 and 6-bit codes");
-  uint32_t* t = reinterpret_cast<uint32_t*>(dst);
-  if constexpr (BW == 4) {
-    for_strided<256 * 64, NTHR>(tid, [&](int i) {
-      const int b = i >> 6;
-      t[i] = tf_word(cb[b & 15] * kCbScale, cb[b >> 4] * kCbScale);
-    });
-  } else {
-    for_strided<(1 << (2 * BW)), NTHR>(tid, [&](int i) { t[i] = tf_word(cb[i & 63] * kCbScale, cb[i >> 6] * kCbScale); });
-  }
+  store_table_tf<BW, NTHR>(load_table_tf<BW, NTHR>(cb, tid), dst, tid);
 }
 
 // A TF table as one lane reads it: the 6-bit table's base; the 4-bit table's address
