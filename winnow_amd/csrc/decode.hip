@@ -217,10 +217,99 @@ __global__ __launch_bounds__(merge_threads<D>()) void merge_kernel(MergeArgs a) 
   store_elem(a.out, (int64_t(b) * a.Hq + kvh * a.n_rep + h) * D + d, a.out_dtype, o);
 }
 
+// merge_kernel<128> for four heads of one (kv head, sequence) per work-group: wave w
+// merges head 4 hg + w (lane l owns dims 2l, 2l+1, loaded as pairs), then thread t
+// forms output dim j = t % 128 of heads 4 hg + 2 (t / 128) + {0, 1}, reading column j
+// of Pi_V inside the product for both. For batches of many (kv head, sequence)
+// pairs, where merge_kernel's per-head work-groups each pull all of Pi_V (64 KB)
+// through the L2, this reads it a quarter as often (config 4's shape, A/B: 11.8 ->
+// 7.8 us); with few pairs it leaves CUs idle and merge_kernel is faster. Every sum
+// runs in merge_kernel's order, so the outputs are the same bits.
+constexpr int kMergeHeads = 4;
+
+__global__ __launch_bounds__(64 * kMergeHeads) void merge4_kernel(MergeArgs a) {
+  constexpr int D = 128;
+  __shared__ float av[kMergeHeads][D];
+  const int hg = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int h = kMergeHeads * hg + wave;
+  const int2 meta = a.unit_meta[b * a.Hkv + kvh];
+  const int64_t r0 = meta.x;
+  const int n = meta.y;
+  auto wexp = [&](float x) { return a.log2_units ? __builtin_amdgcn_exp2f(x) : expf(x); };
+  const int64_t pstride = a.n_rep;
+  if (h < a.n_rep) {  // wave-uniform
+    const float* ml = a.part_ml + 2 * (r0 * pstride + h);
+    const float2* acc = reinterpret_cast<const float2*>(a.part_acc + (r0 * pstride + h) * D) + lane;
+    float M = -INFINITY, den = 0.f;
+    float2 num = make_float2(0.f, 0.f);
+    float2 xv[kMergeBatch];
+    auto load_batch = [&](int first) {
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) xv[k] = acc[int64_t(min(first + k, n - 1)) * pstride * (D / 2)];
+    };
+    for (int s0 = 0; s0 < n; s0 += 64) {
+      const int cnt = min(64, n - s0);
+      float mk = -INFINITY, lk = 0.f;
+      if (lane < cnt) {
+        const float2 x = *reinterpret_cast<const float2*>(ml + 2 * (int64_t(s0 + lane) * pstride));
+        mk = x.x;
+        lk = x.y;
+      }
+      if (s0 == 0) load_batch(0);
+      const float Mn = fmaxf(M, wave_max(mk));
+      const float wk = mk == -INFINITY ? 0.f : wexp(mk - Mn);
+      const float r_old = M == -INFINITY ? 0.f : wexp(M - Mn);
+      den = fmaf(den, r_old, wave_sum(wk * lk));
+      num.x *= r_old;
+      num.y *= r_old;
+      M = Mn;
+      for (int k0 = 0; k0 < cnt; k0 += kMergeBatch) {
+        if (s0 + k0 > 0) load_batch(s0 + k0);
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k) {
+          const float wt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k0 + k));
+          num.x = fmaf(wt, xv[k].x, num.x);
+          num.y = fmaf(wt, xv[k].y, num.y);
+        }
+      }
+    }
+    const bool some = n > 0 && den > 0.f;
+    av[wave][2 * lane] = some ? num.x / fmaxf(den, 1e-30f) : 0.f;
+    av[wave][2 * lane + 1] = some ? num.y / fmaxf(den, 1e-30f) : 0.f;
+  }
+  __syncthreads();
+  const int j = tid & (D - 1), hp = tid >> 7;
+  const int ha = kMergeHeads * hg + 2 * hp;  // heads ha, ha + 1 (past n_rep: not stored)
+  float o0 = 0.f, o1 = 0.f;
+  if (a.pi_v) {
+#pragma unroll 16
+    for (int k = 0; k < D; ++k) {
+      const float pv = a.pi_v[k * D + j];
+      o0 = fmaf(av[2 * hp][k], pv, o0);
+      o1 = fmaf(av[2 * hp + 1][k], pv, o1);
+    }
+  } else {
+    o0 = av[2 * hp][j];
+    o1 = av[2 * hp + 1][j];
+  }
+  const int64_t orow = int64_t(b) * a.Hq + kvh * a.n_rep;
+  if (ha < a.n_rep) store_elem(a.out, (orow + ha) * D + j, a.out_dtype, o0);
+  if (ha + 1 < a.n_rep) store_elem(a.out, (orow + ha + 1) * D + j, a.out_dtype, o1);
+}
+
 using MergeFn = void (*)(MergeArgs);
 
-// The merge for head_dim D and its work-group size.
+// The merge for head_dim D and its work-group size; grid = (n_rep, Hkv, B). At head_dim
+// 128 with 512 or more work-groups of merge4_kernel, that kernel.
 void launch_merge(int D, dim3 grid, hipStream_t st, const MergeArgs& ma) {
+  if (D == 128) {
+    const unsigned groups = (grid.x + kMergeHeads - 1) / kMergeHeads;
+    if (int64_t(groups) * grid.y * grid.z >= 512) {
+      hipLaunchKernelGGL(merge4_kernel, dim3(groups, grid.y, grid.z), dim3(64 * kMergeHeads), 0, st, ma);
+      return;
+    }
+  }
   switch (D) {
     case 16: hipLaunchKernelGGL(merge_kernel<16>, grid, dim3(merge_threads<16>()), 0, st, ma); break;
     case 32: hipLaunchKernelGGL(merge_kernel<32>, grid, dim3(merge_threads<32>()), 0, st, ma); break;
