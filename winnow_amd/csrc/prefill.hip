@@ -86,7 +86,10 @@ __device__ __forceinline__ PfTiles pf_tiles(const PrefillArgs& a, const int32_t*
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int t0 = c0 + 16 * t;
-    o.pid[t] = uint32_t(__builtin_amdgcn_readfirstlane(trow[min(t0 >> a.log2S, col_hi)]));
+    // the page table is not written while the scan runs: const_view keeps these
+    // wave-uniform reads scalar loads (the pacing word's LDS store would otherwise
+    // make the compiler read them with vector loads and wait on them)
+    o.pid[t] = uint32_t(__builtin_amdgcn_readfirstlane(const_view(trow)[min(t0 >> a.log2S, col_hi)]));
     o.slot[t] = uint32_t(t0 & smask);
   }
   return o;
