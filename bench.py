@@ -90,6 +90,14 @@ def tf_kernel_name(c) -> str:
     return scan_kernel_name(c)
 
 
+def prefill_kernel_name(n_rep: int, Q: int) -> str:
+    """Symbol of the prefill scan wn_prefill_attention launches: the shared-tile scan
+    once a kv head has eight 32-row query blocks (n_rep * Q rounded up to 64 rows,
+    at least 256), else the per-wave scan."""
+    rows = (n_rep * Q + 63) // 64 * 64
+    return "pf_tile_kernel" if rows // 32 >= 8 else "pf_scan_kernel"
+
+
 kv_bytes = workloads.kv_bytes
 
 
@@ -689,7 +697,8 @@ def prefill_bench(w, Q: int, nseq: int | None = None, steps: int = 10, warmup: i
     pairs = sum(max(0, min(L, L - Q + i + 1)) for L in lens for i in range(Q))
     flops = 4 * Hq * D * pairs
     out = {"Q": Q, "batch": B, "q_heads": Hq, "kv_heads": c["Hkv"], "seq_lens": f"{min(lens)}..{max(lens)}",
-           "bits_k": c["bwk"], "bits_v": c["bwv"], "splits": ns, "kernel": "pf_scan_kernel",
+           "bits_k": c["bwk"], "bits_v": c["bwv"], "splits": ns,
+           "kernel": prefill_kernel_name(Hq // c["Hkv"], Q),
            "scan_us": scan_ms * 1e3, "us_per_call": ms * 1e3, "prefill_tokens_per_s": B * Q / (ms * 1e-3),
            "hbm": {"algorithmic_bytes": nbytes, "achieved_GBps": nbytes / (scan_ms * 1e-3) / 1e9,
                    "frac": nbytes / (scan_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS},

@@ -62,7 +62,7 @@ def test_layer_bytes_and_history(backend, tol):
     assert layer.get_seq_length() == L and k_hist.shape == (B, H, L, D) and k_hist.dtype == torch.float32
     assert layer.last_dispatch_decision.backend == ("chunked" if backend == "torch_fp32" else "fused")
     oq = oracle_quantizer(bw, D, 42)
-    for xs, grp, hist in ((xs_k, layer._k[0], k_hist), (xs_v, layer._v[0], v_hist)):
+    for xs, grp, hist in ((xs_k, layer._k_groups[0], k_hist), (xs_v, layer._v_groups[0], v_hist)):
         x = torch.cat(xs, dim=2)
         codes, norms = _stored(grp, L, bw, D)
         ocodes, onorms = oq.quantize(x)
@@ -96,12 +96,12 @@ def test_layer_outlier_channels_and_other_widths(D, n_out, bw, bw_out):
         rms = k0.pow(2).mean(dim=(0, 1, 2)).sqrt()
         mask = torch.zeros(D, dtype=torch.bool)
         mask[rms.topk(n_out).indices] = True
-        assert torch.equal(layer._mask.cpu(), mask) and bool(mask[5]) and bool(mask[17])
+        assert torch.equal(layer._outlier_channels.cpu(), mask) and bool(mask[5]) and bool(mask[17])
         groups = [(~mask, bw, D - n_out, 42, 0), (mask, bw_out, n_out, 43, 1)]
     else:
         mask = torch.zeros(D, dtype=torch.bool)
         groups = [(~mask, bw, D, 42, 0)]
-    for xs, side, hist in ((xs_k, layer._k, k_hist), (xs_v, layer._v, v_hist)):
+    for xs, side, hist in ((xs_k, layer._k_groups, k_hist), (xs_v, layer._v_groups, v_hist)):
         x = torch.cat(xs, dim=2)
         want = torch.empty(B, H, L, D, dtype=torch.float64)
         for chan, w, dim, seed, gi in groups:
@@ -133,8 +133,8 @@ def test_explicit_backend_with_outlier_channels_takes_the_chunked_path(backend):
                           kernel_backend=backend)
     k_hist, v_hist = _fill(layer, xs_k, xs_v)
     assert layer.last_dispatch_decision.backend == "chunked"
-    mask = layer._mask.cpu()
-    for xs, side, hist in ((xs_k, layer._k, k_hist), (xs_v, layer._v, v_hist)):
+    mask = layer._outlier_channels.cpu()
+    for xs, side, hist in ((xs_k, layer._k_groups, k_hist), (xs_v, layer._v_groups, v_hist)):
         x = torch.cat(xs, dim=2)
         want = torch.empty(B, H, 13, D, dtype=torch.float64)
         for chan, w, dim, seed, gi in ((~mask, bw, D - n_out, 42, 0), (mask, bw_out, n_out, 43, 1)):

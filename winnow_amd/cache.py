@@ -78,57 +78,57 @@ class TQPackedLayer(DynamicLayer):
             raise ValueError(f"unknown kernel_backend={kernel_backend!r}")
         self.use_kernel, self.allow_tf32, self.kernel_backend = use_kernel, allow_tf32, backend
         self.last_dispatch_decision: DequantChoice | None = None
-        self._hd, self._bw, self._max, self._chunk = head_dim, bit_width, max_cache_len, chunk
+        self._head_dim, self._bits, self._capacity, self._span = head_dim, bit_width, max_cache_len, chunk
         split = num_outlier_channels > 0 and outlier_bits > bit_width
-        self._out_dim = num_outlier_channels if split else 0
-        self._reg_dim = head_dim - self._out_dim
-        self._out_bw = outlier_bits
+        self._n_outlier = num_outlier_channels if split else 0
+        self._n_regular = head_dim - self._n_outlier
+        self._outlier_bits = outlier_bits
         # K and V share each group's quantizer (seed 42 regular, 43 outlier), as the reference's
-        self._tq = get_quantizer(bit_width, self._reg_dim, device)
-        self._tq_out = get_quantizer(outlier_bits, self._out_dim, device, seed=43) if split else None
-        self._nb_reg = packed_bytes(self._reg_dim, bit_width)
-        self._nb_out = packed_bytes(self._out_dim, outlier_bits) if split else 0
-        self._len = 0
-        self._mask = None          # (head_dim,) bool: the outlier channels
-        self._k = self._v = None   # lists of _Group: regular, then outlier
+        self._quant = get_quantizer(bit_width, self._n_regular, device)
+        self._quant_outlier = get_quantizer(outlier_bits, self._n_outlier, device, seed=43) if split else None
+        self._row_bytes = packed_bytes(self._n_regular, bit_width)
+        self._outlier_row_bytes = packed_bytes(self._n_outlier, outlier_bits) if split else 0
+        self._tokens = 0
+        self._outlier_channels = None          # (head_dim,) bool: the outlier channels
+        self._k_groups = self._v_groups = None   # lists of _Group: regular, then outlier
         self._append_table = self._append_start = None   # fused append's (B, 1) table, start positions
         self.is_initialized = False
 
     # ---------------------------------------------------------------- storage
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         B, H, _, D = key_states.shape
-        if D != self._hd:
-            raise ValueError(f"TQPackedLayer: head_dim {D} != {self._hd}")
+        if D != self._head_dim:
+            raise ValueError(f"TQPackedLayer: head_dim {D} != {self._head_dim}")
         self.dtype, self.device = key_states.dtype, key_states.device
         dev = key_states.device
 
         def group(nb):
-            return _Group(torch.empty(B, H, self._max, nb, dtype=torch.uint8, device=dev),
-                          torch.empty(B, H, self._max, dtype=torch.float16, device=dev))
-        widths = [self._nb_reg] + ([self._nb_out] if self._out_dim else [])
-        self._k = [group(nb) for nb in widths]
-        self._v = [group(nb) for nb in widths]
-        if self._out_dim:
+            return _Group(torch.empty(B, H, self._capacity, nb, dtype=torch.uint8, device=dev),
+                          torch.empty(B, H, self._capacity, dtype=torch.float16, device=dev))
+        widths = [self._row_bytes] + ([self._outlier_row_bytes] if self._n_outlier else [])
+        self._k_groups = [group(nb) for nb in widths]
+        self._v_groups = [group(nb) for nb in widths]
+        if self._n_outlier:
             rms = key_states.float().pow(2).mean(dim=(0, 1, 2)).sqrt()
-            self._mask = torch.zeros(D, dtype=torch.bool, device=dev)
-            self._mask[rms.topk(min(self._out_dim, D)).indices] = True
-        self._shape = (B, H, D)
+            self._outlier_channels = torch.zeros(D, dtype=torch.bool, device=dev)
+            self._outlier_channels[rms.topk(min(self._n_outlier, D)).indices] = True
+        self._dims = (B, H, D)
         self.is_initialized = True
 
     def _fused_append_ok(self, x: torch.Tensor) -> bool:
         """One wn_append_kv launch writes both sides: no outlier split, a compiled
         head_dim, rows whose byte strides keep the kernel's 8-byte alignment."""
-        g = self._k[0]
-        return (not self._out_dim and self._hd in _APPEND_HEAD_DIMS and x.dtype in _lib.DTYPE_CODE
-                and (self._max * self._nb_reg) % 8 == 0 and g.codes.data_ptr() % 8 == 0
-                and self._v[0].codes.data_ptr() % 8 == 0)
+        g = self._k_groups[0]
+        return (not self._n_outlier and self._head_dim in _APPEND_HEAD_DIMS and x.dtype in _lib.DTYPE_CODE
+                and (self._capacity * self._row_bytes) % 8 == 0 and g.codes.data_ptr() % 8 == 0
+                and self._v_groups[0].codes.data_ptr() % 8 == 0)
 
     @torch.no_grad()
     def _append_fused(self, k: torch.Tensor, v: torch.Tensor, pos: int) -> None:
         B, H, n, D = k.shape
         k = k if k.stride(-1) == 1 else k.contiguous()
         v = v if (v.stride(-1) == 1 and v.dtype == k.dtype) else v.to(k.dtype).contiguous()
-        S = 1 << max(self._max - 1, 1).bit_length()   # one power-of-two page holds a whole row
+        S = 1 << max(self._capacity - 1, 1).bit_length()   # one power-of-two page holds a whole row
         dev = k.device
         if self._append_table is None or self._append_table.shape[0] != B:
             # row b of the cache is "page" b: a (B, 1) identity table, and the start
@@ -138,11 +138,11 @@ class TQPackedLayer(DynamicLayer):
             self._append_start = torch.empty(B, dtype=torch.int32, device=dev)
         table, start = self._append_table, self._append_start
         start.fill_(pos)
-        kg, vg, q = self._k[0], self._v[0], self._tq
+        kg, vg, q = self._k_groups[0], self._v_groups[0], self._quant
         with torch.cuda.device(dev):
             _lib.call("wn_append_kv",
                       _lib.ptr(k), *k.stride()[:3], _lib.ptr(v), *v.stride()[:3], _lib.DTYPE_CODE[k.dtype],
-                      _lib.ptr(q.Pi), _lib.ptr(q.boundaries), self._bw, _lib.ptr(q.Pi), _lib.ptr(q.boundaries), self._bw,
+                      _lib.ptr(q.Pi), _lib.ptr(q.boundaries), self._bits, _lib.ptr(q.Pi), _lib.ptr(q.boundaries), self._bits,
                       _lib.ptr(table), 1, _lib.ptr(start),
                       _lib.ptr(kg.codes), kg.codes.stride(0), kg.codes.stride(1),
                       _lib.ptr(vg.codes), vg.codes.stride(0), vg.codes.stride(1),
@@ -154,11 +154,11 @@ class TQPackedLayer(DynamicLayer):
     def _append_groups(self, x: torch.Tensor, groups, pos: int) -> None:
         """wn_quantize + wn_pack per channel group, written into [pos, pos + n)."""
         n = x.shape[-2]
-        if self._out_dim:
+        if self._n_outlier:
             xf = x.float()
-            parts = [(xf[..., ~self._mask], self._tq, self._bw), (xf[..., self._mask], self._tq_out, self._out_bw)]
+            parts = [(xf[..., ~self._outlier_channels], self._quant, self._bits), (xf[..., self._outlier_channels], self._quant_outlier, self._outlier_bits)]
         else:
-            parts = [(x, self._tq, self._bw)]
+            parts = [(x, self._quant, self._bits)]
         for (xp, q, bw), g in zip(parts, groups):
             idx, nrm = q.quantize(xp)
             g.codes[:, :, pos:pos + n] = pack(idx, bw)
@@ -169,11 +169,11 @@ class TQPackedLayer(DynamicLayer):
         b = self.kernel_backend
         if b == "torch_fp32":
             return DequantChoice("chunked", False, "kernel_backend torch_fp32")
-        if self._out_dim:
+        if self._n_outlier:
             # the reference uses its kernels only without outlier channels and otherwise
             # takes the chunked path whatever kernel_backend asked for (cache.py:245-246)
             return DequantChoice("chunked", False, f"{b}: outlier channels take the chunked path")
-        fused_ok = self._hd == _FUSED_HEAD_DIM
+        fused_ok = self._head_dim == _FUSED_HEAD_DIM
         if b == "auto":
             if fused_ok:
                 return DequantChoice("fused", self.allow_tf32, "auto: fused kernel (head_dim 128, no outliers)")
@@ -184,7 +184,7 @@ class TQPackedLayer(DynamicLayer):
 
     @torch.no_grad()
     def _history(self, groups, length: int) -> torch.Tensor:
-        B, H, D = self._shape
+        B, H, D = self._dims
         out = torch.empty(B, H, length, D, dtype=self.dtype, device=self.device)
         choice = self._choose()
         self.last_dispatch_decision = choice
@@ -192,22 +192,22 @@ class TQPackedLayer(DynamicLayer):
             return out
         if choice.backend == "fused":
             g = groups[0]
-            tq_dequant(g.codes[:, :, :length], g.norms[:, :, :length], self._tq.centroids, self._tq.Pi,
-                       self._bw, D, out=out, allow_tf32=choice.fast)
+            tq_dequant(g.codes[:, :, :length], g.norms[:, :, :length], self._quant.centroids, self._quant.Pi,
+                       self._bits, D, out=out, allow_tf32=choice.fast)
             return out
-        quants = [(self._tq, self._bw, self._reg_dim)] + \
-            ([(self._tq_out, self._out_bw, self._out_dim)] if self._out_dim else [])
-        for s in range(0, length, self._chunk):
-            e = min(s + self._chunk, length)
+        quants = [(self._quant, self._bits, self._n_regular)] + \
+            ([(self._quant_outlier, self._outlier_bits, self._n_outlier)] if self._n_outlier else [])
+        for s in range(0, length, self._span):
+            e = min(s + self._span, length)
             pieces = []
             for g, (q, bw, dim) in zip(groups, quants):
                 part = torch.empty(B, H, e - s, dim, dtype=self.dtype, device=self.device)
                 q.dequantize_into(unpack(g.codes[:, :, s:e].contiguous(), bw, dim), g.norms[:, :, s:e], part)
                 pieces.append(part)
-            if self._out_dim:
+            if self._n_outlier:
                 sl = out[:, :, s:e]
-                sl[..., ~self._mask] = pieces[0]
-                sl[..., self._mask] = pieces[1]
+                sl[..., ~self._outlier_channels] = pieces[0]
+                sl[..., self._outlier_channels] = pieces[1]
             else:
                 out[:, :, s:e] = pieces[0]
         return out
@@ -217,52 +217,52 @@ class TQPackedLayer(DynamicLayer):
         if not self.is_initialized:
             self.lazy_initialization(key_states, value_states)
         n = key_states.shape[-2]
-        if self._len + n > self._max:
-            raise RuntimeError(f"TQPackedLayer overflow: {self._len}+{n} > max_cache_len={self._max}. "
+        if self._tokens + n > self._capacity:
+            raise RuntimeError(f"TQPackedLayer overflow: {self._tokens}+{n} > max_cache_len={self._capacity}. "
                                f"Raise max_cache_len.")
         if self._fused_append_ok(key_states):
-            self._append_fused(key_states, value_states, self._len)
+            self._append_fused(key_states, value_states, self._tokens)
         else:
-            self._append_groups(key_states, self._k, self._len)
-            self._append_groups(value_states, self._v, self._len)
-        self._len += n
-        return self._history(self._k, self._len), self._history(self._v, self._len)
+            self._append_groups(key_states, self._k_groups, self._tokens)
+            self._append_groups(value_states, self._v_groups, self._tokens)
+        self._tokens += n
+        return self._history(self._k_groups, self._tokens), self._history(self._v_groups, self._tokens)
 
     def get_seq_length(self, *a, **k) -> int:
-        return self._len
+        return self._tokens
 
     def get_mask_sizes(self, query_length: int, *a, **k):
         # asked before the layer stores the query's tokens (transformers' mask preparation)
-        return self._len + query_length, 0
+        return self._tokens + query_length, 0
 
     def get_max_length(self, *a, **k) -> int:
-        return self._max
+        return self._capacity
 
     def get_max_cache_shape(self, *a, **k) -> int:
         return self.get_max_length()
 
     def reset(self) -> None:
-        self._len = 0
+        self._tokens = 0
 
     # ---------------------------------------------------------------- accounting
     def persistent_bytes(self) -> int:
         """Bytes this layer holds between steps (what limits concurrency)."""
         if not self.is_initialized:
             return 0
-        return sum(g.nbytes() for g in self._k + self._v)
+        return sum(g.nbytes() for g in self._k_groups + self._v_groups)
 
     def persistent_bytes_used(self) -> int:
         """The same, counting only the positions written so far."""
-        if not self.is_initialized or self._max == 0:
+        if not self.is_initialized or self._capacity == 0:
             return 0
-        return int(self.persistent_bytes() * self._len / self._max)
+        return int(self.persistent_bytes() * self._tokens / self._capacity)
 
     def transient_bytes(self) -> int:
         """Bytes of the dequantized K and V handed to attention each step."""
         if not self.is_initialized:
             return 0
-        B, H, D = self._shape
-        return 2 * B * H * self._len * D * torch.empty((), dtype=self.dtype).element_size()
+        B, H, D = self._dims
+        return 2 * B * H * self._tokens * D * torch.empty((), dtype=self.dtype).element_size()
 
 
 class TQPackedCache(DynamicCache):
@@ -295,7 +295,7 @@ class TQPackedCache(DynamicCache):
         l = self.layers[0]
         if not l.is_initialized:
             return float("nan")
-        bits = 8 * (l._nb_reg + l._nb_out) + 16 * (2 if l._out_dim else 1)
+        bits = 8 * (l._row_bytes + l._outlier_row_bytes) + 16 * (2 if l._n_outlier else 1)
         return bits / self.head_dim
 
     def get_seq_length(self, layer_idx: int = 0, *a, **k) -> int:
