@@ -1599,7 +1599,7 @@ __device__ __forceinline__ void scan_range16(const DecodeArgs& a, int b, int kvh
     const int pid_after = pid_of(ch + 2);
     const bool more = ch + 1 < n;
     const uint32_t left = uint32_t(n - ch) + left_after;
-    pace.publish(left, lane);
+    pace.publish(left);
     const uint32_t partner_left = pace.partner_left();
     // addresses of the next chunk's four 16-token blocks, for its K and its V rows
     uint64_t kb[4], vb[4];
@@ -1665,7 +1665,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows16_kernel(DecodeArgs a) {
   const bool live = rw.init(a, w, lane);
   store_table16<BWK, 64 * WPB>(lk, lds + Lay::k_off, tid);
   store_table16<BWV, 64 * WPB>(lv, lds + Lay::v_off, tid);
-  const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig, lane);
+  const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);
   Tab<BWK> cbk = make_tab<BWK>(lds, Lay::k_off, lane);
@@ -1675,7 +1675,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows16_kernel(DecodeArgs a) {
       scan_range16<BWK, BWV, NG, false>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile, pace, left);
     });
   }
-  pace.publish(0, lane);
+  pace.publish(0);
 }
 
 // The TF32-class row scan (allow_tf32): 4 or 6-bit K and V, one or two head groups,
@@ -1694,7 +1694,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_tf_kernel(DecodeArgs a) 
   const bool live = rw.init(a, w, lane);
   store_table_tf<BWK, 64 * WPB>(lk, lds + Lay::k_off, tid);
   store_table_tf<BWV, 64 * WPB>(lv, lds + Lay::v_off, tid);
-  const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig, lane);
+  const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   uint32_t* ptile = reinterpret_cast<uint32_t*>(lds + Lay::tiles + wig * Lay::tile_bytes);
   TabTf<BWK> cbk = make_tab_tf<BWK>(lds, Lay::k_off, lane);
@@ -1704,7 +1704,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_rows_tf_kernel(DecodeArgs a) 
       scan_range16<BWK, BWV, NG, true>(a, b, kvh, t_lo, t_hi, prow, lane, cbk, cbv, ptile, pace, left);
     });
   }
-  pace.publish(0, lane);
+  pace.publish(0);
 }
 
 // Waves per work-group: three per SIMD where the scan fits in 168 VGPRs, else two.

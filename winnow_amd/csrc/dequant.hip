@@ -285,7 +285,7 @@ __global__ __launch_bounds__(dq_waves<FAST>() * 64) __attribute__((amdgpu_waves_
   stage_dq_tab<BW, FAST>(a.cb, tab, tid);
   // the accurate mode paces the two waves of a SIMD (Pace); the fast mode's four
   // waves per SIMD come from two work-groups and are not paced
-  const Pace pace = make_pace<8>(pace_words, __builtin_amdgcn_readfirstlane(wave) & 7, lane);
+  const Pace pace = make_pace<8>(pace_words, __builtin_amdgcn_readfirstlane(wave) & 7);
   __syncthreads();
 
   const int g = lane >> 4, c16 = lane & 15;
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(dq_waves<FAST>() * 64) __attribute__((amdgpu_waves_
                   uint32_t (&nnxt)[RT], const int32_t (&pg_nxt)[RT], int32_t (&pg_after)[RT]) {
     uint32_t partner_left = 0;
     if constexpr (!FAST) {
-      pace.publish(left, lane);
+      pace.publish(left);
       partner_left = pace.partner_left();
     }
     page_ids(pass + 2 * stride, pg_after);
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(dq_waves<FAST>() * 64) __attribute__((amdgpu_waves_
     half(pass, b0, n0, b1, n1, pb, pa);
     pass += stride;
   }
-  if constexpr (!FAST) pace.publish(0, lane);
+  if constexpr (!FAST) pace.publish(0);
 }
 
 using DqFn = void (*)(DqArgs);

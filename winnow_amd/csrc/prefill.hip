@@ -459,16 +459,16 @@ struct PfLds {
 template <int BWK, int BWV, int NCT, int WPB>
 __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
   using Lay = PfLds<BWK, BWV>;
-  // the two waves of a SIMD are paced (Pace) with 4-bit V; with 6-bit V the pacing's
-  // registers made the compiler spill in the chunk loop (at Q 16: 6/6 365 -> 522 us,
-  // 4/6 561 -> 795 us), so those scans run unpaced
-  constexpr bool kPace = BWV == 4;
+  // the two waves of a SIMD are paced (Pace) except at 6/6, the one width pair that
+  // ran slower paced (config 3 at Q 16: 335-337 -> 338-349 us; config 2: 423-430 ->
+  // 284-285 us, and 4/6 at config 5: 609 -> 602 us; unpaced, 6/4 spills)
+  constexpr bool kPace = BWK == 4 || BWV == 4;
   __shared__ __align__(16) char lds[Lay::total];
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int wig = __builtin_amdgcn_readfirstlane(tid >> 6);
   stage_table_tf<BWK, 64 * WPB>(a.cb_k, lds + Lay::k_off, tid);
   stage_table_tf<BWV, 64 * WPB>(a.cb_v, lds + Lay::v_off, tid);
-  const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig, lane);
+  const Pace pace = make_pace<WPB>(reinterpret_cast<uint32_t*>(lds + Lay::pace), wig);
   __syncthreads();  // the only block-wide barrier: waves run independently from here
   const int64_t w = int64_t(pf_xcd_major(blockIdx.x, gridDim.x)) * WPB + wig;
   const int64_t items = int64_t(a.B) * a.Hkv * a.nsplit * a.ncb;
@@ -564,7 +564,7 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
       const uint32_t left = uint32_t(n - ch);
       uint32_t partner_left = 0;
       if constexpr (kPace) {
-        pace.publish(left, lane);
+        pace.publish(left);
         partner_left = pace.partner_left();
       }
       // the next chunk's tiles (the last chunk's again on the last step: its loads are
@@ -582,7 +582,7 @@ __global__ __launch_bounds__(64 * WPB) void pf_scan_kernel(PrefillArgs a) {
       pf_load_v<BWV>(a, nx, kvh, lane, V);
       if constexpr (kPace) pace_step(left, partner_left);
     }
-    if constexpr (kPace) pace.publish(0, lane);
+    if constexpr (kPace) pace.publish(0);
   }
   pf_write<NCT>(a, st, row0, lane);
 }

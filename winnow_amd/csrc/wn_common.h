@@ -130,11 +130,16 @@ __device__ __forceinline__ void wave_lds_sync() {
 // of an unpaced scan.
 // The words are read and written with relaxed work-group-scope atomics: a stale
 // value only delays the priority change by a chunk.
+// Neither step branches in the caller's code. Every lane stores the same value (a
+// store under `lane == 0` puts a divergent branch into the caller's loop), and the
+// priority choice sits inside one asm statement (s_setprio takes only an immediate;
+// a branch around two of them splits the loop body into blocks). Either branch made
+// the compiler spill in the 6-bit prefill scan, which sits at 249-253 VGPRs.
 struct Pace {
   uint32_t* mine;     // this wave's word
   uint32_t* partner;  // the word of the other wave on its SIMD
-  __device__ void publish(uint32_t left, int lane) const {
-    if (lane == 0) __hip_atomic_store(mine, left, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __device__ void publish(uint32_t left) const {
+    __hip_atomic_store(mine, left, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   __device__ uint32_t partner_left() const {
     return __hip_atomic_load(partner, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -142,18 +147,28 @@ struct Pace {
 };
 
 template <int WPB>
-__device__ __forceinline__ Pace make_pace(uint32_t* words, int wig, int lane) {
+__device__ __forceinline__ Pace make_pace(uint32_t* words, int wig) {
   static_assert(WPB == 8, "pacing pairs waves k and k ^ 4: two waves per SIMD");
   const Pace p{words + wig, words + (wig ^ 4)};
-  p.publish(0, lane);  // before the work-group barrier
+  p.publish(0);  // before the work-group barrier
   return p;
 }
 
 // Priority for the next chunk: raised while this wave has more chunks left than its
 // partner (a partner without work, or done, shows 0).
 __device__ __forceinline__ void pace_step(uint32_t left, uint32_t partner_left) {
-  if (__builtin_amdgcn_readfirstlane(partner_left) < left) __builtin_amdgcn_s_setprio(1);
-  else __builtin_amdgcn_s_setprio(0);
+  const uint32_t l = __builtin_amdgcn_readfirstlane(left), pl = __builtin_amdgcn_readfirstlane(partner_left);
+  asm volatile(
+      "s_cmp_lt_u32 %0, %1\n\t"
+      "s_cbranch_scc0 .Lpace_low%=\n\t"
+      "s_setprio 1\n\t"
+      "s_branch .Lpace_done%=\n"
+      ".Lpace_low%=:\n\t"
+      "s_setprio 0\n"
+      ".Lpace_done%=:"
+      :
+      : "s"(pl), "s"(l)
+      : "scc");
 }
 
 }  // namespace wn
