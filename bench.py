@@ -579,7 +579,7 @@ def lds_lookup_rate(waves_per_cu: int = 8, iters: int = 8192):
     import ctypes
     from winnow_amd import _lib
     r = ctypes.c_double(0.0)
-    _lib.call("wn_probe_lds_lookup_rate", waves_per_cu, iters, ctypes.byref(r))
+    _lib.probe_call("wn_probe_lds_lookup_rate", waves_per_cu, iters, ctypes.byref(r))
     return r.value
 
 

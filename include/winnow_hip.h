@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define WN_ABI_VERSION 8
+#define WN_ABI_VERSION 9
 
 /* element types of floating-point tensors crossing the ABI */
 enum { WN_F32 = 0, WN_F16 = 1, WN_BF16 = 2 };
@@ -335,15 +335,6 @@ int wn_dense_decode_attention(
     int B, int Hq, int Hkv, int D, int S, int max_pages,
     float scale, int pages_per_split, int num_splits,
     void* stream, void* ev_begin, void* ev_end);
-
-/* Measurement only; no counterpart in the reference. The rate at which one CU's
- * LDS serves the packed row scans' table lookups (8-byte reads at random addresses
- * of a pair table replicated once per lane of a half-wave, as the 4-bit scans read
- * theirs, every address moved to another row by one instruction before its read as
- * the scans form theirs; eight reads in flight per wave) with waves_per_cu waves on
- * every CU (1-16): *lookups_per_us_per_cu, timed with HIP events over `iters` x 8
- * lookups per lane on the null stream. bench.py turns it into the scans' LDS floor. */
-int wn_probe_lds_lookup_rate(int waves_per_cu, int iters, double* lookups_per_us_per_cu);
 
 #ifdef __cplusplus
 }

@@ -46,8 +46,22 @@ def test_every_declared_symbol_is_exported(lib):
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
 
 
+def test_probe_library_is_separate(lib):
+    """The measurement probe lives in libwinnow_probe.so (include/winnow_probe.h), not
+    in the product library or its header."""
+    from winnow_amd import _lib
+    assert not hasattr(lib, "wn_probe_lds_lookup_rate")
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "winnow_probe.h").read_text(), flags=re.S)
+    names = sorted(set(re.findall(r"\b(wn_[a-z_0-9]+)\s*\(", text)))
+    assert names == sorted(_lib.PROBE_SIGNATURES)
+    probe = _lib.probe_lib()
+    for name in names:
+        assert hasattr(probe, name), f"{name} declared in winnow_probe.h but not exported"
+    assert probe.wn_probe_last_error() == b""
+
+
 def test_abi_version_and_error_string(lib):
-    assert lib.wn_abi_version() == 8
+    assert lib.wn_abi_version() == 9
     assert isinstance(lib.wn_last_error(), bytes)
 
 

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libwinnow_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 WN_F32, WN_F16, WN_BF16 = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 32 << 20          # WN_NOALLOC_SCRATCH_BYTES
@@ -117,6 +117,12 @@ SIGNATURES = {
         _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,   # B Hq Hkv Q D S bwk bwv
         _c_f, _c_i,                                 # scale, num_splits
         _c_p, _c_p, _c_p]),                         # stream, ev_begin, ev_end
+}
+
+# bench.py's measurement probes (include/winnow_probe.h): libwinnow_probe.so beside
+# the product library, loaded only by probe_call
+PROBE_SIGNATURES = {
+    "wn_probe_last_error": (ctypes.c_char_p, []),
     "wn_probe_lds_lookup_rate": (_c_i, [_c_i, _c_i, ctypes.POINTER(ctypes.c_double)]),
 }
 
@@ -158,6 +164,36 @@ def lib() -> ctypes.CDLL:
                     f"{LIB_PATH} has ABI {handle.wn_abi_version()}, expected {ABI_VERSION}; rebuild it")
             _lib = handle
     return _lib
+
+
+_probe = None
+
+
+def probe_path() -> Path:
+    return LIB_PATH.with_name("libwinnow_probe.so")
+
+
+def probe_lib() -> ctypes.CDLL:
+    global _probe
+    with _lock:
+        if _probe is None:
+            path = probe_path()
+            if not path.exists():
+                raise HipLibraryMissing(f"{path} is missing: build it with `python -m winnow_amd.build`")
+            handle = ctypes.CDLL(str(path))
+            for name, (res, args) in PROBE_SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype, fn.argtypes = res, args
+            _probe = handle
+    return _probe
+
+
+def probe_call(name: str, *args) -> None:
+    """Invoke a measurement probe; raise ``WinnowHipError`` with its message on failure."""
+    handle = probe_lib()
+    rc = getattr(handle, name)(*args)
+    if rc != 0:
+        raise WinnowHipError(name, rc, handle.wn_probe_last_error().decode(errors="replace"))
 
 
 def call(name: str, *args) -> None:

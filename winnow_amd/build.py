@@ -20,6 +20,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 OUT_DIR = HERE / "_build"
 LIB = HERE / "libwinnow_hip.so"
+PROBE_LIB = HERE / "libwinnow_probe.so"  # bench.py's measurement probes (csrc/probe/), not the product
 ARCH = os.environ.get("WN_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -66,14 +67,17 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         _run(cmd)
         return obj
 
+    probe_srcs = sorted((CSRC / "probe").glob("*.hip"))
+    probe_objs = [OUT_DIR / ("probe_" + s.stem + ".o") for s in probe_srcs]
     jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        list(ex.map(compile_one, zip(srcs, objs)))
-    tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)])
-    os.replace(tmp, LIB)
-    if verbose:
-        print(f"built {LIB}", flush=True)
+        list(ex.map(compile_one, zip(srcs + probe_srcs, objs + probe_objs)))
+    for lib, lib_objs in ((LIB, objs), (PROBE_LIB, probe_objs)):
+        tmp = lib.with_suffix(".so.tmp")
+        _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, lib_objs), "-o", str(tmp)])
+        os.replace(tmp, lib)
+        if verbose:
+            print(f"built {lib}", flush=True)
     return LIB
 
 

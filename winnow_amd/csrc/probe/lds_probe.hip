@@ -8,10 +8,26 @@
 // another row with one XOR before each read (reads that repeat their addresses run
 // faster, so none does), eight reads in flight per wave, one three-input add per
 // read, from `waves` waves on every CU, timed with HIP events.
-#include "wn_common.h"
+// Built into libwinnow_probe.so (include/winnow_probe.h), not into the product library.
+#include <hip/hip_runtime.h>
 
-namespace wn {
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "../../../include/winnow_probe.h"
+
 namespace {
+
+thread_local char g_probe_error[256] = "";
+
+int fail(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_probe_error, sizeof g_probe_error, fmt, ap);
+  va_end(ap);
+  return -1;
+}
 
 __global__ __launch_bounds__(1024) void lds_lookup_probe(int iters, uint32_t* sink) {
   __shared__ __align__(16) uint8_t tab[65536];
@@ -41,24 +57,23 @@ __global__ __launch_bounds__(1024) void lds_lookup_probe(int iters, uint32_t* si
 }
 
 }  // namespace
-}  // namespace wn
+
+extern "C" const char* wn_probe_last_error(void) { return g_probe_error; }
 
 extern "C" int wn_probe_lds_lookup_rate(int waves_per_cu, int iters, double* lookups_per_us_per_cu) {
-  using namespace wn;
-  clear_error();
-  WN_REQUIRE(waves_per_cu >= 1 && waves_per_cu <= 16 && iters > 0 && lookups_per_us_per_cu, WN_E_INVALID,
-             "probe: waves_per_cu %d (1-16), iters %d", waves_per_cu, iters);
+  g_probe_error[0] = '\0';
+  if (!(waves_per_cu >= 1 && waves_per_cu <= 16 && iters > 0 && lookups_per_us_per_cu))
+    return fail("probe: waves_per_cu %d (1-16), iters %d", waves_per_cu, iters);
   int dev = 0, cus = 0;
-  WN_REQUIRE(hipGetDevice(&dev) == hipSuccess &&
-                 hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0,
-             WN_E_LAUNCH, "probe: no device");
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return fail("probe: no device");
   uint32_t* sink = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
-  WN_REQUIRE(hipMalloc(&sink, 64) == hipSuccess, WN_E_LAUNCH, "probe: hipMalloc");
-  int rc = WN_OK;
+  if (hipMalloc(&sink, 64) != hipSuccess) return fail("probe: hipMalloc");
+  int rc = 0;
   if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
-    set_error("probe: hipEventCreate");
-    rc = WN_E_LAUNCH;
+    rc = fail("probe: hipEventCreate");
   } else {
     const dim3 grid(cus), block(64 * waves_per_cu);
     hipLaunchKernelGGL(lds_lookup_probe, grid, block, 0, nullptr, 64, sink);  // warm-up
@@ -67,8 +82,7 @@ extern "C" int wn_probe_lds_lookup_rate(int waves_per_cu, int iters, double* loo
     hipEventRecord(e1, nullptr);
     float ms = 0.f;
     if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess || ms <= 0.f) {
-      set_error("probe: %s", hipGetErrorString(hipGetLastError()));
-      rc = WN_E_LAUNCH;
+      rc = fail("probe: %s", hipGetErrorString(hipGetLastError()));
     } else {
       *lookups_per_us_per_cu = double(waves_per_cu) * iters * 8 / (double(ms) * 1e3);
     }
