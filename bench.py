@@ -271,7 +271,8 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
     separate pool so the decode pool is left as it is. Timed with hipEvents over
     events the library records around the kernel on each of ``reps`` calls (and, as
     ``us_per_call_from_python``, over ``reps`` back-to-back calls of the Python wrapper,
-    whose host overhead is longer than the kernel; as ``us_per_call_graph``, over replays
+    whose host overhead is longer than the kernel; as ``us_per_call_from_python_plan``,
+    the same through the ``AppendPlan`` the cache keeps per layer; as ``us_per_call_graph``, over replays
     of a HIP graph of back-to-back calls, the GPU time per call of a serving loop that
     captures its appends); checked against the CPU
     restatement (codes under the adjudication protocol) and timed beside it.
@@ -331,6 +332,16 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
     e1.record()
     torch.cuda.synchronize()
     host_us = e0.elapsed_time(e1) / reps * 1e3
+    # the same through an AppendPlan, as PagedPackedCache.update appends a layer: the
+    # pages, norms and quantizers checked once, each call checking the step's operands
+    plan = pb.AppendPlan(kq, vq, kp, vp, kn, vn)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        plan.launch(plan.bind(kd, vd, td, sd))
+    e1.record()
+    torch.cuda.synchronize()
+    plan_us = e0.elapsed_time(e1) / reps * 1e3
     # back to back on the GPU with neither events nor Python between the calls: 32 calls
     # captured in one HIP graph (no memsets or allocations inside), replayed; the byte
     # check below reads the pages the replays wrote last
@@ -370,7 +381,8 @@ def append_bench(c, lens, table, quants, dev, reps: int = 200, n_new: int = 16):
         flips += adjudicate_codes(src, sel(gc), sel(wc), tq)
     vectors = 2 * B * Hkv * n_new
     return {"us_per_call": us, "timing": "kernel, hipEvents recorded by wn_append_kv around its launch",
-            "us_per_call_from_python": host_us, "us_per_call_graph": graph_us,
+            "us_per_call_from_python": host_us, "us_per_call_from_python_plan": plan_us,
+            "us_per_call_graph": graph_us,
             "graph": f"{graph_calls} calls per HIP graph, {graph_reps} replays between one event pair",
             "vectors_per_call": vectors, "vectors_per_s": vectors / (us * 1e-6),
             "new_tokens_per_seq": n_new, "bytes_read": 2 * B * Hkv * n_new * D * 2,

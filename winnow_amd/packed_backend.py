@@ -24,6 +24,8 @@ Names, arguments and errors are those of ``turboquant_kv/packed_backend.py``
 """
 from __future__ import annotations
 
+import ctypes
+import weakref
 from collections import Counter
 
 import torch
@@ -119,6 +121,126 @@ def _positions_in_range(start: torch.Tensor, table: torch.Tensor, n: int, num_pa
         raise pa.UnsupportedLayout(f"append: sequence {b} writes to a page outside [0, {num_pages})")
 
 
+class AppendPlan:
+    """The operands of ``append_kv`` that stay the same from one step of a layer to the
+    next: its pages, norms and quantizers, checked once here. ``bind`` checks the
+    step's K/V, page table and start positions, ``launch`` calls ``wn_append_kv`` with
+    the other arguments built once. On the decode path the wrapper's checks and the
+    conversion of forty C arguments otherwise cost more host time than the kernel
+    takes on the GPU.
+
+    Raises ``UnsupportedLayout`` for operands off the GPU or of the wrong shape."""
+
+    def __init__(self, k_tq, v_tq, k_pages: torch.Tensor, v_pages: torch.Tensor | None,
+                 k_norms: torch.Tensor, v_norms: torch.Tensor | None):
+        self.has_v = v_pages is not None or v_norms is not None or v_tq is not None
+        ops = [k_pages, k_norms] + ([v_pages, v_norms] if self.has_v else [])
+        if any(t is None for t in ops) or (self.has_v and v_tq is None):
+            raise pa.UnsupportedLayout("append: V needs its pages and norms")
+        if not all(_lib.is_hip(t) for t in ops) or len({t.device for t in ops}) != 1:
+            raise pa.UnsupportedLayout("append: every operand must be on one HIP device")
+        if k_pages.dim() != 4:
+            raise pa.UnsupportedLayout(f"append: pages must be (P, Hkv, S, NB), got {tuple(k_pages.shape)}")
+        self.device = k_pages.device
+        self.dev_index = k_pages.get_device()
+        self.P, self.Hkv, self.S = k_pages.shape[0], k_pages.shape[1], k_pages.shape[2]
+        self.D = D = k_tq.Pi.shape[-1]
+        P, Hkv, S = self.P, self.Hkv, self.S
+        sides = [(k_pages, k_norms, k_tq)] + ([(v_pages, v_norms, v_tq)] if self.has_v else [])
+        for pages, norms, tq in sides:
+            nb = packed_bytes(D, tq.bit_width)
+            if pages.dtype != torch.uint8 or pages.shape != (P, Hkv, S, nb) or pages.stride(-1) != 1 \
+                    or pages.stride(-2) != nb:
+                raise pa.UnsupportedLayout(f"append: pages must be (P={P}, Hkv={Hkv}, S={S}, NB={nb}) uint8 "
+                                           f"with contiguous rows, got {tuple(pages.shape)}")
+            if norms.dtype != torch.float16 or norms.shape != (P, Hkv, S) or norms.stride(-1) != 1:
+                raise pa.UnsupportedLayout("append: norms must be (P, Hkv, S) fp16 with a contiguous slot axis")
+            if tq.Pi.shape != (D, D) or tq.Pi.device != self.device or tq.boundaries.numel() != 2 ** tq.bit_width - 1:
+                raise pa.UnsupportedLayout("append: quantizer does not match head_dim or device")
+        self._keep = (k_tq, v_tq, k_pages, v_pages, k_norms, v_norms)   # the pointers below stay valid
+        # the C arguments of these operands, as plain integers (None: no V side)
+        self._quant = (k_tq.Pi.data_ptr(), k_tq.boundaries.data_ptr(), k_tq.bit_width,
+                       *((v_tq.Pi.data_ptr(), v_tq.boundaries.data_ptr(), v_tq.bit_width) if self.has_v
+                         else (None, None, 0)))
+        self._store = (k_pages.data_ptr(), k_pages.stride(0), k_pages.stride(1),
+                       *((v_pages.data_ptr(), v_pages.stride(0), v_pages.stride(1)) if self.has_v
+                         else (None, 0, 0)),
+                       k_norms.data_ptr(), k_norms.stride(0), k_norms.stride(1),
+                       *((v_norms.data_ptr(), v_norms.stride(0), v_norms.stride(1)) if self.has_v
+                         else (None, 0, 0)))
+
+    def bind(self, k: torch.Tensor, v: torch.Tensor | None, page_table: torch.Tensor,
+             start_pos: torch.Tensor) -> tuple:
+        """Check one step's operands; returns what ``launch`` takes (None: nothing to write)."""
+        if (v is not None) != self.has_v:
+            raise pa.UnsupportedLayout("append: V needs its pages and norms" if v is not None
+                                       else "append: the pages hold V, but no V was given")
+        for t in ((k, page_table, start_pos, v) if v is not None else (k, page_table, start_pos)):
+            if t is None or not t.is_cuda or t.get_device() != self.dev_index:
+                raise pa.UnsupportedLayout("append: every operand must be on one HIP device")
+        if k.dim() != 4:
+            raise pa.UnsupportedLayout(f"append: K must be (B, Hkv, n, D), got {tuple(k.shape)}")
+        B, Hkv, n, D = k.shape
+        if v is not None and v.shape != k.shape:
+            raise pa.UnsupportedLayout(f"append: V {tuple(v.shape)} differs from K {tuple(k.shape)}")
+        if Hkv != self.Hkv or D != self.D:
+            raise pa.UnsupportedLayout(f"append: K {tuple(k.shape)} does not match pages of {self.Hkv} kv heads "
+                                       f"and a quantizer of head_dim {self.D}")
+        if k.dtype not in _lib.DTYPE_CODE:
+            k = k.float()
+        if v is not None and v.dtype != k.dtype:
+            v = v.to(k.dtype)
+        if k.stride(-1) != 1 or (v is not None and v.stride(-1) != 1):
+            raise pa.UnsupportedLayout("append: K/V need a contiguous head_dim")
+        if page_table.dtype != torch.int32 or page_table.dim() != 2 or page_table.shape[0] != B \
+                or page_table.stride(-1) != 1:
+            raise pa.UnsupportedLayout("append: page_table must be (B, max_pages) int32 with contiguous rows")
+        if start_pos.dtype != torch.int32 or start_pos.shape != (B,):
+            raise pa.UnsupportedLayout("append: start_pos must be (B,) int32")
+        return (k, v, page_table, start_pos, B, n)
+
+    def launch(self, bound: tuple, timing_events=None) -> None:
+        k, v, page_table, start_pos, B, n = bound
+        if B == 0 or n == 0:
+            return
+        # raw integers for the pointers and strides: ctypes converts them faster than
+        # it takes c_void_p objects built in Python
+        ks = k.stride()
+        if v is not None:
+            vs = v.stride()
+            vargs = (v.data_ptr(), vs[0], vs[1], vs[2])
+        else:
+            vargs = (None, 0, 0, 0)
+        ev0, ev1 = timing_events or (None, None)
+        args = (k.data_ptr(), ks[0], ks[1], ks[2], *vargs, _lib.DTYPE_CODE[k.dtype], *self._quant,
+                page_table.data_ptr(), page_table.stride(0), start_pos.data_ptr(), *self._store,
+                B, self.Hkv, n, self.D, self.S, self.P, page_table.shape[1])
+        if torch.cuda.current_device() == self.dev_index:
+            _lib.call("wn_append_kv", *args, _lib.stream_of(self.device), ev0, ev1)
+        else:
+            with torch.cuda.device(self.device):
+                _lib.call("wn_append_kv", *args, _lib.stream_of(self.device), ev0, ev1)
+
+
+# AppendPlans of the layers of live pools, built on a layer's first append and kept
+# with the pool tensors they were built on (a plan is rebuilt if those are replaced)
+_APPEND_PLANS: "weakref.WeakKeyDictionary[PagePool, dict]" = weakref.WeakKeyDictionary()
+
+
+def _layer_append_plan(pool: PagePool, layer: int, kq, vq) -> AppendPlan:
+    plans = _APPEND_PLANS.get(pool)
+    if plans is None:
+        plans = _APPEND_PLANS[pool] = {}
+    key = (layer, id(kq), id(vq))
+    hit = plans.get(key)
+    whole = (pool.k_pages, pool.v_pages, pool.k_norms, pool.v_norms)
+    if hit is not None and all(a is b for a, b in zip(hit[0], whole)):
+        return hit[1]
+    plan = AppendPlan(kq, vq, pool.k_pages[layer], pool.v_pages[layer], pool.k_norms[layer], pool.v_norms[layer])
+    plans[key] = (whole, plan)
+    return plan
+
+
 @torch.no_grad()
 def append_kv(k: torch.Tensor, v: torch.Tensor | None, k_tq, v_tq,
               k_pages: torch.Tensor, v_pages: torch.Tensor | None,
@@ -137,64 +259,21 @@ def append_kv(k: torch.Tensor, v: torch.Tensor | None, k_tq, v_tq,
     id outside the pool. The range check reads ``page_table_host`` /
     ``start_pos_host`` when given, else copies the two small tensors to the host.
     ``timing_events`` is an optional pair of raw ``hipEvent_t`` handles recorded
-    around the kernel.
+    around the kernel. A caller that appends to the same pages step after step can
+    keep an ``AppendPlan`` and skip the checks of the parts that do not change.
     """
-    operands = [k, k_pages, k_norms, page_table, start_pos] + ([v, v_pages, v_norms] if v is not None else [])
-    if any(t is None for t in operands):
+    if v is None and (v_pages is not None or v_norms is not None):
+        v_tq = None
+    if v is not None and (v_pages is None or v_norms is None):
         raise pa.UnsupportedLayout("append: V needs its pages and norms")
-    if not all(_lib.is_hip(t) for t in operands) or len({t.device for t in operands}) != 1:
-        raise pa.UnsupportedLayout("append: every operand must be on one HIP device")
-    if k.dim() != 4:
-        raise pa.UnsupportedLayout(f"append: K must be (B, Hkv, n, D), got {tuple(k.shape)}")
-    B, Hkv, n, D = k.shape
-    if v is not None and v.shape != k.shape:
-        raise pa.UnsupportedLayout(f"append: V {tuple(v.shape)} differs from K {tuple(k.shape)}")
-    if k.dtype not in _lib.DTYPE_CODE:
-        k = k.float()
-    if v is not None and v.dtype != k.dtype:
-        v = v.to(k.dtype)
-    if k.stride(-1) != 1 or (v is not None and v.stride(-1) != 1):
-        raise pa.UnsupportedLayout("append: K/V need a contiguous head_dim")
-    if page_table.dtype != torch.int32 or page_table.dim() != 2 or page_table.shape[0] != B \
-            or page_table.stride(-1) != 1:
-        raise pa.UnsupportedLayout("append: page_table must be (B, max_pages) int32 with contiguous rows")
-    if start_pos.dtype != torch.int32 or start_pos.shape != (B,):
-        raise pa.UnsupportedLayout("append: start_pos must be (B,) int32")
-    P, S = k_pages.shape[0], k_pages.shape[2]
-    sides = [(k_pages, k_norms, k_tq)] + ([(v_pages, v_norms, v_tq)] if v is not None else [])
-    for pages, norms, tq in sides:
-        nb = packed_bytes(D, tq.bit_width)
-        if pages.dtype != torch.uint8 or pages.shape != (P, Hkv, S, nb) or pages.stride(-1) != 1 \
-                or pages.stride(-2) != nb:
-            raise pa.UnsupportedLayout(f"append: pages must be (P={P}, Hkv={Hkv}, S={S}, NB={nb}) uint8 "
-                                       f"with contiguous rows, got {tuple(pages.shape)}")
-        if norms.dtype != torch.float16 or norms.shape != (P, Hkv, S) or norms.stride(-1) != 1:
-            raise pa.UnsupportedLayout("append: norms must be (P, Hkv, S) fp16 with a contiguous slot axis")
-        if tq.Pi.shape != (D, D) or tq.Pi.device != k.device or tq.boundaries.numel() != 2 ** tq.bit_width - 1:
-            raise pa.UnsupportedLayout("append: quantizer does not match head_dim or device")
+    plan = AppendPlan(k_tq, v_tq if v is not None else None, k_pages, v_pages if v is not None else None,
+                      k_norms, v_norms if v is not None else None)
+    bound = plan.bind(k, v, page_table, start_pos)
     if check_ranges:
         table = page_table_host if page_table_host is not None else page_table.cpu()
         start = start_pos_host if start_pos_host is not None else start_pos.cpu()
-        _positions_in_range(start, table, n, P, S)
-    if B == 0 or n == 0:
-        return
-    has_v = v is not None
-    vv, vp, vn = (v, v_pages, v_norms) if has_v else (None, None, None)
-    with torch.cuda.device(k.device):
-        _lib.call(
-            "wn_append_kv",
-            _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
-            _lib.ptr(vv), *((vv.stride(0), vv.stride(1), vv.stride(2)) if has_v else (0, 0, 0)),
-            _lib.DTYPE_CODE[k.dtype],
-            _lib.ptr(k_tq.Pi), _lib.ptr(k_tq.boundaries), k_tq.bit_width,
-            _lib.ptr(v_tq.Pi) if has_v else None, _lib.ptr(v_tq.boundaries) if has_v else None,
-            v_tq.bit_width if has_v else 0,
-            _lib.ptr(page_table), page_table.stride(0), _lib.ptr(start_pos),
-            _lib.ptr(k_pages), k_pages.stride(0), k_pages.stride(1),
-            _lib.ptr(vp), *((vp.stride(0), vp.stride(1)) if has_v else (0, 0)),
-            _lib.ptr(k_norms), k_norms.stride(0), k_norms.stride(1),
-            _lib.ptr(vn), *((vn.stride(0), vn.stride(1)) if has_v else (0, 0)),
-            B, Hkv, n, D, S, P, page_table.shape[1], _lib.stream_of(k.device), *(timing_events or (None, None)))
+        _positions_in_range(start, table, bound[5], plan.P, plan.S)
+    plan.launch(bound, timing_events)
 
 
 def _append_dense_rows(src: torch.Tensor, pages: torch.Tensor, meta: PageTable) -> None:
@@ -263,10 +342,8 @@ class PagedPackedCache:
             handle = pa.DenseKV(pool.k_pages[layer_idx], pool.v_pages[layer_idx], meta.table, meta.seq, D,
                                 seq_lens_host=meta.seq_host, page_table_host=meta.table_host)
         else:
-            append_kv(key_states, value_states, self.kq, self.vq,
-                      pool.k_pages[layer_idx], pool.v_pages[layer_idx],
-                      pool.k_norms[layer_idx], pool.v_norms[layer_idx],
-                      meta.table, meta.start, check_ranges=False)    # checked once in begin()
+            plan = _layer_append_plan(pool, layer_idx, self.kq, self.vq)
+            plan.launch(plan.bind(key_states, value_states, meta.table, meta.start))  # ranges: begin()
             handle = pa.PackedKV(pool.k_pages[layer_idx], pool.k_norms[layer_idx],
                                  pool.v_pages[layer_idx], pool.v_norms[layer_idx],
                                  meta.table, meta.seq, pa.Quantizer.from_tq(self.kq),
