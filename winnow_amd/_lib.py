@@ -205,7 +205,9 @@ def call(name: str, *args) -> None:
 
 
 def ptr(t: torch.Tensor | None):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    """A tensor's device address for a ``void*`` argument (a plain integer: ctypes
+    converts it faster than a c_void_p object built in Python)."""
+    return None if t is None else t.data_ptr()
 
 
 def stream_of(device: torch.device):
