@@ -262,12 +262,11 @@ def append_kv(k: torch.Tensor, v: torch.Tensor | None, k_tq, v_tq,
     around the kernel. A caller that appends to the same pages step after step can
     keep an ``AppendPlan`` and skip the checks of the parts that do not change.
     """
-    if v is None and (v_pages is not None or v_norms is not None):
-        v_tq = None
     if v is not None and (v_pages is None or v_norms is None):
         raise pa.UnsupportedLayout("append: V needs its pages and norms")
-    plan = AppendPlan(k_tq, v_tq if v is not None else None, k_pages, v_pages if v is not None else None,
-                      k_norms, v_norms if v is not None else None)
+    has_v = v is not None   # without V, its pages, norms and quantizer are not used
+    plan = AppendPlan(k_tq, v_tq if has_v else None, k_pages, v_pages if has_v else None,
+                      k_norms, v_norms if has_v else None)
     bound = plan.bind(k, v, page_table, start_pos)
     if check_ranges:
         table = page_table_host if page_table_host is not None else page_table.cpu()
