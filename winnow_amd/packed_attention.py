@@ -25,9 +25,11 @@ Page layout (packed_attention.py:23-28):
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from winnow_amd import _lib
@@ -177,17 +179,19 @@ def check_page_ranges(seq_lens: torch.Tensor, page_table: torch.Tensor, num_page
                       page_size: int) -> None:
     """Every length fits the table and every page id a sequence reads (those below
     cdiv(len, page_size)) lies in [0, num_pages): the scan kernels index pages with
-    these ids unchecked. Copies the two small tensors to the host."""
-    lens = seq_lens.to("cpu", torch.int64)
-    if (lens < 0).any() or (lens > page_table.shape[1] * page_size).any():
+    these ids unchecked. Copies the two small tensors to the host (host mirrors are
+    read in place); the checks run in numpy, whose small-array operations cost far
+    less host time than torch's."""
+    lens = seq_lens.detach().to("cpu").numpy().astype(np.int64)
+    table = page_table.detach().to("cpu").numpy()
+    width = table.shape[1]
+    if lens.size and (lens.min() < 0 or lens.max() > width * page_size):
         raise UnsupportedLayout("seq_lens out of range for the page table")
     used = (lens + page_size - 1) // page_size
-    table = page_table.to("cpu", torch.int64)
-    width = torch.arange(table.shape[1])[None, :]
-    live = width < used[:, None]
+    live = np.arange(width)[None, :] < used[:, None]
     bad = live & ((table < 0) | (table >= num_pages))
     if bad.any():
-        b = int(bad.any(1).nonzero()[0])
+        b = int(np.flatnonzero(bad.any(1))[0])
         raise UnsupportedLayout(f"sequence {b} references a page outside [0, {num_pages})")
 
 
@@ -248,18 +252,26 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
     return pps.value, ns.value
 
 
+@functools.lru_cache(maxsize=1024)
 def workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
                     pages_per_split: int, num_splits: int) -> int:
     return int(_lib.lib().wn_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim,
                                                     pages_per_split, num_splits))
 
 
+# The library's plan depends only on the shape and on the device (its occupancy), so a
+# decode step, which asks for the same shape layer after layer, looks it up once.
+@functools.lru_cache(maxsize=1024)
+def _device_plan(device_index: int, *shape_and_options) -> tuple[int, int]:
+    with torch.cuda.device(device_index):
+        return decode_plan(*shape_and_options)
+
+
 def plan_for(q: torch.Tensor, kv: PackedKV, num_splits: int | None = None, allow_tf32: bool = False):
     """decode_plan for a query and a PackedKV handle, on the query's device."""
     B, Hq, _, D = q.shape
-    with torch.cuda.device(q.device):
-        return decode_plan(B, Hq, kv.num_kv_heads, D, kv.page_size, kv.k_quant.bit_width,
-                           kv.v_quant.bit_width, kv.page_table.shape[1], num_splits, allow_tf32)
+    return _device_plan(q.get_device(), B, Hq, kv.num_kv_heads, D, kv.page_size, kv.k_quant.bit_width,
+                        kv.v_quant.bit_width, kv.page_table.shape[1], num_splits, allow_tf32)
 
 
 def packed_decode_attention(q: torch.Tensor, kv: PackedKV, scale: float, *,

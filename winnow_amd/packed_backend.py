@@ -28,6 +28,7 @@ import ctypes
 import weakref
 from collections import Counter
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -102,22 +103,24 @@ def quantizers_for(config, bit_width: int, device, k_seed: int = 42, v_seed: int
 def _positions_in_range(start: torch.Tensor, table: torch.Tensor, n: int, num_pages: int,
                         page_size: int) -> None:
     """Every position start[b] + i (i < n) lies inside row b of the table and names a
-    page in [0, num_pages). Reads host tensors only."""
-    start = start.to(torch.int64)
+    page in [0, num_pages). Reads host tensors only (in numpy: small-array operations
+    cost far less host time there than in torch)."""
+    start = start.detach().numpy().astype(np.int64)
     width = table.shape[1]
-    if n == 0 or start.numel() == 0:
+    if n == 0 or start.size == 0:
         return
-    if (start < 0).any() or (start + n > width * page_size).any():
-        b = int(((start < 0) | (start + n > width * page_size)).nonzero()[0])
+    out = (start < 0) | (start + n > width * page_size)
+    if out.any():
+        b = int(np.flatnonzero(out)[0])
         raise pa.UnsupportedLayout(f"append: sequence {b} writes positions {int(start[b])}.."
                                    f"{int(start[b]) + n - 1} outside its {width}-page table row")
-    cols = torch.arange(width)[None, :]
+    cols = np.arange(width)[None, :]
     first, last = start // page_size, (start + n - 1) // page_size
     touched = (cols >= first[:, None]) & (cols <= last[:, None])
-    ids = table.to(torch.int64)
+    ids = table.detach().numpy()
     bad = touched & ((ids < 0) | (ids >= num_pages))
     if bad.any():
-        b = int(bad.any(1).nonzero()[0])
+        b = int(np.flatnonzero(bad.any(1))[0])
         raise pa.UnsupportedLayout(f"append: sequence {b} writes to a page outside [0, {num_pages})")
 
 
