@@ -172,6 +172,39 @@ def test_append_k_only_leaves_v_alone():
     assert torch.equal(dv.cpu(), vp0) and torch.equal(dvn.cpu().view(torch.int16), vn0.view(torch.int16))
 
 
+def test_append_plan_matches_append_kv():
+    """An AppendPlan kept across steps (as PagedPackedCache keeps one per layer) writes the
+    same bytes as append_kv, step after step, and refuses a step whose operands do not
+    match the pages it was built on."""
+    from winnow_amd import packed_attention as pa
+    from winnow_amd import packed_backend as pb
+    B, Hkv, n, D, S, bw = 4, 8, 3, 128, 16, 6
+    g = torch.Generator().manual_seed(33)
+    prior = torch.tensor([0, 17, 40, 5])
+    P, table, (kp0, vp0), (kn0, vn0) = _shuffled_pool(g, B, Hkv, 3 * n, D, S, bw, prior)
+    kq, vq = _q(bw, D, 42), _q(bw, D, 43)
+    a = [t.to(DEV) for t in (kp0, vp0, kn0, vn0)]
+    b = [t.clone() for t in a]
+    plan = pb.AppendPlan(kq, vq, *b[:2], *b[2:])
+    dtab = table.to(DEV)
+    for step in range(3):
+        start = (prior + step * n).to(torch.int32).to(DEV)
+        k = torch.randn(B, Hkv, n, D, generator=g).bfloat16().to(DEV)
+        v = torch.randn(B, Hkv, n, D, generator=g).bfloat16().to(DEV)
+        pb.append_kv(k, v, kq, vq, a[0], a[1], a[2], a[3], dtab, start)
+        plan.launch(plan.bind(k, v, dtab, start))
+    for x, y in zip(a, b):
+        assert torch.equal(x.view(torch.uint8), y.view(torch.uint8))
+    k = torch.randn(B, Hkv, n, D, device=DEV)
+    start = prior.to(torch.int32).to(DEV)
+    with pytest.raises(pa.UnsupportedLayout, match="does not match pages"):
+        plan.bind(k[:, :4], k[:, :4], dtab, start)                # fewer kv heads than the pages
+    with pytest.raises(pa.UnsupportedLayout, match="no V"):
+        plan.bind(k, None, dtab, start)                           # V pages without V
+    with pytest.raises(pa.UnsupportedLayout, match="page_table"):
+        plan.bind(k, k, dtab[:2], start)                          # table rows != batch
+
+
 def test_append_rejects_before_launch():
     """Positions past the table row, pages outside the pool and V of another shape are
     refused before any launch, and the pool is left as it was (the reference raises in
