@@ -1,8 +1,8 @@
 /* Measurement probes for bench.py: libwinnow_probe.so, built beside libwinnow_hip.so.
  *
  * Not part of the drop-in and with no counterpart in the reference: nothing in
- * libwinnow_hip.so calls these, and the reference-side bindings of INTEGRATION.md
- * do not load this library. Entry points return 0 on success and a negative status
+ * libwinnow_hip.so calls these, and a caller of the decode path has no reason to
+ * load this library. Entry points return 0 on success and a negative status
  * otherwise, with the reason in wn_probe_last_error(). */
 #ifndef WINNOW_PROBE_H
 #define WINNOW_PROBE_H
