@@ -205,6 +205,43 @@ def test_append_plan_matches_append_kv():
         plan.bind(k, k, dtab[:2], start)                          # table rows != batch
 
 
+def test_pages_from_dense_matches_oracle():
+    """pages_from_dense on the GPU (packed_attention.py:341-377): with the generator in the
+    same state, the reference's page table; codes and fp16 norms of every stored token
+    as the oracle's under the adjudication protocol; the unused bytes zero."""
+    from oracle.attention import pages_from_dense as oracle_pages
+    from winnow_amd import packed_attention as pa
+    B, Hkv, D, S = 4, 4, 128, 16
+    lens = [37, 0, 70, 16]
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(B, Hkv, max(lens), D, generator=g)
+    v = torch.randn(B, Hkv, max(lens), D, generator=g)
+    okq, ovq = oracle_quantizer(4, D, 42), oracle_quantizer(6, D, 43)
+    want = oracle_pages(k, v, lens, okq, ovq, S, num_pages=16, generator=torch.Generator().manual_seed(9))
+    got = pa.pages_from_dense(k.to(DEV), v.to(DEV), lens, _q(4, D, 42), _q(6, D, 43), S, num_pages=16,
+                              generator=torch.Generator().manual_seed(9))
+    assert torch.equal(got.page_table.cpu(), want.page_table) and torch.equal(got.page_table_host, want.page_table)
+    assert torch.equal(got.seq_lens.cpu(), want.seq_lens)
+    flips = 0
+    for src, gp, wp, gn, wn, oq, bw in ((k, got.k_pages, want.k_pages, got.k_norms, want.k_norms, okq, 4),
+                                        (v, got.v_pages, want.v_pages, got.v_norms, want.v_norms, ovq, 6)):
+        gp, gn = gp.cpu(), gn.cpu()
+        for b, L in enumerate(lens):
+            for t in range((L + S - 1) // S):
+                pid, lo, hi = int(want.page_table[b, t]), t * S, min((t + 1) * S, L)
+                x = src[b, :, lo:hi]
+                flips += adjudicate_codes(x, oapp_unpack(gp[pid, :, :hi - lo], bw, D),
+                                          oapp_unpack(wp[pid, :, :hi - lo], bw, D), oq)
+                n32 = x.float().norm(dim=-1).clamp(min=1e-10)
+                adjudicate_fp16_norms(n32, n32, gn[pid, :, :hi - lo], wn[pid, :, :hi - lo])
+                assert not gp[pid, :, hi - lo:].any() and not gn[pid, :, hi - lo:].view(torch.int16).any()
+    print(f"pages_from_dense: {flips} adjudicated code flips", flush=True)
+
+
+def oapp_unpack(packed, bw, D):
+    return torch.from_numpy(opk.unpack(packed.numpy(), bw, D))
+
+
 def test_append_rejects_before_launch():
     """Positions past the table row, pages outside the pool and V of another shape are
     refused before any launch, and the pool is left as it was (the reference raises in

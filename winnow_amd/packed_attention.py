@@ -120,6 +120,47 @@ def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
 
 
+@torch.no_grad()
+def pages_from_dense(k: torch.Tensor, v: torch.Tensor, seq_lens, k_tq, v_tq, page_size: int,
+                     num_pages: int | None = None, generator: torch.Generator | None = None) -> PackedKV:
+    """Quantize dense (B, Hkv, Lmax, D) K/V on the GPU into pages taken in a random order
+    (packed_attention.py:341-377). Unused table slots hold -1 and the bytes of a page past
+    its sequence's last token stay zero. The page order comes from
+    ``torch.randperm(total, generator)`` on the host, as the reference draws it, so a
+    generator in the same state gives the reference's page table. Each sequence's
+    history goes through one ``wn_append_kv`` launch (quantize, pack, scatter).
+
+    K and V must be on a HIP device; the handle carries host mirrors of its table and
+    lengths."""
+    from winnow_amd.packed_backend import append_kv
+
+    B, Hkv, _, D = k.shape
+    lens = [int(x) for x in seq_lens]
+    need = [(L + page_size - 1) // page_size for L in lens]
+    total = num_pages or max(sum(need), 1)
+    order = torch.randperm(total, generator=generator).tolist()
+    dev = k.device
+    kp = torch.zeros(total, Hkv, page_size, packed_bytes(D, k_tq.bit_width), dtype=torch.uint8, device=dev)
+    vp = torch.zeros(total, Hkv, page_size, packed_bytes(D, v_tq.bit_width), dtype=torch.uint8, device=dev)
+    kn = torch.zeros(total, Hkv, page_size, dtype=torch.float16, device=dev)
+    vn = torch.zeros(total, Hkv, page_size, dtype=torch.float16, device=dev)
+    table = torch.full((B, max(max(need, default=0), 1)), -1, dtype=torch.int32)
+    nxt = 0
+    for b in range(B):
+        table[b, :need[b]] = torch.tensor(order[nxt:nxt + need[b]], dtype=torch.int32)
+        nxt += need[b]
+    dtable = table.to(dev)
+    zero = torch.zeros(1, dtype=torch.int32)
+    dzero = zero.to(dev)
+    for b in range(B):
+        if lens[b]:
+            append_kv(k[b:b + 1, :, :lens[b]], v[b:b + 1, :, :lens[b]], k_tq, v_tq, kp, vp, kn, vn,
+                      dtable[b:b + 1], dzero, page_table_host=table[b:b + 1], start_pos_host=zero)
+    return PackedKV(kp, kn, vp, vn, dtable, torch.tensor(lens, dtype=torch.int32, device=dev),
+                    Quantizer.from_tq(k_tq), Quantizer.from_tq(v_tq), D,
+                    seq_lens_host=torch.tensor(lens, dtype=torch.int32), page_table_host=table)
+
+
 def check_contract(q: torch.Tensor, kv: PackedKV, *, check_ranges: bool = True) -> None:
     """Reject anything the operator does not support, with the reason (packed_attention.py:114-163).
 
