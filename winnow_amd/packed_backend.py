@@ -237,10 +237,11 @@ def _layer_append_plan(pool: PagePool, layer: int, kq, vq) -> AppendPlan:
     key = (layer, id(kq), id(vq))
     hit = plans.get(key)
     whole = (pool.k_pages, pool.v_pages, pool.k_norms, pool.v_norms)
-    if hit is not None and all(a is b for a, b in zip(hit[0], whole)):
-        return hit[1]
+    ptrs = tuple(t.data_ptr() for t in whole)   # a tensor given new storage in place gets a new plan
+    if hit is not None and hit[1] == ptrs and all(a is b for a, b in zip(hit[0], whole)):
+        return hit[2]
     plan = AppendPlan(kq, vq, pool.k_pages[layer], pool.v_pages[layer], pool.k_norms[layer], pool.v_norms[layer])
-    plans[key] = (whole, plan)
+    plans[key] = (whole, ptrs, plan)
     return plan
 
 
